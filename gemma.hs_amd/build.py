@@ -1,0 +1,101 @@
+"""Build libgemma_hip.so (hipcc, gfx950) and the oracle's liboracle.so (gcc).
+
+Usage: python gemma.hs_amd/build.py [--only lib|oracle] [-j N]
+
+Objects go to gemma.hs_amd/_build/, the library to
+gemma.hs_amd/gemma_hip/libgemma_hip.so and the oracle to
+oracle/build/liboracle.so (all git-ignored; the built .so files travel to
+the GPU box with the source tree).
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+OBJ = PKG / "_build"
+LIB = PKG / "gemma_hip" / "libgemma_hip.so"
+ORACLE_DIR = REPO / "oracle"
+ORACLE_LIB = ORACLE_DIR / "build" / "liboracle.so"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# Packed FP32 (v_pk_*_f32) is disabled for every HIP translation unit.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result", "-Wno-unused-value",
+]
+HOST_CXX = shutil.which("g++") or "c++"
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", "-Wno-unused-value",
+              "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
+        raise SystemExit(f"build failed: {cmd[-1] if cmd else ''}")
+    # surface real warnings only (the host pass warns about the packed-fp32 feature flag)
+    for line in (r.stdout + r.stderr).splitlines():
+        if "packed-fp32-ops" in line or "target-feature" in line:
+            continue
+        if "warning" in line or "error" in line:
+            sys.stderr.write(line + "\n")
+
+
+def build_lib(jobs: int = 8) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    units = []
+    for src in sorted(CSRC.iterdir()):
+        if src.suffix == ".hip":
+            units.append((src, [HIPCC, *DEVICE_FLAGS, "-x", "hip"]))
+        elif src.suffix == ".cpp":
+            units.append((src, [HOST_CXX, *HOST_FLAGS]))
+    objs = []
+
+    def compile_one(item):
+        src, cmd = item
+        obj = OBJ / (src.stem + ".o")
+        _run([*cmd, "-c", str(src), "-o", str(obj)])
+        return obj
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, units))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+          "-lpthread"])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    ORACLE_LIB.parent.mkdir(exist_ok=True)
+    cc = shutil.which("gcc") or "cc"
+    tmp = ORACLE_LIB.with_suffix(".so.tmp")
+    _run([cc, "-O2", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off", "-std=c11",
+          "-Wall", str(ORACLE_DIR / "gemma_oracle.c"), "-o", str(tmp), "-lm"])
+    os.replace(tmp, ORACLE_LIB)
+    return ORACLE_LIB
+
+
+def main(argv=None) -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", choices=["lib", "oracle"])
+    ap.add_argument("-j", type=int, default=8)
+    a = ap.parse_args(argv)
+    if a.only in (None, "oracle"):
+        print("built", build_oracle())
+    if a.only in (None, "lib"):
+        print("built", build_lib(a.j))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,200 @@
+// Host-side shared definitions of libgemma_hip: handles, device matrix
+// descriptors, error helpers.  Included by both the host .cpp files and the
+// .hip kernel file.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <functional>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/gemma_hip.h"
+
+namespace gh {
+
+int set_error(int code, const char* fmt, ...);
+
+#define GH_HIP(expr)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return ::gh::set_error(GH_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define GH_CHECK(expr)            \
+    do {                          \
+        int rc_ = (expr);         \
+        if (rc_ != GH_OK) return rc_; \
+    } while (0)
+
+uint16_t f32_to_f16_rne(float f);
+float f16_to_f32(uint16_t h, bool ftz);
+
+// Matrix storage formats on the device.
+enum Fmt : int { FMT_Q4 = 0, FMT_F32 = 1 };
+
+// Rows per tile of the device layout.  A tile stores, for every column
+// block kb, the 16-byte payloads of its 128 rows contiguously:
+//   payload[tile][kb][row 0..127]   (Q4_0: 16 code bytes = 32 weights;
+//                                    F32: 4 floats = 4 weights)
+//   scale  [tile][kb][row 0..127]   (Q4_0 only: fp16 d, FTZ applied)
+// so a wavefront reading block kb of rows lane and lane+64 issues two
+// contiguous 1 KB loads.
+constexpr int TILE_ROWS = 128;
+
+struct DMat {
+    const void* codes = nullptr;
+    const uint16_t* scales = nullptr;
+    int fmt = FMT_F32;
+    int rows = 0;   // logical rows
+    int cols = 0;   // logical columns
+    int nblk = 0;   // column blocks (cols/32 for Q4_0, cols/4 for F32)
+    int tiles = 0;  // ceil(rows / 128)
+};
+
+inline int block_cols(int fmt) { return fmt == FMT_Q4 ? 32 : 4; }
+inline int pad_rows(int r) { return (r + TILE_ROWS - 1) / TILE_ROWS * TILE_ROWS; }
+
+// Device-side per-sequence step state (one per KV handle).
+struct StepState {
+    int32_t pos;        // position of the token being processed
+    int32_t token;      // token being processed
+    int32_t last;       // argmax of the last finished step
+    int32_t start;      // position of prompt[0] (device-fed generation)
+    int32_t n_prompt;   // prompt length (device-fed generation)
+    int32_t nan_flag;   // set when a logit is NaN
+    int32_t gen_count;  // generated ids written so far
+    int32_t gen_cap;    // capacity of the ids buffer
+    unsigned long long keys[2];  // argmax keys, slot pos & 1
+};
+
+// Work split of one matvec phase: S column splits per 128-row tile, each
+// wave of a 4-wave workgroup covering at most `kbw` column blocks in one
+// register batch.
+struct Plan {
+    int S = 1;
+    int kbw = 1;
+};
+
+struct LayerDev {
+    DMat qkv, o, gu, down;
+    float* attn_norm = nullptr;
+    float* q_norm = nullptr;
+    float* k_norm = nullptr;
+    float* post_attn = nullptr;
+    float* ffn_norm = nullptr;
+    float* post_ffw = nullptr;
+    bool global = true;
+    int p_codes[4] = {0, 0, 0, 0};  // bitmask of sub-tensors uploaded
+};
+
+// Allocation with a byte count, freed by the owner.
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace gh
+
+struct gh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::recursive_mutex mu;
+    std::vector<void*> bufs;  // gh_buf_alloc allocations
+};
+
+struct gh_q4 {
+    gh_ctx* ctx = nullptr;
+    gh::DMat m;
+    void* codes = nullptr;
+    uint16_t* scales = nullptr;
+    gh::Plan plan;
+    float* part = nullptr;  // [S][rows_pad] partial sums
+};
+
+struct gh_kv;
+
+struct gh_model {
+    gh_ctx* ctx = nullptr;
+    gh_config cfg{};
+    int fmt = -1;  // projection format, fixed by the first projection upload
+    std::vector<gh::LayerDev> layers;
+    std::vector<gh::DevBuf> owned;
+    gh::DMat embd;  // token_embd (tied LM head)
+    float* out_norm = nullptr;
+    float* inv_freq = nullptr;  // [2][head_dim/2]: local, global
+    // rows of the fused QKV matrix: [q (nq*hd) | k | v], each padded to 128
+    int q_rows_pad = 0, kv_rows_pad = 0;
+    int f_pad = 0;  // padded ffn rows (gate block, then up block)
+    // plans
+    gh::Plan pa, pc, pd, pe, plm;
+    int attn_nc = 16;  // attention chunks per kv head
+    // scratch
+    float* x_res = nullptr;
+    float* x1 = nullptr;
+    float* part_qkv = nullptr;
+    float* part_o = nullptr;
+    float* part_gu = nullptr;
+    float* part_d = nullptr;
+    float* attn_part = nullptr;
+    float* logits = nullptr;
+    float* layer_out = nullptr;
+    // presence tracking
+    bool has_embd = false, has_out_norm = false;
+    std::vector<uint32_t> present;  // per layer bitmask of tensor kinds
+    std::vector<gh_kv*> kvs;
+};
+
+struct gh_kv {
+    gh_model* m = nullptr;
+    int max_seq = 0;
+    int len = 0;
+    float* k = nullptr;  // [n_layers][max_seq][nkv][hd]
+    float* v = nullptr;
+    gh::StepState* st = nullptr;
+    int32_t* d_prompt = nullptr;  // [max_seq]
+    int32_t* d_ids = nullptr;     // [max_seq]
+    gh::StepState* h_st = nullptr;  // pinned staging
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+};
+
+namespace gh {
+
+// Per-kernel event timing used by gh_profile_steps.
+struct Profiler {
+    struct Rec {
+        int kind;
+        double bytes;
+        hipEvent_t a, b;
+    };
+    std::vector<Rec> recs;
+    std::vector<std::string> names;
+    int kind_of(const char* name);
+};
+
+// kernels.hip
+int enqueue_step(gh_model* m, gh_kv* kv, hipStream_t s, Profiler* prof);
+int launch_q4_dequant(const DMat& w, float* out, hipStream_t s);
+int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* part, float* y,
+                        int softcap, float cap, hipStream_t s);
+int launch_rmsnorm(const float* x, const float* w, int n, float eps, int zc, float* y, hipStream_t s);
+int launch_qk_norm(const float* x, const float* w, int n_heads, int hd, float eps, int zc, float* y,
+                   hipStream_t s);
+int launch_rope(float* x, int n_heads, int hd, float theta, int pos, hipStream_t s);
+int launch_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
+                     int p_begin, int p_end, int n_splits, float* part, float* out, hipStream_t s);
+int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t s);
+int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
+
+// repack.cpp
+void repack_q4_0(const uint8_t* raw, int64_t rows, int64_t cols, bool ftz, uint8_t* codes,
+                 uint16_t* scales, int64_t tiles);
+void repack_f32(const float* src, int64_t rows, int64_t cols, float* dst, int64_t tiles);
+Plan choose_plan(int fmt, int tiles, int nblk, int target_wgs);
+
+}  // namespace gh

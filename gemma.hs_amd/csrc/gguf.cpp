@@ -1,0 +1,261 @@
+// GGUF v3 reader: configFromGGUF (src/Gemma/Model.hs:843-902) and
+// loadGemmaModelFromGGUF (src/Gemma/Model.hs:908-1234), with the tensor
+// format of src/Gemma/GGUF.hs:186-239 (header, metadata, tensor infos,
+// aligned data section).  Differences from the reference, on purpose:
+//  - vocab comes from the token_embd.weight shape (the reference reads the
+//    tokenizer array it skipped while parsing and so always gets 256000);
+//  - the Q4_0 projections and the tied LM head reach the device (the
+//    reference uploads zero placeholders and leaves the LM head undefined).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstring>
+#include <map>
+#include <string>
+
+#include "common.h"
+
+using namespace gh;
+
+namespace {
+
+enum : uint32_t { GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_0 = 2 };
+
+struct Meta {
+    uint32_t type = 0;
+    double num = 0.0;  // numeric scalars
+    std::string str;
+    uint64_t arr_len = 0;
+};
+
+struct TInfo {
+    std::vector<uint64_t> dims;
+    uint32_t type = 0;
+    uint64_t offset = 0;
+};
+
+struct Reader {
+    const uint8_t* p;
+    size_t n, off = 0;
+    bool ok = true;
+    bool need(size_t k) {
+        if (!ok || off + k > n) ok = false;
+        return ok;
+    }
+    template <class T>
+    T get() {
+        T v{};
+        if (need(sizeof(T))) {
+            std::memcpy(&v, p + off, sizeof(T));
+            off += sizeof(T);
+        }
+        return v;
+    }
+    std::string str() {
+        uint64_t len = get<uint64_t>();
+        if (!need(len)) return {};
+        std::string s((const char*)p + off, (size_t)len);
+        off += len;
+        return s;
+    }
+};
+
+size_t scalar_size(uint32_t t) {
+    switch (t) {
+        case 0: case 1: case 7: return 1;
+        case 2: case 3: return 2;
+        case 4: case 5: case 6: return 4;
+        case 10: case 11: case 12: return 8;
+        default: return 0;
+    }
+}
+
+double scalar_value(Reader& r, uint32_t t) {
+    switch (t) {
+        case 0: return r.get<uint8_t>();
+        case 1: return r.get<int8_t>();
+        case 2: return r.get<uint16_t>();
+        case 3: return r.get<int16_t>();
+        case 4: return r.get<uint32_t>();
+        case 5: return r.get<int32_t>();
+        case 6: return r.get<float>();
+        case 7: return r.get<uint8_t>();
+        case 10: return (double)r.get<uint64_t>();
+        case 11: return (double)r.get<int64_t>();
+        case 12: return r.get<double>();
+        default: r.ok = false; return 0;
+    }
+}
+
+bool read_value(Reader& r, uint32_t t, Meta& m) {
+    m.type = t;
+    if (t == 8) {
+        m.str = r.str();
+    } else if (t == 9) {
+        uint32_t et = r.get<uint32_t>();
+        uint64_t cnt = r.get<uint64_t>();
+        m.arr_len = cnt;
+        if (et == 8) {
+            for (uint64_t i = 0; i < cnt && r.ok; ++i) r.str();
+        } else if (et == 9) {
+            return false;  // nested arrays are not used by GGUF models
+        } else {
+            size_t es = scalar_size(et);
+            if (!es || !r.need(es * cnt)) return false;
+            r.off += es * cnt;
+        }
+    } else {
+        m.num = scalar_value(r, t);
+    }
+    return r.ok;
+}
+
+struct Mapped {
+    void* p = MAP_FAILED;
+    size_t n = 0;
+    int fd = -1;
+    ~Mapped() {
+        if (p != MAP_FAILED) munmap(p, n);
+        if (fd >= 0) close(fd);
+    }
+};
+
+struct Parsed {
+    Mapped mp;
+    std::map<std::string, Meta> meta;
+    std::map<std::string, TInfo> tens;
+    uint64_t data0 = 0;
+    gh_config cfg{};
+};
+
+// Parse header, metadata and tensor infos; build the config (configFromGGUF).
+int parse_gguf(const char* path, int32_t max_seq, Parsed& P) {
+    Mapped& mp = P.mp;
+    mp.fd = open(path, O_RDONLY);
+    if (mp.fd < 0) return set_error(GH_ERR_NOT_FOUND, "cannot open '%s'", path);
+    struct stat stt;
+    if (fstat(mp.fd, &stt) != 0 || stt.st_size < 24) return set_error(GH_ERR_FORMAT, "'%s' is too small for GGUF", path);
+    mp.n = (size_t)stt.st_size;
+    mp.p = mmap(nullptr, mp.n, PROT_READ, MAP_PRIVATE, mp.fd, 0);
+    if (mp.p == MAP_FAILED) return set_error(GH_ERR_FORMAT, "mmap of '%s' failed", path);
+    Reader r{(const uint8_t*)mp.p, mp.n};
+    // src/Gemma/GGUF.hs:244-265: magic 0x46554747, version 3
+    const uint32_t magic = r.get<uint32_t>(), version = r.get<uint32_t>();
+    if (magic != 0x46554747u) return set_error(GH_ERR_FORMAT, "invalid GGUF magic 0x%08x", magic);
+    if (version != 3) return set_error(GH_ERR_FORMAT, "unsupported GGUF version %u (only 3)", version);
+    const uint64_t n_tensors = r.get<uint64_t>(), n_kv = r.get<uint64_t>();
+    if (n_tensors > (1u << 20) || n_kv > (1u << 20)) return set_error(GH_ERR_FORMAT, "implausible GGUF counts");
+    for (uint64_t i = 0; i < n_kv; ++i) {
+        std::string key = r.str();
+        uint32_t t = r.get<uint32_t>();
+        Meta m;
+        if (!r.ok || !read_value(r, t, m)) return set_error(GH_ERR_FORMAT, "truncated GGUF metadata at '%s'", key.c_str());
+        P.meta[key] = m;
+    }
+    for (uint64_t i = 0; i < n_tensors; ++i) {
+        std::string name = r.str();
+        TInfo ti;
+        uint32_t nd = r.get<uint32_t>();
+        if (nd > 4) return set_error(GH_ERR_FORMAT, "tensor '%s' has %u dims", name.c_str(), nd);
+        for (uint32_t d = 0; d < nd; ++d) ti.dims.push_back(r.get<uint64_t>());
+        ti.type = r.get<uint32_t>();
+        ti.offset = r.get<uint64_t>();
+        if (!r.ok) return set_error(GH_ERR_FORMAT, "truncated GGUF tensor infos");
+        P.tens[name] = ti;
+    }
+    uint64_t align = 32;
+    auto ia = P.meta.find("general.alignment");
+    if (ia != P.meta.end() && ia->second.num > 0) align = (uint64_t)ia->second.num;
+    P.data0 = (r.off + align - 1) / align * align;
+
+    auto num = [&](const char* key, bool required, double def, double& v) -> int {
+        auto it = P.meta.find(key);
+        if (it == P.meta.end() || it->second.type == 8 || it->second.type == 9) {
+            if (required) return set_error(GH_ERR_FORMAT, "missing or invalid metadata: %s", key);
+            v = def;
+            return GH_OK;
+        }
+        v = it->second.num;
+        return GH_OK;
+    };
+    gh_config& c = P.cfg;
+    double v;
+    GH_CHECK(num("gemma3.block_count", true, 0, v)); c.n_layers = (int)v;
+    GH_CHECK(num("gemma3.embedding_length", true, 0, v)); c.hidden = (int)v;
+    GH_CHECK(num("gemma3.feed_forward_length", true, 0, v)); c.ffn = (int)v;
+    GH_CHECK(num("gemma3.attention.head_count", true, 0, v)); c.n_heads = (int)v;
+    GH_CHECK(num("gemma3.attention.head_count_kv", true, 0, v)); c.n_kv_heads = (int)v;
+    GH_CHECK(num("gemma3.attention.key_length", true, 0, v)); c.head_dim = (int)v;
+    GH_CHECK(num("gemma3.rope.freq_base", true, 0, v)); c.rope_theta_global = (float)v;
+    GH_CHECK(num("gemma3.attention.sliding_window", false, 512, v)); c.sliding_window = (int)v;
+    GH_CHECK(num("gemma3.attention.layer_norm_rms_epsilon", false, 1e-6, v)); c.rms_eps = (float)v;
+    c.rope_theta_local = 10000.0f;
+    c.global_every = 6;
+    c.mode = GH_MODE_GEMMA3;
+    c.flags = GH_FLAG_QK_NORM | GH_FLAG_POST_ATTN_NORM | GH_FLAG_POST_FFN_NORM | GH_FLAG_ZERO_CENTERED;
+    c.max_seq = max_seq > 0 ? max_seq : 2048;
+    auto te = P.tens.find("token_embd.weight");
+    if (te == P.tens.end() || te->second.dims.size() != 2)
+        return set_error(GH_ERR_NOT_FOUND, "missing tensor token_embd.weight");
+    c.vocab = (int)te->second.dims[1];
+    if ((int64_t)te->second.dims[0] != c.hidden)
+        return set_error(GH_ERR_FORMAT, "token_embd.weight width %llu != embedding_length %d",
+                         (unsigned long long)te->second.dims[0], c.hidden);
+    if (P.tens.count("output.weight"))
+        return set_error(GH_ERR_FORMAT, "untied output.weight is not supported (Gemma 3 ties the LM head)");
+    return GH_OK;
+}
+
+}  // namespace
+
+extern "C" int gh_gguf_inspect(const char* path, gh_config* out) {
+    if (!path || !out) return set_error(GH_ERR_INVALID, "null argument");
+    Parsed P;
+    GH_CHECK(parse_gguf(path, 0, P));
+    *out = P.cfg;
+    return GH_OK;
+}
+
+extern "C" int gh_model_load_gguf(gh_ctx* ctx, const char* path, int32_t max_seq, gh_model** out) {
+    if (!ctx || !path || !out) return set_error(GH_ERR_INVALID, "null argument");
+    Parsed P;
+    GH_CHECK(parse_gguf(path, max_seq, P));
+    gh_model* m = nullptr;
+    GH_CHECK(gh_model_create(ctx, &P.cfg, &m));
+    for (auto& kvp : P.tens) {
+        const std::string& name = kvp.first;
+        const TInfo& ti = kvp.second;
+        uint64_t ne = 1;
+        for (uint64_t d : ti.dims) ne *= d;
+        uint64_t bytes;
+        int dtype;
+        if (ti.type == GGML_F32) { bytes = ne * 4; dtype = GH_DTYPE_F32; }
+        else if (ti.type == GGML_F16) { bytes = ne * 2; dtype = GH_DTYPE_F16; }
+        else if (ti.type == GGML_Q4_0) {
+            if (ne % 32) { gh_model_destroy(m); return set_error(GH_ERR_FORMAT, "Q4_0 tensor '%s' not a multiple of 32", name.c_str()); }
+            bytes = ne / 32 * 18; dtype = GH_DTYPE_Q4_0;
+        } else {
+            gh_model_destroy(m);
+            return set_error(GH_ERR_FORMAT, "tensor '%s' has unsupported ggml type %u", name.c_str(), ti.type);
+        }
+        if (P.data0 + ti.offset + bytes > P.mp.n) {
+            gh_model_destroy(m);
+            return set_error(GH_ERR_FORMAT, "tensor '%s' extends past the end of the file", name.c_str());
+        }
+        int rc = gh_model_set_tensor(m, name.c_str(), dtype, (const uint8_t*)P.mp.p + P.data0 + ti.offset, bytes);
+        if (rc == GH_ERR_NOT_FOUND) continue;  // tensors the decode step does not use (e.g. rope_freqs)
+        if (rc != GH_OK) {
+            gh_model_destroy(m);
+            return rc;
+        }
+    }
+    int rc = gh_model_check(m);
+    if (rc != GH_OK) {
+        gh_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return GH_OK;
+}

@@ -1,0 +1,909 @@
+// Host side of the C ABI: contexts, buffers, Q4_0 tensors, op-level entry
+// points, the model / KV-cache handles and the step/generate drivers.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "common.h"
+
+using namespace gh;
+
+namespace {
+
+using Lock = std::lock_guard<std::recursive_mutex>;
+
+int ctx_bind(gh_ctx* ctx) {
+    if (!ctx) return set_error(GH_ERR_INVALID, "null context");
+    GH_HIP(hipSetDevice(ctx->device));
+    return GH_OK;
+}
+
+template <class T>
+int dev_alloc(gh_model* m, T** out, size_t count) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 16);
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return set_error(GH_ERR_OOM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    m->owned.push_back({p, bytes});
+    *out = (T*)p;
+    return GH_OK;
+}
+
+int upload(gh_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    GH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+// Allocate a device matrix in tile layout.
+int alloc_mat(gh_model* m, DMat& d, int fmt, int rows, int cols) {
+    d.fmt = fmt;
+    d.rows = rows;
+    d.cols = cols;
+    d.nblk = cols / block_cols(fmt);
+    d.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    const size_t nb = (size_t)d.tiles * d.nblk * TILE_ROWS;
+    uint8_t* codes = nullptr;
+    GH_CHECK(dev_alloc(m, &codes, nb * 16));
+    d.codes = codes;
+    if (fmt == FMT_Q4) {
+        uint16_t* sc = nullptr;
+        GH_CHECK(dev_alloc(m, &sc, nb));
+        d.scales = sc;
+    }
+    return GH_OK;
+}
+
+// Upload host rows [rows x cols] of `dtype` into the device matrix at a row
+// offset that is a multiple of TILE_ROWS.
+int upload_rows(gh_ctx* ctx, const DMat& d, int row_off, int dtype, const void* data, size_t nbytes,
+                int rows, int cols, bool ftz) {
+    if (row_off % TILE_ROWS) return set_error(GH_ERR_INVALID, "internal: unaligned row offset");
+    const int64_t tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    const int64_t t0 = row_off / TILE_ROWS;
+    if (d.fmt == FMT_Q4) {
+        if (dtype != GH_DTYPE_Q4_0) return set_error(GH_ERR_INVALID, "projection dtype differs from model format (Q4_0)");
+        if (cols % 32) return set_error(GH_ERR_INVALID, "Q4_0 tensor with cols %% 32 != 0");
+        const size_t need = (size_t)rows * (cols / 32) * 18;
+        if (nbytes != need) return set_error(GH_ERR_INVALID, "Q4_0 tensor has %zu bytes, expected %zu", nbytes, need);
+        const size_t nb = (size_t)tiles * d.nblk * TILE_ROWS;
+        std::vector<uint8_t> codes(nb * 16);
+        std::vector<uint16_t> sc(nb);
+        repack_q4_0((const uint8_t*)data, rows, cols, ftz, codes.data(), sc.data(), tiles);
+        const size_t off = (size_t)t0 * d.nblk * TILE_ROWS;
+        GH_CHECK(upload(ctx, (uint8_t*)d.codes + off * 16, codes.data(), codes.size()));
+        GH_CHECK(upload(ctx, (uint16_t*)d.scales + off, sc.data(), sc.size() * 2));
+    } else {
+        std::vector<float> f32;
+        const float* src = (const float*)data;
+        if (dtype == GH_DTYPE_F16) {
+            if (nbytes != (size_t)rows * cols * 2) return set_error(GH_ERR_INVALID, "F16 tensor size mismatch");
+            f32.resize((size_t)rows * cols);
+            for (size_t i = 0; i < f32.size(); ++i) f32[i] = f16_to_f32(((const uint16_t*)data)[i], false);
+            src = f32.data();
+        } else if (dtype == GH_DTYPE_F32) {
+            if (nbytes != (size_t)rows * cols * 4) return set_error(GH_ERR_INVALID, "F32 tensor size mismatch");
+        } else {
+            return set_error(GH_ERR_INVALID, "projection dtype differs from model format (F32)");
+        }
+        if (cols % 4) return set_error(GH_ERR_INVALID, "F32 matrix with cols %% 4 != 0");
+        std::vector<float> tiled((size_t)tiles * d.nblk * TILE_ROWS * 4);
+        repack_f32(src, rows, cols, tiled.data(), tiles);
+        const size_t off = (size_t)t0 * d.nblk * TILE_ROWS * 4;
+        GH_CHECK(upload(ctx, (float*)d.codes + off, tiled.data(), tiled.size() * 4));
+    }
+    return GH_OK;
+}
+
+int vec_to_f32(int dtype, const void* data, size_t nbytes, int n, std::vector<float>& out) {
+    out.resize(n);
+    if (dtype == GH_DTYPE_F32 && nbytes == (size_t)n * 4) {
+        std::memcpy(out.data(), data, nbytes);
+    } else if (dtype == GH_DTYPE_F16 && nbytes == (size_t)n * 2) {
+        for (int i = 0; i < n; ++i) out[i] = f16_to_f32(((const uint16_t*)data)[i], false);
+    } else {
+        return set_error(GH_ERR_INVALID, "vector tensor: dtype %d with %zu bytes, expected %d elements", dtype, nbytes, n);
+    }
+    return GH_OK;
+}
+
+enum Kind {
+    K_ATTN_NORM, K_Q, K_K, K_V, K_QN, K_KN, K_O, K_POST_ATTN, K_FFN_NORM, K_GATE, K_UP, K_DOWN, K_POST_FFN, K_N
+};
+const char* kKindNames[K_N] = {"attn_norm.weight",   "attn_q.weight",      "attn_k.weight",
+                               "attn_v.weight",      "attn_q_norm.weight", "attn_k_norm.weight",
+                               "attn_output.weight", "post_attention_norm.weight",
+                               "ffn_norm.weight",    "ffn_gate.weight",    "ffn_up.weight",
+                               "ffn_down.weight",    "post_ffw_norm.weight"};
+
+uint32_t required_mask(const gh_config& c) {
+    uint32_t m = (1u << K_ATTN_NORM) | (1u << K_Q) | (1u << K_K) | (1u << K_V) | (1u << K_O) |
+                 (1u << K_GATE) | (1u << K_UP) | (1u << K_DOWN);
+    if (c.flags & GH_FLAG_QK_NORM) m |= (1u << K_QN) | (1u << K_KN);
+    if (c.flags & GH_FLAG_POST_ATTN_NORM) m |= 1u << K_POST_ATTN;
+    if (c.flags & GH_FLAG_POST_FFN_NORM) m |= 1u << K_POST_FFN;
+    return m;
+}
+
+int env_int(const char* name, int def) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : def;
+}
+
+// Work-split plans, overridable for tuning sweeps with GH_PLAN_{A,C,D,E}_S.
+void make_plans(gh_model* m) {
+    const LayerDev& L = m->layers[0];
+    m->pa = choose_plan(m->fmt, L.qkv.tiles, L.qkv.nblk, 256);
+    m->pc = choose_plan(m->fmt, L.o.tiles, L.o.nblk, 256);
+    m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, 320);
+    m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 128);
+    m->plm = choose_plan(m->fmt, m->embd.tiles, m->embd.nblk, 1);
+    auto over = [&](Plan& p, const char* env, const DMat& d) {
+        int s = env_int(env, 0);
+        if (s > 0) {
+            Plan q = choose_plan(m->fmt, d.tiles, d.nblk, 1);
+            q.S = std::min(s, d.nblk);
+            int per_wave = ((d.nblk + q.S - 1) / q.S + 3) / 4;
+            static const int kQ4[] = {1, 2, 3, 4, 6, 9};
+            q.kbw = 9;
+            if (m->fmt == FMT_Q4) {
+                for (int k : kQ4)
+                    if (k >= per_wave) { q.kbw = k; break; }
+            } else {
+                q.kbw = 8;
+            }
+            p = q;
+        }
+    };
+    over(m->pa, "GH_PLAN_A_S", L.qkv);
+    over(m->pc, "GH_PLAN_C_S", L.o);
+    over(m->pd, "GH_PLAN_D_S", L.gu);
+    over(m->pe, "GH_PLAN_E_S", L.down);
+    m->attn_nc = std::max(1, env_int("GH_ATTN_NC", 16));
+}
+
+int ensure_scratch(gh_model* m) {
+    if (m->x_res) return GH_OK;
+    const gh_config& c = m->cfg;
+    const LayerDev& L = m->layers[0];
+    make_plans(m);
+    const int G = c.n_heads / c.n_kv_heads;
+    GH_CHECK(dev_alloc(m, &m->x_res, c.hidden));
+    GH_CHECK(dev_alloc(m, &m->x1, c.hidden));
+    GH_CHECK(dev_alloc(m, &m->part_qkv, (size_t)m->pa.S * L.qkv.tiles * TILE_ROWS));
+    GH_CHECK(dev_alloc(m, &m->part_o, (size_t)m->pc.S * L.o.tiles * TILE_ROWS));
+    GH_CHECK(dev_alloc(m, &m->part_gu, (size_t)m->pd.S * L.gu.tiles * TILE_ROWS));
+    GH_CHECK(dev_alloc(m, &m->part_d, (size_t)m->pe.S * L.down.tiles * TILE_ROWS));
+    GH_CHECK(dev_alloc(m, &m->attn_part, (size_t)c.n_kv_heads * m->attn_nc * G * (c.head_dim + 2)));
+    GH_CHECK(dev_alloc(m, &m->logits, (size_t)m->embd.tiles * TILE_ROWS));
+    GH_CHECK(dev_alloc(m, &m->layer_out, (size_t)c.n_layers * c.hidden));
+    return GH_OK;
+}
+
+int model_ready(gh_model* m) {
+    if (!m) return set_error(GH_ERR_INVALID, "null model");
+    GH_CHECK(gh_model_check(m));
+    return ensure_scratch(m);
+}
+
+int kv_graph(gh_kv* kv) {
+    if (kv->graph_exec) return GH_OK;
+    gh_model* m = kv->m;
+    hipStream_t s = m->ctx->stream;
+    GH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(m, kv, s, nullptr);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc != GH_OK) {
+        if (g) hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return set_error(GH_ERR_HIP, "stream capture failed: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&kv->graph_exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(g);
+        return set_error(GH_ERR_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+    }
+    kv->graph = g;
+    return GH_OK;
+}
+
+// One step on the stream: graph replay (default) or eager launches.
+int launch_step(gh_kv* kv) {
+    hipStream_t s = kv->m->ctx->stream;
+    if (env_int("GH_NO_GRAPH", 0)) return enqueue_step(kv->m, kv, s, nullptr);
+    GH_CHECK(kv_graph(kv));
+    GH_HIP(hipGraphLaunch(kv->graph_exec, s));
+    return GH_OK;
+}
+
+// Host -> device step state (everything but the argmax keys).
+int put_state(gh_kv* kv, int pos, int token, int start, int n_prompt, int gen_cap) {
+    StepState* h = kv->h_st;
+    h->pos = pos;
+    h->token = token;
+    h->last = -1;
+    h->start = start;
+    h->n_prompt = n_prompt;
+    h->nan_flag = 0;
+    h->gen_count = 0;
+    h->gen_cap = gen_cap;
+    GH_HIP(hipMemcpyAsync(kv->st, h, offsetof(StepState, keys), hipMemcpyHostToDevice, kv->m->ctx->stream));
+    return GH_OK;
+}
+
+int get_state(gh_kv* kv) {
+    GH_HIP(hipMemcpyAsync(kv->h_st, kv->st, sizeof(StepState), hipMemcpyDeviceToHost, kv->m->ctx->stream));
+    return GH_OK;
+}
+
+}  // namespace
+
+// =====================================================================
+// context and buffers
+// =====================================================================
+extern "C" int gh_device_count(int* n) {
+    if (!n) return set_error(GH_ERR_INVALID, "null output");
+    int c = 0;
+    hipError_t e = hipGetDeviceCount(&c);
+    if (e != hipSuccess) c = 0;
+    *n = c;
+    return GH_OK;
+}
+
+extern "C" int gh_ctx_create(int device, gh_ctx** out) {
+    if (!out) return set_error(GH_ERR_INVALID, "null output");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return set_error(GH_ERR_HIP, "no HIP device available");
+    if (device < 0 || device >= n) return set_error(GH_ERR_INVALID, "device %d out of range (%d devices)", device, n);
+    GH_HIP(hipSetDevice(device));
+    std::unique_ptr<gh_ctx> c(new gh_ctx);
+    c->device = device;
+    GH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    *out = c.release();
+    return GH_OK;
+}
+
+extern "C" int gh_ctx_destroy(gh_ctx* ctx) {
+    if (!ctx) return GH_OK;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    for (void* p : ctx->bufs) hipFree(p);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return GH_OK;
+}
+
+extern "C" int gh_ctx_sync(gh_ctx* ctx) {
+    GH_CHECK(ctx_bind(ctx));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_buf_alloc(gh_ctx* ctx, size_t bytes, void** dev) {
+    GH_CHECK(ctx_bind(ctx));
+    if (!dev) return set_error(GH_ERR_INVALID, "null output");
+    Lock lk(ctx->mu);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, std::max<size_t>(bytes, 16));
+    if (e != hipSuccess) return set_error(GH_ERR_OOM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    ctx->bufs.push_back(p);
+    *dev = p;
+    return GH_OK;
+}
+
+extern "C" int gh_buf_free(gh_ctx* ctx, void* dev) {
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    auto it = std::find(ctx->bufs.begin(), ctx->bufs.end(), dev);
+    if (it == ctx->bufs.end()) return set_error(GH_ERR_INVALID, "buffer not owned by this context");
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    GH_HIP(hipFree(dev));
+    ctx->bufs.erase(it);
+    return GH_OK;
+}
+
+extern "C" int gh_buf_upload(gh_ctx* ctx, void* dev, const void* host, size_t bytes) {
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    GH_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_buf_download(gh_ctx* ctx, void* host, const void* dev, size_t bytes) {
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    GH_HIP(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+// =====================================================================
+// Q4_0 tensors
+// =====================================================================
+extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_t cols, int flags, gh_q4** out) {
+    GH_CHECK(ctx_bind(ctx));
+    if (!raw || !out || rows <= 0 || cols <= 0 || cols % 32 || rows > (1 << 30) || cols > (1 << 24))
+        return set_error(GH_ERR_INVALID, "gh_q4_0_upload: bad shape %lld x %lld (cols %% 32 must be 0)", (long long)rows, (long long)cols);
+    Lock lk(ctx->mu);
+    std::unique_ptr<gh_q4> t(new gh_q4);
+    t->ctx = ctx;
+    DMat& d = t->m;
+    d.fmt = FMT_Q4;
+    d.rows = (int)rows;
+    d.cols = (int)cols;
+    d.nblk = (int)(cols / 32);
+    d.tiles = (int)((rows + TILE_ROWS - 1) / TILE_ROWS);
+    const size_t nb = (size_t)d.tiles * d.nblk * TILE_ROWS;
+    std::vector<uint8_t> codes(nb * 16);
+    std::vector<uint16_t> sc(nb);
+    repack_q4_0((const uint8_t*)raw, rows, cols, !(flags & GH_FLAG_IEEE_SCALES), codes.data(), sc.data(), d.tiles);
+    GH_HIP(hipMalloc(&t->codes, codes.size()));
+    GH_HIP(hipMalloc((void**)&t->scales, sc.size() * 2));
+    d.codes = t->codes;
+    d.scales = t->scales;
+    GH_CHECK(upload(ctx, t->codes, codes.data(), codes.size()));
+    GH_CHECK(upload(ctx, t->scales, sc.data(), sc.size() * 2));
+    t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, 512);
+    if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
+    *out = t.release();
+    return GH_OK;
+}
+
+extern "C" int gh_q4_0_free(gh_q4* t) {
+    if (!t) return GH_OK;
+    hipSetDevice(t->ctx->device);
+    hipStreamSynchronize(t->ctx->stream);
+    hipFree(t->codes);
+    hipFree(t->scales);
+    if (t->part) hipFree(t->part);
+    delete t;
+    return GH_OK;
+}
+
+extern "C" int gh_q4_0_dequant(gh_q4* t, float* out) {
+    if (!t || !out) return set_error(GH_ERR_INVALID, "null argument");
+    GH_CHECK(ctx_bind(t->ctx));
+    Lock lk(t->ctx->mu);
+    GH_CHECK(launch_q4_dequant(t->m, out, t->ctx->stream));
+    GH_HIP(hipStreamSynchronize(t->ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_q4_0_matvec(gh_q4* t, const float* x, float* y, int softcap, float cap) {
+    if (!t || !x || !y) return set_error(GH_ERR_INVALID, "null argument");
+    if (softcap && !(cap > 0.0f)) return set_error(GH_ERR_INVALID, "soft-cap value must be > 0");
+    GH_CHECK(ctx_bind(t->ctx));
+    Lock lk(t->ctx->mu);
+    GH_CHECK(launch_matvec_plain(t->m, t->plan, x, t->part, y, softcap, cap, t->ctx->stream));
+    GH_HIP(hipStreamSynchronize(t->ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_linear_q4(gh_ctx* ctx, const uint32_t* raw_words, size_t n_words, const float* x, int rows,
+                            int cols, int softcap, float cap, float* y) {
+    GH_CHECK(ctx_bind(ctx));
+    if (!raw_words || !x || !y || rows <= 0 || cols <= 0 || cols % 32)
+        return set_error(GH_ERR_INVALID, "gh_linear_q4: bad arguments (cols %% 32 must be 0)");
+    const size_t need = (size_t)rows * (cols / 32) * 18;
+    if (n_words * 4 < need) return set_error(GH_ERR_INVALID, "gh_linear_q4: %zu words hold fewer than %zu bytes", n_words, need);
+    gh_q4* t = nullptr;
+    GH_CHECK(gh_q4_0_upload(ctx, raw_words, rows, cols, 0, &t));
+    float *dx = nullptr, *dy = nullptr;
+    int rc = GH_OK;
+    if (hipMalloc((void**)&dx, sizeof(float) * cols) != hipSuccess || hipMalloc((void**)&dy, sizeof(float) * rows) != hipSuccess) {
+        rc = set_error(GH_ERR_OOM, "gh_linear_q4: allocation failed");
+    }
+    if (rc == GH_OK) rc = upload(ctx, dx, x, sizeof(float) * cols);
+    if (rc == GH_OK) rc = gh_q4_0_matvec(t, dx, dy, softcap, cap);
+    if (rc == GH_OK && hipMemcpy(y, dy, sizeof(float) * rows, hipMemcpyDeviceToHost) != hipSuccess)
+        rc = set_error(GH_ERR_HIP, "gh_linear_q4: download failed");
+    if (dx) hipFree(dx);
+    if (dy) hipFree(dy);
+    gh_q4_0_free(t);
+    return rc;
+}
+
+// =====================================================================
+// op-level entry points (device pointers)
+// =====================================================================
+#define OP_ENTER(ctx)             \
+    GH_CHECK(ctx_bind(ctx));      \
+    Lock lk((ctx)->mu)
+
+extern "C" int gh_rmsnorm(gh_ctx* ctx, const float* x, const float* w, int n, float eps, int zc, float* y) {
+    OP_ENTER(ctx);
+    if (!x || !w || !y || n <= 0) return set_error(GH_ERR_INVALID, "gh_rmsnorm: bad arguments");
+    GH_CHECK(launch_rmsnorm(x, w, n, eps, zc, y, ctx->stream));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_qk_norm(gh_ctx* ctx, const float* x, const float* w, int n_heads, int hd, float eps, int zc, float* y) {
+    OP_ENTER(ctx);
+    if (!x || !w || !y || n_heads <= 0) return set_error(GH_ERR_INVALID, "gh_qk_norm: bad arguments");
+    GH_CHECK(launch_qk_norm(x, w, n_heads, hd, eps, zc, y, ctx->stream));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_rope(gh_ctx* ctx, float* x, int n_heads, int hd, float theta, int pos) {
+    OP_ENTER(ctx);
+    if (!x || n_heads <= 0 || pos < 0) return set_error(GH_ERR_INVALID, "gh_rope: bad arguments");
+    GH_CHECK(launch_rope(x, n_heads, hd, theta, pos, ctx->stream));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_attention_decode(gh_ctx* ctx, const float* q, const float* kc, const float* vc, int nq, int nkv,
+                                   int hd, int p_begin, int p_end, int n_splits, float* out) {
+    OP_ENTER(ctx);
+    if (!q || !kc || !vc || !out || nkv <= 0 || nq % nkv || p_begin < 0 || p_end <= p_begin)
+        return set_error(GH_ERR_INVALID, "gh_attention_decode: bad arguments");
+    const int n_pos = p_end - p_begin;
+    if (n_splits <= 0) n_splits = std::max(1, std::min(n_pos / 64, std::max(1, 1024 / nkv)));
+    n_splits = std::min(n_splits, n_pos);
+    float* part = nullptr;
+    const int G = nq / nkv;
+    GH_HIP(hipMallocAsync((void**)&part, sizeof(float) * nkv * n_splits * G * (hd + 2), ctx->stream));
+    int rc = launch_attention(q, kc, vc, nq, nkv, hd, p_begin, p_end, n_splits, part, out, ctx->stream);
+    hipFreeAsync(part, ctx->stream);
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+extern "C" int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, float* h) {
+    OP_ENTER(ctx);
+    if (!g || !u || !h || n <= 0) return set_error(GH_ERR_INVALID, "gh_gelu_mul: bad arguments");
+    GH_CHECK(launch_gelu_mul(g, u, n, h, ctx->stream));
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx) {
+    OP_ENTER(ctx);
+    if (!v || !idx || n <= 0) return set_error(GH_ERR_INVALID, "gh_argmax: bad arguments");
+    unsigned long long* key = nullptr;
+    GH_HIP(hipMallocAsync((void**)&key, 8, ctx->stream));
+    int rc = launch_argmax(v, n, key, ctx->stream);
+    unsigned long long h = 0;
+    if (rc == GH_OK) {
+        GH_HIP(hipMemcpyAsync(&h, key, 8, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    hipFreeAsync(key, ctx->stream);
+    GH_HIP(hipStreamSynchronize(ctx->stream));
+    if (rc == GH_OK) *idx = (int32_t)(0xFFFFFFFFu - (uint32_t)(h & 0xFFFFFFFFull));
+    return rc;
+}
+
+// =====================================================================
+// configs and models
+// =====================================================================
+extern "C" int gh_config_preset(const char* name, gh_config* out) {
+    if (!name || !out) return set_error(GH_ERR_INVALID, "null argument");
+    gh_config c{};
+    c.rms_eps = 1e-6f;
+    c.mode = GH_MODE_GEMMA3;
+    c.flags = GH_FLAG_QK_NORM | GH_FLAG_POST_ATTN_NORM | GH_FLAG_POST_FFN_NORM | GH_FLAG_ZERO_CENTERED;
+    if (!std::strcmp(name, "tiny")) {
+        c.vocab = 1024; c.hidden = 128; c.n_layers = 2; c.n_heads = 4; c.n_kv_heads = 1;
+        c.head_dim = 32; c.ffn = 512; c.max_seq = 2048; c.sliding_window = 0; c.global_every = 0;
+        c.rope_theta_local = 10000.0f; c.rope_theta_global = 10000.0f;
+    } else if (!std::strcmp(name, "gemma3-1b")) {
+        // src/Gemma/Model.hs:213-237 plus the Gemma-3 5:1 local/global layout
+        c.vocab = 262144; c.hidden = 1152; c.n_layers = 26; c.n_heads = 4; c.n_kv_heads = 1;
+        c.head_dim = 256; c.ffn = 6912; c.max_seq = 2048; c.sliding_window = 512; c.global_every = 6;
+        c.rope_theta_local = 10000.0f; c.rope_theta_global = 1000000.0f;
+    } else if (!std::strcmp(name, "gemma3-4b")) {
+        c.vocab = 262144; c.hidden = 2560; c.n_layers = 34; c.n_heads = 8; c.n_kv_heads = 4;
+        c.head_dim = 256; c.ffn = 10240; c.max_seq = 8192; c.sliding_window = 1024; c.global_every = 6;
+        c.rope_theta_local = 10000.0f; c.rope_theta_global = 1000000.0f;
+    } else {
+        return set_error(GH_ERR_NOT_FOUND, "unknown preset '%s'", name);
+    }
+    *out = c;
+    return GH_OK;
+}
+
+extern "C" int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out) {
+    GH_CHECK(ctx_bind(ctx));
+    if (!cfg || !out) return set_error(GH_ERR_INVALID, "null argument");
+    const gh_config& c = *cfg;
+    if (c.vocab <= 0 || c.hidden <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.ffn <= 0 ||
+        c.head_dim <= 0 || c.max_seq <= 0)
+        return set_error(GH_ERR_INVALID, "config: dimensions must be positive");
+    if (c.n_heads % c.n_kv_heads) return set_error(GH_ERR_INVALID, "config: n_heads %% n_kv_heads != 0");
+    const int G = c.n_heads / c.n_kv_heads;
+    if (!(c.head_dim == 32 || c.head_dim == 128 || c.head_dim == 256) || !(G == 1 || G == 2 || G == 4 || G == 8))
+        return set_error(GH_ERR_INVALID, "config: head_dim %d / group %d not supported", c.head_dim, G);
+    if (c.hidden % 32 || c.ffn % 32 || (c.n_heads * c.head_dim) % 32)
+        return set_error(GH_ERR_INVALID, "config: hidden, ffn and n_heads*head_dim must be multiples of 32");
+    if (c.mode != GH_MODE_GEMMA3 && c.mode != GH_MODE_REF) return set_error(GH_ERR_INVALID, "config: bad mode");
+    Lock lk(ctx->mu);
+    std::unique_ptr<gh_model> m(new gh_model);
+    m->ctx = ctx;
+    m->cfg = c;
+    m->layers.resize(c.n_layers);
+    m->present.assign(c.n_layers, 0);
+    m->q_rows_pad = pad_rows(c.n_heads * c.head_dim);
+    m->kv_rows_pad = pad_rows(c.n_kv_heads * c.head_dim);
+    m->f_pad = pad_rows(c.ffn);
+    for (int l = 0; l < c.n_layers; ++l)
+        m->layers[l].global = c.global_every <= 0 || ((l + 1) % c.global_every) == 0;
+    // RoPE inverse frequencies, ropeShader's formula (AttentionGPU.hs:98-99)
+    std::vector<float> f(c.head_dim);
+    for (int i = 0; i < c.head_dim / 2; ++i) {
+        const float e = (float)(i * 2) / (float)c.head_dim;
+        f[i] = 1.0f / powf(c.rope_theta_local, e);
+        f[c.head_dim / 2 + i] = 1.0f / powf(c.rope_theta_global, e);
+    }
+    GH_CHECK(dev_alloc(m.get(), &m->inv_freq, c.head_dim));
+    GH_CHECK(upload(ctx, m->inv_freq, f.data(), sizeof(float) * c.head_dim));
+    *out = m.release();
+    return GH_OK;
+}
+
+extern "C" int gh_model_destroy(gh_model* m) {
+    if (!m) return GH_OK;
+    hipSetDevice(m->ctx->device);
+    hipStreamSynchronize(m->ctx->stream);
+    for (gh_kv* kv : std::vector<gh_kv*>(m->kvs)) gh_kv_destroy(kv);
+    for (auto& b : m->owned) hipFree(b.p);
+    delete m;
+    return GH_OK;
+}
+
+static int ensure_fmt(gh_model* m, int dtype) {
+    const int want = dtype == GH_DTYPE_Q4_0 ? FMT_Q4 : FMT_F32;
+    if (m->fmt < 0) {
+        m->fmt = want;
+        const gh_config& c = m->cfg;
+        for (auto& L : m->layers) {
+            GH_CHECK(alloc_mat(m, L.qkv, want, m->q_rows_pad + 2 * m->kv_rows_pad, c.hidden));
+            GH_CHECK(alloc_mat(m, L.o, want, c.hidden, c.n_heads * c.head_dim));
+            GH_CHECK(alloc_mat(m, L.gu, want, 2 * m->f_pad, c.hidden));
+            GH_CHECK(alloc_mat(m, L.down, want, c.hidden, c.ffn));
+        }
+        GH_CHECK(alloc_mat(m, m->embd, want, c.vocab, c.hidden));
+    } else if (m->fmt != want) {
+        return set_error(GH_ERR_INVALID, "all projections and the embedding must share one format");
+    }
+    return GH_OK;
+}
+
+extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, const void* data, size_t nbytes) {
+    if (!m || !name || !data) return set_error(GH_ERR_INVALID, "null argument");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    const gh_config& c = m->cfg;
+    const bool ftz = !(c.flags & GH_FLAG_IEEE_SCALES);
+    std::vector<float> v;
+    if (!std::strcmp(name, "token_embd.weight")) {
+        GH_CHECK(ensure_fmt(m, dtype));
+        GH_CHECK(upload_rows(m->ctx, m->embd, 0, dtype, data, nbytes, c.vocab, c.hidden, ftz));
+        m->has_embd = true;
+        return GH_OK;
+    }
+    if (!std::strcmp(name, "output_norm.weight")) {
+        GH_CHECK(vec_to_f32(dtype, data, nbytes, c.hidden, v));
+        if (!m->out_norm) GH_CHECK(dev_alloc(m, &m->out_norm, c.hidden));
+        GH_CHECK(upload(m->ctx, m->out_norm, v.data(), v.size() * 4));
+        m->has_out_norm = true;
+        return GH_OK;
+    }
+    if (std::strncmp(name, "blk.", 4))
+        return set_error(GH_ERR_NOT_FOUND, "unknown tensor '%s'", name);
+    char* end = nullptr;
+    long l = std::strtol(name + 4, &end, 10);
+    if (!end || *end != '.' || l < 0 || l >= c.n_layers) return set_error(GH_ERR_NOT_FOUND, "bad layer in '%s'", name);
+    int kind = -1;
+    for (int k = 0; k < K_N; ++k)
+        if (!std::strcmp(end + 1, kKindNames[k])) kind = k;
+    if (kind < 0) return set_error(GH_ERR_NOT_FOUND, "unknown tensor '%s'", name);
+    LayerDev& L = m->layers[l];
+    const int H = c.hidden, hd = c.head_dim;
+    auto vec = [&](float*& dst, int n) -> int {
+        GH_CHECK(vec_to_f32(dtype, data, nbytes, n, v));
+        if (!dst) GH_CHECK(dev_alloc(m, &dst, n));
+        return upload(m->ctx, dst, v.data(), (size_t)n * 4);
+    };
+    switch (kind) {
+        case K_ATTN_NORM: GH_CHECK(vec(L.attn_norm, H)); break;
+        case K_QN: GH_CHECK(vec(L.q_norm, hd)); break;
+        case K_KN: GH_CHECK(vec(L.k_norm, hd)); break;
+        case K_POST_ATTN: GH_CHECK(vec(L.post_attn, H)); break;
+        case K_FFN_NORM: GH_CHECK(vec(L.ffn_norm, H)); break;
+        case K_POST_FFN: GH_CHECK(vec(L.post_ffw, H)); break;
+        case K_Q:
+            GH_CHECK(ensure_fmt(m, dtype));
+            GH_CHECK(upload_rows(m->ctx, L.qkv, 0, dtype, data, nbytes, c.n_heads * hd, H, ftz));
+            break;
+        case K_K:
+            GH_CHECK(ensure_fmt(m, dtype));
+            GH_CHECK(upload_rows(m->ctx, L.qkv, m->q_rows_pad, dtype, data, nbytes, c.n_kv_heads * hd, H, ftz));
+            break;
+        case K_V:
+            GH_CHECK(ensure_fmt(m, dtype));
+            GH_CHECK(upload_rows(m->ctx, L.qkv, m->q_rows_pad + m->kv_rows_pad, dtype, data, nbytes, c.n_kv_heads * hd, H, ftz));
+            break;
+        case K_O:
+            GH_CHECK(ensure_fmt(m, dtype));
+            GH_CHECK(upload_rows(m->ctx, L.o, 0, dtype, data, nbytes, H, c.n_heads * hd, ftz));
+            break;
+        case K_GATE:
+            GH_CHECK(ensure_fmt(m, dtype));
+            GH_CHECK(upload_rows(m->ctx, L.gu, 0, dtype, data, nbytes, c.ffn, H, ftz));
+            break;
+        case K_UP:
+            GH_CHECK(ensure_fmt(m, dtype));
+            GH_CHECK(upload_rows(m->ctx, L.gu, m->f_pad, dtype, data, nbytes, c.ffn, H, ftz));
+            break;
+        case K_DOWN:
+            GH_CHECK(ensure_fmt(m, dtype));
+            GH_CHECK(upload_rows(m->ctx, L.down, 0, dtype, data, nbytes, H, c.ffn, ftz));
+            break;
+    }
+    m->present[l] |= 1u << kind;
+    return GH_OK;
+}
+
+extern "C" int gh_model_check(gh_model* m) {
+    if (!m) return set_error(GH_ERR_INVALID, "null model");
+    if (!m->has_embd) return set_error(GH_ERR_NOT_FOUND, "missing tensor token_embd.weight");
+    if (!m->has_out_norm) return set_error(GH_ERR_NOT_FOUND, "missing tensor output_norm.weight");
+    const uint32_t need = required_mask(m->cfg);
+    for (int l = 0; l < m->cfg.n_layers; ++l) {
+        const uint32_t miss = need & ~m->present[l];
+        if (miss) {
+            for (int k = 0; k < K_N; ++k)
+                if (miss & (1u << k)) return set_error(GH_ERR_NOT_FOUND, "missing tensor blk.%d.%s", l, kKindNames[k]);
+        }
+        if (!m->layers[l].ffn_norm && !m->layers[l].post_attn)
+            return set_error(GH_ERR_NOT_FOUND, "missing tensor blk.%d.ffn_norm.weight", l);
+    }
+    return GH_OK;
+}
+
+extern "C" int gh_model_config(gh_model* m, gh_config* out) {
+    if (!m || !out) return set_error(GH_ERR_INVALID, "null argument");
+    *out = m->cfg;
+    return GH_OK;
+}
+
+// =====================================================================
+// KV cache handle
+// =====================================================================
+extern "C" int gh_kv_create(gh_model* m, int32_t max_seq, gh_kv** out) {
+    if (!m || !out) return set_error(GH_ERR_INVALID, "null argument");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    if (max_seq <= 0) max_seq = m->cfg.max_seq;
+    const gh_config& c = m->cfg;
+    std::unique_ptr<gh_kv> kv(new gh_kv);
+    kv->m = m;
+    kv->max_seq = max_seq;
+    const size_t n = (size_t)c.n_layers * max_seq * c.n_kv_heads * c.head_dim;
+    hipError_t e1 = hipMalloc((void**)&kv->k, n * 4);
+    hipError_t e2 = hipMalloc((void**)&kv->v, n * 4);
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+        if (kv->k) hipFree(kv->k);
+        if (kv->v) hipFree(kv->v);
+        return set_error(GH_ERR_OOM, "KV cache of %zu bytes does not fit", 2 * n * 4);
+    }
+    GH_HIP(hipMalloc((void**)&kv->st, sizeof(StepState)));
+    GH_HIP(hipMalloc((void**)&kv->d_prompt, sizeof(int32_t) * max_seq));
+    GH_HIP(hipMalloc((void**)&kv->d_ids, sizeof(int32_t) * max_seq));
+    GH_HIP(hipHostMalloc((void**)&kv->h_st, sizeof(StepState), hipHostMallocDefault));
+    std::memset(kv->h_st, 0, sizeof(StepState));
+    GH_HIP(hipMemcpy(kv->st, kv->h_st, sizeof(StepState), hipMemcpyHostToDevice));
+    m->kvs.push_back(kv.get());
+    *out = kv.release();
+    return GH_OK;
+}
+
+extern "C" int gh_kv_destroy(gh_kv* kv) {
+    if (!kv) return GH_OK;
+    gh_model* m = kv->m;
+    hipSetDevice(m->ctx->device);
+    hipStreamSynchronize(m->ctx->stream);
+    if (kv->graph_exec) hipGraphExecDestroy(kv->graph_exec);
+    if (kv->graph) hipGraphDestroy(kv->graph);
+    hipFree(kv->k);
+    hipFree(kv->v);
+    hipFree(kv->st);
+    hipFree(kv->d_prompt);
+    hipFree(kv->d_ids);
+    hipHostFree(kv->h_st);
+    m->kvs.erase(std::remove(m->kvs.begin(), m->kvs.end(), kv), m->kvs.end());
+    delete kv;
+    return GH_OK;
+}
+
+extern "C" int gh_kv_reset(gh_kv* kv) {
+    if (!kv) return set_error(GH_ERR_INVALID, "null kv");
+    kv->len = 0;
+    return GH_OK;
+}
+
+extern "C" int gh_kv_length(gh_kv* kv, int32_t* len) {
+    if (!kv || !len) return set_error(GH_ERR_INVALID, "null argument");
+    *len = kv->len;
+    return GH_OK;
+}
+
+// =====================================================================
+// step / generate / bench / profile
+// =====================================================================
+extern "C" int gh_step(gh_model* m, gh_kv* kv, int32_t token, float* logits, float* layer_out, int32_t* argmax_out) {
+    if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    const gh_config& c = m->cfg;
+    if (token < 0 || token >= c.vocab) return set_error(GH_ERR_INVALID, "token %d outside [0, %d)", token, c.vocab);
+    if (kv->len >= kv->max_seq) return set_error(GH_ERR_RANGE, "KV cache full (%d positions)", kv->max_seq);
+    hipStream_t s = m->ctx->stream;
+    GH_CHECK(put_state(kv, kv->len, token, kv->len, 0, 0));
+    GH_CHECK(launch_step(kv));
+    GH_CHECK(get_state(kv));
+    if (logits) GH_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * c.vocab, hipMemcpyDeviceToHost, s));
+    if (layer_out)
+        GH_HIP(hipMemcpyAsync(layer_out, m->layer_out, sizeof(float) * c.n_layers * c.hidden, hipMemcpyDeviceToHost, s));
+    GH_HIP(hipStreamSynchronize(s));
+    kv->len += 1;
+    if (argmax_out) *argmax_out = kv->h_st->last;
+    if (kv->h_st->nan_flag) return set_error(GH_ERR_NAN, "NaN in logits at position %d", kv->len - 1);
+    return GH_OK;
+}
+
+static int run_device_fed(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_before,
+                          int32_t n_timed, int32_t gen_cap, float* ms_out, int32_t* ids_out) {
+    const gh_config& c = m->cfg;
+    if (!prompt || n_prompt <= 0) return set_error(GH_ERR_INVALID, "empty prompt");
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab) return set_error(GH_ERR_INVALID, "prompt token %d out of range", prompt[i]);
+    const long long steps = (long long)n_before + n_timed;
+    if (kv->len + steps > kv->max_seq)
+        return set_error(GH_ERR_RANGE, "generation needs %lld positions from %d; KV holds %d", steps, kv->len, kv->max_seq);
+    hipStream_t s = m->ctx->stream;
+    GH_HIP(hipMemcpyAsync(kv->d_prompt, prompt, sizeof(int32_t) * n_prompt, hipMemcpyHostToDevice, s));
+    GH_CHECK(put_state(kv, kv->len, prompt[0], kv->len, n_prompt, gen_cap));
+    for (int i = 0; i < n_before; ++i) GH_CHECK(launch_step(kv));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (ms_out) {
+        GH_HIP(hipStreamSynchronize(s));
+        GH_HIP(hipDeviceSynchronize());
+        GH_HIP(hipEventCreate(&e0));
+        GH_HIP(hipEventCreate(&e1));
+        GH_HIP(hipEventRecord(e0, s));
+    }
+    for (int i = 0; i < n_timed; ++i) GH_CHECK(launch_step(kv));
+    if (ms_out) GH_HIP(hipEventRecord(e1, s));
+    GH_CHECK(get_state(kv));
+    GH_HIP(hipStreamSynchronize(s));
+    if (ms_out) {
+        GH_HIP(hipDeviceSynchronize());
+        float ms = 0.0f;
+        GH_HIP(hipEventElapsedTime(&ms, e0, e1));
+        *ms_out = ms;
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+    }
+    kv->len += (int)steps;
+    const int got = kv->h_st->gen_count;
+    if (ids_out && got > 0) GH_HIP(hipMemcpy(ids_out, kv->d_ids, sizeof(int32_t) * got, hipMemcpyDeviceToHost));
+    if (kv->h_st->nan_flag) return set_error(GH_ERR_NAN, "NaN in logits during generation");
+    if (got != gen_cap) return set_error(GH_ERR_STATE, "generated %d ids, expected %d", got, gen_cap);
+    return GH_OK;
+}
+
+extern "C" int gh_generate(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
+                           int32_t* ids_out) {
+    if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
+    if (n_gen <= 0 || !ids_out) return set_error(GH_ERR_INVALID, "n_gen must be > 0 with an output buffer");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    return run_device_fed(m, kv, prompt, n_prompt, n_prompt + n_gen - 1, 0, n_gen, nullptr, ids_out);
+}
+
+extern "C" int gh_bench_decode(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_warmup,
+                               int32_t n_steps, float* ms_out, int32_t* ids_out) {
+    if (!m || !kv || kv->m != m || !ms_out) return set_error(GH_ERR_INVALID, "bad arguments");
+    if (n_warmup < 0 || n_steps <= 0) return set_error(GH_ERR_INVALID, "bad step counts");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    return run_device_fed(m, kv, prompt, n_prompt, n_prompt + n_warmup, n_steps, n_warmup + n_steps + 1, ms_out,
+                          ids_out);
+}
+
+extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kernel_stat* stats, int32_t max_stats,
+                                int32_t* n_stats) {
+    if (!m || !kv || kv->m != m || !stats || !n_stats || n_steps <= 0)
+        return set_error(GH_ERR_INVALID, "bad arguments");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    if (kv->len + n_steps > kv->max_seq) return set_error(GH_ERR_RANGE, "KV cache full");
+    hipStream_t s = m->ctx->stream;
+    int tok = kv->h_st->last >= 0 && kv->h_st->last < m->cfg.vocab ? kv->h_st->last : 0;
+    GH_CHECK(put_state(kv, kv->len, tok, kv->len, 0, 0));
+    Profiler prof;
+    int rc = GH_OK;
+    for (int i = 0; i < n_steps && rc == GH_OK; ++i) {
+        rc = enqueue_step(m, kv, s, &prof);
+        kv->len += 1;  // position advances on device inside the step
+    }
+    GH_CHECK(get_state(kv));
+    GH_HIP(hipStreamSynchronize(s));
+    std::vector<double> tot(prof.names.size(), 0.0), bytes(prof.names.size(), 0.0);
+    std::vector<int> cnt(prof.names.size(), 0);
+    for (auto& r : prof.recs) {
+        float ms = 0.0f;
+        hipEventElapsedTime(&ms, r.a, r.b);
+        tot[r.kind] += ms;
+        bytes[r.kind] += r.bytes;
+        cnt[r.kind] += 1;
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+    }
+    if (rc != GH_OK) return rc;
+    const int n = std::min<int>((int)prof.names.size(), max_stats);
+    for (int i = 0; i < n; ++i) {
+        std::memset(&stats[i], 0, sizeof(gh_kernel_stat));
+        std::snprintf(stats[i].name, sizeof(stats[i].name), "%s", prof.names[i].c_str());
+        stats[i].launches = cnt[i];
+        stats[i].total_ms = tot[i];
+        stats[i].bytes = cnt[i] ? bytes[i] / cnt[i] : 0.0;
+    }
+    *n_stats = n;
+    return GH_OK;
+}
+
+// =====================================================================
+// synthetic model
+// =====================================================================
+extern "C" int gh_synth_model(gh_model* m, uint64_t seed, int q4, float w_sigma, float scale_sigma, float norm_sigma) {
+    if (!m) return set_error(GH_ERR_INVALID, "null model");
+    const gh_config& c = m->cfg;
+    const int H = c.hidden, hd = c.head_dim, F = c.ffn;
+    auto mat = [&](const std::string& name, int rows, int cols) -> int {
+        if (q4) {
+            std::vector<uint8_t> raw((size_t)rows * (cols / 32) * 18);
+            GH_CHECK(gh_synth_q4_0(seed, name.c_str(), scale_sigma, rows, cols, raw.data()));
+            return gh_model_set_tensor(m, name.c_str(), GH_DTYPE_Q4_0, raw.data(), raw.size());
+        }
+        std::vector<float> w((size_t)rows * cols);
+        GH_CHECK(gh_synth_f32(seed, name.c_str(), w_sigma, w.data(), w.size()));
+        return gh_model_set_tensor(m, name.c_str(), GH_DTYPE_F32, w.data(), w.size() * 4);
+    };
+    auto vec = [&](const std::string& name, int n) -> int {
+        std::vector<float> w(n);
+        GH_CHECK(gh_synth_f32(seed, name.c_str(), norm_sigma, w.data(), n));
+        return gh_model_set_tensor(m, name.c_str(), GH_DTYPE_F32, w.data(), w.size() * 4);
+    };
+    GH_CHECK(mat("token_embd.weight", c.vocab, H));
+    GH_CHECK(vec("output_norm.weight", H));
+    for (int l = 0; l < c.n_layers; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        GH_CHECK(vec(p + "attn_norm.weight", H));
+        GH_CHECK(mat(p + "attn_q.weight", c.n_heads * hd, H));
+        GH_CHECK(mat(p + "attn_k.weight", c.n_kv_heads * hd, H));
+        GH_CHECK(mat(p + "attn_v.weight", c.n_kv_heads * hd, H));
+        GH_CHECK(vec(p + "attn_q_norm.weight", hd));
+        GH_CHECK(vec(p + "attn_k_norm.weight", hd));
+        GH_CHECK(mat(p + "attn_output.weight", H, c.n_heads * hd));
+        GH_CHECK(vec(p + "post_attention_norm.weight", H));
+        GH_CHECK(vec(p + "ffn_norm.weight", H));
+        GH_CHECK(mat(p + "ffn_gate.weight", F, H));
+        GH_CHECK(mat(p + "ffn_up.weight", F, H));
+        GH_CHECK(mat(p + "ffn_down.weight", H, F));
+        GH_CHECK(vec(p + "post_ffw_norm.weight", H));
+    }
+    return GH_OK;
+}

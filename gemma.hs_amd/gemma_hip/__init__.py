@@ -1,0 +1,446 @@
+"""Python host binding of libgemma_hip (MI355X decode step of gemma.hs).
+
+The names mirror the reference's Haskell API so that code and tests read
+alike:
+
+  Gemma.Model.GemmaConfig / gemma3_1BConfig   -> GemmaConfig, preset()
+  Gemma.Model.loadGemmaModelFromGGUF          -> GemmaModel.load_gguf
+  Gemma.Model.runGemmaInferenceCached         -> runGemmaInferenceCached
+  Gemma.Model.runGemmaInferenceCachedWithLayer0 -> runGemmaInferenceCachedWithLayer0
+  Gemma.KVCache (initKVCache, cacheLength)    -> KVCache
+  Gemma.Layers.LinearQ4.runLinearQ4           -> runLinearQ4
+  app/Main.hs sampleToken                     -> on-device argmax inside the step
+
+Everything runs through the C ABI of include/gemma_hip.h; there is no CPU
+fallback: without libgemma_hip.so (or without a GPU) the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q4_0, FLAG_IEEE_SCALES, FLAG_POST_ATTN_NORM,
+                   FLAG_POST_FFN_NORM, FLAG_QK_NORM, FLAG_ZERO_CENTERED, MODE_GEMMA3, MODE_REF,
+                   GemmaHipError, GhConfig, GhKernelStat, check, lib)
+
+GemmaConfig = GhConfig
+
+__all__ = [
+    "GemmaConfig", "GemmaHipError", "Context", "DeviceBuffer", "Q4Tensor", "GemmaModel", "KVCache",
+    "preset", "runLinearQ4", "runGemmaInferenceCached", "runGemmaInferenceCachedWithLayer0",
+    "generate", "bench_decode", "profile_steps", "synth_f32", "synth_q4_0", "synth_tokens",
+    "tensor_list", "synth_tensors", "device_count", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q4_0",
+    "MODE_GEMMA3", "MODE_REF", "FLAG_QK_NORM", "FLAG_POST_ATTN_NORM", "FLAG_POST_FFN_NORM",
+    "FLAG_ZERO_CENTERED", "FLAG_IEEE_SCALES",
+]
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data)
+
+
+def device_count() -> int:
+    n = C.c_int32()
+    check(lib().gh_device_count(C.byref(n)))
+    return n.value
+
+
+def preset(name: str) -> GemmaConfig:
+    """Config presets: 'tiny', 'gemma3-1b' (src/Gemma/Model.hs:213-237), 'gemma3-4b'."""
+    c = GemmaConfig()
+    check(lib().gh_config_preset(name.encode(), C.byref(c)))
+    return c
+
+
+# ---------------------------------------------------------------- context
+class Context:
+    """createContext / waitAll of the Dawn layer (src/Gemma/Model.hs:419)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib().gh_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def sync(self) -> None:
+        check(lib().gh_ctx_sync(self.h))
+
+    def close(self) -> None:
+        if self.h:
+            lib().gh_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """createTensorWithData / fromGPU equivalents (device memory owned by the library)."""
+
+    def __init__(self, ctx: Context, nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        h = C.c_void_p()
+        check(lib().gh_buf_alloc(ctx.h, self.nbytes, C.byref(h)))
+        self.ptr = h
+
+    @classmethod
+    def from_numpy(cls, ctx: Context, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(ctx, a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib().gh_buf_upload(self.ctx.h, self.ptr, _ptr(a), a.nbytes))
+
+    def numpy(self, dtype=np.float32, count: int | None = None) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = self.nbytes // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        check(lib().gh_buf_download(self.ctx.h, _ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().gh_buf_free(self.ctx.h, self.ptr)
+            self.ptr = None
+
+
+# ---------------------------------------------------------------- Q4_0
+class Q4Tensor:
+    """A GGUF Q4_0 matrix resident on the device (repacked on upload)."""
+
+    def __init__(self, ctx: Context, raw: np.ndarray, rows: int, cols: int, ieee_scales: bool = False):
+        raw = np.ascontiguousarray(raw).view(np.uint8)
+        if raw.nbytes < rows * (cols // 32) * 18:
+            raise ValueError("raw Q4_0 buffer too small")
+        h = C.c_void_p()
+        check(lib().gh_q4_0_upload(ctx.h, _ptr(raw), rows, cols, FLAG_IEEE_SCALES if ieee_scales else 0,
+                                   C.byref(h)))
+        self.ctx, self.h, self.rows, self.cols = ctx, h, rows, cols
+
+    def dequant(self) -> np.ndarray:
+        out = DeviceBuffer(self.ctx, 4 * self.rows * self.cols)
+        try:
+            check(lib().gh_q4_0_dequant(self.h, out.ptr))
+            return out.numpy().reshape(self.rows, self.cols)
+        finally:
+            out.free()
+
+    def matvec(self, x: np.ndarray, softcap: bool = False, cap: float = 30.0) -> np.ndarray:
+        xb = DeviceBuffer.from_numpy(self.ctx, np.asarray(x, dtype=np.float32))
+        yb = DeviceBuffer(self.ctx, 4 * self.rows)
+        try:
+            check(lib().gh_q4_0_matvec(self.h, xb.ptr, yb.ptr, int(softcap), float(cap)))
+            return yb.numpy()
+        finally:
+            xb.free()
+            yb.free()
+
+    def close(self) -> None:
+        if self.h:
+            lib().gh_q4_0_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def runLinearQ4(ctx: Context, weights_q4: np.ndarray, x: np.ndarray, n_rows: int, n_cols: int,
+                softcap: bool = False, cap: float = 30.0) -> np.ndarray:
+    """runLinearQ4 (src/Gemma/Layers/LinearQ4.hs:41-48): raw GGUF bytes as
+    little-endian uint32 words, x[n_cols] -> y[n_rows]."""
+    words = np.ascontiguousarray(weights_q4)
+    if words.dtype != np.uint32:
+        b = words.view(np.uint8)
+        pad = (-b.nbytes) % 4
+        words = np.concatenate([b, np.zeros(pad, np.uint8)]).view(np.uint32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(n_rows, dtype=np.float32)
+    check(lib().gh_linear_q4(ctx.h, _ptr(words), words.size, _ptr(x), n_rows, n_cols, int(softcap),
+                             float(cap), _ptr(y)))
+    return y
+
+
+# ---------------------------------------------------------------- ops
+def _dev(ctx, a):
+    return DeviceBuffer.from_numpy(ctx, np.ascontiguousarray(a, dtype=np.float32))
+
+
+def rmsnorm(ctx: Context, x, w, eps: float = 1e-6, zero_centered: bool = True) -> np.ndarray:
+    xb, wb, yb = _dev(ctx, x), _dev(ctx, w), DeviceBuffer(ctx, 4 * len(x))
+    check(lib().gh_rmsnorm(ctx.h, xb.ptr, wb.ptr, len(x), eps, int(zero_centered), yb.ptr))
+    out = yb.numpy()
+    for b in (xb, wb, yb):
+        b.free()
+    return out
+
+
+def qk_norm(ctx: Context, x, w, n_heads: int, head_dim: int, eps: float = 1e-6,
+            zero_centered: bool = True) -> np.ndarray:
+    xb, wb, yb = _dev(ctx, x), _dev(ctx, w), DeviceBuffer(ctx, 4 * n_heads * head_dim)
+    check(lib().gh_qk_norm(ctx.h, xb.ptr, wb.ptr, n_heads, head_dim, eps, int(zero_centered), yb.ptr))
+    out = yb.numpy()
+    for b in (xb, wb, yb):
+        b.free()
+    return out
+
+
+def rope(ctx: Context, x, n_heads: int, head_dim: int, theta: float, pos: int) -> np.ndarray:
+    xb = _dev(ctx, x)
+    check(lib().gh_rope(ctx.h, xb.ptr, n_heads, head_dim, theta, pos))
+    out = xb.numpy()
+    xb.free()
+    return out
+
+
+def attention_decode(ctx: Context, q, k_cache, v_cache, nq: int, nkv: int, head_dim: int,
+                     p_begin: int, p_end: int, n_splits: int = 0) -> np.ndarray:
+    qb, kb, vb = _dev(ctx, q), _dev(ctx, k_cache), _dev(ctx, v_cache)
+    ob = DeviceBuffer(ctx, 4 * nq * head_dim)
+    try:
+        check(lib().gh_attention_decode(ctx.h, qb.ptr, kb.ptr, vb.ptr, nq, nkv, head_dim, p_begin, p_end,
+                                        n_splits, ob.ptr))
+        return ob.numpy()
+    finally:
+        for b in (qb, kb, vb, ob):
+            b.free()
+
+
+def gelu_mul(ctx: Context, g, u) -> np.ndarray:
+    gb, ub, hb = _dev(ctx, g), _dev(ctx, u), DeviceBuffer(ctx, 4 * len(g))
+    check(lib().gh_gelu_mul(ctx.h, gb.ptr, ub.ptr, len(g), hb.ptr))
+    out = hb.numpy()
+    for b in (gb, ub, hb):
+        b.free()
+    return out
+
+
+def argmax(ctx: Context, v) -> int:
+    vb = _dev(ctx, v)
+    idx = C.c_int32()
+    try:
+        check(lib().gh_argmax(ctx.h, vb.ptr, len(v), C.byref(idx)))
+    finally:
+        vb.free()
+    return idx.value
+
+
+# ---------------------------------------------------------------- synthetic data
+def synth_f32(seed: int, name: str, sigma: float, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    check(lib().gh_synth_f32(seed, name.encode(), sigma, _ptr(out), n))
+    return out
+
+
+def synth_q4_0(seed: int, name: str, scale_sigma: float, rows: int, cols: int) -> np.ndarray:
+    out = np.empty(rows * (cols // 32) * 18, dtype=np.uint8)
+    check(lib().gh_synth_q4_0(seed, name.encode(), scale_sigma, rows, cols, _ptr(out)))
+    return out
+
+
+def synth_tokens(seed: int, name: str, n: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    check(lib().gh_synth_tokens(seed, name.encode(), n, vocab, _ptr(out)))
+    return out
+
+
+def tensor_list(cfg: GemmaConfig):
+    """(name, kind, shape) of every tensor a config needs; kind 'mat' or 'vec'.
+    GGUF names; the same order gh_synth_model uses."""
+    H, hd, F = cfg.hidden, cfg.head_dim, cfg.ffn
+    out = [("token_embd.weight", "mat", (cfg.vocab, H)), ("output_norm.weight", "vec", (H,))]
+    for l in range(cfg.n_layers):
+        p = f"blk.{l}."
+        out += [
+            (p + "attn_norm.weight", "vec", (H,)),
+            (p + "attn_q.weight", "mat", (cfg.n_heads * hd, H)),
+            (p + "attn_k.weight", "mat", (cfg.n_kv_heads * hd, H)),
+            (p + "attn_v.weight", "mat", (cfg.n_kv_heads * hd, H)),
+            (p + "attn_q_norm.weight", "vec", (hd,)),
+            (p + "attn_k_norm.weight", "vec", (hd,)),
+            (p + "attn_output.weight", "mat", (H, cfg.n_heads * hd)),
+            (p + "post_attention_norm.weight", "vec", (H,)),
+            (p + "ffn_norm.weight", "vec", (H,)),
+            (p + "ffn_gate.weight", "mat", (F, H)),
+            (p + "ffn_up.weight", "mat", (F, H)),
+            (p + "ffn_down.weight", "mat", (H, F)),
+            (p + "post_ffw_norm.weight", "vec", (H,)),
+        ]
+    return out
+
+
+def synth_tensors(cfg: GemmaConfig, seed: int, q4: bool, w_sigma: float = 0.02,
+                  scale_sigma: float = 0.01, norm_sigma: float = 0.02):
+    """Yield (name, dtype, array) with exactly the bytes gh_synth_model uploads."""
+    for name, kind, shape in tensor_list(cfg):
+        if kind == "vec":
+            yield name, DTYPE_F32, synth_f32(seed, name, norm_sigma, shape[0])
+        elif q4:
+            yield name, DTYPE_Q4_0, synth_q4_0(seed, name, scale_sigma, shape[0], shape[1])
+        else:
+            yield name, DTYPE_F32, synth_f32(seed, name, w_sigma, shape[0] * shape[1])
+
+
+# ---------------------------------------------------------------- model
+class GemmaModel:
+    """GemmaModel (src/Gemma/Model.hs:243-257) with device-resident weights."""
+
+    def __init__(self, ctx: Context, cfg: GemmaConfig, handle=None):
+        self.ctx = ctx
+        if handle is None:
+            h = C.c_void_p()
+            check(lib().gh_model_create(ctx.h, C.byref(cfg), C.byref(h)))
+            handle = h
+        self.h = handle
+        self.cfg = self.config()
+
+    @classmethod
+    def load_gguf(cls, ctx: Context, path: str, max_seq: int = 0) -> "GemmaModel":
+        """loadGemmaModelFromGGUF (src/Gemma/Model.hs:908)."""
+        h = C.c_void_p()
+        check(lib().gh_model_load_gguf(ctx.h, str(path).encode(), max_seq, C.byref(h)))
+        return cls(ctx, None, handle=h)
+
+    def config(self) -> GemmaConfig:
+        c = GemmaConfig()
+        check(lib().gh_model_config(self.h, C.byref(c)))
+        return c
+
+    def set_tensor(self, name: str, a: np.ndarray, dtype: int) -> None:
+        a = np.ascontiguousarray(a)
+        check(lib().gh_model_set_tensor(self.h, name.encode(), dtype, _ptr(a), a.nbytes))
+
+    def synth(self, seed: int, q4: bool, w_sigma: float = 0.02, scale_sigma: float = 0.01,
+              norm_sigma: float = 0.02) -> None:
+        check(lib().gh_synth_model(self.h, seed, int(q4), w_sigma, scale_sigma, norm_sigma))
+
+    def check(self) -> None:
+        check(lib().gh_model_check(self.h))
+
+    def close(self) -> None:
+        if self.h:
+            lib().gh_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KVCache:
+    """Gemma.KVCache handle (src/Gemma/KVCache.hs:45-82): device K/V plus the length."""
+
+    def __init__(self, model: GemmaModel, max_seq: int = 0):
+        h = C.c_void_p()
+        check(lib().gh_kv_create(model.h, max_seq, C.byref(h)))
+        self.model, self.h = model, h
+
+    def cacheLength(self) -> int:
+        n = C.c_int32()
+        check(lib().gh_kv_length(self.h, C.byref(n)))
+        return n.value
+
+    __len__ = cacheLength
+
+    def reset(self) -> None:
+        check(lib().gh_kv_reset(self.h))
+
+    def close(self) -> None:
+        if self.h and self.model.h:
+            lib().gh_kv_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def runGemmaInferenceCached(model: GemmaModel, token: int, cache: KVCache | None = None,
+                            want_logits: bool = True):
+    """One decode step (src/Gemma/Model.hs:1313-1437).  Returns
+    (logits or None, cache, greedy next token)."""
+    if cache is None:
+        cache = KVCache(model)
+    logits = np.empty(model.cfg.vocab, np.float32) if want_logits else None
+    nxt = C.c_int32()
+    check(lib().gh_step(model.h, cache.h, int(token), _ptr(logits) if want_logits else None, None,
+                        C.byref(nxt)))
+    return logits, cache, nxt.value
+
+
+def runGemmaInferenceCachedWithLayer0(model: GemmaModel, token: int, cache: KVCache | None = None):
+    """Step that also returns the hidden state after every layer
+    (generalises src/Gemma/Model.hs:1441): (logits, cache, layers[L, H], next)."""
+    if cache is None:
+        cache = KVCache(model)
+    c = model.cfg
+    logits = np.empty(c.vocab, np.float32)
+    layers = np.empty((c.n_layers, c.hidden), np.float32)
+    nxt = C.c_int32()
+    check(lib().gh_step(model.h, cache.h, int(token), _ptr(logits), _ptr(layers), C.byref(nxt)))
+    return logits, cache, layers, nxt.value
+
+
+def generate(model: GemmaModel, cache: KVCache, prompt, n_gen: int) -> np.ndarray:
+    """Greedy generation loop on device (app/Main.hs:372-463)."""
+    p = np.ascontiguousarray(prompt, dtype=np.int32)
+    ids = np.empty(n_gen, np.int32)
+    check(lib().gh_generate(model.h, cache.h, _ptr(p), len(p), n_gen, _ptr(ids)))
+    return ids
+
+
+def bench_decode(model: GemmaModel, cache: KVCache, prompt, n_warmup: int, n_steps: int):
+    """(ms for n_steps timed greedy steps, ids[n_warmup + n_steps + 1])."""
+    p = np.ascontiguousarray(prompt, dtype=np.int32)
+    ids = np.empty(n_warmup + n_steps + 1, np.int32)
+    ms = C.c_float()
+    check(lib().gh_bench_decode(model.h, cache.h, _ptr(p), len(p), n_warmup, n_steps, C.byref(ms),
+                                _ptr(ids)))
+    return ms.value, ids
+
+
+@dataclass
+class KernelStat:
+    name: str
+    launches: int
+    total_ms: float
+    bytes_per_launch: float
+
+    @property
+    def avg_us(self) -> float:
+        return 1e3 * self.total_ms / max(1, self.launches)
+
+    @property
+    def gbps(self) -> float:
+        return self.bytes_per_launch / (self.avg_us * 1e-6) / 1e9 if self.total_ms > 0 else 0.0
+
+
+def profile_steps(model: GemmaModel, cache: KVCache, n_steps: int) -> list[KernelStat]:
+    """Per-kernel event timing over n_steps greedy steps (replaces the
+    reference's gpu_print_profile_stats hook)."""
+    arr = (GhKernelStat * 32)()
+    n = C.c_int32()
+    check(lib().gh_profile_steps(model.h, cache.h, n_steps, arr, 32, C.byref(n)))
+    return [KernelStat(arr[i].name.decode(), arr[i].launches, arr[i].total_ms, arr[i].bytes)
+            for i in range(n.value)]

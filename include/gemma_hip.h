@@ -1,0 +1,228 @@
+/*
+ * gemma_hip.h -- C ABI of libgemma_hip, the MI355X (gfx950) replacement for
+ * the Dawn/WebGPU Graphics layer under gemma.hs's per-token decode loop.
+ *
+ * Conventions
+ *  - Every function returns int: GH_OK (0) or a negative GH_ERR_* code, and
+ *    on failure sets a thread-local message readable with gh_last_error().
+ *  - Host pointers are borrowed for the duration of the call (the Haskell
+ *    side passes Storable.unsafeWith pointers); the library copies what it
+ *    keeps.  Device memory is owned by the library (contexts, models,
+ *    caches, gh_q4 tensors and gh_buf_alloc buffers).
+ *  - One HIP stream per context; calls on one context are serialised by a
+ *    mutex, so a Haskell RTS running with -N may call from any thread.
+ *  - Plain C types only: no HIP or torch types cross this boundary.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the reference repository root).
+ */
+#ifndef GEMMA_HIP_H
+#define GEMMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes ---- */
+#define GH_OK 0
+#define GH_ERR_INVALID (-1)   /* bad argument / shape */
+#define GH_ERR_HIP (-2)       /* HIP runtime failure (incl. no device) */
+#define GH_ERR_OOM (-3)       /* device or host allocation failed */
+#define GH_ERR_STATE (-4)     /* model incomplete / wrong object state */
+#define GH_ERR_RANGE (-5)     /* position >= max_seq (KV cache full) */
+#define GH_ERR_NAN (-6)       /* NaN in logits */
+#define GH_ERR_FORMAT (-7)    /* malformed GGUF file */
+#define GH_ERR_NOT_FOUND (-8) /* missing tensor / unknown tensor name */
+
+/* ---- tensor dtypes ---- */
+#define GH_DTYPE_F32 0
+#define GH_DTYPE_F16 1
+#define GH_DTYPE_Q4_0 2 /* raw GGUF Q4_0 bytes: 18-byte blocks along the row */
+
+/* ---- gh_config.mode ---- */
+#define GH_MODE_GEMMA3 0 /* local layers attend to the last W positions; per-type theta */
+#define GH_MODE_REF 1    /* the reference's quirks Q2/Q3: one theta, prefix window */
+
+/* ---- gh_config.flags ---- */
+#define GH_FLAG_QK_NORM 1
+#define GH_FLAG_POST_ATTN_NORM 2
+#define GH_FLAG_POST_FFN_NORM 4
+#define GH_FLAG_ZERO_CENTERED 8
+#define GH_FLAG_IEEE_SCALES 16 /* keep fp16 subnormal Q4_0 scales (default: flush to zero) */
+
+const char* gh_last_error(void);
+/* Library version string. */
+const char* gh_version(void);
+
+/* ================================================================
+ * Context: replaces Graphics.WebGPU.Dawn createContext / waitAll
+ * (used at src/Gemma/Model.hs:419 and src/Gemma/Model.hs:1432).
+ * ================================================================ */
+typedef struct gh_ctx gh_ctx;
+int gh_device_count(int* n_out);
+int gh_ctx_create(int device, gh_ctx** out);
+int gh_ctx_destroy(gh_ctx* ctx);
+/* waitAll (src/Gemma/Model.hs:1432) */
+int gh_ctx_sync(gh_ctx* ctx);
+
+/* ================================================================
+ * Buffers: replace createTensor / createTensorWithData / fromGPU
+ * (e.g. src/Gemma/Model.hs:588-616, src/Gemma/Model.hs:1435).
+ * ================================================================ */
+int gh_buf_alloc(gh_ctx* ctx, size_t bytes, void** dev_out);
+int gh_buf_free(gh_ctx* ctx, void* dev);
+int gh_buf_upload(gh_ctx* ctx, void* dev, const void* host, size_t bytes);
+int gh_buf_download(gh_ctx* ctx, void* host, const void* dev, size_t bytes);
+
+/* ================================================================
+ * GGUF Q4_0 tensors.  Replaces Gemma.GGUF.loadQ4_0Tensor's dequant
+ * (src/Gemma/GGUF.hs:726-760) and Gemma.Layers.LinearQ4.runLinearQ4
+ * (src/Gemma/Layers/LinearQ4.hs:41-48, body runMatmulQ4_0DSL).
+ * ================================================================ */
+typedef struct gh_q4 gh_q4;
+/* raw: rows*cols/32 GGUF blocks of 18 bytes, row-major, cols % 32 == 0.
+ * flags: GH_FLAG_IEEE_SCALES or 0.  The bytes are repacked on upload into
+ * the device tile layout; dequantised values are bit-identical. */
+int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_t cols, int flags, gh_q4** out);
+int gh_q4_0_free(gh_q4* t);
+/* out_dev: rows*cols f32, row-major (loadQ4_0Tensor's result). */
+int gh_q4_0_dequant(gh_q4* t, float* out_dev);
+/* y_dev[rows] = W x_dev[cols]; softcap != 0 applies cap*tanh(y/cap). */
+int gh_q4_0_matvec(gh_q4* t, const float* x_dev, float* y_dev, int softcap, float cap);
+/* runLinearQ4 signature: raw GGUF bytes packed little-endian into 32-bit
+ * words (a block straddles words), host x[cols] -> host y[rows]. */
+int gh_linear_q4(gh_ctx* ctx, const uint32_t* raw_words, size_t n_words, const float* x, int rows,
+                 int cols, int softcap, float cap, float* y);
+
+/* ================================================================
+ * Op-level entry points on device pointers (parity hooks for the
+ * individual shaders of the step).
+ * ================================================================ */
+/* rmsNormShader, src/Gemma/Layers/RMSNorm.hs:45-154 */
+int gh_rmsnorm(gh_ctx* ctx, const float* x, const float* w, int n, float eps, int zero_centered,
+               float* y);
+/* qkNormShader, src/Gemma/Layers/AttentionGPU.hs:218-257 */
+int gh_qk_norm(gh_ctx* ctx, const float* x, const float* w, int n_heads, int head_dim, float eps,
+               int zero_centered, float* y);
+/* ropeShader, src/Gemma/Layers/AttentionGPU.hs:68-115 (in place) */
+int gh_rope(gh_ctx* ctx, float* x, int n_heads, int head_dim, float theta, int pos);
+/* attentionScoresShader + attentionOutputShader,
+ * src/Gemma/Layers/AttentionGPU.hs:292-352,382-423: one query token over
+ * cache rows [p_begin, p_end) of a [pos][nkv][hd] f32 cache.  n_splits = 0
+ * picks the split count. */
+int gh_attention_decode(gh_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
+                        int nq, int nkv, int head_dim, int p_begin, int p_end, int n_splits,
+                        float* out);
+/* geluMultiplyFusedShader, src/Gemma/Layers/MLP.hs:384-447 */
+int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, float* h);
+/* sampleToken / sampleWithTemperature, app/Main.hs:488-507 (first max) */
+int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx_out);
+
+/* ================================================================
+ * Model: replaces GemmaConfig / loadGemmaModel / loadGemmaModelFromGGUF
+ * (src/Gemma/Model.hs:106-129, 276, 908) and the per-token step
+ * runGemmaInferenceCached (src/Gemma/Model.hs:1313-1437).
+ * ================================================================ */
+typedef struct gh_config {
+    int32_t vocab, hidden, n_layers, n_heads, n_kv_heads, head_dim, ffn;
+    int32_t max_seq;        /* default KV capacity (reference: 2048) */
+    int32_t sliding_window; /* 0 = none */
+    int32_t global_every;   /* layer i global iff (i+1) % global_every == 0; 0 = all global */
+    float rope_theta_local, rope_theta_global;
+    float rms_eps;
+    int32_t mode;  /* GH_MODE_* */
+    int32_t flags; /* GH_FLAG_* */
+} gh_config;
+
+/* Presets: name in {"tiny", "gemma3-1b", "gemma3-4b"}. */
+int gh_config_preset(const char* name, gh_config* out);
+
+typedef struct gh_model gh_model;
+int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out);
+int gh_model_destroy(gh_model* m);
+/* name: GGUF tensor name (token_embd.weight, output_norm.weight,
+ * blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_q_norm,attn_k_norm,
+ * attn_output,post_attention_norm,ffn_norm,ffn_gate,ffn_up,ffn_down,
+ * post_ffw_norm}.weight).  dtype GH_DTYPE_F32 / F16 / Q4_0 (raw bytes). */
+int gh_model_set_tensor(gh_model* m, const char* name, int dtype, const void* data, size_t nbytes);
+/* 0 when every tensor the config needs is present. */
+int gh_model_check(gh_model* m);
+int gh_model_config(gh_model* m, gh_config* out);
+/* loadGemmaModelFromGGUF (src/Gemma/Model.hs:908-1234) + configFromGGUF
+ * (src/Gemma/Model.hs:843-902): parse a GGUF v3 file, build the config from
+ * its metadata (vocab from the token_embd shape) and upload every tensor. */
+int gh_model_load_gguf(gh_ctx* ctx, const char* path, int32_t max_seq, gh_model** out);
+/* configFromGGUF alone (src/Gemma/Model.hs:843-902): parse the header,
+ * metadata and tensor infos of a GGUF v3 file into a config; no device. */
+int gh_gguf_inspect(const char* path, gh_config* out);
+
+/* ================================================================
+ * KV cache handle: replaces Gemma.KVCache (src/Gemma/KVCache.hs:20-35,
+ * initKVCache 78-82, cacheLength 146-147).  Device K/V of shape
+ * [n_layers][max_seq][n_kv_heads][head_dim] f32.
+ * ================================================================ */
+typedef struct gh_kv gh_kv;
+int gh_kv_create(gh_model* m, int32_t max_seq, gh_kv** out);
+int gh_kv_destroy(gh_kv* kv);
+int gh_kv_reset(gh_kv* kv);
+int gh_kv_length(gh_kv* kv, int32_t* len_out);
+
+/* runGemmaInferenceCached (src/Gemma/Model.hs:1313-1437) and its layer-0
+ * variant runGemmaInferenceCachedWithLayer0 (src/Gemma/Model.hs:1441):
+ * one token at position = cache length; the cache grows by one.
+ * logits[vocab], layer_out[n_layers*hidden] (hidden state after each
+ * layer) may be NULL; argmax_out receives the greedy next token. */
+int gh_step(gh_model* m, gh_kv* kv, int32_t token, float* logits, float* layer_out,
+            int32_t* argmax_out);
+
+/* The generation loop of app/Main.hs:372-463 / examples/BenchmarkKVCache.hs
+ * :166-220 (prompt one token per step, then greedy), run on device with no
+ * host round trip per token: ids_out[n_gen]. */
+int gh_generate(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
+                int32_t* ids_out);
+
+/* Decode benchmark (examples/BenchmarkKVCache.hs:56-165): feeds the prompt,
+ * runs n_warmup greedy steps, then times n_steps greedy steps with HIP
+ * events.  ids_out[n_warmup + n_steps + 1] may be NULL. */
+int gh_bench_decode(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt,
+                    int32_t n_warmup, int32_t n_steps, float* ms_out, int32_t* ids_out);
+
+/* ================================================================
+ * Profiling: replaces the gpu_print_profile_stats /
+ * gpu_reset_profile_stats hooks (examples/BenchmarkKVCache.hs:38-42).
+ * Runs n_steps greedy steps with HIP events around every kernel and
+ * reports per-kernel-kind statistics.
+ * ================================================================ */
+typedef struct gh_kernel_stat {
+    char name[32];
+    int32_t launches;   /* launches over the n_steps steps */
+    double total_ms;    /* summed event durations */
+    double bytes;       /* algorithmic bytes per launch, averaged */
+} gh_kernel_stat;
+int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kernel_stat* stats,
+                     int32_t max_stats, int32_t* n_stats_out);
+
+/* ================================================================
+ * Seeded synthetic weights (SplitMix64 + Box-Muller), identical on every
+ * host, so a GPU box can regenerate the exact bytes of a test model.
+ * ================================================================ */
+/* N(0, sigma) f32 values for tensor `name`. */
+int gh_synth_f32(uint64_t seed, const char* name, float sigma, float* out, size_t n);
+/* GGUF Q4_0 raw blocks: codes uniform in [0,15], scale |N(0,scale_sigma)|
+ * rounded to fp16 (round to nearest even). */
+int gh_synth_q4_0(uint64_t seed, const char* name, float scale_sigma, int64_t rows, int64_t cols,
+                  uint8_t* out);
+/* token ids uniform in [0, vocab) */
+int gh_synth_tokens(uint64_t seed, const char* name, int32_t n, int32_t vocab, int32_t* out);
+/* Populate every tensor of `m` from the seed (Q4_0 projections and
+ * embedding when q4 != 0, else f32; norm weights f32 N(0, norm_sigma)). */
+int gh_synth_model(gh_model* m, uint64_t seed, int q4, float w_sigma, float scale_sigma,
+                   float norm_sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GEMMA_HIP_H */

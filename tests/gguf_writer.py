@@ -1,0 +1,97 @@
+"""Minimal GGUF v3 writer for tests (synthetic Gemma-3 files).
+
+Layout per the GGUF v3 format read by src/Gemma/GGUF.hs:186-239: magic,
+version 3, tensor count, metadata count, metadata key/values, tensor infos
+(name, dims innermost first, ggml type, offset), data section aligned to
+general.alignment (32).
+"""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+
+GGML = {"f32": 0, "f16": 1, "q4_0": 2}
+T_U32, T_I32, T_F32, T_STR, T_ARR = 4, 5, 6, 8, 9
+
+
+def _s(b: bytearray, s: str) -> None:
+    e = s.encode()
+    b += struct.pack("<Q", len(e)) + e
+
+
+def write_gguf(path, meta: dict, tensors: list, version: int = 3, magic: int = 0x46554747,
+               truncate: int | None = None) -> None:
+    """meta: key -> (type, value); tensors: (name, kind, rows, cols or None, bytes)."""
+    b = bytearray()
+    b += struct.pack("<IIQQ", magic, version, len(tensors), len(meta))
+    for k, (t, v) in meta.items():
+        _s(b, k)
+        b += struct.pack("<I", t)
+        if t == T_U32:
+            b += struct.pack("<I", v)
+        elif t == T_I32:
+            b += struct.pack("<i", v)
+        elif t == T_F32:
+            b += struct.pack("<f", v)
+        elif t == T_STR:
+            _s(b, v)
+        elif t == T_ARR:  # array of strings
+            b += struct.pack("<IQ", T_STR, len(v))
+            for s in v:
+                _s(b, s)
+        else:
+            raise ValueError(t)
+    off = 0
+    datas = []
+    for name, kind, rows, cols, data in tensors:
+        _s(b, name)
+        dims = [rows] if cols is None else [cols, rows]
+        b += struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        b += struct.pack("<IQ", GGML[kind], off)
+        data = bytes(np.ascontiguousarray(data).view(np.uint8))
+        datas.append((off, data))
+        off += (len(data) + 31) // 32 * 32
+    pad = (-len(b)) % 32
+    b += b"\0" * pad
+    base = len(b)
+    body = bytearray(off)
+    for o, d in datas:
+        body[o:o + len(d)] = d
+    b += body
+    assert len(b) - base == off
+    if truncate is not None:
+        b = b[:truncate]
+    with open(path, "wb") as f:
+        f.write(b)
+
+
+def gemma3_meta(cfg) -> dict:
+    return {
+        "general.architecture": (T_STR, "gemma3"),
+        "gemma3.block_count": (T_U32, cfg.n_layers),
+        "gemma3.embedding_length": (T_U32, cfg.hidden),
+        "gemma3.feed_forward_length": (T_U32, cfg.ffn),
+        "gemma3.attention.head_count": (T_U32, cfg.n_heads),
+        "gemma3.attention.head_count_kv": (T_U32, cfg.n_kv_heads),
+        "gemma3.attention.key_length": (T_U32, cfg.head_dim),
+        "gemma3.attention.value_length": (T_U32, cfg.head_dim),
+        "gemma3.rope.freq_base": (T_F32, cfg.rope_theta_global),
+        "gemma3.attention.sliding_window": (T_U32, cfg.sliding_window),
+        "gemma3.attention.layer_norm_rms_epsilon": (T_F32, cfg.rms_eps),
+        "tokenizer.ggml.tokens": (T_ARR, [f"t{i}" for i in range(8)]),
+    }
+
+
+def synth_gguf(path, cfg, seed: int, q4: bool, **kw) -> None:
+    """The seeded synthetic model of gemma_hip.synth_tensors as a GGUF file."""
+    import gemma_hip as gh
+    shapes = {n: (k, s) for n, k, s in gh.tensor_list(cfg)}
+    tensors = []
+    for name, dtype, arr in gh.synth_tensors(cfg, seed, q4):
+        kind, shape = shapes[name]
+        if kind == "vec":
+            tensors.append((name, "f32", shape[0], None, arr))
+        else:
+            tensors.append((name, "q4_0" if dtype == gh.DTYPE_Q4_0 else "f32", shape[0], shape[1], arr))
+    write_gguf(path, gemma3_meta(cfg), tensors, **kw)

@@ -1,0 +1,149 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/gemma_hip.h declares, host-only entry points (presets, synthetic
+data, GGUF parsing) behave, and error codes are forced from the host."""
+from __future__ import annotations
+
+import re
+
+import numpy as np
+import pytest
+
+import gemma_hip as gh
+from conftest import REPO
+from gguf_writer import gemma3_meta, synth_gguf, write_gguf
+
+HEADER = REPO / "include" / "gemma_hip.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = gh.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 40
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    # and the Python binding declares a signature for each
+    from gemma_hip._lib import SIGNATURES
+    assert set(syms) <= set(SIGNATURES), set(syms) - set(SIGNATURES)
+
+
+def test_version_and_presets():
+    assert b"gfx950" in gh.lib().gh_version()
+    c = gh.preset("gemma3-1b")
+    assert (c.vocab, c.hidden, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn) == \
+        (262144, 1152, 26, 4, 1, 256, 6912)
+    assert (c.sliding_window, c.global_every, c.rope_theta_local, c.rope_theta_global) == (512, 6, 1e4, 1e6)
+    t = gh.preset("tiny")
+    assert (t.vocab, t.hidden, t.n_layers, t.n_heads, t.n_kv_heads, t.head_dim, t.ffn) == \
+        (1024, 128, 2, 4, 1, 32, 512)
+    f = gh.preset("gemma3-4b")
+    assert (f.hidden, f.n_layers, f.n_heads, f.n_kv_heads, f.ffn, f.sliding_window) == (2560, 34, 8, 4, 10240, 1024)
+    with pytest.raises(gh.GemmaHipError) as e:
+        gh.preset("gemma3-27b")
+    assert e.value.name == "GH_ERR_NOT_FOUND"
+
+
+def test_synth_is_deterministic_and_distributed_as_specified():
+    a = gh.synth_q4_0(1234, "blk.0.ffn_gate.weight", 0.01, 6912, 1152)
+    b = gh.synth_q4_0(1234, "blk.0.ffn_gate.weight", 0.01, 6912, 1152)
+    c = gh.synth_q4_0(1234, "blk.0.ffn_up.weight", 0.01, 6912, 1152)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    blk = a.reshape(-1, 18)
+    scales = blk[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+    assert np.all(scales >= 0)
+    # |N(0, 0.01)|: mean 0.01*sqrt(2/pi); fraction below the fp16 normal range ~0.49 %
+    assert abs(scales.mean() - 0.01 * np.sqrt(2 / np.pi)) < 2e-4
+    sub = np.mean((blk[:, 1] & 0x7C) == 0)
+    assert 0.003 < sub < 0.007
+    codes = np.concatenate([blk[:, 2:] & 15, blk[:, 2:] >> 4]).ravel()
+    counts = np.bincount(codes, minlength=16) / codes.size
+    assert np.all(np.abs(counts - 1 / 16) < 2e-3)
+    x = gh.synth_f32(7, "w", 0.02, 200000)
+    assert abs(x.std() - 0.02) < 5e-4 and abs(x.mean()) < 5e-4
+    t = gh.synth_tokens(1, "prompt", 128, 262144)
+    assert t.min() >= 0 and t.max() < 262144 and len(set(t.tolist())) > 120
+    assert np.array_equal(t, gh.synth_tokens(1, "prompt", 128, 262144))
+
+
+def test_synth_rounds_scales_to_nearest_even_fp16():
+    """Scales are |N| values rounded to fp16 RNE: re-rounding the fp16 value
+    through numpy is the identity and the distribution of the last bit is even."""
+    a = gh.synth_q4_0(5, "s", 0.01, 2048, 1152).reshape(-1, 18)
+    h = a[:, :2].copy().view(np.uint16).ravel()
+    f = h.view(np.float16)
+    assert np.array_equal(f.astype(np.float32).astype(np.float16).view(np.uint16), h)
+
+
+def test_synth_rejects_bad_shapes():
+    with pytest.raises(gh.GemmaHipError):
+        gh.synth_q4_0(1, "x", 0.01, 4, 33)
+
+
+def test_context_without_device_reports_hip_error():
+    if gh.device_count() > 0:
+        pytest.skip("a device is visible; this checks the no-device error path")
+    with pytest.raises(gh.GemmaHipError) as e:
+        gh.Context(0)
+    assert e.value.name == "GH_ERR_HIP" and "no HIP device" in str(e.value)
+
+
+def _inspect(path):
+    import ctypes as C
+    c = gh.GemmaConfig()
+    gh._lib.check(gh.lib().gh_gguf_inspect(str(path).encode(), C.byref(c)))
+    return c
+
+
+def test_gguf_inspect_config_from_metadata(tmp_path):
+    cfg = gh.preset("tiny")
+    cfg.sliding_window = 7
+    p = tmp_path / "tiny.gguf"
+    synth_gguf(p, cfg, 3, q4=False)
+    c = _inspect(p)
+    assert (c.vocab, c.hidden, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn) == \
+        (cfg.vocab, cfg.hidden, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn)
+    # vocab from token_embd's shape, not the (8-entry) tokenizer array
+    assert c.vocab == 1024 and c.sliding_window == 7 and c.global_every == 6
+    assert c.rope_theta_global == cfg.rope_theta_global and c.rope_theta_local == 1e4
+
+
+@pytest.mark.parametrize("bad", ["magic", "version", "truncated", "missing_meta", "missing_embd"])
+def test_gguf_malformed_files_are_rejected(tmp_path, bad):
+    cfg = gh.preset("tiny")
+    cfg.n_layers = 1
+    p = tmp_path / "bad.gguf"
+    meta = gemma3_meta(cfg)
+    emb = ("token_embd.weight", "f32", cfg.vocab, cfg.hidden, np.zeros(cfg.vocab * cfg.hidden, np.float32))
+    tensors = [emb]
+    kw = {}
+    if bad == "magic":
+        kw["magic"] = 0x12345678
+    elif bad == "version":
+        kw["version"] = 2
+    elif bad == "truncated":
+        kw["truncate"] = 40
+    elif bad == "missing_meta":
+        del meta["gemma3.block_count"]
+    elif bad == "missing_embd":
+        tensors = []
+    write_gguf(p, meta, tensors, **kw)
+    with pytest.raises(gh.GemmaHipError) as e:
+        _inspect(p)
+    want = "GH_ERR_NOT_FOUND" if bad == "missing_embd" else "GH_ERR_FORMAT"
+    assert e.value.name == want, str(e.value)
+    with pytest.raises(gh.GemmaHipError) as e:
+        _inspect(tmp_path / "does-not-exist.gguf")
+    assert e.value.name == "GH_ERR_NOT_FOUND"
+
+
+def test_tensor_list_matches_header_names():
+    names = {n.split(".", 2)[-1] if n.startswith("blk.") else n for n, _, _ in gh.tensor_list(gh.preset("tiny"))}
+    text = HEADER.read_text()
+    for n in names:
+        stem = n.replace(".weight", "")
+        assert stem in text, n

@@ -1,0 +1,142 @@
+"""Op-level parity on the MI355X through the C ABI (marked gpu).
+
+Bars: Q4_0 dequant bit-exact (incl. fp16 subnormal scales, both modes);
+matvec within the fp32 accumulation bound of an fp64 dot product; norms,
+RoPE, GELU, attention within the stated relative tolerances of the oracle;
+argmax exact (first maximum).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import gemma_hip as gh
+import pyoracle as orc
+from conftest import rel_err
+from numpy_ref import q4_0_dequant_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _random_q4(rows, cols, seed, subnormal_frac=0.0):
+    rng = np.random.default_rng(seed)
+    nb = rows * cols // 32
+    b = rng.integers(0, 256, size=(nb, 18), dtype=np.uint8)
+    sc = np.abs(rng.normal(0, 0.01, nb)).astype(np.float16)
+    if subnormal_frac:
+        m = rng.random(nb) < subnormal_frac
+        sub = rng.integers(1, 1024, size=nb).astype(np.uint16) | (rng.integers(0, 2, nb).astype(np.uint16) << 15)
+        sc = np.where(m, sub.view(np.float16), sc)
+    b[:, :2] = sc.view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("ieee", [False, True])
+def test_q4_0_dequant_bit_exact(ctx, ieee):
+    rows, cols = 300, 1152  # ragged last tile
+    raw = _random_q4(rows, cols, 1, subnormal_frac=0.05)
+    t = gh.Q4Tensor(ctx, raw, rows, cols, ieee_scales=ieee)
+    got = t.dequant()
+    want = orc.q4_0_dequant(raw, ftz=not ieee).reshape(rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q4_0_dequant_all_scale_patterns(ctx):
+    """Every fp16 bit pattern as a block scale, FTZ mode: bit-exact."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rows = 65536 // 36 + 1
+    h = np.resize(h, rows * 36)
+    b = np.empty((h.size, 18), np.uint8)
+    b[:, :2] = h.astype("<u2").view(np.uint8).reshape(-1, 2)
+    b[:, 2:] = np.random.default_rng(3).integers(0, 256, size=(h.size, 16), dtype=np.uint8)
+    raw = b.reshape(-1)
+    got = gh.Q4Tensor(ctx, raw, rows, 1152).dequant()
+    want = orc.q4_0_dequant(raw).reshape(rows, 1152)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(6912, 1152), (1152, 6912), (262144, 1152), (1536, 1152),
+                                       (1152, 1024), (4, 64), (130, 96)])
+def test_q4_0_matvec_shapes(ctx, rows, cols):
+    raw = _random_q4(rows, cols, rows + cols, subnormal_frac=0.005)
+    x = np.random.default_rng(rows).normal(size=cols).astype(np.float32)
+    t = gh.Q4Tensor(ctx, raw, rows, cols)
+    y = t.matvec(x)
+    y64, ay = orc.q4_0_matvec_f64(raw, x, rows, cols)
+    # fp32 accumulation bound of any summation order: |err| <= n*eps*sum|w x|
+    bound = 2 * cols * np.finfo(np.float32).eps * ay
+    assert np.all(np.abs(y - y64) <= bound + 1e-30)
+    assert rel_err(y, orc.q4_0_matvec(raw, x, rows, cols)) < 1e-5
+
+
+def test_runLinearQ4_reference_api(ctx):
+    """runLinearQ4 (src/Gemma/Layers/LinearQ4.hs:41-48) on the 4x64 case of
+    test/Gemma/Layers/DequantQ4GGUFSpec.hs: raw bytes as uint32 words."""
+    rows, cols = 4, 64
+    raw = _random_q4(rows, cols, 9)
+    words = np.concatenate([raw, np.zeros((-raw.size) % 4, np.uint8)]).view(np.uint32)
+    x = np.random.default_rng(9).normal(size=cols).astype(np.float32)
+    y = gh.runLinearQ4(ctx, words, x, rows, cols, False, 30.0)
+    W = q4_0_dequant_np(raw, rows, cols)
+    np.testing.assert_allclose(y, W @ x, rtol=1e-5, atol=1e-6)
+    ys = gh.runLinearQ4(ctx, words, 50 * x, rows, cols, True, 30.0)
+    np.testing.assert_allclose(ys, orc.softcap(W @ (50 * x), 30.0), rtol=1e-5, atol=1e-5)
+
+
+def test_linear_q4_rejects_bad_shapes(ctx):
+    with pytest.raises(gh.GemmaHipError) as e:
+        gh.runLinearQ4(ctx, np.zeros(9, np.uint32), np.zeros(48, np.float32), 1, 48)
+    assert e.value.name == "GH_ERR_INVALID"
+
+
+@pytest.mark.parametrize("n", [4, 128, 1152, 2560])
+def test_rmsnorm(ctx, n):
+    rng = np.random.default_rng(n)
+    x = rng.normal(0, 2, n).astype(np.float32)
+    w = rng.normal(0, 0.02, n).astype(np.float32)
+    assert rel_err(gh.rmsnorm(ctx, x, w), orc.rmsnorm_tree(x, w)) < 1e-6
+    assert rel_err(gh.rmsnorm(ctx, x, w + 1, zero_centered=False), orc.rmsnorm_tree(x, w + 1, zc=False)) < 1e-6
+
+
+@pytest.mark.parametrize("hd,nh", [(256, 4), (256, 8), (32, 4), (128, 2)])
+def test_qk_norm_and_rope(ctx, hd, nh):
+    rng = np.random.default_rng(hd + nh)
+    x = rng.normal(0, 3, nh * hd).astype(np.float32)
+    w = rng.normal(0, 0.02, hd).astype(np.float32)
+    assert rel_err(gh.qk_norm(ctx, x, w, nh, hd), orc.qk_norm(x, w, nh, hd)) < 1e-6
+    for pos, theta in ((0, 1e4), (1, 1e4), (383, 1e6), (4351, 1e4)):
+        got = gh.rope(ctx, x, nh, hd, theta, pos)
+        want = orc.rope(x, nh, hd, theta, pos)
+        assert rel_err(got, want) < 2e-6, (pos, theta)
+
+
+def test_gelu_mul_and_argmax(ctx):
+    rng = np.random.default_rng(5)
+    g = rng.normal(0, 3, 6912).astype(np.float32)
+    u = rng.normal(0, 1, 6912).astype(np.float32)
+    assert rel_err(gh.gelu_mul(ctx, g, u), orc.geglu(g, u)) < 1e-6
+    v = rng.normal(size=262144).astype(np.float32)
+    assert gh.argmax(ctx, v) == int(np.argmax(v))
+    v[[17, 100000, 262143]] = 50.0  # ties -> first index
+    assert gh.argmax(ctx, v) == 17
+    assert gh.argmax(ctx, -np.abs(v)) == int(np.argmax(-np.abs(v)))
+
+
+@pytest.mark.parametrize("nq,nkv,hd,L", [(4, 1, 256, 8192), (4, 1, 256, 32768), (8, 4, 256, 4352),
+                                         (4, 1, 32, 300), (4, 2, 128, 1000)])
+def test_attention_decode_global_and_local(ctx, nq, nkv, hd, L):
+    """Config C4 shapes: global layer over all L, local layer over the last 512."""
+    rng = np.random.default_rng(L)
+    q = rng.normal(size=nq * hd).astype(np.float32)
+    K = rng.normal(size=(L, nkv, hd)).astype(np.float32)
+    V = rng.normal(size=(L, nkv, hd)).astype(np.float32)
+    for lo in (0, max(0, L - 512)):
+        got = gh.attention_decode(ctx, q, K, V, nq, nkv, hd, lo, L)
+        want = orc.attention(q, K, V, nq, nkv, hd, lo, L)
+        assert rel_err(got, want) < 1e-5, lo
+    # split count does not change the result beyond rounding
+    a = gh.attention_decode(ctx, q, K, V, nq, nkv, hd, 0, L, n_splits=1)
+    b = gh.attention_decode(ctx, q, K, V, nq, nkv, hd, 0, L, n_splits=min(L, 64))
+    assert rel_err(a, b) < 1e-5
