@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <functional>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -118,6 +119,37 @@ struct gh_q4 {
 
 struct gh_kv;
 
+namespace gh {
+
+// Kernel arguments kept alive for a graph node; ptrs is the kernelParams array.
+struct NodeArgsBase {
+    virtual ~NodeArgsBase() = default;
+    std::vector<void*> ptrs;
+};
+
+// A graph kernel node whose `pos` argument is rewritten before each replay
+// (the position is host-known: one step = one position).
+struct PosPatch {
+    hipGraphNode_t node;
+    hipKernelNodeParams params;
+    int* pos;
+};
+
+struct Profiler;
+
+// Where enqueue_step puts its kernels: a stream (eager, optionally event
+// profiled) or a graph under construction (linear chain of kernel nodes).
+struct Sink {
+    hipStream_t s = nullptr;
+    Profiler* prof = nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphNode_t last = nullptr;
+    std::vector<std::unique_ptr<NodeArgsBase>>* store = nullptr;
+    std::vector<PosPatch>* patches = nullptr;
+};
+
+}  // namespace gh
+
 struct gh_model {
     gh_ctx* ctx = nullptr;
     gh_config cfg{};
@@ -126,7 +158,7 @@ struct gh_model {
     std::vector<gh::DevBuf> owned;
     gh::DMat embd;  // token_embd (tied LM head)
     float* out_norm = nullptr;
-    float* inv_freq = nullptr;  // [2][head_dim/2]: local, global
+    std::vector<float> inv_freq;  // [2][head_dim/2]: local, global (host)
     // rows of the fused QKV matrix: [q (nq*hd) | k | v], each padded to 128
     int q_rows_pad = 0, kv_rows_pad = 0;
     int f_pad = 0;  // padded ffn rows (gate block, then up block)
@@ -143,6 +175,8 @@ struct gh_model {
     float* attn_part = nullptr;
     float* logits = nullptr;
     float* layer_out = nullptr;
+    float* xn_final = nullptr;               // final-norm output, input of the LM head
+    unsigned long long* lm_cand = nullptr;   // per-tile argmax keys of the LM head
     // presence tracking
     bool has_embd = false, has_out_norm = false;
     std::vector<uint32_t> present;  // per layer bitmask of tensor kinds
@@ -156,11 +190,14 @@ struct gh_kv {
     float* k = nullptr;  // [n_layers][max_seq][nkv][hd]
     float* v = nullptr;
     gh::StepState* st = nullptr;
+    float* rope = nullptr;        // [2 (local, global)][max_seq][head_dim/2] (cos, sin) pairs
     int32_t* d_prompt = nullptr;  // [max_seq]
     int32_t* d_ids = nullptr;     // [max_seq]
     gh::StepState* h_st = nullptr;  // pinned staging
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    std::vector<std::unique_ptr<gh::NodeArgsBase>> graph_args;
+    std::vector<gh::PosPatch> patches;
 };
 
 namespace gh {
@@ -177,15 +214,15 @@ struct Profiler {
     int kind_of(const char* name);
 };
 
-// kernels.hip
-int enqueue_step(gh_model* m, gh_kv* kv, hipStream_t s, Profiler* prof);
+// kernels.hip: one decode step at position `pos` (patched per replay in graphs)
+int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos);
 int launch_q4_dequant(const DMat& w, float* out, hipStream_t s);
 int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* part, float* y,
                         int softcap, float cap, hipStream_t s);
 int launch_rmsnorm(const float* x, const float* w, int n, float eps, int zc, float* y, hipStream_t s);
 int launch_qk_norm(const float* x, const float* w, int n_heads, int hd, float eps, int zc, float* y,
                    hipStream_t s);
-int launch_rope(float* x, int n_heads, int hd, float theta, int pos, hipStream_t s);
+int launch_rope(float* x, int n_heads, int hd, const float* cs_dev, hipStream_t s);
 int launch_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
                      int p_begin, int p_end, int n_splits, float* part, float* out, hipStream_t s);
 int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t s);
@@ -195,6 +232,9 @@ int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s)
 void repack_q4_0(const uint8_t* raw, int64_t rows, int64_t cols, bool ftz, uint8_t* codes,
                  uint16_t* scales, int64_t tiles);
 void repack_f32(const float* src, int64_t rows, int64_t cols, float* dst, int64_t tiles);
-Plan choose_plan(int fmt, int tiles, int nblk, int target_wgs);
+Plan choose_plan(int fmt, int tiles, int nblk, int target_wgs, int max_s = 8);
+int kbw_for(int fmt, int per_wave);
+// cos/sin of pos * inv_freq[i] in f32, as ropeShader computes the angle
+void rope_table(const float* inv_freq, int half, int pos0, int n_pos, float* out);
 
 }  // namespace gh

@@ -1,17 +1,24 @@
 // gfx950 kernels of the batch-1 decode step and the op-level entry points.
 //
+// The step is 5 kernels per layer + final norm + LM head + finish, replayed
+// from one hipGraph.  On MI355X a graph kernel boundary costs ~1.6 us while a
+// correct chip-wide barrier inside a persistent kernel costs more (agent-scope
+// fences serialise per XCD), so the design minimises the latency *inside*
+// each kernel: one global round trip per prologue, DPP/readlane reductions,
+// weights in flight before the prologue starts.
+//
 // Every matvec-shaped kernel follows one pattern (k_matvec):
 //   1. each wave issues the loads of its weight blocks into registers
 //      (two rows per lane: lane and lane+64 of a 128-row tile; one 1 KB
 //      contiguous wave load per row and column block),
-//   2. the prologue builds the input-vector slice the workgroup needs in LDS
-//      (residual + RMSNorm, attention combine, GeGLU, ...) while those loads
+//   2. the prologue builds the input-vector slice of the workgroup in LDS
+//      (residual + RMSNorm, attention merge, GeGLU, ...) while those loads
 //      are in flight,
-//   3. dequant-dot: nibbles -> f32 via byte conversions, x broadcast from
-//      LDS, f32 accumulation, scale applied once per 32-weight block,
-//   4. the four waves' row partials are summed in LDS and the epilogue
-//      writes a split partial (summed by the next kernel's prologue) or the
-//      logits plus a grid-wide argmax key.
+//   3. dequant-dot: nibbles -> f32 with byte conversions, x broadcast from
+//      LDS, f32 accumulation, block scale applied once per 32 weights,
+//   4. the four waves' row partials are summed in LDS; the epilogue writes a
+//      split partial (summed by the next kernel's prologue) or the logits
+//      and a per-tile argmax key.
 // No MFMA: batch-1 decode is HBM-bound (3.5 flop/byte for Q4_0).
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -24,27 +31,111 @@
 namespace gh {
 
 constexpr int NT = 256;  // threads per workgroup (4 wave64)
+constexpr int MAXS = 8;  // max column splits reduced by a prologue in one round trip
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------
-// reductions
+// cross-lane reductions (DPP within 16-lane rows, row broadcasts + readlane across rows)
 // ------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_ROR4 = 0x124;
+constexpr int DPP_ROW_ROR8 = 0x128;
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+
+__device__ __forceinline__ float readlane(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// every lane of a 16-lane row gets the row sum
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<DPP_QUAD_XOR1>(v);
+    v += dpp<DPP_QUAD_XOR2>(v);
+    v += dpp<DPP_ROW_ROR4>(v);
+    v += dpp<DPP_ROW_ROR8>(v);
     return v;
 }
 
-// Sum over the 256 threads; `red` holds 4 floats of LDS.  Every thread gets
-// the result.  Contains two barriers; call from uniform control flow.
-__device__ __forceinline__ float block_sum(float v, float* red) {
+// Combine the four 16-lane rows (each already holding its row result in
+// every lane): row_bcast:15 folds row 0 into row 1 and row 2 into row 3,
+// row_bcast:31 folds row 1 into rows 2-3, so lane 63 holds the result,
+// which readlane makes wave-uniform.  (gfx950's permlane16/32_swap would
+// avoid the SGPR, but the ROCm 7.2 compiler returns the first swap output
+// for both halves of the builtin's result, so they are not used.)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_rows(float old, float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                                 CTRL, ROW_MASK, 0xF, false));
+}
+constexpr int DPP_ROW_BCAST15 = 0x142;
+constexpr int DPP_ROW_BCAST31 = 0x143;
+
+template <class Op>
+__device__ __forceinline__ float rows_combine(float v, float ident, Op op) {
+    v = op(v, dpp_rows<DPP_ROW_BCAST15, 0xA>(ident, v));
+    v = op(v, dpp_rows<DPP_ROW_BCAST31, 0xC>(ident, v));
+    return readlane(v, 63);
+}
+
+// wave-uniform sum of the 64 lanes
+__device__ __forceinline__ float wave_sum(float v) {
+    return rows_combine(row16_sum(v), 0.0f, [](float x, float y) { return x + y; });
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp<DPP_QUAD_XOR2>(v));
+    v = fmaxf(v, dpp<DPP_ROW_ROR4>(v));
+    v = fmaxf(v, dpp<DPP_ROW_ROR8>(v));
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    return rows_combine(row16_max(v), -INFINITY, [](float x, float y) { return fmaxf(x, y); });
+}
+
+// sum over aligned groups of LP lanes (result in every lane of the group)
+template <int LP>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (LP == 64) {
+        return wave_sum(v);
+    } else if constexpr (LP == 32) {
+        v = row16_sum(v);
+        return v + __shfl_xor(v, 16, 64);
+    } else if constexpr (LP == 16) {
+        return row16_sum(v);
+    } else {
+        static_assert(LP == 8, "lanes per position must be 8, 16, 32 or 64");
+        v += dpp<DPP_QUAD_XOR1>(v);
+        v += dpp<DPP_QUAD_XOR2>(v);
+        return v + dpp<DPP_ROW_HALF_MIRROR>(v);
+    }
+}
+
+// Sum over the 256 threads, one barrier; `slot` (4 floats of LDS) must not
+// be reused before every thread has returned.
+__device__ __forceinline__ float block_sum(float v, float* slot) {
     v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = v;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
+    return (slot[0] + slot[1]) + (slot[2] + slot[3]);
+}
+
+// Order-preserving argmax key: larger value wins, then lower index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    unsigned b = __float_as_uint(v);
+    unsigned ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)idx);
+}
+
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) {
+    return a > b ? a : b;
 }
 
 __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int o) {
@@ -54,11 +145,13 @@ __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v,
     return ((unsigned long long)hi << 32) | lo;
 }
 
-// Order-preserving argmax key: larger value wins, then lower index.
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
-    unsigned b = __float_as_uint(v);
-    unsigned ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)idx);
+// block-wide max key (one barrier), result valid in every thread
+__device__ __forceinline__ unsigned long long block_max_key(unsigned long long k, unsigned long long* slot) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) k = umax64(k, shfl_xor_u64(k, o));
+    if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = k;
+    __syncthreads();
+    return umax64(umax64(slot[0], slot[1]), umax64(slot[2], slot[3]));
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
@@ -69,6 +162,19 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     float t = 0.7978845608f * (x + 0.044715f * x3);
     t = fminf(fmaxf(t, -10.0f), 10.0f);
     return x * 0.5f * (1.0f + tanhf(t));
+}
+
+__device__ __forceinline__ float norm_apply(float x, float rms, float w, int zc) {
+    return zc ? (x / rms) * (1.0f + w) : (x / rms) * w;
+}
+
+__device__ __forceinline__ float4 operator+(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+__device__ __forceinline__ float4 norm4(float4 x, float rms, float4 w, int zc) {
+    return make_float4(norm_apply(x.x, rms, w.x, zc), norm_apply(x.y, rms, w.y, zc), norm_apply(x.z, rms, w.z, zc),
+                       norm_apply(x.w, rms, w.w, zc));
 }
 
 // Element (r, c) of a tiled matrix, dequantised exactly: (q - 8) * d.
@@ -85,17 +191,20 @@ __device__ __forceinline__ float dq_elem(const DMat& w, int r, int c) {
     return ((const float*)w.codes)[idx * 4 + (c & 3)];
 }
 
-// RMS of a vector held in LDS (or any memory), block-wide; zero-centred
-// norm weight gives (x / rms) * (1 + w) as the reference's shaders do.
-__device__ __forceinline__ float block_rms(const float* v, int n, float eps, float* red) {
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += NT) ss += v[i] * v[i];
-    ss = block_sum(ss, red);
-    return sqrtf(ss / (float)n + eps);
-}
-
-__device__ __forceinline__ float norm_apply(float x, float rms, float w, int zc) {
-    return zc ? (x / rms) * (1.0f + w) : (x / rms) * w;
+// Elements c..c+3 (c % 4 == 0) of row r, dequantised exactly.
+__device__ __forceinline__ float4 dq_elem4(const DMat& w, int r, int c) {
+    const int t = r >> 7, lr = r & 127;
+    if (w.fmt == FMT_Q4) {
+        const int b = c >> 5, e = c & 31;
+        const size_t idx = ((size_t)t * w.nblk + b) * TILE_ROWS + lr;
+        const uint32_t word = ((const uint32_t*)w.codes)[idx * 4 + ((e & 15) >> 2)];
+        const uint32_t q = (e < 16) ? (word & 0x0F0F0F0Fu) : ((word >> 4) & 0x0F0F0F0Fu);
+        const float d = h2f(w.scales[idx]);
+        return make_float4(((float)(q & 0xFF) - 8.0f) * d, ((float)((q >> 8) & 0xFF) - 8.0f) * d,
+                           ((float)((q >> 16) & 0xFF) - 8.0f) * d, ((float)(q >> 24) - 8.0f) * d);
+    }
+    const size_t idx = ((size_t)t * w.nblk + (c >> 2)) * TILE_ROWS + lr;
+    return ((const float4*)w.codes)[idx];
 }
 
 // ------------------------------------------------------------------
@@ -119,81 +228,104 @@ struct WRegs {
 };
 
 template <int FMT, int KBW>
-__device__ __forceinline__ void mv_load(WRegs<FMT, KBW>& r, const DMat& w, int tile, int base,
-                                        int kw1) {
+__device__ __forceinline__ void mv_load(WRegs<FMT, KBW>& r, const DMat& w, int tile, int base, int kw1) {
     const int lane = threadIdx.x & 63;
     const u32x4* cp = (const u32x4*)w.codes + (size_t)tile * w.nblk * TILE_ROWS;
-#pragma unroll
-    for (int i = 0; i < KBW; ++i) {
-        const int kb = base + i;
-        if (kb < kw1) {
-            r.c0[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + lane);
-            r.c1[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + 64 + lane);
-            if (FMT == FMT_Q4) {
-                const uint16_t* sp = w.scales + (size_t)tile * w.nblk * TILE_ROWS;
-                r.s0[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + lane);
-                r.s1[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + 64 + lane);
-            }
+    const uint16_t* sp = w.scales + (size_t)tile * w.nblk * TILE_ROWS;
+    auto one = [&](int i, int kb) {
+        r.c0[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + lane);
+        r.c1[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + 64 + lane);
+        if (FMT == FMT_Q4) {
+            r.s0[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + lane);
+            r.s1[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + 64 + lane);
         }
+    };
+    if (base + KBW <= kw1) {  // full batch (kw1 is wave-uniform)
+#pragma unroll
+        for (int i = 0; i < KBW; ++i) one(i, base + i);
+    } else {
+#pragma unroll
+        for (int i = 0; i < KBW; ++i)
+            if (base + i < kw1) one(i, base + i);
     }
 }
 
-__device__ __forceinline__ float dot_q4_word(uint32_t w, float4 xl, float4 xh) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
-    float d = (float)(lo & 0xFF) * xl.x;
-    d += (float)((lo >> 8) & 0xFF) * xl.y;
-    d += (float)((lo >> 16) & 0xFF) * xl.z;
-    d += (float)(lo >> 24) * xl.w;
-    d += (float)(hi & 0xFF) * xh.x;
-    d += (float)((hi >> 8) & 0xFF) * xh.y;
-    d += (float)((hi >> 16) & 0xFF) * xh.z;
-    d += (float)(hi >> 24) * xh.w;
-    return d;
+// Opaque nibble masks: hiding the AND from the optimiser keeps each byte
+// conversion a single v_cvt_f32_ubyteN (it would otherwise fold the mask
+// into a 4-bit v_bfe_u32 plus v_cvt_f32_ubyte0).
+__device__ __forceinline__ uint32_t mask_lo(uint32_t w) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+__device__ __forceinline__ uint32_t mask_hi(uint32_t w) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0xf0f0f0f0, %1" : "=v"(r) : "v"(w));
+    return r;
 }
 
-// Accumulate the dot products of one register batch.  xs/sxs index the
-// LDS slice starting at column block kb0.
+// acc + sum_e q_e x_e over one 32-bit word of codes.  Bytes of `lo` are
+// elements 4j..4j+3 (low nibbles, value q); bytes of `hi` are elements
+// 16+4j.. (high nibbles kept in place, value 16q) and meet x/16, which the
+// prologue stores for the upper half of every block: 16q * (x/16) == q x.
+__device__ __forceinline__ float dot_q4_word(uint32_t w, float4 xl, float4 xh, float acc) {
+    const uint32_t lo = mask_lo(w), hi = mask_hi(w);
+    acc = fmaf((float)(lo & 0xFF), xl.x, acc);
+    acc = fmaf((float)((lo >> 8) & 0xFF), xl.y, acc);
+    acc = fmaf((float)((lo >> 16) & 0xFF), xl.z, acc);
+    acc = fmaf((float)(lo >> 24), xl.w, acc);
+    acc = fmaf((float)(hi & 0xFF), xh.x, acc);
+    acc = fmaf((float)((hi >> 8) & 0xFF), xh.y, acc);
+    acc = fmaf((float)((hi >> 16) & 0xFF), xh.z, acc);
+    acc = fmaf((float)(hi >> 24), xh.w, acc);
+    return acc;
+}
+
 template <int FMT, int KBW>
-__device__ __forceinline__ void mv_compute(const WRegs<FMT, KBW>& r, int base, int kw1, int kb0,
-                                           const float* xs, const float* sxs, float& acc0,
-                                           float& acc1) {
+__device__ __forceinline__ void mv_block(const WRegs<FMT, KBW>& r, int i, int kb, int kb0, const float* xs,
+                                         const float* sxs, float& acc0, float& acc1) {
+    if (FMT == FMT_Q4) {
+        const float4* xv = (const float4*)(xs + (kb - kb0) * 32);
+        float d0 = 0.0f, d1 = 0.0f;
+        const uint32_t w0[4] = {r.c0[i].x, r.c0[i].y, r.c0[i].z, r.c0[i].w};
+        const uint32_t w1[4] = {r.c1[i].x, r.c1[i].y, r.c1[i].z, r.c1[i].w};
 #pragma unroll
-    for (int i = 0; i < KBW; ++i) {
-        const int kb = base + i;
-        if (kb < kw1) {
-            if (FMT == FMT_Q4) {
-                const float4* xv = (const float4*)(xs + (kb - kb0) * 32);
-                // element e<16 <- low nibble of byte e, e>=16 <- high nibble of byte e-16
-                float d0 = 0.0f, d1 = 0.0f;
-                const uint32_t w0[4] = {r.c0[i].x, r.c0[i].y, r.c0[i].z, r.c0[i].w};
-                const uint32_t w1[4] = {r.c1[i].x, r.c1[i].y, r.c1[i].z, r.c1[i].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float4 xl = xv[j], xh = xv[4 + j];
-                    d0 += dot_q4_word(w0[j], xl, xh);
-                    d1 += dot_q4_word(w1[j], xl, xh);
-                }
-                // sum (q-8) x = sum q x - 8 sum x ; sxs holds sum x per block
-                const float sx8 = 8.0f * sxs[kb - kb0];
-                acc0 += h2f(r.s0[i]) * (d0 - sx8);
-                acc1 += h2f(r.s1[i]) * (d1 - sx8);
-            } else {
-                const float4 x = *(const float4*)(xs + (kb - kb0) * 4);
-                const f32x4 a = __builtin_bit_cast(f32x4, r.c0[i]);
-                const f32x4 b = __builtin_bit_cast(f32x4, r.c1[i]);
-                acc0 += a.x * x.x + a.y * x.y + a.z * x.z + a.w * x.w;
-                acc1 += b.x * x.x + b.y * x.y + b.z * x.z + b.w * x.w;
-            }
+        for (int j = 0; j < 4; ++j) {
+            const float4 xl = xv[j], xh = xv[4 + j];
+            d0 = dot_q4_word(w0[j], xl, xh, d0);
+            d1 = dot_q4_word(w1[j], xl, xh, d1);
         }
+        // sum (q-8) x = sum q x - 8 sum x ; sxs holds sum x per block
+        const float sx8 = 8.0f * sxs[kb - kb0];
+        acc0 = fmaf(h2f(r.s0[i]), d0 - sx8, acc0);
+        acc1 = fmaf(h2f(r.s1[i]), d1 - sx8, acc1);
+    } else {
+        const float4 x = *(const float4*)(xs + (kb - kb0) * 4);
+        const f32x4 a = __builtin_bit_cast(f32x4, r.c0[i]);
+        const f32x4 b = __builtin_bit_cast(f32x4, r.c1[i]);
+        acc0 += a.x * x.x + a.y * x.y + a.z * x.z + a.w * x.w;
+        acc1 += b.x * x.x + b.y * x.y + b.z * x.z + b.w * x.w;
+    }
+}
+
+template <int FMT, int KBW>
+__device__ __forceinline__ void mv_compute(const WRegs<FMT, KBW>& r, int base, int kw1, int kb0, const float* xs,
+                                           const float* sxs, float& acc0, float& acc1) {
+    if (base + KBW <= kw1) {  // full batch: no per-block predication (kw1 is wave-uniform)
+#pragma unroll
+        for (int i = 0; i < KBW; ++i) mv_block<FMT, KBW>(r, i, base + i, kb0, xs, sxs, acc0, acc1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < KBW; ++i)
+            if (base + i < kw1) mv_block<FMT, KBW>(r, i, base + i, kb0, xs, sxs, acc0, acc1);
     }
 }
 
 // LDS layout of k_matvec (floats):
-//   red [512] | misc [64] | xs [per_split*BK] | sxs [per_split] | tmp [...]
+//   red [512] | misc [64] | xs [per_split*BK] | sxs [per_split, padded to 4] | tmp [...]
 struct MvLds {
     float* red;
-    float* misc;
+    float* misc;  // 16 slots of 4 floats for block reductions
     float* xs;
     float* sxs;
     float* tmp;
@@ -205,17 +337,26 @@ inline size_t mv_lds_bytes(int fmt, int per_split, int tmp_floats) {
     return f * sizeof(float);
 }
 
-// Sum of x over each 32-element block of the slice (Q4_0 only).
+// Per 32-element block: sxs = sum x, then x[16..31] *= 1/16 (exact) for the
+// high-nibble products of dot_q4_word.
 template <int FMT>
 __device__ __forceinline__ void fill_block_sums(const MvLds& L, int nk) {
     if (FMT == FMT_Q4) {
         __syncthreads();
         for (int b = threadIdx.x; b < nk; b += NT) {
-            const float* x = L.xs + b * 32;
+            float4* x = (float4*)(L.xs + b * 32);
             float s = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 32; ++e) s += x[e];
+            for (int e = 0; e < 8; ++e) {
+                const float4 v = x[e];
+                s += (v.x + v.y) + (v.z + v.w);
+            }
             L.sxs[b] = s;
+#pragma unroll
+            for (int e = 4; e < 8; ++e) {
+                const float4 v = x[e];
+                x[e] = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
+            }
         }
     }
 }
@@ -240,21 +381,24 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
     L.sxs = L.xs + per_split * BK;
     L.tmp = L.sxs + ((per_split + 3) & ~3);
 
-    // 1. weights of the first batch in flight
+    // 1. the prologue's input loads go out first (they are waited on first),
+    // 2. then the weights of the first register batch,
+    // 3. the prologue builds the input slice [kb0*BK, kb1*BK) in LDS.
+    typename Pro::Regs pr;
+    pro.load(pr, kb0 * BK, nk * BK);
     WRegs<FMT, KBW> r;
     mv_load<FMT, KBW>(r, w, tile, kw0, kw1);
-    // 2. input slice [kb0*BK, kb1*BK) into LDS
-    pro(L, kb0 * BK, nk * BK);
+    pro.finish(L, pr, kb0 * BK, nk * BK);
     fill_block_sums<FMT>(L, nk);
     __syncthreads();
-    // 3. dot products
+    // 4. dot products
     float acc0 = 0.0f, acc1 = 0.0f;
     mv_compute<FMT, KBW>(r, kw0, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     for (int base = kw0 + KBW; base < kw1; base += KBW) {
         mv_load<FMT, KBW>(r, w, tile, base, kw1);
         mv_compute<FMT, KBW>(r, base, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     }
-    // 4. reduce the four waves
+    // 5. reduce the four waves
     L.red[wave * TILE_ROWS + lane] = acc0;
     L.red[wave * TILE_ROWS + 64 + lane] = acc1;
     __syncthreads();
@@ -265,66 +409,144 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
 }
 
 // ------------------------------------------------------------------
-// prologues: build xs[0 .. n) = input[c0 .. c0+n)
+// prologues: load() issues the global loads of the input, finish() builds
+// xs[0 .. n) = input[c0 .. c0+n) in LDS
 // ------------------------------------------------------------------
+__device__ __forceinline__ float4 fma4(float w, float4 o, float4 acc) {
+    return make_float4(acc.x + w * o.x, acc.y + w * o.y, acc.z + w * o.z, acc.w + w * o.w);
+}
+__device__ __forceinline__ float4 f4z() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// sum over s < S of the float4 group g of part[s][ld]: all loads issued
+// before the first add, so the sum costs one round trip.
+__device__ __forceinline__ float4 sum_splits4(const float* part, int S, int ld, int g) {
+    float4 v[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) v[s] = s < S ? ((const float4*)(part + (size_t)s * ld))[g] : f4z();
+    float4 r = v[0];
+#pragma unroll
+    for (int s = 1; s < MAXS; ++s)
+        if (s < S) r = r + v[s];
+    return r;
+}
+
+// A vector already in global memory (2 float4 per thread prefetched).
 struct ProPlain {
     const float* x;
-    __device__ void operator()(const MvLds& L, int c0, int n) const {
-        for (int i = threadIdx.x; i < n; i += NT) L.xs[i] = x[c0 + i];
+    struct Regs {
+        float4 v[2];
+    };
+    __device__ void load(Regs& r, int c0, int n) const {
+        const float4* x4 = (const float4*)(x + c0);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int gi = threadIdx.x + k * NT;
+            r.v[k] = gi < (n >> 2) ? x4[gi] : f4z();
+        }
+    }
+    __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
+        const int ng = n >> 2;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int gi = threadIdx.x + k * NT;
+            if (gi < ng) ((float4*)L.xs)[gi] = r.v[k];
+        }
+        for (int gi = threadIdx.x + 2 * NT; gi < ng; gi += NT) ((float4*)L.xs)[gi] = ((const float4*)(x + c0))[gi];
     }
 };
 
-// Residual stream entering a layer (or the final norm) followed by RMSNorm:
-//   layer 0 : x = E[token] * sqrt(H)  (src/Gemma/Model.hs:1346-1361)
-//   else    : x = x1 + postnorm(sum_s d_s)  (TBG:413-444)
-//   xs      = norm(x) with w_norm  (TBG:110, or the final norm RMSNorm.hs:343-386)
-// Block 0 stores x (the residual input of this layer) and, when asked, the
-// hidden state after the previous layer.
-struct ProResidNorm {
+// Residual stream update followed by an RMSNorm (MG = float4 groups per thread):
+//   x  = base + postnorm(sum_s part_s)        (residual add, TBG:305-343 / TBG:413-444)
+//     or E[token] * sqrt(H) for layer 0        (src/Gemma/Model.hs:1346-1361)
+//   xs = norm(x) with w_norm                   (TBG:110, MLP.hs:507-622, RMSNorm.hs:343-386)
+// Block 0 stores x to x_out and, when asked, to layer_out_row.  All split
+// partials (S <= MAXS) are loaded in one round trip.
+template <int MG>
+struct ProResid {
     int from_embedding;
     DMat embd;
     const StepState* st;
     float escale;
-    const float* x1;
-    const float* part_d;
-    int Sd, ld_d;
+    const float* base;
+    const float* part;
+    int S, ld;
     const float* w_post;  // nullable
     const float* w_norm;
     float eps;
     int zc, H;
-    float* x_res;          // nullable
+    float* x_out;          // nullable
     float* layer_out_row;  // nullable
-    __device__ void operator()(const MvLds& L, int c0, int n) const {
-        float* x = L.tmp;
+    struct Regs {
+        float4 pv[MAXS][MG];
+        float4 bv[MG], wp[MG];
+        float wn;
+    };
+    __device__ void load(Regs& r, int c0, int n) const {
+        const int NG = H >> 2, tid = threadIdx.x;
+        r.wn = tid < n ? w_norm[c0 + tid] : 0.0f;
+        if (from_embedding) return;
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            if (g < NG) {
+                r.bv[k] = ((const float4*)base)[g];
+                r.wp[k] = w_post ? ((const float4*)w_post)[g] : f4z();
+#pragma unroll
+                for (int s = 0; s < MAXS; ++s) r.pv[s][k] = s < S ? ((const float4*)(part + (size_t)s * ld))[g] : f4z();
+            }
+        }
+    }
+    __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
+        const int NG = H >> 2, tid = threadIdx.x;
+        float4 xv[MG];
         if (from_embedding) {
             // the host validates tokens; the clamp keeps a corrupted state in bounds
             const int tok = min(max(st->token, 0), embd.rows - 1);
-            for (int i = threadIdx.x; i < H; i += NT) x[i] = dq_elem(embd, tok, i) * escale;
+#pragma unroll
+            for (int k = 0; k < MG; ++k) {
+                const int g = tid + k * NT;
+                if (g < NG) {
+                    const float4 e = dq_elem4(embd, tok, 4 * g);
+                    xv[k] = make_float4(e.x * escale, e.y * escale, e.z * escale, e.w * escale);
+                }
+            }
         } else {
-            for (int i = threadIdx.x; i < H; i += NT) {
-                float a = 0.0f;
-                for (int s = 0; s < Sd; ++s) a += part_d[(size_t)s * ld_d + i];
-                x[i] = a;
+            float4 dv[MG];
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < MG; ++k) {
+                dv[k] = r.pv[0][k];
+#pragma unroll
+                for (int s = 1; s < MAXS; ++s)
+                    if (s < S) dv[k] = dv[k] + r.pv[s][k];
+                if (tid + k * NT < NG) ss += dot4(dv[k], dv[k]);
             }
-            if (w_post) {
-                const float rms = block_rms(x, H, eps, L.misc);
-                for (int i = threadIdx.x; i < H; i += NT) x[i] = x1[i] + norm_apply(x[i], rms, w_post[i], zc);
-            } else {
-                for (int i = threadIdx.x; i < H; i += NT) x[i] = x1[i] + x[i];
+            float rms = 1.0f;
+            if (w_post) rms = sqrtf(block_sum(ss, L.misc) / (float)H + eps);
+#pragma unroll
+            for (int k = 0; k < MG; ++k)
+                if (tid + k * NT < NG) xv[k] = r.bv[k] + (w_post ? norm4(dv[k], rms, r.wp[k], zc) : dv[k]);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            if (g < NG) {
+                ((float4*)L.tmp)[g] = xv[k];
+                ss += dot4(xv[k], xv[k]);
+                if (blockIdx.x == 0) {
+                    if (x_out) ((float4*)x_out)[g] = xv[k];
+                    if (layer_out_row) ((float4*)layer_out_row)[g] = xv[k];
+                }
             }
         }
-        if (blockIdx.x == 0) {
-            for (int i = threadIdx.x; i < H; i += NT) {
-                if (x_res) x_res[i] = x[i];
-                if (layer_out_row) layer_out_row[i] = x[i];
-            }
-        }
-        const float rms = block_rms(x, H, eps, L.misc);  // has barriers: x complete
-        for (int i = threadIdx.x; i < n; i += NT) L.xs[i] = norm_apply(x[c0 + i], rms, w_norm[c0 + i], zc);
+        const float rms = sqrtf(block_sum(ss, L.misc + 4) / (float)H + eps);  // barrier: tmp complete
+        if (tid < n) L.xs[tid] = norm_apply(L.tmp[c0 + tid], rms, r.wn, zc);
+        for (int i = tid + NT; i < n; i += NT) L.xs[i] = norm_apply(L.tmp[c0 + i], rms, w_norm[c0 + i], zc);
     }
 };
 
-// Attention window of the current token (see k_attn).
+// Attention window of the current token.
 __device__ __forceinline__ void attn_window(int pos, int global, int window, int mode, int& pb, int& pe) {
     pb = 0;
     pe = pos + 1;
@@ -342,69 +564,77 @@ __device__ __forceinline__ void attn_chunks(int n_pos, int nc, int& ch, int& n_u
     n_used = (n_pos + ch - 1) / ch;
 }
 
-// Merge the split-K attention partials {m[G], l[G], o[G][HD]} of kv group g.
-__device__ __forceinline__ float attn_merge(const float* part, int nc, int n_used, int G, int HD,
-                                            int g, int hl, int d) {
-    const int stride = G * (HD + 2);
-    const float* base = part + (size_t)g * nc * stride;
-    float M = -INFINITY;
-    for (int j = 0; j < n_used; ++j) M = fmaxf(M, base[(size_t)j * stride + hl]);
-    float den = 0.0f, num = 0.0f;
-    for (int j = 0; j < n_used; ++j) {
-        const float* p = base + (size_t)j * stride;
-        const float wgt = expf(p[hl] - M);
-        den += p[G + hl] * wgt;
-        num += p[2 * G + hl * HD + d] * wgt;
-    }
-    return num / den;
-}
+constexpr int ATTN_MAX_NC = 64;
 
-// O-projection input: the merged attention output of the slice.
+// O-projection input: merge the split-K attention partials {m[G], l[G],
+// o[G][HD]} of every chunk for the slice [c0, c0+n) of o = [nq][hd].
 struct ProAttnCombine {
     const float* part;
-    const StepState* st;
+    int pos;  // current position (kernel argument, patched per step)
     int nc, G, HD;
     int global, window, mode;
-    __device__ void operator()(const MvLds& L, int c0, int n) const {
-        int pb, pe, ch, n_used;
-        attn_window(st->pos, global, window, mode, pb, pe);
-        attn_chunks(pe - pb, nc, ch, n_used);
-        for (int i = threadIdx.x; i < n; i += NT) {
-            const int c = c0 + i;
-            const int h = c / HD, d = c % HD;
-            L.xs[i] = attn_merge(part, nc, n_used, G, HD, h / G, h % G, d);
+    struct Regs {
+        float4 ov[8];
+        float mj, lj;
+        int n_used;
+    };
+    __device__ void load(Regs& r, int c0, int n) const {
+        int pb, pe, ch;
+        attn_window(pos, global, window, mode, pb, pe);
+        attn_chunks(pe - pb, nc, ch, r.n_used);
+        const int stride = G * (HD + 2), tid = threadIdx.x;
+        // this thread's column group (one per thread up to 1024 columns)
+        const int c = c0 + 4 * tid, h = c / HD, d = c % HD;
+        const float* pbase = part + (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r.ov[j] = (tid < (n >> 2) && j < r.n_used) ? *(const float4*)(pbase + (size_t)j * stride) : f4z();
+        // (m, l) of chunk j = lane for head h0 + wave
+        const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
+        const int hh = tid >> 6, j = tid & 63;
+        r.mj = -INFINITY;
+        r.lj = 0.0f;
+        if (hh < nh && j < r.n_used) {
+            const int hg = h0 + hh;
+            const float* bj = part + ((size_t)(hg / G) * nc + j) * stride;
+            r.mj = bj[hg % G];
+            r.lj = bj[G + hg % G];
         }
     }
-};
-
-// Gate/up input: x1 = x + postnorm(sum_s o_s) (TBG:305-343), then the
-// pre-FFN norm (MLP.hs:507-622).  Block 0 stores x1.
-struct ProPostAttn {
-    const float* part_o;
-    int So, ld_o;
-    const float* w_post;  // nullable
-    const float* x_res;
-    float* x1_out;
-    const float* w_ffn;
-    float eps;
-    int zc, H;
-    __device__ void operator()(const MvLds& L, int c0, int n) const {
-        float* x = L.tmp;
-        for (int i = threadIdx.x; i < H; i += NT) {
-            float a = 0.0f;
-            for (int s = 0; s < So; ++s) a += part_o[(size_t)s * ld_o + i];
-            x[i] = a;
+    __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
+        const int stride = G * (HD + 2), tid = threadIdx.x, n_used = r.n_used;
+        const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
+        float* wts = L.tmp;  // [nh][ATTN_MAX_NC] merge weights exp(m_j - M) / sum_j l_j exp(m_j - M)
+        for (int hh = tid >> 6; hh < nh; hh += 4) {
+            const int j = tid & 63;
+            float mj = r.mj, lj = r.lj;
+            if (hh >= 4) {  // heads beyond the first four of the slice
+                const int hg = h0 + hh;
+                const float* bj = part + ((size_t)(hg / G) * nc + j) * stride;
+                mj = j < n_used ? bj[hg % G] : -INFINITY;
+                lj = j < n_used ? bj[G + hg % G] : 0.0f;
+            }
+            const float M = wave_max(mj);
+            const float e = j < n_used ? expf(mj - M) : 0.0f;
+            const float den = wave_sum(lj * e);
+            wts[hh * ATTN_MAX_NC + j] = e / den;
         }
-        if (w_post) {
-            const float rms = block_rms(x, H, eps, L.misc);
-            for (int i = threadIdx.x; i < H; i += NT) x[i] = x_res[i] + norm_apply(x[i], rms, w_post[i], zc);
-        } else {
-            for (int i = threadIdx.x; i < H; i += NT) x[i] = x_res[i] + x[i];
+        __syncthreads();
+        const int ng = n >> 2;
+        for (int gi = tid; gi < ng; gi += NT) {
+            const int c = c0 + 4 * gi, h = c / HD, d = c % HD;
+            const float* pbase = part + (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
+            const float* wv = wts + (h - h0) * ATTN_MAX_NC;
+            float4 acc = f4z();
+            int j = 0;
+            if (gi == tid) {  // chunks 0..7 were loaded by load()
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+                    if (jj < n_used) acc = fma4(wv[jj], r.ov[jj], acc);
+                j = 8;
+            }
+            for (; j < n_used; ++j) acc = fma4(wv[j], *(const float4*)(pbase + (size_t)j * stride), acc);
+            ((float4*)L.xs)[gi] = acc;
         }
-        if (blockIdx.x == 0)
-            for (int i = threadIdx.x; i < H; i += NT) x1_out[i] = x[i];
-        const float rms = block_rms(x, H, eps, L.misc);
-        for (int i = threadIdx.x; i < n; i += NT) L.xs[i] = norm_apply(x[c0 + i], rms, w_ffn[c0 + i], zc);
     }
 };
 
@@ -412,15 +642,41 @@ struct ProPostAttn {
 struct ProGeglu {
     const float* part_gu;
     int Sg, ld_g, up_off;
-    __device__ void operator()(const MvLds& L, int c0, int n) const {
-        for (int i = threadIdx.x; i < n; i += NT) {
-            const int c = c0 + i;
-            float g = 0.0f, u = 0.0f;
-            for (int s = 0; s < Sg; ++s) {
-                g += part_gu[(size_t)s * ld_g + c];
-                u += part_gu[(size_t)s * ld_g + up_off + c];
+    struct Regs {
+        float4 g[MAXS], u[MAXS];
+    };
+    __device__ void load(Regs& r, int c0, int n) const {
+        const int gi = threadIdx.x, g = (c0 >> 2) + gi;
+        const bool ok = gi < (n >> 2);
+#pragma unroll
+        for (int s = 0; s < MAXS; ++s) {
+            r.g[s] = ok && s < Sg ? ((const float4*)(part_gu + (size_t)s * ld_g))[g] : f4z();
+            r.u[s] = ok && s < Sg ? ((const float4*)(part_gu + (size_t)s * ld_g + up_off))[g] : f4z();
+        }
+    }
+    __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
+        const int ng = n >> 2;
+        for (int gi = threadIdx.x; gi < ng; gi += NT) {
+            float4 gs, us;
+            if (gi == (int)threadIdx.x) {
+                gs = r.g[0];
+                us = r.u[0];
+#pragma unroll
+                for (int s = 1; s < MAXS; ++s)
+                    if (s < Sg) {
+                        gs = gs + r.g[s];
+                        us = us + r.u[s];
+                    }
+            } else {
+                const int g = (c0 >> 2) + gi;
+                gs = us = f4z();
+                for (int s = 0; s < Sg; ++s) {
+                    gs = gs + ((const float4*)(part_gu + (size_t)s * ld_g))[g];
+                    us = us + ((const float4*)(part_gu + (size_t)s * ld_g + up_off))[g];
+                }
             }
-            L.xs[i] = gelu_tanh(g) * u;
+            ((float4*)L.xs)[gi] = make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y,
+                                              gelu_tanh(gs.z) * us.z, gelu_tanh(gs.w) * us.w);
         }
     }
 };
@@ -446,10 +702,12 @@ struct EpiOut {
     }
 };
 
-// Logits + grid-wide greedy argmax (first maximum) into st->keys[pos & 1].
+// Logits + this tile's greedy argmax key (first maximum); the finish kernel
+// reduces the per-tile keys (no same-address atomics on the step path).
 struct EpiLogits {
     float* logits;  // nullable
     int V;
+    unsigned long long* cand;
     StepState* st;
     __device__ void operator()(const MvLds& L, int tile, int, int t, float y) const {
         const int row = tile * TILE_ROWS + t;
@@ -459,44 +717,129 @@ struct EpiLogits {
             key = argmax_key(y, row);
             if (isnan(y)) atomicOr(&st->nan_flag, 1);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const unsigned long long k2 = shfl_xor_u64(key, o);
-            key = k2 > key ? k2 : key;
-        }
-        unsigned long long* sk = (unsigned long long*)L.misc;
-        __syncthreads();
-        if ((t & 63) == 0) sk[t >> 6] = key;
-        __syncthreads();
-        if (t == 0) {
-            unsigned long long b = sk[0];
-            for (int i = 1; i < 4; ++i) b = sk[i] > b ? sk[i] : b;
-            atomicMax(&st->keys[st->pos & 1], b);
-        }
+        const unsigned long long b = block_max_key(key, (unsigned long long*)(L.misc + 32));
+        if (t == 0) cand[tile] = b;
     }
 };
 
-template <class Pro, class Epi>
-static int launch_mv(const DMat& w, const Plan& p, const Pro& pro, const Epi& epi, int tmp_floats,
-                     hipStream_t s) {
+// ------------------------------------------------------------------
+// launching into a Sink (stream or graph)
+// ------------------------------------------------------------------
+template <class... P>
+struct NodeArgs : NodeArgsBase {
+    std::tuple<P...> t;
+    explicit NodeArgs(P... a) : t(a...) {
+        std::apply([this](auto&... x) { ptrs = {(void*)&x...}; }, t);
+    }
+};
+
+namespace {
+struct ProfScope {
+    Profiler* p;
+    hipStream_t s;
+    int idx = -1;
+    ProfScope(Profiler* p_, hipStream_t s_, const char* name, double bytes) : p(p_), s(s_) {
+        if (!p) return;
+        Profiler::Rec r;
+        r.kind = p->kind_of(name);
+        r.bytes = bytes;
+        (void)hipEventCreate(&r.a);
+        (void)hipEventCreate(&r.b);
+        (void)hipEventRecord(r.a, s);
+        p->recs.push_back(r);
+        idx = (int)p->recs.size() - 1;
+    }
+    ~ProfScope() {
+        if (p && idx >= 0) (void)hipEventRecord(p->recs[idx].b, s);
+    }
+};
+
+template <int I, class Tup>
+int* pos_field(Tup& t) {
+    auto& a = std::get<I>(t);
+    if constexpr (std::is_same_v<std::decay_t<decltype(a)>, int>) return &a;
+    else return &a.pos;
+}
+}  // namespace
+
+// Launch fn<<<grid, block, lds>>>(args...) on the sink.  POS_ARG >= 0 names
+// the argument holding the step position (an int, or a struct with .pos),
+// which graph replays rewrite per step.
+template <int POS_ARG = -1, class... P>
+static int sink_launch(Sink& k, const char* name, double bytes, void (*fn)(P...), dim3 grid, dim3 block, size_t lds,
+                       P... args) {
+    auto blob = std::make_unique<NodeArgs<P...>>(args...);
+    if (k.g) {
+        hipKernelNodeParams prm{};
+        prm.func = (void*)fn;
+        prm.gridDim = grid;
+        prm.blockDim = block;
+        prm.sharedMemBytes = (unsigned)lds;
+        prm.kernelParams = blob->ptrs.data();
+        prm.extra = nullptr;
+        hipGraphNode_t node;
+        GH_HIP(hipGraphAddKernelNode(&node, k.g, k.last ? &k.last : nullptr, k.last ? 1 : 0, &prm));
+        k.last = node;
+        if constexpr (POS_ARG >= 0) k.patches->push_back({node, prm, pos_field<POS_ARG>(blob->t)});
+        k.store->push_back(std::move(blob));
+        return GH_OK;
+    }
+    ProfScope ps(k.prof, k.s, name, bytes);
+    GH_HIP(hipLaunchKernel((const void*)fn, grid, block, blob->ptrs.data(), lds, k.s));
+    return GH_OK;
+}
+
+template <int POS_ARG = -1, class Pro, class Epi>
+static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const Pro& pro,
+                     const Epi& epi, int tmp_floats) {
     const int per_split = (w.nblk + p.S - 1) / p.S;
     const size_t lds = mv_lds_bytes(w.fmt, per_split, tmp_floats);
     const dim3 grid(w.tiles * p.S), block(NT);
+    // POS_ARG counts kernel arguments (DMat, S, Pro, Epi): the prologue is 2
+    auto go = [&](void (*fn)(DMat, int, Pro, Epi)) {
+        return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, w, p.S, pro, epi);
+    };
     if (w.fmt == FMT_Q4) {
         switch (p.kbw) {
-            case 1: hipLaunchKernelGGL((k_matvec<FMT_Q4, 1, Pro, Epi>), grid, block, lds, s, w, p.S, pro, epi); break;
-            case 2: hipLaunchKernelGGL((k_matvec<FMT_Q4, 2, Pro, Epi>), grid, block, lds, s, w, p.S, pro, epi); break;
-            case 3: hipLaunchKernelGGL((k_matvec<FMT_Q4, 3, Pro, Epi>), grid, block, lds, s, w, p.S, pro, epi); break;
-            case 4: hipLaunchKernelGGL((k_matvec<FMT_Q4, 4, Pro, Epi>), grid, block, lds, s, w, p.S, pro, epi); break;
-            case 6: hipLaunchKernelGGL((k_matvec<FMT_Q4, 6, Pro, Epi>), grid, block, lds, s, w, p.S, pro, epi); break;
-            case 9: hipLaunchKernelGGL((k_matvec<FMT_Q4, 9, Pro, Epi>), grid, block, lds, s, w, p.S, pro, epi); break;
+            case 1: return go(k_matvec<FMT_Q4, 1, Pro, Epi>);
+            case 2: return go(k_matvec<FMT_Q4, 2, Pro, Epi>);
+            case 3: return go(k_matvec<FMT_Q4, 3, Pro, Epi>);
+            case 4: return go(k_matvec<FMT_Q4, 4, Pro, Epi>);
+            case 6: return go(k_matvec<FMT_Q4, 6, Pro, Epi>);
+            case 9: return go(k_matvec<FMT_Q4, 9, Pro, Epi>);
             default: return set_error(GH_ERR_INVALID, "unsupported register batch %d", p.kbw);
         }
-    } else {
-        hipLaunchKernelGGL((k_matvec<FMT_F32, 8, Pro, Epi>), grid, block, lds, s, w, p.S, pro, epi);
     }
-    GH_HIP(hipGetLastError());
-    return GH_OK;
+    return go(k_matvec<FMT_F32, 8, Pro, Epi>);
+}
+
+// float4 groups per thread of the residual prologue: ceil(H / 1024)
+template <class F>
+static int with_mg(int H, F&& f) {
+    const int mg = (H / 4 + NT - 1) / NT;
+    switch (mg) {
+        case 1: return f(std::integral_constant<int, 1>{});
+        case 2: return f(std::integral_constant<int, 2>{});
+        case 3: return f(std::integral_constant<int, 3>{});
+        default: return set_error(GH_ERR_INVALID, "hidden size %d above 3072", H);
+    }
+}
+
+// Final norm (once per step): xn = norm(x1 + postnorm(sum_s d_s), w_out).
+template <int MG>
+__global__ __launch_bounds__(NT) void k_final_norm(ProResid<MG> pro, float* xn) {
+    extern __shared__ float lds[];
+    MvLds L;
+    L.red = lds;
+    L.misc = lds + 512;
+    L.xs = lds + 576;
+    L.sxs = L.xs + pro.H;
+    L.tmp = L.sxs;
+    typename ProResid<MG>::Regs r;
+    pro.load(r, 0, pro.H);
+    pro.finish(L, r, 0, pro.H);
+    __syncthreads();
+    for (int i = threadIdx.x; i < pro.H; i += NT) xn[i] = L.xs[i];
 }
 
 // ------------------------------------------------------------------
@@ -510,8 +853,8 @@ struct AttnArgs {
     const float* k_norm;
     int use_qk_norm, zc;
     float eps;
-    const float* inv_freq;  // [HD/2]
-    const StepState* st;
+    const float* rope;  // [max_seq][HD/2] (cos, sin) of this layer type
+    int pos;            // current position (kernel argument, patched per step)
     int global, window, mode;
     // raw mode: q given, window given
     const float* q;
@@ -531,38 +874,45 @@ __device__ __forceinline__ void wave_head_norm(float* p, const float* w, float e
     const int lane = threadIdx.x & 63;
     float ss = 0.0f;
     for (int i = lane; i < HD; i += 64) ss += p[i] * p[i];
-    ss = wave_sum(ss);
-    const float rms = sqrtf(ss / (float)HD + eps);
+    const float rms = sqrtf(wave_sum(ss) / (float)HD + eps);
     for (int i = lane; i < HD; i += 64) p[i] = norm_apply(p[i], rms, w[i], zc);
 }
 
-// In-place split-half RoPE of one head vector by one wave (ropeShader).
+// In-place split-half RoPE of one head vector by one wave (ropeShader),
+// cs = (cos, sin) of pos * f_i for i < HD/2.
 template <int HD>
-__device__ __forceinline__ void wave_head_rope(float* p, const float* inv_freq, int pos) {
+__device__ __forceinline__ void wave_head_rope(float* p, const float2* cs) {
     const int lane = threadIdx.x & 63;
     for (int i = lane; i < HD / 2; i += 64) {
-        const float ang = (float)pos * inv_freq[i];
-        float sn, cs;
-        sincosf(ang, &sn, &cs);
+        const float2 t = cs[i];
         const float a = p[i], b = p[i + HD / 2];
-        p[i] = a * cs - b * sn;
-        p[i + HD / 2] = a * sn + b * cs;
+        p[i] = a * t.x - b * t.y;
+        p[i + HD / 2] = a * t.y + b * t.x;
     }
 }
 
+// One query token over cache positions [pb, pe), split-K: workgroup (g, j)
+// handles kv head g and chunk j, and writes {m[G], l[G], o[G][HD]} (running
+// max, sum of exp, unnormalised output) for the merge.  In step mode the K/V
+// rows of the chunk are loaded at kernel start, together with the QKV split
+// partials, so the kernel waits for one global round trip before computing.
 template <int HD, int G, bool STEP>
 __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     constexpr int LP = HD / 4;    // lanes per position (each lane owns 4 dims)
     constexpr int PPW = 64 / LP;  // positions per wave step
     constexpr int NS = 4 * PPW;   // softmax states per workgroup
+    constexpr int NB = 8;         // positions per group per batch (loads in flight)
+    constexpr int NG4 = (G + 2) * HD / 4;      // float4 groups of q|k|v
+    constexpr int MG4 = (NG4 + NT - 1) / NT;   // per thread
     __shared__ float qs[G * HD], ks[HD], vs[HD];
+    __shared__ float2 cs[HD / 2];
     __shared__ float sm[NS][G], sl[NS][G];
     __shared__ float so[NS][G * HD];
 
     const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
     int pos = -1, pb, pe;
     if (STEP) {
-        pos = a.st->pos;
+        pos = a.pos;
         attn_window(pos, a.global, a.window, a.mode, pb, pe);
     } else {
         pb = a.p_begin;
@@ -572,31 +922,60 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     attn_chunks(pe - pb, a.nc, ch, n_used);
     if (j >= n_used) return;  // uniform per workgroup
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c0 = pb + j * ch, c1 = min(pe, c0 + ch);
+    const int grp = lane / LP, lp = lane % LP;
+    const size_t pstride = (size_t)a.nkv * HD;
+    const float* kb = a.kc + (size_t)g * HD + 4 * lp;
+    const float* vb = a.vc + (size_t)g * HD + 4 * lp;
 
-    if (STEP) {
-        for (int i = tid; i < (G + 2) * HD; i += NT) {
-            int row;
-            float* dst;
-            if (i < G * HD) {
-                row = a.q_off + g * G * HD + i;
-                dst = &qs[i];
-            } else if (i < (G + 1) * HD) {
-                row = a.k_off + g * HD + (i - G * HD);
-                dst = &ks[i - G * HD];
-            } else {
-                row = a.v_off + g * HD + (i - (G + 1) * HD);
-                dst = &vs[i - (G + 1) * HD];
+    // 1. first batch of K/V rows in flight (row pos comes from LDS below)
+    float4 kk[NB], vv[NB];
+    bool val[NB];
+    int p0 = c0 + wave * PPW;
+    auto load_batch = [&]() {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int p = p0 + grp + k * 4 * PPW;
+            val[k] = p < c1;
+            kk[k] = vv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (val[k] && !(STEP && p == pos)) {
+                kk[k] = *(const float4*)(kb + (size_t)p * pstride);
+                vv[k] = *(const float4*)(vb + (size_t)p * pstride);
             }
-            float v = 0.0f;
-            for (int s = 0; s < a.Sa; ++s) v += a.part_qkv[(size_t)s * a.ld_qkv + row];
-            *dst = v;
+        }
+    };
+    if (p0 < c1) load_batch();
+
+    // 2. q (and in step mode k, v of this token) into LDS
+    if (STEP) {
+        float4 pv[MG4];
+#pragma unroll
+        for (int m = 0; m < MG4; ++m) {
+            const int gi = tid + m * NT;
+            if (gi < NG4) {
+                const int i = 4 * gi;
+                const int row = i < G * HD ? a.q_off + g * G * HD + i
+                              : i < (G + 1) * HD ? a.k_off + g * HD + (i - G * HD)
+                                                 : a.v_off + g * HD + (i - (G + 1) * HD);
+                pv[m] = sum_splits4(a.part_qkv, a.Sa, a.ld_qkv, row >> 2);
+            }
+        }
+        for (int i = tid; i < HD / 2; i += NT) cs[i] = ((const float2*)a.rope)[(size_t)pos * (HD / 2) + i];
+#pragma unroll
+        for (int m = 0; m < MG4; ++m) {
+            const int gi = tid + m * NT;
+            if (gi < NG4) {
+                const int i = 4 * gi;
+                float* dst = i < G * HD ? &qs[i] : i < (G + 1) * HD ? &ks[i - G * HD] : &vs[i - (G + 1) * HD];
+                *(float4*)dst = pv[m];
+            }
         }
         __syncthreads();
         // QK-norm (TBG:171-179), then RoPE, on the G q heads and the k head
         for (int vec = wave; vec < G + 1; vec += 4) {
             float* p = vec < G ? qs + vec * HD : ks;
             if (a.use_qk_norm) wave_head_norm<HD>(p, vec < G ? a.q_norm : a.k_norm, a.eps, a.zc);
-            wave_head_rope<HD>(p, a.inv_freq, pos);
+            wave_head_rope<HD>(p, cs);
         }
         __syncthreads();
         if (j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
@@ -610,8 +989,6 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
         __syncthreads();
     }
 
-    const int c0 = pb + j * ch, c1 = min(pe, c0 + ch);
-    const int grp = lane / LP, lp = lane % LP;
     float q[G][4], m[G], l[G], acc[G][4];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -621,45 +998,51 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
         l[h] = 0.0f;
         acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.0f;
     }
-    const size_t pstride = (size_t)a.nkv * HD;
-    const float* kb = a.kc + (size_t)g * HD + 4 * lp;
-    const float* vb = a.vc + (size_t)g * HD + 4 * lp;
-    for (int p0 = c0 + wave * PPW; p0 < c1; p0 += 4 * PPW) {
-        const int p = p0 + grp;
-        const bool valid = p < c1;
-        float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
-        if (valid) {
-            if (STEP && p == pos) {
-                kk = *(const float4*)&ks[4 * lp];
-                vv = *(const float4*)&vs[4 * lp];
-            } else {
-                kk = *(const float4*)(kb + (size_t)p * pstride);
-                vv = *(const float4*)(vb + (size_t)p * pstride);
-            }
+    // 3. online softmax over the batches
+    for (; p0 < c1; p0 += NB * 4 * PPW) {
+        if (STEP) {
+#pragma unroll
+            for (int k = 0; k < NB; ++k)
+                if (val[k] && p0 + grp + k * 4 * PPW == pos) {
+                    kk[k] = *(const float4*)&ks[4 * lp];
+                    vv[k] = *(const float4*)&vs[4 * lp];
+                }
         }
-        float sc[G];
 #pragma unroll
-        for (int h = 0; h < G; ++h) sc[h] = q[h][0] * kk.x + q[h][1] * kk.y + q[h][2] * kk.z + q[h][3] * kk.w;
+        for (int h = 0; h < G; ++h) {
+            float sc[NB];
+            float bmax = -INFINITY;
 #pragma unroll
-        for (int o = LP / 2; o > 0; o >>= 1)
-#pragma unroll
-            for (int h = 0; h < G; ++h) sc[h] += __shfl_xor(sc[h], o, 64);
-        if (valid) {
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float s = sc[h] * a.scale;
-                const float mn = fmaxf(m[h], s);
-                const float corr = expf(m[h] - mn);
-                const float pe_ = expf(s - mn);
-                l[h] = l[h] * corr + pe_;
-                acc[h][0] = acc[h][0] * corr + pe_ * vv.x;
-                acc[h][1] = acc[h][1] * corr + pe_ * vv.y;
-                acc[h][2] = acc[h][2] * corr + pe_ * vv.z;
-                acc[h][3] = acc[h][3] * corr + pe_ * vv.w;
-                m[h] = mn;
+            for (int k = 0; k < NB; ++k) {
+                const float d = group_sum<LP>(q[h][0] * kk[k].x + q[h][1] * kk[k].y + q[h][2] * kk[k].z +
+                                              q[h][3] * kk[k].w);
+                sc[k] = val[k] ? d * a.scale : -INFINITY;
+                bmax = fmaxf(bmax, sc[k]);
             }
+            const float mn = fmaxf(m[h], bmax);
+            const float corr = m[h] == -INFINITY ? 0.0f : __expf(m[h] - mn);
+            float ls = l[h] * corr;
+            float a0 = acc[h][0] * corr, a1 = acc[h][1] * corr, a2 = acc[h][2] * corr, a3 = acc[h][3] * corr;
+#pragma unroll
+            for (int k = 0; k < NB; ++k) {
+                const float pexp = val[k] ? __expf(sc[k] - mn) : 0.0f;
+                ls += pexp;
+                a0 += pexp * vv[k].x;
+                a1 += pexp * vv[k].y;
+                a2 += pexp * vv[k].z;
+                a3 += pexp * vv[k].w;
+            }
+            m[h] = mn;
+            l[h] = ls;
+            acc[h][0] = a0; acc[h][1] = a1; acc[h][2] = a2; acc[h][3] = a3;
+        }
+        if (p0 + NB * 4 * PPW < c1) {
+            p0 += NB * 4 * PPW;
+            load_batch();
+            p0 -= NB * 4 * PPW;
         }
     }
+    // 4. merge the NS softmax states of the workgroup
     const int si = wave * PPW + grp;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -677,7 +1060,7 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
         for (int s2 = 0; s2 < NS; ++s2) M = fmaxf(M, sm[s2][h]);
         float Lsum = 0.0f, O = 0.0f;
         for (int s2 = 0; s2 < NS; ++s2) {
-            const float wgt = expf(sm[s2][h] - M);  // empty states: exp(-inf) = 0
+            const float wgt = sm[s2][h] == -INFINITY ? 0.0f : expf(sm[s2][h] - M);
             Lsum += sl[s2][h] * wgt;
             O += so[s2][idx] * wgt;
         }
@@ -690,14 +1073,11 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
 }
 
 template <bool STEP>
-static int launch_attn_t(int hd, int G, const AttnArgs& a, int nkv, hipStream_t s) {
+static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
+    if (a.nc > ATTN_MAX_NC) return set_error(GH_ERR_INVALID, "attention: more than %d splits", ATTN_MAX_NC);
     const dim3 grid(nkv * a.nc), block(NT);
-#define GH_ATTN_CASE(HD_, G_)                                                         \
-    if (hd == HD_ && G == G_) {                                                       \
-        hipLaunchKernelGGL((k_attn<HD_, G_, STEP>), grid, block, 0, s, a);            \
-        GH_HIP(hipGetLastError());                                                    \
-        return GH_OK;                                                                 \
-    }
+#define GH_ATTN_CASE(HD_, G_) \
+    if (hd == HD_ && G == G_) return sink_launch<STEP ? 0 : -1>(k, "attention", bytes, k_attn<HD_, G_, STEP>, grid, block, 0, a);
     GH_ATTN_CASE(256, 1) GH_ATTN_CASE(256, 2) GH_ATTN_CASE(256, 4) GH_ATTN_CASE(256, 8)
     GH_ATTN_CASE(128, 1) GH_ATTN_CASE(128, 2) GH_ATTN_CASE(128, 4) GH_ATTN_CASE(128, 8)
     GH_ATTN_CASE(32, 1) GH_ATTN_CASE(32, 2) GH_ATTN_CASE(32, 4) GH_ATTN_CASE(32, 8)
@@ -705,21 +1085,36 @@ static int launch_attn_t(int hd, int G, const AttnArgs& a, int nkv, hipStream_t 
     return set_error(GH_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
 
+// Merge of the split-K partials for the op-level entry point.
 __global__ void k_attn_combine(const float* part, int nc, int n_used, int G, int HD, int nq, float* out) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= nq * HD) return;
-    const int h = idx / HD, d = idx % HD;
-    out[idx] = attn_merge(part, nc, n_used, G, HD, h / G, h % G, d);
+    const int h = idx / HD, d = idx % HD, g = h / G, hl = h % G;
+    const int stride = G * (HD + 2);
+    const float* base = part + (size_t)g * nc * stride;
+    float M = -INFINITY;
+    for (int j = 0; j < n_used; ++j) M = fmaxf(M, base[(size_t)j * stride + hl]);
+    float den = 0.0f, num = 0.0f;
+    for (int j = 0; j < n_used; ++j) {
+        const float* p = base + (size_t)j * stride;
+        const float wgt = expf(p[hl] - M);
+        den += p[G + hl] * wgt;
+        num += p[2 * G + hl * HD + d] * wgt;
+    }
+    out[idx] = num / den;
 }
 
 // ------------------------------------------------------------------
-// step epilogue: next token, position, argmax slot reset
+// step epilogue: greedy token from the per-tile keys, next token, position
 // ------------------------------------------------------------------
-__global__ void k_step_finish(StepState* st, const int32_t* prompt, int32_t* ids) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    const int pos = st->pos;
-    const unsigned long long key = st->keys[pos & 1];
-    const int tok = (int)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
+__global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, const unsigned long long* cand, int n_cand,
+                                                    const int32_t* prompt, int32_t* ids) {
+    __shared__ unsigned long long slot[4];
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < n_cand; i += NT) best = umax64(best, cand[i]);
+    best = block_max_key(best, slot);
+    if (threadIdx.x != 0) return;
+    const int tok = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFull));
     st->last = tok;
     const int rel = pos + 1 - st->start;
     int next = tok;
@@ -730,12 +1125,11 @@ __global__ void k_step_finish(StepState* st, const int32_t* prompt, int32_t* ids
         st->gen_count = st->gen_count + 1;
     }
     st->token = next;
-    st->keys[(pos + 1) & 1] = 0ull;
     st->pos = pos + 1;
 }
 
 // ------------------------------------------------------------------
-// the decode step: 5 kernels per layer + LM head + finish
+// the decode step
 // ------------------------------------------------------------------
 int Profiler::kind_of(const char* name) {
     for (size_t i = 0; i < names.size(); ++i)
@@ -745,66 +1139,45 @@ int Profiler::kind_of(const char* name) {
 }
 
 namespace {
-struct ProfScope {
-    Profiler* p;
-    hipStream_t s;
-    int idx = -1;
-    ProfScope(Profiler* p_, hipStream_t s_, const char* name, double bytes) : p(p_), s(s_) {
-        if (!p) return;
-        Profiler::Rec r;
-        r.kind = p->kind_of(name);
-        r.bytes = bytes;
-        hipEventCreate(&r.a);
-        hipEventCreate(&r.b);
-        hipEventRecord(r.a, s);
-        p->recs.push_back(r);
-        idx = (int)p->recs.size() - 1;
-    }
-    ~ProfScope() {
-        if (p && idx >= 0) hipEventRecord(p->recs[idx].b, s);
-    }
-};
-
 double mat_bytes(const DMat& w) {
     const double wb = w.fmt == FMT_Q4 ? (double)w.rows * w.cols / 32.0 * 18.0 : (double)w.rows * w.cols * 4.0;
     return wb + 4.0 * w.cols + 4.0 * w.rows;
 }
 }  // namespace
 
-int enqueue_step(gh_model* m, gh_kv* kv, hipStream_t s, Profiler* prof) {
+int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     const gh_config& c = m->cfg;
-    const int H = c.hidden, nq = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
-    const int G = nq / nkv;
+    const int H = c.hidden, nkv = c.n_kv_heads, hd = c.head_dim;
+    const int G = c.n_heads / nkv;
     const int zc = (c.flags & GH_FLAG_ZERO_CENTERED) ? 1 : 0;
     const float eps = c.rms_eps;
     const size_t kv_layer = (size_t)kv->max_seq * nkv * hd;
-    const int n_pos_host = std::min(kv->len + 1, kv->max_seq);  // for profiling byte counts only
+    const int n_pos_host = std::min(pos + 1, kv->max_seq);  // profiling byte counts only
 
     for (int li = 0; li < c.n_layers; ++li) {
         LayerDev& L = m->layers[li];
         const LayerDev* P = li > 0 ? &m->layers[li - 1] : nullptr;
         // A: residual + pre-attention norm + fused QKV matvec
-        {
-            ProResidNorm pro;
+        GH_CHECK(with_mg(H, [&](auto mg) {
+            ProResid<decltype(mg)::value> pro;
             pro.from_embedding = li == 0;
             pro.embd = m->embd;
             pro.st = kv->st;
             pro.escale = sqrtf((float)H);
-            pro.x1 = m->x1;
-            pro.part_d = m->part_d;
-            pro.Sd = m->pe.S;
-            pro.ld_d = P ? P->down.tiles * TILE_ROWS : 0;
+            pro.base = m->x1;
+            pro.part = m->part_d;
+            pro.S = m->pe.S;
+            pro.ld = P ? P->down.tiles * TILE_ROWS : 0;
             pro.w_post = P && (c.flags & GH_FLAG_POST_FFN_NORM) ? P->post_ffw : nullptr;
             pro.w_norm = L.attn_norm;
             pro.eps = eps;
             pro.zc = zc;
             pro.H = H;
-            pro.x_res = m->x_res;
+            pro.x_out = m->x_res;
             pro.layer_out_row = li > 0 ? m->layer_out + (size_t)(li - 1) * H : nullptr;
             EpiPartial epi{m->part_qkv, L.qkv.tiles * TILE_ROWS};
-            ProfScope ps(prof, s, "qkv", mat_bytes(L.qkv));
-            GH_CHECK(launch_mv(L.qkv, m->pa, pro, epi, H, s));
-        }
+            return launch_mv(sink, "qkv", mat_bytes(L.qkv), L.qkv, m->pa, pro, epi, H);
+        }));
         // B: QK-norm + RoPE + KV append + split-K attention
         {
             AttnArgs a{};
@@ -819,9 +1192,9 @@ int enqueue_step(gh_model* m, gh_kv* kv, hipStream_t s, Profiler* prof) {
             a.use_qk_norm = (c.flags & GH_FLAG_QK_NORM) && L.q_norm && L.k_norm;
             a.zc = zc;
             a.eps = eps;
-            const bool global = c.mode == GH_MODE_REF ? true : L.global;
-            a.inv_freq = m->inv_freq + (global ? hd / 2 : 0);
-            a.st = kv->st;
+            const bool global_theta = c.mode == GH_MODE_REF ? true : L.global;
+            a.rope = kv->rope + (global_theta ? (size_t)kv->max_seq * hd : 0);
+            a.pos = pos;
             a.global = L.global;
             a.window = c.sliding_window;
             a.mode = c.mode;
@@ -831,71 +1204,78 @@ int enqueue_step(gh_model* m, gh_kv* kv, hipStream_t s, Profiler* prof) {
             a.scale = 1.0f / sqrtf((float)hd);
             a.part = m->attn_part;
             a.nc = m->attn_nc;
-            ProfScope ps(prof, s, "attention", 2.0 * 4.0 * hd * nkv * n_pos_host);
-            GH_CHECK(launch_attn_t<true>(hd, G, a, nkv, s));
+            GH_CHECK(launch_attn_t<true>(sink, 2.0 * 4.0 * hd * nkv * n_pos_host, hd, G, a, nkv));
         }
         // C: attention merge + O projection
         {
-            ProAttnCombine pro{m->attn_part, kv->st, m->attn_nc, G, hd, L.global ? 1 : 0,
-                               c.sliding_window, c.mode};
+            ProAttnCombine pro{m->attn_part, pos, m->attn_nc, G, hd, L.global ? 1 : 0, c.sliding_window, c.mode};
             EpiPartial epi{m->part_o, L.o.tiles * TILE_ROWS};
-            ProfScope ps(prof, s, "o_proj", mat_bytes(L.o));
-            GH_CHECK(launch_mv(L.o, m->pc, pro, epi, 0, s));
+            const int per_split = (L.o.nblk + m->pc.S - 1) / m->pc.S * block_cols(L.o.fmt);
+            GH_CHECK(launch_mv<2>(sink, "o_proj", mat_bytes(L.o), L.o, m->pc, pro, epi,
+                                  (per_split / hd + 2) * ATTN_MAX_NC));
         }
         // D: post-attention norm + residual + pre-FFN norm + gate/up matvec
-        {
-            ProPostAttn pro;
-            pro.part_o = m->part_o;
-            pro.So = m->pc.S;
-            pro.ld_o = L.o.tiles * TILE_ROWS;
+        GH_CHECK(with_mg(H, [&](auto mg) {
+            ProResid<decltype(mg)::value> pro;
+            pro.from_embedding = 0;
+            pro.embd = m->embd;
+            pro.st = kv->st;
+            pro.escale = 1.0f;
+            pro.base = m->x_res;
+            pro.part = m->part_o;
+            pro.S = m->pc.S;
+            pro.ld = L.o.tiles * TILE_ROWS;
             pro.w_post = (c.flags & GH_FLAG_POST_ATTN_NORM) ? L.post_attn : nullptr;
-            pro.x_res = m->x_res;
-            pro.x1_out = m->x1;
-            pro.w_ffn = L.ffn_norm ? L.ffn_norm : L.post_attn;
+            pro.w_norm = L.ffn_norm ? L.ffn_norm : L.post_attn;
             pro.eps = eps;
             pro.zc = zc;
             pro.H = H;
+            pro.x_out = m->x1;
+            pro.layer_out_row = nullptr;
             EpiPartial epi{m->part_gu, L.gu.tiles * TILE_ROWS};
-            ProfScope ps(prof, s, "gate_up", mat_bytes(L.gu));
-            GH_CHECK(launch_mv(L.gu, m->pd, pro, epi, H, s));
-        }
+            return launch_mv(sink, "gate_up", mat_bytes(L.gu), L.gu, m->pd, pro, epi, H);
+        }));
         // E: GeGLU + down projection
         {
             ProGeglu pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad};
             EpiPartial epi{m->part_d, L.down.tiles * TILE_ROWS};
-            ProfScope ps(prof, s, "down", mat_bytes(L.down));
-            GH_CHECK(launch_mv(L.down, m->pe, pro, epi, 0, s));
+            GH_CHECK(launch_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, pro, epi, 0));
         }
     }
-    // final norm + LM head + argmax
+    // final residual + norm, once
     {
         const LayerDev& P = m->layers[c.n_layers - 1];
-        ProResidNorm pro;
-        pro.from_embedding = 0;
-        pro.embd = m->embd;
-        pro.st = kv->st;
-        pro.escale = 1.0f;
-        pro.x1 = m->x1;
-        pro.part_d = m->part_d;
-        pro.Sd = m->pe.S;
-        pro.ld_d = P.down.tiles * TILE_ROWS;
-        pro.w_post = (c.flags & GH_FLAG_POST_FFN_NORM) ? P.post_ffw : nullptr;
-        pro.w_norm = m->out_norm;
-        pro.eps = eps;
-        pro.zc = zc;
-        pro.H = H;
-        pro.x_res = nullptr;
-        pro.layer_out_row = m->layer_out + (size_t)(c.n_layers - 1) * H;
-        EpiLogits epi{m->logits, c.vocab, kv->st};
-        ProfScope ps(prof, s, "lm_head", mat_bytes(m->embd));
-        GH_CHECK(launch_mv(m->embd, m->plm, pro, epi, H, s));
+        GH_CHECK(with_mg(H, [&](auto mg) {
+            constexpr int MG = decltype(mg)::value;
+            ProResid<MG> pro;
+            pro.from_embedding = 0;
+            pro.embd = m->embd;
+            pro.st = kv->st;
+            pro.escale = 1.0f;
+            pro.base = m->x1;
+            pro.part = m->part_d;
+            pro.S = m->pe.S;
+            pro.ld = P.down.tiles * TILE_ROWS;
+            pro.w_post = (c.flags & GH_FLAG_POST_FFN_NORM) ? P.post_ffw : nullptr;
+            pro.w_norm = m->out_norm;
+            pro.eps = eps;
+            pro.zc = zc;
+            pro.H = H;
+            pro.x_out = nullptr;
+            pro.layer_out_row = m->layer_out + (size_t)(c.n_layers - 1) * H;
+            const size_t lds = (576 + 2 * (size_t)H) * sizeof(float);
+            return sink_launch(sink, "final_norm", 0.0, k_final_norm<MG>, dim3(1), dim3(NT), lds, pro, m->xn_final);
+        }));
     }
+    // LM head (tied embedding) + per-tile argmax keys
     {
-        ProfScope ps(prof, s, "finish", 0.0);
-        hipLaunchKernelGGL(k_step_finish, dim3(1), dim3(64), 0, s, kv->st, kv->d_prompt, kv->d_ids);
-        GH_HIP(hipGetLastError());
+        ProPlain pro{m->xn_final};
+        EpiLogits epi{m->logits, c.vocab, m->lm_cand, kv->st};
+        GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(m->embd), m->embd, m->plm, pro, epi, 0));
     }
-    return GH_OK;
+    return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
+                          (const unsigned long long*)m->lm_cand, (int)m->embd.tiles, (const int32_t*)kv->d_prompt,
+                          kv->d_ids);
 }
 
 // ------------------------------------------------------------------
@@ -917,8 +1297,7 @@ int launch_q4_dequant(const DMat& w, float* out, hipStream_t s) {
     return GH_OK;
 }
 
-__global__ void k_sum_partials(const float* part, int S, int ld, int rows, int softcap, float cap,
-                               float* y) {
+__global__ void k_sum_partials(const float* part, int S, int ld, int rows, int softcap, float cap, float* y) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
     float a = 0.0f;
@@ -926,25 +1305,28 @@ __global__ void k_sum_partials(const float* part, int S, int ld, int rows, int s
     y[r] = softcap ? cap * tanhf(a / cap) : a;
 }
 
-int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* part, float* y,
-                        int softcap, float cap, hipStream_t s) {
+int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* part, float* y, int softcap, float cap,
+                        hipStream_t s) {
     ProPlain pro{x};
+    Sink k;
+    k.s = s;
     if (p.S == 1) {
         EpiOut epi{y, w.rows, softcap, cap};
-        return launch_mv(w, p, pro, epi, 0, s);
+        return launch_mv(k, "matvec", 0.0, w, p, pro, epi, 0);
     }
     EpiPartial epi{part, w.tiles * TILE_ROWS};
-    GH_CHECK(launch_mv(w, p, pro, epi, 0, s));
-    hipLaunchKernelGGL(k_sum_partials, dim3((w.rows + 255) / 256), dim3(256), 0, s, part, p.S,
-                       w.tiles * TILE_ROWS, w.rows, softcap, cap, y);
+    GH_CHECK(launch_mv(k, "matvec", 0.0, w, p, pro, epi, 0));
+    hipLaunchKernelGGL(k_sum_partials, dim3((w.rows + 255) / 256), dim3(256), 0, s, part, p.S, w.tiles * TILE_ROWS,
+                       w.rows, softcap, cap, y);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }
 
-__global__ __launch_bounds__(NT) void k_rmsnorm(const float* x, const float* w, int n, float eps, int zc,
-                                                float* y) {
-    __shared__ float red[4];
-    const float rms = block_rms(x, n, eps, red);
+__global__ __launch_bounds__(NT) void k_rmsnorm(const float* x, const float* w, int n, float eps, int zc, float* y) {
+    __shared__ float slot[4];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += NT) ss += x[i] * x[i];
+    const float rms = sqrtf(block_sum(ss, slot) / (float)n + eps);
     for (int i = threadIdx.x; i < n; i += NT) y[i] = norm_apply(x[i], rms, w[i], zc);
 }
 
@@ -965,8 +1347,7 @@ __global__ void k_qk_norm(const float* x, const float* w, int n_heads, float eps
     wave_head_norm<HD>(y + h * HD, w, eps, zc);
 }
 
-int launch_qk_norm(const float* x, const float* w, int n_heads, int hd, float eps, int zc, float* y,
-                   hipStream_t s) {
+int launch_qk_norm(const float* x, const float* w, int n_heads, int hd, float eps, int zc, float* y, hipStream_t s) {
     const dim3 grid((n_heads + 3) / 4), block(NT);
     if (hd == 256) hipLaunchKernelGGL(k_qk_norm<256>, grid, block, 0, s, x, w, n_heads, eps, zc, y);
     else if (hd == 128) hipLaunchKernelGGL(k_qk_norm<128>, grid, block, 0, s, x, w, n_heads, eps, zc, y);
@@ -977,35 +1358,25 @@ int launch_qk_norm(const float* x, const float* w, int n_heads, int hd, float ep
 }
 
 template <int HD>
-__global__ void k_rope(float* x, int n_heads, const float* inv_freq, int pos) {
+__global__ void k_rope(float* x, int n_heads, const float2* cs) {
     const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (h >= n_heads) return;
-    wave_head_rope<HD>(x + h * HD, inv_freq, pos);
+    wave_head_rope<HD>(x + h * HD, cs);
 }
 
-int launch_rope(float* x, int n_heads, int hd, float theta, int pos, hipStream_t s) {
-    // inverse frequencies computed on the host with ropeShader's formula
-    std::vector<float> f(hd / 2);
-    for (int i = 0; i < hd / 2; ++i) f[i] = 1.0f / powf(theta, (float)(i * 2) / (float)hd);
-    float* d = nullptr;
-    GH_HIP(hipMallocAsync((void**)&d, sizeof(float) * f.size(), s));
-    GH_HIP(hipMemcpyAsync(d, f.data(), sizeof(float) * f.size(), hipMemcpyHostToDevice, s));
+int launch_rope(float* x, int n_heads, int hd, const float* cs_dev, hipStream_t s) {
     const dim3 grid((n_heads + 3) / 4), block(NT);
-    if (hd == 256) hipLaunchKernelGGL(k_rope<256>, grid, block, 0, s, x, n_heads, d, pos);
-    else if (hd == 128) hipLaunchKernelGGL(k_rope<128>, grid, block, 0, s, x, n_heads, d, pos);
-    else if (hd == 32) hipLaunchKernelGGL(k_rope<32>, grid, block, 0, s, x, n_heads, d, pos);
-    else {
-        hipFreeAsync(d, s);
-        return set_error(GH_ERR_INVALID, "rope: unsupported head_dim %d", hd);
-    }
+    const float2* cs = (const float2*)cs_dev;
+    if (hd == 256) hipLaunchKernelGGL(k_rope<256>, grid, block, 0, s, x, n_heads, cs);
+    else if (hd == 128) hipLaunchKernelGGL(k_rope<128>, grid, block, 0, s, x, n_heads, cs);
+    else if (hd == 32) hipLaunchKernelGGL(k_rope<32>, grid, block, 0, s, x, n_heads, cs);
+    else return set_error(GH_ERR_INVALID, "rope: unsupported head_dim %d", hd);
     GH_HIP(hipGetLastError());
-    GH_HIP(hipStreamSynchronize(s));  // f is a host temporary
-    GH_HIP(hipFreeAsync(d, s));
     return GH_OK;
 }
 
-int launch_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
-                     int p_begin, int p_end, int n_splits, float* part, float* out, hipStream_t s) {
+int launch_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd, int p_begin, int p_end,
+                     int n_splits, float* part, float* out, hipStream_t s) {
     AttnArgs a{};
     a.q = q;
     a.p_begin = p_begin;
@@ -1016,11 +1387,13 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     a.scale = 1.0f / sqrtf((float)hd);
     a.part = part;
     a.nc = n_splits;
-    GH_CHECK(launch_attn_t<false>(hd, nq / nkv, a, nkv, s));
-    int n_pos = p_end - p_begin, ch = (n_pos + n_splits - 1) / n_splits;
-    int n_used = (n_pos + ch - 1) / ch;
-    hipLaunchKernelGGL(k_attn_combine, dim3((nq * hd + 255) / 256), dim3(256), 0, s, part, n_splits,
-                       n_used, nq / nkv, hd, nq, out);
+    Sink k;
+    k.s = s;
+    GH_CHECK(launch_attn_t<false>(k, 0.0, hd, nq / nkv, a, nkv));
+    const int n_pos = p_end - p_begin, ch = (n_pos + n_splits - 1) / n_splits;
+    const int n_used = (n_pos + ch - 1) / ch;
+    hipLaunchKernelGGL(k_attn_combine, dim3((nq * hd + 255) / 256), dim3(256), 0, s, part, n_splits, n_used, nq / nkv,
+                       hd, nq, out);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }
@@ -1036,33 +1409,28 @@ int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t
     return GH_OK;
 }
 
-__global__ void k_fill_u64(unsigned long long* p, unsigned long long v) { *p = v; }
-
-__global__ __launch_bounds__(NT) void k_argmax(const float* v, int n, unsigned long long* key) {
-    __shared__ unsigned long long sk[4];
+// per-block argmax keys, then one block reduces them
+__global__ __launch_bounds__(NT) void k_argmax_blocks(const float* v, int n, unsigned long long* cand) {
+    __shared__ unsigned long long slot[4];
     unsigned long long best = 0ull;
-    for (int i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
-        const unsigned long long k = argmax_key(v[i], i);
-        best = k > best ? k : best;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const unsigned long long k2 = shfl_xor_u64(best, o);
-        best = k2 > best ? k2 : best;
-    }
-    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int i = 1; i < 4; ++i) best = sk[i] > best ? sk[i] : best;
-        best = sk[0] > best ? sk[0] : best;
-        atomicMax(key, best);
-    }
+    for (int i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) best = umax64(best, argmax_key(v[i], i));
+    best = block_max_key(best, slot);
+    if (threadIdx.x == 0) cand[blockIdx.x] = best;
+}
+
+__global__ __launch_bounds__(NT) void k_argmax_final(const unsigned long long* cand, int n, unsigned long long* key) {
+    __shared__ unsigned long long slot[4];
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < n; i += NT) best = umax64(best, cand[i]);
+    best = block_max_key(best, slot);
+    if (threadIdx.x == 0) *key = best;
 }
 
 int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s) {
-    hipLaunchKernelGGL(k_fill_u64, dim3(1), dim3(1), 0, s, key, 0ull);
     const int blocks = std::max(1, std::min(1024, (n + NT - 1) / NT));
-    hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(NT), 0, s, v, n, key);
+    // key points at a buffer of 1 + 1024 entries: [0] result, [1..] per-block keys
+    hipLaunchKernelGGL(k_argmax_blocks, dim3(blocks), dim3(NT), 0, s, v, n, key + 1);
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(NT), 0, s, key + 1, blocks, key);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }

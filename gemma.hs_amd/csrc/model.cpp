@@ -146,23 +146,20 @@ void make_plans(gh_model* m) {
         if (s > 0) {
             Plan q = choose_plan(m->fmt, d.tiles, d.nblk, 1);
             q.S = std::min(s, d.nblk);
-            int per_wave = ((d.nblk + q.S - 1) / q.S + 3) / 4;
-            static const int kQ4[] = {1, 2, 3, 4, 6, 9};
-            q.kbw = 9;
-            if (m->fmt == FMT_Q4) {
-                for (int k : kQ4)
-                    if (k >= per_wave) { q.kbw = k; break; }
-            } else {
-                q.kbw = 8;
-            }
             p = q;
         }
     };
+    auto capped = [](Plan& p) { p.S = std::min(p.S, 8); };
     over(m->pa, "GH_PLAN_A_S", L.qkv);
     over(m->pc, "GH_PLAN_C_S", L.o);
     over(m->pd, "GH_PLAN_D_S", L.gu);
     over(m->pe, "GH_PLAN_E_S", L.down);
-    m->attn_nc = std::max(1, env_int("GH_ATTN_NC", 16));
+    for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe}) {
+        capped(*p);
+        const DMat& d = p == &m->pa ? L.qkv : p == &m->pc ? L.o : p == &m->pd ? L.gu : L.down;
+        p->kbw = kbw_for(m->fmt, ((d.nblk + p->S - 1) / p->S + 3) / 4);
+    }
+    m->attn_nc = std::max(1, std::min(64, env_int("GH_ATTN_NC", 16)));
 }
 
 int ensure_scratch(gh_model* m) {
@@ -180,6 +177,8 @@ int ensure_scratch(gh_model* m) {
     GH_CHECK(dev_alloc(m, &m->attn_part, (size_t)c.n_kv_heads * m->attn_nc * G * (c.head_dim + 2)));
     GH_CHECK(dev_alloc(m, &m->logits, (size_t)m->embd.tiles * TILE_ROWS));
     GH_CHECK(dev_alloc(m, &m->layer_out, (size_t)c.n_layers * c.hidden));
+    GH_CHECK(dev_alloc(m, &m->xn_final, c.hidden));
+    GH_CHECK(dev_alloc(m, &m->lm_cand, (size_t)m->embd.tiles));
     return GH_OK;
 }
 
@@ -189,20 +188,25 @@ int model_ready(gh_model* m) {
     return ensure_scratch(m);
 }
 
+// The step as a graph: a linear chain of kernel nodes built explicitly, so
+// the nodes whose arguments hold the position can be patched per replay.
 int kv_graph(gh_kv* kv) {
     if (kv->graph_exec) return GH_OK;
     gh_model* m = kv->m;
-    hipStream_t s = m->ctx->stream;
-    GH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(m, kv, s, nullptr);
     hipGraph_t g = nullptr;
-    hipError_t e = hipStreamEndCapture(s, &g);
+    GH_HIP(hipGraphCreate(&g, 0));
+    Sink sink;
+    sink.g = g;
+    sink.store = &kv->graph_args;
+    sink.patches = &kv->patches;
+    kv->graph_args.clear();
+    kv->patches.clear();
+    int rc = enqueue_step(m, kv, sink, 0);
     if (rc != GH_OK) {
-        if (g) hipGraphDestroy(g);
+        hipGraphDestroy(g);
         return rc;
     }
-    if (e != hipSuccess) return set_error(GH_ERR_HIP, "stream capture failed: %s", hipGetErrorString(e));
-    e = hipGraphInstantiate(&kv->graph_exec, g, nullptr, nullptr, 0);
+    hipError_t e = hipGraphInstantiate(&kv->graph_exec, g, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         hipGraphDestroy(g);
         return set_error(GH_ERR_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
@@ -211,11 +215,20 @@ int kv_graph(gh_kv* kv) {
     return GH_OK;
 }
 
-// One step on the stream: graph replay (default) or eager launches.
-int launch_step(gh_kv* kv) {
+// One step at position `pos` on the stream: graph replay with the position
+// patched into its nodes (default), or eager launches (GH_NO_GRAPH=1).
+int launch_step(gh_kv* kv, int pos) {
     hipStream_t s = kv->m->ctx->stream;
-    if (env_int("GH_NO_GRAPH", 0)) return enqueue_step(kv->m, kv, s, nullptr);
+    if (env_int("GH_NO_GRAPH", 0)) {
+        Sink sink;
+        sink.s = s;
+        return enqueue_step(kv->m, kv, sink, pos);
+    }
     GH_CHECK(kv_graph(kv));
+    for (auto& p : kv->patches) {
+        *p.pos = pos;
+        GH_HIP(hipGraphExecKernelNodeSetParams(kv->graph_exec, p.node, &p.params));
+    }
     GH_HIP(hipGraphLaunch(kv->graph_exec, s));
     return GH_OK;
 }
@@ -433,10 +446,18 @@ extern "C" int gh_qk_norm(gh_ctx* ctx, const float* x, const float* w, int n_hea
 
 extern "C" int gh_rope(gh_ctx* ctx, float* x, int n_heads, int hd, float theta, int pos) {
     OP_ENTER(ctx);
-    if (!x || n_heads <= 0 || pos < 0) return set_error(GH_ERR_INVALID, "gh_rope: bad arguments");
-    GH_CHECK(launch_rope(x, n_heads, hd, theta, pos, ctx->stream));
-    GH_HIP(hipStreamSynchronize(ctx->stream));
-    return GH_OK;
+    if (!x || n_heads <= 0 || pos < 0 || hd <= 0 || hd % 2) return set_error(GH_ERR_INVALID, "gh_rope: bad arguments");
+    const int half = hd / 2;
+    std::vector<float> f(half), tab((size_t)half * 2);
+    for (int i = 0; i < half; ++i) f[i] = 1.0f / powf(theta, (float)(i * 2) / (float)hd);
+    rope_table(f.data(), half, pos, 1, tab.data());
+    float* d = nullptr;
+    GH_HIP(hipMalloc((void**)&d, tab.size() * sizeof(float)));
+    int rc = upload(ctx, d, tab.data(), tab.size() * sizeof(float));
+    if (rc == GH_OK) rc = launch_rope(x, n_heads, hd, d, ctx->stream);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess && rc == GH_OK) rc = set_error(GH_ERR_HIP, "gh_rope: sync failed");
+    hipFree(d);
+    return rc;
 }
 
 extern "C" int gh_attention_decode(gh_ctx* ctx, const float* q, const float* kc, const float* vc, int nq, int nkv,
@@ -445,8 +466,8 @@ extern "C" int gh_attention_decode(gh_ctx* ctx, const float* q, const float* kc,
     if (!q || !kc || !vc || !out || nkv <= 0 || nq % nkv || p_begin < 0 || p_end <= p_begin)
         return set_error(GH_ERR_INVALID, "gh_attention_decode: bad arguments");
     const int n_pos = p_end - p_begin;
-    if (n_splits <= 0) n_splits = std::max(1, std::min(n_pos / 64, std::max(1, 1024 / nkv)));
-    n_splits = std::min(n_splits, n_pos);
+    if (n_splits <= 0) n_splits = std::max(1, std::min(n_pos / 64, 64));
+    n_splits = std::min(std::min(n_splits, n_pos), 64);
     float* part = nullptr;
     const int G = nq / nkv;
     GH_HIP(hipMallocAsync((void**)&part, sizeof(float) * nkv * n_splits * G * (hd + 2), ctx->stream));
@@ -467,8 +488,8 @@ extern "C" int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, f
 extern "C" int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx) {
     OP_ENTER(ctx);
     if (!v || !idx || n <= 0) return set_error(GH_ERR_INVALID, "gh_argmax: bad arguments");
-    unsigned long long* key = nullptr;
-    GH_HIP(hipMallocAsync((void**)&key, 8, ctx->stream));
+    unsigned long long* key = nullptr;  // [0] result, [1..1024] per-block keys
+    GH_HIP(hipMallocAsync((void**)&key, 8 * 1025, ctx->stream));
     int rc = launch_argmax(v, n, key, ctx->stream);
     unsigned long long h = 0;
     if (rc == GH_OK) {
@@ -535,14 +556,12 @@ extern "C" int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out
     for (int l = 0; l < c.n_layers; ++l)
         m->layers[l].global = c.global_every <= 0 || ((l + 1) % c.global_every) == 0;
     // RoPE inverse frequencies, ropeShader's formula (AttentionGPU.hs:98-99)
-    std::vector<float> f(c.head_dim);
+    m->inv_freq.resize(c.head_dim);
     for (int i = 0; i < c.head_dim / 2; ++i) {
         const float e = (float)(i * 2) / (float)c.head_dim;
-        f[i] = 1.0f / powf(c.rope_theta_local, e);
-        f[c.head_dim / 2 + i] = 1.0f / powf(c.rope_theta_global, e);
+        m->inv_freq[i] = 1.0f / powf(c.rope_theta_local, e);
+        m->inv_freq[c.head_dim / 2 + i] = 1.0f / powf(c.rope_theta_global, e);
     }
-    GH_CHECK(dev_alloc(m.get(), &m->inv_freq, c.head_dim));
-    GH_CHECK(upload(ctx, m->inv_freq, f.data(), sizeof(float) * c.head_dim));
     *out = m.release();
     return GH_OK;
 }
@@ -695,6 +714,15 @@ extern "C" int gh_kv_create(gh_model* m, int32_t max_seq, gh_kv** out) {
         return set_error(GH_ERR_OOM, "KV cache of %zu bytes does not fit", 2 * n * 4);
     }
     GH_HIP(hipMalloc((void**)&kv->st, sizeof(StepState)));
+    {
+        // (cos, sin) of pos * inv_freq for both layer types, positions [0, max_seq)
+        const int half = c.head_dim / 2;
+        std::vector<float> tab((size_t)2 * max_seq * half * 2);
+        rope_table(m->inv_freq.data(), half, 0, max_seq, tab.data());
+        rope_table(m->inv_freq.data() + half, half, 0, max_seq, tab.data() + (size_t)max_seq * half * 2);
+        GH_HIP(hipMalloc((void**)&kv->rope, tab.size() * sizeof(float)));
+        GH_HIP(hipMemcpy(kv->rope, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
+    }
     GH_HIP(hipMalloc((void**)&kv->d_prompt, sizeof(int32_t) * max_seq));
     GH_HIP(hipMalloc((void**)&kv->d_ids, sizeof(int32_t) * max_seq));
     GH_HIP(hipHostMalloc((void**)&kv->h_st, sizeof(StepState), hipHostMallocDefault));
@@ -715,6 +743,7 @@ extern "C" int gh_kv_destroy(gh_kv* kv) {
     hipFree(kv->k);
     hipFree(kv->v);
     hipFree(kv->st);
+    hipFree(kv->rope);
     hipFree(kv->d_prompt);
     hipFree(kv->d_ids);
     hipHostFree(kv->h_st);
@@ -748,7 +777,7 @@ extern "C" int gh_step(gh_model* m, gh_kv* kv, int32_t token, float* logits, flo
     if (kv->len >= kv->max_seq) return set_error(GH_ERR_RANGE, "KV cache full (%d positions)", kv->max_seq);
     hipStream_t s = m->ctx->stream;
     GH_CHECK(put_state(kv, kv->len, token, kv->len, 0, 0));
-    GH_CHECK(launch_step(kv));
+    GH_CHECK(launch_step(kv, kv->len));
     GH_CHECK(get_state(kv));
     if (logits) GH_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * c.vocab, hipMemcpyDeviceToHost, s));
     if (layer_out)
@@ -772,7 +801,8 @@ static int run_device_fed(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t
     hipStream_t s = m->ctx->stream;
     GH_HIP(hipMemcpyAsync(kv->d_prompt, prompt, sizeof(int32_t) * n_prompt, hipMemcpyHostToDevice, s));
     GH_CHECK(put_state(kv, kv->len, prompt[0], kv->len, n_prompt, gen_cap));
-    for (int i = 0; i < n_before; ++i) GH_CHECK(launch_step(kv));
+    const int pos0 = kv->len;
+    for (int i = 0; i < n_before; ++i) GH_CHECK(launch_step(kv, pos0 + i));
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (ms_out) {
         GH_HIP(hipStreamSynchronize(s));
@@ -781,7 +811,7 @@ static int run_device_fed(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t
         GH_HIP(hipEventCreate(&e1));
         GH_HIP(hipEventRecord(e0, s));
     }
-    for (int i = 0; i < n_timed; ++i) GH_CHECK(launch_step(kv));
+    for (int i = 0; i < n_timed; ++i) GH_CHECK(launch_step(kv, pos0 + n_before + i));
     if (ms_out) GH_HIP(hipEventRecord(e1, s));
     GH_CHECK(get_state(kv));
     GH_HIP(hipStreamSynchronize(s));
@@ -834,10 +864,13 @@ extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kern
     int tok = kv->h_st->last >= 0 && kv->h_st->last < m->cfg.vocab ? kv->h_st->last : 0;
     GH_CHECK(put_state(kv, kv->len, tok, kv->len, 0, 0));
     Profiler prof;
+    Sink sink;
+    sink.s = s;
+    sink.prof = &prof;
     int rc = GH_OK;
     for (int i = 0; i < n_steps && rc == GH_OK; ++i) {
-        rc = enqueue_step(m, kv, s, &prof);
-        kv->len += 1;  // position advances on device inside the step
+        rc = enqueue_step(m, kv, sink, kv->len);
+        kv->len += 1;
     }
     GH_CHECK(get_state(kv));
     GH_HIP(hipStreamSynchronize(s));

@@ -1,5 +1,6 @@
 // Host-side layout conversion (GGUF Q4_0 rows / f32 rows -> device tiles),
 // work-split planning, and the thread-local error slot of the C ABI.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -78,25 +79,31 @@ void repack_f32(const float* src, int64_t rows, int64_t cols, float* dst, int64_
 
 // Pick S (column splits) so that tiles*S approaches target_wgs while each
 // split keeps at least 4 column blocks, then the per-wave register batch.
-Plan choose_plan(int fmt, int tiles, int nblk, int target_wgs) {
-    Plan p;
-    int max_s = std::max(1, nblk / 4);
-    int s = (target_wgs + tiles - 1) / tiles;
-    p.S = std::max(1, std::min(s, max_s));
-    int per_wg = (nblk + p.S - 1) / p.S;
-    int per_wave = (per_wg + 3) / 4;
+int kbw_for(int fmt, int per_wave) {
+    if (fmt != FMT_Q4) return 8;
     static const int kQ4[] = {1, 2, 3, 4, 6, 9};
-    if (fmt == FMT_Q4) {
-        p.kbw = 9;
-        for (int k : kQ4)
-            if (k >= per_wave) {
-                p.kbw = k;
-                break;
-            }
-    } else {
-        p.kbw = 8;
-    }
+    for (int k : kQ4)
+        if (k >= per_wave) return k;
+    return 9;
+}
+
+Plan choose_plan(int fmt, int tiles, int nblk, int target_wgs, int max_s) {
+    Plan p;
+    int cap = std::max(1, std::min(max_s, nblk / 4));
+    int s = (target_wgs + tiles - 1) / tiles;
+    p.S = std::max(1, std::min(s, cap));
+    int per_wg = (nblk + p.S - 1) / p.S;
+    p.kbw = kbw_for(fmt, (per_wg + 3) / 4);
     return p;
+}
+
+void rope_table(const float* inv_freq, int half, int pos0, int n_pos, float* out) {
+    for (int p = 0; p < n_pos; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float ang = (float)(pos0 + p) * inv_freq[i];
+            out[((size_t)p * half + i) * 2] = cosf(ang);
+            out[((size_t)p * half + i) * 2 + 1] = sinf(ang);
+        }
 }
 
 }  // namespace gh

@@ -63,6 +63,7 @@ def main(argv=None):
     n_steps = n_greedy + case["n_forced"]
     ids, margins, layers, top_idx, top_val = [], [], {}, {}, {}
     f_ids, f_margins = [], []
+    topk_idx, topk_val = [], []  # every step from the last prompt token on
     tok = int(prompt[0])
     t0 = time.time()
     for pos in range(n_steps):
@@ -73,6 +74,10 @@ def main(argv=None):
             o = np.argsort(-logits, kind="stable")[:8]
             top_idx[pos], top_val[pos] = o.astype(np.int32), logits[o]
         srt = np.sort(logits)
+        if pos + 1 >= case["n_prompt"]:
+            o = np.argsort(-logits, kind="stable")[:8]
+            topk_idx.append(o.astype(np.int32))
+            topk_val.append(logits[o])
         if pos + 1 < case["n_prompt"]:
             tok = int(prompt[pos + 1])
         elif pos < n_greedy:
@@ -93,6 +98,7 @@ def main(argv=None):
         q4=np.int32(case["q4"]), prompt=prompt, ids=np.array(ids, np.int32),
         margins=np.array(margins, np.float32), forced=forced, forced_ids=np.array(f_ids, np.int32),
         forced_margins=np.array(f_margins, np.float32), dump_steps=dump,
+        topk_idx=np.stack(topk_idx), topk_val=np.stack(topk_val),
         layers=np.stack([layers[p] for p in dump]), top_idx=np.stack([top_idx[p] for p in dump]),
         top_val=np.stack([top_val[p] for p in dump]))
     print(f"wrote {out}; min greedy margin {min(margins):.3g}, min forced margin {min(f_margins):.3g}, "

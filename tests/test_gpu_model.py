@@ -73,6 +73,10 @@ def test_per_layer_activations_and_argmaxes_match_oracle_fixture(ctx, name):
             assert rel_err(logits[fx["top_idx"][i]], fx["top_val"][i]) < ACT_TOL
         if expect[pos] is not None:
             assert nxt == expect[pos], pos
+            # the oracle's top-8 logits of this step, within the activation tolerance
+            k = pos - (n_p - 1)
+            ti, tv = fx["topk_idx"][k], fx["topk_val"][k]
+            assert rel_err(logits[ti], tv) < ACT_TOL, pos
 
 
 def test_step_and_generate_agree_and_cache_grows(ctx):
