@@ -28,6 +28,12 @@
 
 #include "common.h"
 
+// Phase timestamp hook for latency studies; compiles to nothing unless a
+// timing harness defines it before including this file.
+#ifndef GH_MARK
+#define GH_MARK(slot)
+#endif
+
 namespace gh {
 
 constexpr int NT = 256;  // threads per workgroup (4 wave64)
@@ -384,13 +390,16 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
     // 1. the prologue's input loads go out first (they are waited on first),
     // 2. then the weights of the first register batch,
     // 3. the prologue builds the input slice [kb0*BK, kb1*BK) in LDS.
+    GH_MARK(0);
     typename Pro::Regs pr;
     pro.load(pr, kb0 * BK, nk * BK);
     WRegs<FMT, KBW> r;
     mv_load<FMT, KBW>(r, w, tile, kw0, kw1);
     pro.finish(L, pr, kb0 * BK, nk * BK);
+    GH_MARK(1);
     fill_block_sums<FMT>(L, nk);
     __syncthreads();
+    GH_MARK(2);
     // 4. dot products
     float acc0 = 0.0f, acc1 = 0.0f;
     mv_compute<FMT, KBW>(r, kw0, kw1, kb0, L.xs, L.sxs, acc0, acc1);
@@ -399,13 +408,16 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
         mv_compute<FMT, KBW>(r, base, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     }
     // 5. reduce the four waves
+    GH_MARK(3);
     L.red[wave * TILE_ROWS + lane] = acc0;
     L.red[wave * TILE_ROWS + 64 + lane] = acc1;
     __syncthreads();
+    GH_MARK(4);
     float y = 0.0f;
     const int t = threadIdx.x;
     if (t < TILE_ROWS) y = (L.red[t] + L.red[TILE_ROWS + t]) + (L.red[2 * TILE_ROWS + t] + L.red[3 * TILE_ROWS + t]);
     epi(L, tile, s, t, y);
+    GH_MARK(5);
 }
 
 // ------------------------------------------------------------------
@@ -547,7 +559,7 @@ struct ProResid {
 };
 
 // Attention window of the current token.
-__device__ __forceinline__ void attn_window(int pos, int global, int window, int mode, int& pb, int& pe) {
+__host__ __device__ __forceinline__ void attn_window(int pos, int global, int window, int mode, int& pb, int& pe) {
     pb = 0;
     pe = pos + 1;
     if (window > 0) {
@@ -559,12 +571,16 @@ __device__ __forceinline__ void attn_window(int pos, int global, int window, int
     }
 }
 
-__device__ __forceinline__ void attn_chunks(int n_pos, int nc, int& ch, int& n_used) {
-    ch = (n_pos + nc - 1) / nc;
+constexpr int ATTN_SUB = 64;      // positions per attention sub-chunk (one per lane)
+constexpr int ATTN_MAX_NC = 64;   // chunks per kv head
+
+// Chunking of n_pos positions over at most nc workgroups: chunk length is a
+// multiple of ATTN_SUB, n_used chunks are non-empty.
+__host__ __device__ __forceinline__ void attn_chunks(int n_pos, int nc, int& ch, int& n_used) {
+    const int per = (n_pos + nc - 1) / nc;
+    ch = (per + ATTN_SUB - 1) / ATTN_SUB * ATTN_SUB;
     n_used = (n_pos + ch - 1) / ch;
 }
-
-constexpr int ATTN_MAX_NC = 64;
 
 // O-projection input: merge the split-K attention partials {m[G], l[G],
 // o[G][HD]} of every chunk for the slice [c0, c0+n) of o = [nq][hd].
@@ -891,24 +907,46 @@ __device__ __forceinline__ void wave_head_rope(float* p, const float2* cs) {
     }
 }
 
-// One query token over cache positions [pb, pe), split-K: workgroup (g, j)
-// handles kv head g and chunk j, and writes {m[G], l[G], o[G][HD]} (running
-// max, sum of exp, unnormalised output) for the merge.  In step mode the K/V
-// rows of the chunk are loaded at kernel start, together with the QKV split
-// partials, so the kernel waits for one global round trip before computing.
+// One query token over cache positions [pb, pe), split-K over chunks of
+// ATTN_SUB-multiple length: workgroup (g, j) handles kv head g and chunk j
+// and writes {m[G], l[G], o[G][HD]} (running max, sum of exp, unnormalised
+// output) for the merge.
+//
+// Layout (flash-decoding): per sub-chunk of 64 positions,
+//   scores  8 lanes per position, each lane 16 B of every 128 B line of the
+//           K row (one instruction reads 8 whole lines), q from LDS; one
+//           3-step in-row DPP sum per score;
+//   softmax wave w owns heads w, w+4: one wave max + one wave sum per head;
+//   P.V     lane = 4 dims, the 64 positions spread over NSLOT slots; the
+//           slot partials are summed in LDS at the end.
+// All K/V loads of the first sub-chunk are issued at kernel start, with the
+// QKV split partials, so the kernel waits for one global round trip.
+// In step mode the prologue also applies QK-norm and RoPE to this token's
+// q/k, appends k/v to the cache (appendKVCacheShader, AttentionGPU.hs:502-534)
+// and uses them for the p == pos row.
 template <int HD, int G, bool STEP>
 __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
-    constexpr int LP = HD / 4;    // lanes per position (each lane owns 4 dims)
-    constexpr int PPW = 64 / LP;  // positions per wave step
-    constexpr int NS = 4 * PPW;   // softmax states per workgroup
-    constexpr int NB = 8;         // positions per group per batch (loads in flight)
-    constexpr int NG4 = (G + 2) * HD / 4;      // float4 groups of q|k|v
-    constexpr int MG4 = (NG4 + NT - 1) / NT;   // per thread
-    __shared__ float qs[G * HD], ks[HD], vs[HD];
-    __shared__ float2 cs[HD / 2];
-    __shared__ float sm[NS][G], sl[NS][G];
-    __shared__ float so[NS][G * HD];
+    constexpr int SUB = ATTN_SUB;
+    constexpr int K4 = HD / 32;               // score phase: float4 per lane per position
+    constexpr int RND = SUB / 32;             // score rounds of 8 positions per wave
+    constexpr int LPV = HD / 4;               // P.V phase: lanes per position (4 dims each)
+    constexpr int PGW = 64 / LPV;             // position groups per wave
+    constexpr int NSLOT = 4 * PGW;            // position slots per workgroup
+    constexpr int VPS = SUB / NSLOT;          // positions per slot per sub-chunk
+    constexpr int NG4 = (G + 2) * HD / 4;     // float4 groups of q|k|v
+    constexpr int MG4 = (NG4 + NT - 1) / NT;  // per thread
+    constexpr int NWR = (HD + 63) / 64;       // norm weights per lane
+    constexpr int HPW = (G + 3) / 4;          // heads owned per wave in the softmax
+    __shared__ __align__(16) float qs[G * HD];
+    __shared__ __align__(16) float ks[HD];
+    __shared__ __align__(16) float vs[HD];
+    __shared__ __align__(16) float2 cs[HD / 2];
+    __shared__ __align__(16) float sc[G][SUB];
+    __shared__ __align__(16) float pr[SUB][G];
+    __shared__ float corr_s[G];
+    __shared__ __align__(16) float so[NSLOT][G * HD];
 
+    GH_MARK(0);
     const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
     int pos = -1, pb, pe;
     if (STEP) {
@@ -923,28 +961,31 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     if (j >= n_used) return;  // uniform per workgroup
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c0 = pb + j * ch, c1 = min(pe, c0 + ch);
-    const int grp = lane / LP, lp = lane % LP;
     const size_t pstride = (size_t)a.nkv * HD;
-    const float* kb = a.kc + (size_t)g * HD + 4 * lp;
-    const float* vb = a.vc + (size_t)g * HD + 4 * lp;
+    const int pg = lane / LPV, dq = lane % LPV, slot = wave * PGW + pg;
+    const int kq = lane & 7;  // score phase: lane within the position's 8
+    const float* kbase = a.kc + (size_t)g * HD + 4 * kq;
+    const float* vbase = a.vc + (size_t)g * HD + 4 * dq;
 
-    // 1. first batch of K/V rows in flight (row pos comes from LDS below)
-    float4 kk[NB], vv[NB];
-    bool val[NB];
-    int p0 = c0 + wave * PPW;
-    auto load_batch = [&]() {
+    // 1. K/V of the first sub-chunk in flight (row pos comes from LDS below)
+    float4 kr[RND][K4], vr[VPS];
+    auto kpos = [&](int r) { return (wave * RND + r) * 8 + (lane >> 3); };  // position in the sub-chunk
+    auto load_kv = [&](int s0) {
 #pragma unroll
-        for (int k = 0; k < NB; ++k) {
-            const int p = p0 + grp + k * 4 * PPW;
-            val[k] = p < c1;
-            kk[k] = vv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (val[k] && !(STEP && p == pos)) {
-                kk[k] = *(const float4*)(kb + (size_t)p * pstride);
-                vv[k] = *(const float4*)(vb + (size_t)p * pstride);
-            }
+        for (int r = 0; r < RND; ++r) {
+            const int pk = s0 + kpos(r);
+            const bool okk = pk < c1 && !(STEP && pk == pos);
+#pragma unroll
+            for (int i = 0; i < K4; ++i) kr[r][i] = okk ? *(const float4*)(kbase + (size_t)pk * pstride + 32 * i) : f4z();
+        }
+#pragma unroll
+        for (int k = 0; k < VPS; ++k) {
+            const int pv = s0 + slot + k * NSLOT;
+            vr[k] = (pv < c1 && !(STEP && pv == pos)) ? *(const float4*)(vbase + (size_t)pv * pstride) : f4z();
         }
     };
-    if (p0 < c1) load_batch();
+    load_kv(c0);
+    GH_MARK(1);
 
     // 2. q (and in step mode k, v of this token) into LDS
     if (STEP) {
@@ -960,7 +1001,14 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
                 pv[m] = sum_splits4(a.part_qkv, a.Sa, a.ld_qkv, row >> 2);
             }
         }
-        for (int i = tid; i < HD / 2; i += NT) cs[i] = ((const float2*)a.rope)[(size_t)pos * (HD / 2) + i];
+        float wq[NWR], wk[NWR];
+#pragma unroll
+        for (int r = 0; r < NWR; ++r) {
+            const int i = lane + 64 * r;
+            wq[r] = (a.use_qk_norm && i < HD) ? a.q_norm[i] : 0.0f;
+            wk[r] = (a.use_qk_norm && i < HD) ? a.k_norm[i] : 0.0f;
+        }
+        if (tid < HD / 2) cs[tid] = ((const float2*)a.rope)[(size_t)pos * (HD / 2) + tid];
 #pragma unroll
         for (int m = 0; m < MG4; ++m) {
             const int gi = tid + m * NT;
@@ -971,13 +1019,28 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
             }
         }
         __syncthreads();
+        GH_MARK(2);
         // QK-norm (TBG:171-179), then RoPE, on the G q heads and the k head
         for (int vec = wave; vec < G + 1; vec += 4) {
             float* p = vec < G ? qs + vec * HD : ks;
-            if (a.use_qk_norm) wave_head_norm<HD>(p, vec < G ? a.q_norm : a.k_norm, a.eps, a.zc);
+            if (a.use_qk_norm) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int r = 0; r < NWR; ++r) {
+                    const int i = lane + 64 * r;
+                    if (i < HD) ss += p[i] * p[i];
+                }
+                const float rms = sqrtf(wave_sum(ss) / (float)HD + a.eps);
+#pragma unroll
+                for (int r = 0; r < NWR; ++r) {
+                    const int i = lane + 64 * r;
+                    if (i < HD) p[i] = norm_apply(p[i], rms, vec < G ? wq[r] : wk[r], a.zc);
+                }
+            }
             wave_head_rope<HD>(p, cs);
         }
         __syncthreads();
+        GH_MARK(3);
         if (j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
             for (int i = tid; i < HD; i += NT) {
                 a.kc[((size_t)pos * a.nkv + g) * HD + i] = ks[i];
@@ -989,87 +1052,114 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
         __syncthreads();
     }
 
-    float q[G][4], m[G], l[G], acc[G][4];
+    float mrun[HPW], lrun[HPW];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        const float4 qq = *(const float4*)&qs[h * HD + 4 * lp];
-        q[h][0] = qq.x; q[h][1] = qq.y; q[h][2] = qq.z; q[h][3] = qq.w;
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-        acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.0f;
+    for (int hi = 0; hi < HPW; ++hi) {
+        mrun[hi] = -INFINITY;
+        lrun[hi] = 0.0f;
     }
-    // 3. online softmax over the batches
-    for (; p0 < c1; p0 += NB * 4 * PPW) {
+    float4 acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h] = f4z();
+
+    for (int s0 = c0; s0 < c1; s0 += SUB) {
+        if (s0 != c0) {
+            __syncthreads();  // sc / pr of the previous sub-chunk consumed
+            load_kv(s0);
+        }
         if (STEP) {
 #pragma unroll
-            for (int k = 0; k < NB; ++k)
-                if (val[k] && p0 + grp + k * 4 * PPW == pos) {
-                    kk[k] = *(const float4*)&ks[4 * lp];
-                    vv[k] = *(const float4*)&vs[4 * lp];
+            for (int r = 0; r < RND; ++r)
+                if (s0 + kpos(r) == pos) {
+#pragma unroll
+                    for (int i = 0; i < K4; ++i) kr[r][i] = *(const float4*)&ks[32 * i + 4 * kq];
                 }
+#pragma unroll
+            for (int k = 0; k < VPS; ++k)
+                if (s0 + slot + k * NSLOT == pos) vr[k] = *(const float4*)&vs[4 * dq];
         }
+        // 3. scores of this wave's positions
+#pragma unroll
+        for (int r = 0; r < RND; ++r) {
+            float sv[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) sv[h] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < K4; ++i) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) sv[h] += dot4(*(const float4*)&qs[h * HD + 32 * i + 4 * kq], kr[r][i]);
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                sv[h] = group_sum<8>(sv[h]);
+                if (kq == 0) sc[h][kpos(r)] = sv[h];
+            }
+        }
+        __syncthreads();
+        // 4. softmax update of the heads this wave owns
+        const bool valid = s0 + lane < c1;
+#pragma unroll
+        for (int hi = 0; hi < HPW; ++hi) {
+            const int h = wave + 4 * hi;
+            if (h < G) {
+                const float v = valid ? sc[h][lane] * a.scale : -INFINITY;
+                const float mn = fmaxf(mrun[hi], wave_max(v));
+                const float e = valid ? __expf(v - mn) : 0.0f;
+                const float corr = mrun[hi] == -INFINITY ? 0.0f : __expf(mrun[hi] - mn);
+                lrun[hi] = lrun[hi] * corr + wave_sum(e);
+                mrun[hi] = mn;
+                pr[lane][h] = e;
+                if (lane == 0) corr_s[h] = corr;
+            }
+        }
+        __syncthreads();
+        // 5. P.V over this slot's positions
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            float sc[NB];
-            float bmax = -INFINITY;
-#pragma unroll
-            for (int k = 0; k < NB; ++k) {
-                const float d = group_sum<LP>(q[h][0] * kk[k].x + q[h][1] * kk[k].y + q[h][2] * kk[k].z +
-                                              q[h][3] * kk[k].w);
-                sc[k] = val[k] ? d * a.scale : -INFINITY;
-                bmax = fmaxf(bmax, sc[k]);
-            }
-            const float mn = fmaxf(m[h], bmax);
-            const float corr = m[h] == -INFINITY ? 0.0f : __expf(m[h] - mn);
-            float ls = l[h] * corr;
-            float a0 = acc[h][0] * corr, a1 = acc[h][1] * corr, a2 = acc[h][2] * corr, a3 = acc[h][3] * corr;
-#pragma unroll
-            for (int k = 0; k < NB; ++k) {
-                const float pexp = val[k] ? __expf(sc[k] - mn) : 0.0f;
-                ls += pexp;
-                a0 += pexp * vv[k].x;
-                a1 += pexp * vv[k].y;
-                a2 += pexp * vv[k].z;
-                a3 += pexp * vv[k].w;
-            }
-            m[h] = mn;
-            l[h] = ls;
-            acc[h][0] = a0; acc[h][1] = a1; acc[h][2] = a2; acc[h][3] = a3;
+            const float c = corr_s[h];
+            acc[h] = make_float4(acc[h].x * c, acc[h].y * c, acc[h].z * c, acc[h].w * c);
         }
-        if (p0 + NB * 4 * PPW < c1) {
-            p0 += NB * 4 * PPW;
-            load_batch();
-            p0 -= NB * 4 * PPW;
+#pragma unroll
+        for (int k = 0; k < VPS; ++k) {
+            const int pl = slot + k * NSLOT;
+            if (s0 + pl < c1) {
+                float pw[G];
+#pragma unroll
+                for (int h4 = 0; h4 < G; h4 += 4) {
+                    if (G >= 4) {
+                        const float4 t = *(const float4*)&pr[pl][h4];
+                        pw[h4] = t.x; pw[h4 + 1] = t.y; pw[h4 + 2] = t.z; pw[h4 + 3] = t.w;
+                    } else {
+                        for (int h = 0; h < G; ++h) pw[h] = pr[pl][h];
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < G; ++h) acc[h] = fma4(pw[h], vr[k], acc[h]);
+            }
         }
     }
-    // 4. merge the NS softmax states of the workgroup
-    const int si = wave * PPW + grp;
+    GH_MARK(4);
+    // 6. sum the slot partials; write the chunk's state
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        if (lp == 0) {
-            sm[si][h] = m[h];
-            sl[si][h] = l[h];
-        }
-        *(float4*)&so[si][h * HD + 4 * lp] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-    }
+    for (int h = 0; h < G; ++h) *(float4*)&so[slot][h * HD + 4 * dq] = acc[h];
     __syncthreads();
+    GH_MARK(5);
     float* out = a.part + ((size_t)g * a.nc + j) * (G * (HD + 2));
     for (int idx = tid; idx < G * HD; idx += NT) {
-        const int h = idx / HD;
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < NS; ++s2) M = fmaxf(M, sm[s2][h]);
-        float Lsum = 0.0f, O = 0.0f;
-        for (int s2 = 0; s2 < NS; ++s2) {
-            const float wgt = sm[s2][h] == -INFINITY ? 0.0f : expf(sm[s2][h] - M);
-            Lsum += sl[s2][h] * wgt;
-            O += so[s2][idx] * wgt;
-        }
+        float O = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < NSLOT; ++s2) O += so[s2][idx];
         out[2 * G + idx] = O;
-        if (idx % HD == 0) {
-            out[h] = M;
-            out[G + h] = Lsum;
+    }
+#pragma unroll
+    for (int hi = 0; hi < HPW; ++hi) {
+        const int h = wave + 4 * hi;
+        if (h < G && lane == 0) {
+            out[h] = mrun[hi];
+            out[G + h] = lrun[hi];
         }
     }
+    GH_MARK(6);
 }
 
 template <bool STEP>
@@ -1390,8 +1480,8 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     Sink k;
     k.s = s;
     GH_CHECK(launch_attn_t<false>(k, 0.0, hd, nq / nkv, a, nkv));
-    const int n_pos = p_end - p_begin, ch = (n_pos + n_splits - 1) / n_splits;
-    const int n_used = (n_pos + ch - 1) / ch;
+    int ch, n_used;
+    attn_chunks(p_end - p_begin, n_splits, ch, n_used);
     hipLaunchKernelGGL(k_attn_combine, dim3((nq * hd + 255) / 256), dim3(256), 0, s, part, n_splits, n_used, nq / nkv,
                        hd, nq, out);
     GH_HIP(hipGetLastError());
