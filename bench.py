@@ -9,9 +9,10 @@ one token per step (untimed, as in the reference's generation loop), then W
 warmup steps, then exactly K timed greedy steps (HIP events on the step
 stream, device-synchronised on both sides).
 
-Prints ONE JSON line with tok/s, the roofline of the dominant kernel (its
-average duration measured with HIP events in an event-timed pass of the same
-decode), and the CPU baseline (the C oracle on the host cores, bounded
+Prints ONE JSON line with tok/s; per-kernel-kind durations (HIP events
+around back-to-back replays of that kernel kind at the last decoded
+position, on the step stream); the roofline of the LM head, the largest
+Q4_0 matvec; and the CPU baseline (the C oracle on the host cores, bounded
 sample).
 """
 from __future__ import annotations
@@ -31,6 +32,9 @@ HBM_PEAK_GBPS = 8000.0
 WEIGHT_SEED = 1234
 PROMPT_SEED = 1
 N_PROMPT = 128
+# back-to-back replays per kernel kind in the event-timed pass (a few ms each)
+KERNEL_REPS = {"qkv": 40, "attention": 40, "o_proj": 40, "gate_up": 40, "down": 40, "final_norm": 400,
+               "lm_head": 200}
 
 
 def log(msg: str) -> None:
@@ -66,7 +70,6 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args(argv)
@@ -92,18 +95,17 @@ def main(argv=None) -> int:
     tok_s = a.steps / (ms / 1e3)
     log(f"decode: {a.steps} steps in {ms:.3f} ms -> {tok_s:.1f} tok/s")
 
-    # event-timed pass over the same positions (kernel durations for the roofline)
-    kv2 = gh.KVCache(model, max_seq)
-    gh.generate(model, kv2, prompt, a.warmup + 1)
-    stats = gh.profile_steps(model, kv2, a.profile_steps)
-    for s in stats:
-        log(f"  {s.name:10s} launches {s.launches:5d} avg {s.avg_us:8.2f} us  {s.gbps:8.1f} GB/s")
-    dom = max((s for s in stats if s.bytes_per_launch > 0), key=lambda s: s.total_ms)
-    achieved = dom.gbps
-    step_bytes = sum(s.bytes_per_launch * s.launches for s in stats) / a.profile_steps
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": dom.name,
-                "bytes_per_launch": int(dom.bytes_per_launch), "avg_us": round(dom.avg_us, 3)}
+    # per-kernel HIP-event timing at the last decoded position: each kernel
+    # kind replayed back to back on the step stream (state unchanged)
+    timings = {name: gh.time_kernel(model, kv, name, KERNEL_REPS[name]) for name in gh.STEP_KERNELS}
+    for t in timings.values():
+        log(f"  {t.name:10s} x{t.launches_per_step:3d}/step avg {t.avg_us:8.2f} us  {t.gbps:8.1f} GB/s")
+    step_bytes = sum(t.bytes_per_launch * t.launches_per_step for t in timings.values())
+    # roofline kernel: the LM head, the largest Q4_0 matvec (262144 x 1152)
+    lm = timings["lm_head"]
+    roofline = {"bound": "hbm", "achieved": round(lm.gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(lm.gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "lm_head",
+                "bytes_per_launch": int(lm.bytes_per_launch), "avg_us": round(lm.avg_us, 3)}
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
@@ -115,8 +117,10 @@ def main(argv=None) -> int:
                    "step_algorithmic_bytes": int(step_bytes),
                    "step_frac_of_hbm_peak": round(step_bytes / (ms / a.steps * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
         "roofline": roofline,
-        "kernels": {s.name: {"avg_us": round(s.avg_us, 3), "gbps": round(s.gbps, 1), "launches": s.launches}
-                    for s in stats},
+        "kernels": {t.name: {"avg_us": round(t.avg_us, 3), "gbps": round(t.gbps, 1),
+                             "frac": round(t.gbps / HBM_PEAK_GBPS, 4), "per_step": t.launches_per_step,
+                             "step_us": round(t.avg_us * t.launches_per_step, 1)}
+                    for t in timings.values()},
     }
     if not a.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)

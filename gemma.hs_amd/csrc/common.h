@@ -146,6 +146,9 @@ struct Sink {
     hipGraphNode_t last = nullptr;
     std::vector<std::unique_ptr<NodeArgsBase>>* store = nullptr;
     std::vector<PosPatch>* patches = nullptr;
+    const char* only = nullptr;  // launch only the kernels of this name (timing)
+    int launched = 0;            // kernels enqueued
+    double bytes = 0.0;          // their algorithmic bytes
 };
 
 }  // namespace gh

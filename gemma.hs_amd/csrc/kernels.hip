@@ -25,6 +25,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 
 #include "common.h"
 
@@ -784,6 +785,9 @@ int* pos_field(Tup& t) {
 template <int POS_ARG = -1, class... P>
 static int sink_launch(Sink& k, const char* name, double bytes, void (*fn)(P...), dim3 grid, dim3 block, size_t lds,
                        P... args) {
+    if (k.only && std::strcmp(k.only, name) != 0) return GH_OK;
+    k.launched += 1;
+    k.bytes += bytes;
     auto blob = std::make_unique<NodeArgs<P...>>(args...);
     if (k.g) {
         hipKernelNodeParams prm{};

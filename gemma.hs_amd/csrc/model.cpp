@@ -898,6 +898,44 @@ extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kern
     return GH_OK;
 }
 
+extern "C" int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t n_reps, double* avg_us_out,
+                              double* bytes_per_launch_out, int32_t* launches_per_step_out) {
+    if (!m || !kv || kv->m != m || !name || n_reps <= 0 || !avg_us_out)
+        return set_error(GH_ERR_INVALID, "bad arguments");
+    static const char* kinds[] = {"qkv", "attention", "o_proj", "gate_up", "down", "final_norm", "lm_head"};
+    bool known = false;
+    for (const char* k : kinds) known = known || std::strcmp(k, name) == 0;
+    if (!known) return set_error(GH_ERR_INVALID, "gh_time_kernel: unknown or non-idempotent kernel '%s'", name);
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    if (kv->len >= kv->max_seq) return set_error(GH_ERR_RANGE, "KV cache full");
+    hipStream_t s = m->ctx->stream;
+    gh::Sink sink;
+    sink.s = s;
+    sink.only = name;
+    GH_CHECK(enqueue_step(m, kv, sink, kv->len));  // warm-up
+    const int per_step = sink.launched;
+    const double bytes = per_step ? sink.bytes / per_step : 0.0;
+    hipEvent_t a, b;
+    GH_HIP(hipEventCreate(&a));
+    GH_HIP(hipEventCreate(&b));
+    int rc = GH_OK;
+    if (hipEventRecord(a, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
+    for (int i = 0; i < n_reps && rc == GH_OK; ++i) rc = enqueue_step(m, kv, sink, kv->len);
+    float ms = 0.0f;
+    if (rc == GH_OK && hipEventRecord(b, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
+    if (rc == GH_OK && hipEventSynchronize(b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventSynchronize failed");
+    if (rc == GH_OK && hipEventElapsedTime(&ms, a, b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventElapsedTime failed");
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    GH_CHECK(rc);
+    *avg_us_out = per_step ? 1e3 * ms / ((double)n_reps * per_step) : 0.0;
+    if (bytes_per_launch_out) *bytes_per_launch_out = bytes;
+    if (launches_per_step_out) *launches_per_step_out = per_step;
+    return GH_OK;
+}
+
 // =====================================================================
 // synthetic model
 // =====================================================================

@@ -30,7 +30,7 @@ GemmaConfig = GhConfig
 __all__ = [
     "GemmaConfig", "GemmaHipError", "Context", "DeviceBuffer", "Q4Tensor", "GemmaModel", "KVCache",
     "preset", "runLinearQ4", "runGemmaInferenceCached", "runGemmaInferenceCachedWithLayer0",
-    "generate", "bench_decode", "profile_steps", "synth_f32", "synth_q4_0", "synth_tokens",
+    "generate", "bench_decode", "profile_steps", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
     "tensor_list", "synth_tensors", "device_count", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q4_0",
     "MODE_GEMMA3", "MODE_REF", "FLAG_QK_NORM", "FLAG_POST_ATTN_NORM", "FLAG_POST_FFN_NORM",
     "FLAG_ZERO_CENTERED", "FLAG_IEEE_SCALES",
@@ -444,3 +444,27 @@ def profile_steps(model: GemmaModel, cache: KVCache, n_steps: int) -> list[Kerne
     check(lib().gh_profile_steps(model.h, cache.h, n_steps, arr, 32, C.byref(n)))
     return [KernelStat(arr[i].name.decode(), arr[i].launches, arr[i].total_ms, arr[i].bytes)
             for i in range(n.value)]
+
+
+STEP_KERNELS = ("qkv", "attention", "o_proj", "gate_up", "down", "final_norm", "lm_head")
+
+
+@dataclass
+class KernelTiming:
+    name: str
+    avg_us: float            # HIP-event time per launch, launches back to back
+    bytes_per_launch: float  # algorithmic HBM bytes per launch
+    launches_per_step: int
+
+    @property
+    def gbps(self) -> float:
+        return self.bytes_per_launch / (self.avg_us * 1e-6) / 1e9 if self.avg_us > 0 else 0.0
+
+
+def time_kernel(model: GemmaModel, cache: KVCache, name: str, n_reps: int = 50) -> KernelTiming:
+    """Replay only the step kernels called `name` at the cache's current
+    position n_reps times between two HIP events (model and cache state are
+    unchanged); see gh_time_kernel."""
+    us, nb, per = C.c_double(), C.c_double(), C.c_int32()
+    check(lib().gh_time_kernel(model.h, cache.h, name.encode(), n_reps, C.byref(us), C.byref(nb), C.byref(per)))
+    return KernelTiming(name, us.value, nb.value, per.value)

@@ -204,6 +204,16 @@ typedef struct gh_kernel_stat {
 } gh_kernel_stat;
 int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kernel_stat* stats,
                      int32_t max_stats, int32_t* n_stats_out);
+/* Kernel timing for the roofline: replays only the step kernels named
+ * `name` ("qkv", "attention", "o_proj", "gate_up", "down", "final_norm",
+ * "lm_head") of one step at the cache's current position, n_reps times
+ * back to back on the context stream between two HIP events, and returns
+ * the average duration per launch, the algorithmic HBM bytes per launch
+ * and the launches per step.  The replayed kernels are idempotent (same
+ * inputs, same outputs), so the model and cache state are unchanged.
+ * Also replaces the gpu_print_profile_stats hook (BenchmarkKVCache.hs:38-42). */
+int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t n_reps, double* avg_us_out,
+                   double* bytes_per_launch_out, int32_t* launches_per_step_out);
 
 /* ================================================================
  * Seeded synthetic weights (SplitMix64 + Box-Muller), identical on every

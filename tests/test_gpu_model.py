@@ -146,3 +146,24 @@ def test_errors_kv_full_bad_token_incomplete_model(ctx):
     assert e.value.name == "GH_ERR_NOT_FOUND"
     with pytest.raises(gh.GemmaHipError):
         bare.set_tensor("blk.0.nonsense.weight", np.zeros(4, np.float32), gh.DTYPE_F32)
+
+
+@pytest.mark.gpu
+def test_time_kernel_leaves_state_unchanged(ctx):
+    """gh_time_kernel replays step kernels at the current position; the
+    decode that follows must be the one without the timing pass."""
+    cfg = gh.preset("tiny")
+    m = _gpu_model(ctx, cfg, 7, True)
+    prompt = gh.synth_tokens(3, "prompt", 9, cfg.vocab)
+    kv_a = gh.KVCache(m, 64)
+    ref = gh.generate(m, kv_a, prompt, 12)
+    kv_b = gh.KVCache(m, 64)
+    first = gh.generate(m, kv_b, prompt, 4)
+    for name in gh.STEP_KERNELS:
+        t = gh.time_kernel(m, kv_b, name, 3)
+        assert t.avg_us > 0 and t.launches_per_step >= 1, name
+        assert t.bytes_per_launch >= 0
+    rest = gh.generate(m, kv_b, [int(first[-1])], 8)
+    np.testing.assert_array_equal(np.concatenate([first, rest]), ref)
+    with pytest.raises(gh.GemmaHipError):
+        gh.time_kernel(m, kv_b, "finish", 1)
