@@ -127,12 +127,13 @@ struct NodeArgsBase {
     std::vector<void*> ptrs;
 };
 
-// A graph kernel node whose `pos` argument is rewritten before each replay
-// (the position is host-known: one step = one position).
+// A graph kernel node whose position-dependent arguments are rewritten
+// before each replay (the position is host-known: one step = one position);
+// `set` updates the node's argument blob for a position.
 struct PosPatch {
     hipGraphNode_t node;
     hipKernelNodeParams params;
-    int* pos;
+    std::function<void(int)> set;
 };
 
 struct Profiler;

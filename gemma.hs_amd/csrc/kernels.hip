@@ -572,7 +572,7 @@ __host__ __device__ __forceinline__ void attn_window(int pos, int global, int wi
     }
 }
 
-constexpr int ATTN_SUB = 64;      // positions per attention sub-chunk (one per lane)
+constexpr int ATTN_SUB = 32;      // positions per attention sub-chunk
 constexpr int ATTN_MAX_NC = 64;   // chunks per kv head
 
 // Chunking of n_pos positions over at most nc workgroups: chunk length is a
@@ -587,30 +587,34 @@ __host__ __device__ __forceinline__ void attn_chunks(int n_pos, int nc, int& ch,
 // o[G][HD]} of every chunk for the slice [c0, c0+n) of o = [nq][hd].
 struct ProAttnCombine {
     const float* part;
-    int pos;  // current position (kernel argument, patched per step)
+    int pos;  // current position (patched per step with set_pos)
     int nc, G, HD;
     int global, window, mode;
+    int n_used;  // chunks of this position, derived on the host
+    __host__ __device__ void set_pos(int p) {
+        int pb, pe, ch;
+        pos = p;
+        attn_window(p, global, window, mode, pb, pe);
+        attn_chunks(pe - pb, nc, ch, n_used);
+    }
+    static constexpr int PRE = 16;  // chunk states loaded by load()
     struct Regs {
-        float4 ov[8];
+        float4 ov[PRE];
         float mj, lj;
-        int n_used;
     };
     __device__ void load(Regs& r, int c0, int n) const {
-        int pb, pe, ch;
-        attn_window(pos, global, window, mode, pb, pe);
-        attn_chunks(pe - pb, nc, ch, r.n_used);
         const int stride = G * (HD + 2), tid = threadIdx.x;
         // this thread's column group (one per thread up to 1024 columns)
         const int c = c0 + 4 * tid, h = c / HD, d = c % HD;
         const float* pbase = part + (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r.ov[j] = (tid < (n >> 2) && j < r.n_used) ? *(const float4*)(pbase + (size_t)j * stride) : f4z();
+        for (int j = 0; j < PRE; ++j) r.ov[j] = (tid < (n >> 2) && j < n_used) ? *(const float4*)(pbase + (size_t)j * stride) : f4z();
         // (m, l) of chunk j = lane for head h0 + wave
         const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
         const int hh = tid >> 6, j = tid & 63;
         r.mj = -INFINITY;
         r.lj = 0.0f;
-        if (hh < nh && j < r.n_used) {
+        if (hh < nh && j < n_used) {
             const int hg = h0 + hh;
             const float* bj = part + ((size_t)(hg / G) * nc + j) * stride;
             r.mj = bj[hg % G];
@@ -618,7 +622,7 @@ struct ProAttnCombine {
         }
     }
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
-        const int stride = G * (HD + 2), tid = threadIdx.x, n_used = r.n_used;
+        const int stride = G * (HD + 2), tid = threadIdx.x;
         const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
         float* wts = L.tmp;  // [nh][ATTN_MAX_NC] merge weights exp(m_j - M) / sum_j l_j exp(m_j - M)
         for (int hh = tid >> 6; hh < nh; hh += 4) {
@@ -643,11 +647,11 @@ struct ProAttnCombine {
             const float* wv = wts + (h - h0) * ATTN_MAX_NC;
             float4 acc = f4z();
             int j = 0;
-            if (gi == tid) {  // chunks 0..7 were loaded by load()
+            if (gi == tid) {  // chunks 0..PRE-1 were loaded by load()
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj)
+                for (int jj = 0; jj < PRE; ++jj)
                     if (jj < n_used) acc = fma4(wv[jj], r.ov[jj], acc);
-                j = 8;
+                j = PRE;
             }
             for (; j < n_used; ++j) acc = fma4(wv[j], *(const float4*)(pbase + (size_t)j * stride), acc);
             ((float4*)L.xs)[gi] = acc;
@@ -771,17 +775,19 @@ struct ProfScope {
     }
 };
 
+// Setter of the position-dependent argument I: an int, or a struct with
+// set_pos(int) that also recomputes what derives from the position.
 template <int I, class Tup>
-int* pos_field(Tup& t) {
-    auto& a = std::get<I>(t);
-    if constexpr (std::is_same_v<std::decay_t<decltype(a)>, int>) return &a;
-    else return &a.pos;
+std::function<void(int)> pos_setter(Tup& t) {
+    auto* a = &std::get<I>(t);
+    if constexpr (std::is_same_v<std::decay_t<decltype(*a)>, int>) return [a](int pos) { *a = pos; };
+    else return [a](int pos) { a->set_pos(pos); };
 }
 }  // namespace
 
 // Launch fn<<<grid, block, lds>>>(args...) on the sink.  POS_ARG >= 0 names
-// the argument holding the step position (an int, or a struct with .pos),
-// which graph replays rewrite per step.
+// the argument holding the step position (an int, or a struct with
+// set_pos), which graph replays rewrite per step.
 template <int POS_ARG = -1, class... P>
 static int sink_launch(Sink& k, const char* name, double bytes, void (*fn)(P...), dim3 grid, dim3 block, size_t lds,
                        P... args) {
@@ -800,7 +806,7 @@ static int sink_launch(Sink& k, const char* name, double bytes, void (*fn)(P...)
         hipGraphNode_t node;
         GH_HIP(hipGraphAddKernelNode(&node, k.g, k.last ? &k.last : nullptr, k.last ? 1 : 0, &prm));
         k.last = node;
-        if constexpr (POS_ARG >= 0) k.patches->push_back({node, prm, pos_field<POS_ARG>(blob->t)});
+        if constexpr (POS_ARG >= 0) k.patches->push_back({node, prm, pos_setter<POS_ARG>(blob->t)});
         k.store->push_back(std::move(blob));
         return GH_OK;
     }
@@ -874,11 +880,10 @@ struct AttnArgs {
     int use_qk_norm, zc;
     float eps;
     const float* rope;  // [max_seq][HD/2] (cos, sin) of this layer type
-    int pos;            // current position (kernel argument, patched per step)
+    int pos;            // current position (patched per step with set_pos)
     int global, window, mode;
-    // raw mode: q given, window given
+    // raw mode: q given
     const float* q;
-    int p_begin, p_end;
     // common
     float* kc;
     float* vc;
@@ -886,6 +891,19 @@ struct AttnArgs {
     float scale;
     float* part;
     int nc;
+    // attended positions [pb, pe) in chunks of ch, n_used of them (host-derived)
+    int pb, pe, ch, n_used;
+    __host__ __device__ void set_range(int b, int e) {
+        pb = b;
+        pe = e;
+        attn_chunks(e - b, nc, ch, n_used);
+    }
+    __host__ __device__ void set_pos(int p) {
+        int b, e;
+        pos = p;
+        attn_window(p, global, window, mode, b, e);
+        set_range(b, e);
+    }
 };
 
 // In-place per-vector RMSNorm by one wave (qkNormShader semantics).
@@ -916,27 +934,29 @@ __device__ __forceinline__ void wave_head_rope(float* p, const float2* cs) {
 // and writes {m[G], l[G], o[G][HD]} (running max, sum of exp, unnormalised
 // output) for the merge.
 //
-// Layout (flash-decoding): per sub-chunk of 64 positions,
+// Layout (flash-decoding): per sub-chunk of ATTN_SUB = 32 positions,
 //   scores  8 lanes per position, each lane 16 B of every 128 B line of the
 //           K row (one instruction reads 8 whole lines), q from LDS; one
 //           3-step in-row DPP sum per score;
 //   softmax wave w owns heads w, w+4: one wave max + one wave sum per head;
-//   P.V     lane = 4 dims, the 64 positions spread over NSLOT slots; the
-//           slot partials are summed in LDS at the end.
-// All K/V loads of the first sub-chunk are issued at kernel start, with the
-// QKV split partials, so the kernel waits for one global round trip.
+//   P.V     lane = 4 dims, the positions spread over NSLOT slots; the slot
+//           partials are summed in LDS at the end.
+// The K/V of the first sub-chunk are loaded at kernel start, with the QKV
+// split partials (one global round trip); the next sub-chunk's K (V) is
+// loaded as soon as the current one's K (V) registers are consumed.
 // In step mode the prologue also applies QK-norm and RoPE to this token's
 // q/k, appends k/v to the cache (appendKVCacheShader, AttentionGPU.hs:502-534)
-// and uses them for the p == pos row.
+// and uses them for the p == pos row.  The window and the chunking come from
+// the host (AttnArgs::set_pos).
 template <int HD, int G, bool STEP>
 __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     constexpr int SUB = ATTN_SUB;
     constexpr int K4 = HD / 32;               // score phase: float4 per lane per position
-    constexpr int RND = SUB / 32;             // score rounds of 8 positions per wave
+    static_assert(SUB == 32, "one score round of 8 positions per wave");
     constexpr int LPV = HD / 4;               // P.V phase: lanes per position (4 dims each)
     constexpr int PGW = 64 / LPV;             // position groups per wave
     constexpr int NSLOT = 4 * PGW;            // position slots per workgroup
-    constexpr int VPS = SUB / NSLOT;          // positions per slot per sub-chunk
+    constexpr int VPS = (SUB + NSLOT - 1) / NSLOT;  // positions per slot per sub-chunk
     constexpr int NG4 = (G + 2) * HD / 4;     // float4 groups of q|k|v
     constexpr int MG4 = (NG4 + NT - 1) / NT;  // per thread
     constexpr int NWR = (HD + 63) / 64;       // norm weights per lane
@@ -952,43 +972,35 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
 
     GH_MARK(0);
     const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
-    int pos = -1, pb, pe;
-    if (STEP) {
-        pos = a.pos;
-        attn_window(pos, a.global, a.window, a.mode, pb, pe);
-    } else {
-        pb = a.p_begin;
-        pe = a.p_end;
-    }
-    int ch, n_used;
-    attn_chunks(pe - pb, a.nc, ch, n_used);
-    if (j >= n_used) return;  // uniform per workgroup
+    if (j >= a.n_used) return;  // uniform per workgroup
+    const int pos = STEP ? a.pos : -1;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int c0 = pb + j * ch, c1 = min(pe, c0 + ch);
+    const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
     const size_t pstride = (size_t)a.nkv * HD;
     const int pg = lane / LPV, dq = lane % LPV, slot = wave * PGW + pg;
-    const int kq = lane & 7;  // score phase: lane within the position's 8
+    const int kq = lane & 7;                       // score phase: lane within the position's 8
+    const int kp = wave * 8 + (lane >> 3);         // score phase: position within the sub-chunk
     const float* kbase = a.kc + (size_t)g * HD + 4 * kq;
     const float* vbase = a.vc + (size_t)g * HD + 4 * dq;
 
-    // 1. K/V of the first sub-chunk in flight (row pos comes from LDS below)
-    float4 kr[RND][K4], vr[VPS];
-    auto kpos = [&](int r) { return (wave * RND + r) * 8 + (lane >> 3); };  // position in the sub-chunk
-    auto load_kv = [&](int s0) {
+    // Loads are unconditional, from rows clamped into [c0, c1): rows past the
+    // chunk are masked in the softmax / P.V, and row pos is replaced from LDS.
+    float4 kr[K4], vr[VPS];
+    auto load_k = [&](int s0) {
+        const float* src = kbase + (size_t)min(s0 + kp, c1 - 1) * pstride;
 #pragma unroll
-        for (int r = 0; r < RND; ++r) {
-            const int pk = s0 + kpos(r);
-            const bool okk = pk < c1 && !(STEP && pk == pos);
-#pragma unroll
-            for (int i = 0; i < K4; ++i) kr[r][i] = okk ? *(const float4*)(kbase + (size_t)pk * pstride + 32 * i) : f4z();
-        }
+        for (int i = 0; i < K4; ++i) kr[i] = *(const float4*)(src + 32 * i);
+    };
+    auto load_v = [&](int s0) {
 #pragma unroll
         for (int k = 0; k < VPS; ++k) {
-            const int pv = s0 + slot + k * NSLOT;
-            vr[k] = (pv < c1 && !(STEP && pv == pos)) ? *(const float4*)(vbase + (size_t)pv * pstride) : f4z();
+            const int pl = min(slot + k * NSLOT, SUB - 1);
+            vr[k] = *(const float4*)(vbase + (size_t)min(s0 + pl, c1 - 1) * pstride);
         }
     };
-    load_kv(c0);
+    // 1. K/V of the first sub-chunk in flight (row pos comes from LDS below)
+    load_k(c0);
+    load_v(c0);
     GH_MARK(1);
 
     // 2. q (and in step mode k, v of this token) into LDS
@@ -1066,42 +1078,37 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h] = f4z();
 
-    for (int s0 = c0; s0 < c1; s0 += SUB) {
-        if (s0 != c0) {
-            __syncthreads();  // sc / pr of the previous sub-chunk consumed
-            load_kv(s0);
-        }
+    // one sub-chunk; `more` issues the next sub-chunk's loads as registers free up
+    auto sub_chunk = [&](int s0, bool more) {
         if (STEP) {
+            if (s0 + kp == pos) {
 #pragma unroll
-            for (int r = 0; r < RND; ++r)
-                if (s0 + kpos(r) == pos) {
-#pragma unroll
-                    for (int i = 0; i < K4; ++i) kr[r][i] = *(const float4*)&ks[32 * i + 4 * kq];
-                }
+                for (int i = 0; i < K4; ++i) kr[i] = *(const float4*)&ks[32 * i + 4 * kq];
+            }
 #pragma unroll
             for (int k = 0; k < VPS; ++k)
                 if (s0 + slot + k * NSLOT == pos) vr[k] = *(const float4*)&vs[4 * dq];
         }
-        // 3. scores of this wave's positions
-#pragma unroll
-        for (int r = 0; r < RND; ++r) {
+        // 3. scores of this wave's 8 positions
+        {
             float sv[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) sv[h] = 0.0f;
 #pragma unroll
             for (int i = 0; i < K4; ++i) {
 #pragma unroll
-                for (int h = 0; h < G; ++h) sv[h] += dot4(*(const float4*)&qs[h * HD + 32 * i + 4 * kq], kr[r][i]);
+                for (int h = 0; h < G; ++h) sv[h] += dot4(*(const float4*)&qs[h * HD + 32 * i + 4 * kq], kr[i]);
             }
+            if (more) load_k(s0 + SUB);
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 sv[h] = group_sum<8>(sv[h]);
-                if (kq == 0) sc[h][kpos(r)] = sv[h];
+                if (kq == 0) sc[h][kp] = sv[h];
             }
         }
         __syncthreads();
         // 4. softmax update of the heads this wave owns
-        const bool valid = s0 + lane < c1;
+        const bool valid = lane < SUB && s0 + lane < c1;
 #pragma unroll
         for (int hi = 0; hi < HPW; ++hi) {
             const int h = wave + 4 * hi;
@@ -1112,7 +1119,7 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
                 const float corr = mrun[hi] == -INFINITY ? 0.0f : __expf(mrun[hi] - mn);
                 lrun[hi] = lrun[hi] * corr + wave_sum(e);
                 mrun[hi] = mn;
-                pr[lane][h] = e;
+                if (lane < SUB) pr[lane][h] = e;
                 if (lane == 0) corr_s[h] = corr;
             }
         }
@@ -1126,21 +1133,31 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int k = 0; k < VPS; ++k) {
             const int pl = slot + k * NSLOT;
-            if (s0 + pl < c1) {
+            if (pl < SUB && s0 + pl < c1) {
                 float pw[G];
+                if constexpr (G >= 4) {
 #pragma unroll
-                for (int h4 = 0; h4 < G; h4 += 4) {
-                    if (G >= 4) {
+                    for (int h4 = 0; h4 < G; h4 += 4) {
                         const float4 t = *(const float4*)&pr[pl][h4];
                         pw[h4] = t.x; pw[h4 + 1] = t.y; pw[h4 + 2] = t.z; pw[h4 + 3] = t.w;
-                    } else {
-                        for (int h = 0; h < G; ++h) pw[h] = pr[pl][h];
                     }
+                } else {
+#pragma unroll
+                    for (int h = 0; h < G; ++h) pw[h] = pr[pl][h];
                 }
 #pragma unroll
                 for (int h = 0; h < G; ++h) acc[h] = fma4(pw[h], vr[k], acc[h]);
             }
         }
+        if (more) {
+            load_v(s0 + SUB);
+            __syncthreads();  // sc / pr of this sub-chunk consumed
+        }
+    };
+    if (c1 - c0 <= SUB) {
+        sub_chunk(c0, false);  // chunks up to 32 positions: straight-line code
+    } else {
+        for (int s0 = c0; s0 < c1; s0 += SUB) sub_chunk(s0, s0 + SUB < c1);
     }
     GH_MARK(4);
     // 6. sum the slot partials; write the chunk's state
@@ -1246,7 +1263,6 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     const int zc = (c.flags & GH_FLAG_ZERO_CENTERED) ? 1 : 0;
     const float eps = c.rms_eps;
     const size_t kv_layer = (size_t)kv->max_seq * nkv * hd;
-    const int n_pos_host = std::min(pos + 1, kv->max_seq);  // profiling byte counts only
 
     for (int li = 0; li < c.n_layers; ++li) {
         LayerDev& L = m->layers[li];
@@ -1288,7 +1304,6 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             a.eps = eps;
             const bool global_theta = c.mode == GH_MODE_REF ? true : L.global;
             a.rope = kv->rope + (global_theta ? (size_t)kv->max_seq * hd : 0);
-            a.pos = pos;
             a.global = L.global;
             a.window = c.sliding_window;
             a.mode = c.mode;
@@ -1298,11 +1313,13 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             a.scale = 1.0f / sqrtf((float)hd);
             a.part = m->attn_part;
             a.nc = m->attn_nc;
-            GH_CHECK(launch_attn_t<true>(sink, 2.0 * 4.0 * hd * nkv * n_pos_host, hd, G, a, nkv));
+            a.set_pos(pos);
+            GH_CHECK(launch_attn_t<true>(sink, 2.0 * 4.0 * hd * nkv * (a.pe - a.pb), hd, G, a, nkv));
         }
         // C: attention merge + O projection
         {
-            ProAttnCombine pro{m->attn_part, pos, m->attn_nc, G, hd, L.global ? 1 : 0, c.sliding_window, c.mode};
+            ProAttnCombine pro{m->attn_part, pos, m->attn_nc, G, hd, L.global ? 1 : 0, c.sliding_window, c.mode, 0};
+            pro.set_pos(pos);
             EpiPartial epi{m->part_o, L.o.tiles * TILE_ROWS};
             const int per_split = (L.o.nblk + m->pc.S - 1) / m->pc.S * block_cols(L.o.fmt);
             GH_CHECK(launch_mv<2>(sink, "o_proj", mat_bytes(L.o), L.o, m->pc, pro, epi,
@@ -1473,20 +1490,17 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
                      int n_splits, float* part, float* out, hipStream_t s) {
     AttnArgs a{};
     a.q = q;
-    a.p_begin = p_begin;
-    a.p_end = p_end;
     a.kc = const_cast<float*>(kc);
     a.vc = const_cast<float*>(vc);
     a.nkv = nkv;
     a.scale = 1.0f / sqrtf((float)hd);
     a.part = part;
     a.nc = n_splits;
+    a.set_range(p_begin, p_end);
     Sink k;
     k.s = s;
     GH_CHECK(launch_attn_t<false>(k, 0.0, hd, nq / nkv, a, nkv));
-    int ch, n_used;
-    attn_chunks(p_end - p_begin, n_splits, ch, n_used);
-    hipLaunchKernelGGL(k_attn_combine, dim3((nq * hd + 255) / 256), dim3(256), 0, s, part, n_splits, n_used, nq / nkv,
+    hipLaunchKernelGGL(k_attn_combine, dim3((nq * hd + 255) / 256), dim3(256), 0, s, part, n_splits, a.n_used, nq / nkv,
                        hd, nq, out);
     GH_HIP(hipGetLastError());
     return GH_OK;

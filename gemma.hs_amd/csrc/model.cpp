@@ -159,7 +159,7 @@ void make_plans(gh_model* m) {
         const DMat& d = p == &m->pa ? L.qkv : p == &m->pc ? L.o : p == &m->pd ? L.gu : L.down;
         p->kbw = kbw_for(m->fmt, ((d.nblk + p->S - 1) / p->S + 3) / 4);
     }
-    m->attn_nc = std::max(1, std::min(64, env_int("GH_ATTN_NC", 32)));
+    m->attn_nc = std::max(1, std::min(64, env_int("GH_ATTN_NC", 64)));
 }
 
 int ensure_scratch(gh_model* m) {
@@ -226,7 +226,7 @@ int launch_step(gh_kv* kv, int pos) {
     }
     GH_CHECK(kv_graph(kv));
     for (auto& p : kv->patches) {
-        *p.pos = pos;
+        p.set(pos);
         GH_HIP(hipGraphExecKernelNodeSetParams(kv->graph_exec, p.node, &p.params));
     }
     GH_HIP(hipGraphLaunch(kv->graph_exec, s));
