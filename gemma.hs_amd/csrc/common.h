@@ -79,6 +79,8 @@ struct StepState {
 struct Plan {
     int S = 1;
     int kbw = 1;
+    int rl = 2;  // rows per lane: 2 = 128-row workgroups, 1 = 64-row workgroups
+    int row_tiles(int tiles) const { return rl == 2 ? tiles : 2 * tiles; }
 };
 
 struct LayerDev {

@@ -234,17 +234,19 @@ struct WRegs {
     uint16_t s0[KBW], s1[KBW];
 };
 
-template <int FMT, int KBW>
-__device__ __forceinline__ void mv_load(WRegs<FMT, KBW>& r, const DMat& w, int tile, int base, int kw1) {
+// Loads of one register batch: rows rbase+lane (and rbase+lane+64 when a
+// lane holds RL = 2 rows) of column blocks [base, min(base+KBW, kw1)).
+template <int FMT, int KBW, int RL>
+__device__ __forceinline__ void mv_load(WRegs<FMT, KBW>& r, const DMat& w, int tile, int rbase, int base, int kw1) {
     const int lane = threadIdx.x & 63;
-    const u32x4* cp = (const u32x4*)w.codes + (size_t)tile * w.nblk * TILE_ROWS;
-    const uint16_t* sp = w.scales + (size_t)tile * w.nblk * TILE_ROWS;
+    const u32x4* cp = (const u32x4*)w.codes + (size_t)tile * w.nblk * TILE_ROWS + rbase;
+    const uint16_t* sp = w.scales + (size_t)tile * w.nblk * TILE_ROWS + rbase;
     auto one = [&](int i, int kb) {
         r.c0[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + lane);
-        r.c1[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + 64 + lane);
+        if (RL == 2) r.c1[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + 64 + lane);
         if (FMT == FMT_Q4) {
             r.s0[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + lane);
-            r.s1[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + 64 + lane);
+            if (RL == 2) r.s1[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + 64 + lane);
         }
     };
     if (base + KBW <= kw1) {  // full batch (kw1 is wave-uniform)
@@ -288,7 +290,7 @@ __device__ __forceinline__ float dot_q4_word(uint32_t w, float4 xl, float4 xh, f
     return acc;
 }
 
-template <int FMT, int KBW>
+template <int FMT, int KBW, int RL>
 __device__ __forceinline__ void mv_block(const WRegs<FMT, KBW>& r, int i, int kb, int kb0, const float* xs,
                                          const float* sxs, float& acc0, float& acc1) {
     if (FMT == FMT_Q4) {
@@ -300,31 +302,33 @@ __device__ __forceinline__ void mv_block(const WRegs<FMT, KBW>& r, int i, int kb
         for (int j = 0; j < 4; ++j) {
             const float4 xl = xv[j], xh = xv[4 + j];
             d0 = dot_q4_word(w0[j], xl, xh, d0);
-            d1 = dot_q4_word(w1[j], xl, xh, d1);
+            if (RL == 2) d1 = dot_q4_word(w1[j], xl, xh, d1);
         }
         // sum (q-8) x = sum q x - 8 sum x ; sxs holds sum x per block
         const float sx8 = 8.0f * sxs[kb - kb0];
         acc0 = fmaf(h2f(r.s0[i]), d0 - sx8, acc0);
-        acc1 = fmaf(h2f(r.s1[i]), d1 - sx8, acc1);
+        if (RL == 2) acc1 = fmaf(h2f(r.s1[i]), d1 - sx8, acc1);
     } else {
         const float4 x = *(const float4*)(xs + (kb - kb0) * 4);
         const f32x4 a = __builtin_bit_cast(f32x4, r.c0[i]);
-        const f32x4 b = __builtin_bit_cast(f32x4, r.c1[i]);
         acc0 += a.x * x.x + a.y * x.y + a.z * x.z + a.w * x.w;
-        acc1 += b.x * x.x + b.y * x.y + b.z * x.z + b.w * x.w;
+        if (RL == 2) {
+            const f32x4 b = __builtin_bit_cast(f32x4, r.c1[i]);
+            acc1 += b.x * x.x + b.y * x.y + b.z * x.z + b.w * x.w;
+        }
     }
 }
 
-template <int FMT, int KBW>
+template <int FMT, int KBW, int RL>
 __device__ __forceinline__ void mv_compute(const WRegs<FMT, KBW>& r, int base, int kw1, int kb0, const float* xs,
                                            const float* sxs, float& acc0, float& acc1) {
     if (base + KBW <= kw1) {  // full batch: no per-block predication (kw1 is wave-uniform)
 #pragma unroll
-        for (int i = 0; i < KBW; ++i) mv_block<FMT, KBW>(r, i, base + i, kb0, xs, sxs, acc0, acc1);
+        for (int i = 0; i < KBW; ++i) mv_block<FMT, KBW, RL>(r, i, base + i, kb0, xs, sxs, acc0, acc1);
     } else {
 #pragma unroll
         for (int i = 0; i < KBW; ++i)
-            if (base + i < kw1) mv_block<FMT, KBW>(r, i, base + i, kb0, xs, sxs, acc0, acc1);
+            if (base + i < kw1) mv_block<FMT, KBW, RL>(r, i, base + i, kb0, xs, sxs, acc0, acc1);
     }
 }
 
@@ -344,35 +348,15 @@ inline size_t mv_lds_bytes(int fmt, int per_split, int tmp_floats) {
     return f * sizeof(float);
 }
 
-// Per 32-element block: sxs = sum x, then x[16..31] *= 1/16 (exact) for the
-// high-nibble products of dot_q4_word.
-template <int FMT>
-__device__ __forceinline__ void fill_block_sums(const MvLds& L, int nk) {
-    if (FMT == FMT_Q4) {
-        __syncthreads();
-        for (int b = threadIdx.x; b < nk; b += NT) {
-            float4* x = (float4*)(L.xs + b * 32);
-            float s = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float4 v = x[e];
-                s += (v.x + v.y) + (v.z + v.w);
-            }
-            L.sxs[b] = s;
-#pragma unroll
-            for (int e = 4; e < 8; ++e) {
-                const float4 v = x[e];
-                x[e] = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
-            }
-        }
-    }
-}
-
-template <int FMT, int KBW, class Pro, class Epi>
+// One workgroup = 64*RL rows (one or both halves of a 128-row tile) x one
+// column split.  Rows: lane (RL 1) or lane and lane+64 (RL 2) of the
+// workgroup's rows; the four waves split the split's column blocks.
+template <int FMT, int KBW, int RL, class Pro, class Epi>
 __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) {
     extern __shared__ float lds[];
     constexpr int BK = Blk<FMT>::BK;
-    const int tile = blockIdx.x / S, s = blockIdx.x % S;
+    const int rt = blockIdx.x / S, s = blockIdx.x % S;
+    const int tile = RL == 2 ? rt : rt >> 1, rbase = RL == 2 ? 0 : (rt & 1) * 64;
     const int nb = w.nblk;
     const int per_split = (nb + S - 1) / S;
     const int kb0 = min(nb, s * per_split), kb1 = min(nb, kb0 + per_split);
@@ -395,40 +379,59 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
     typename Pro::Regs pr;
     pro.load(pr, kb0 * BK, nk * BK);
     WRegs<FMT, KBW> r;
-    mv_load<FMT, KBW>(r, w, tile, kw0, kw1);
-    pro.finish(L, pr, kb0 * BK, nk * BK);
+    mv_load<FMT, KBW, RL>(r, w, tile, rbase, kw0, kw1);
+    pro.template finish<FMT>(L, pr, kb0 * BK, nk * BK);
     GH_MARK(1);
-    fill_block_sums<FMT>(L, nk);
     __syncthreads();
     GH_MARK(2);
     // 4. dot products
     float acc0 = 0.0f, acc1 = 0.0f;
-    mv_compute<FMT, KBW>(r, kw0, kw1, kb0, L.xs, L.sxs, acc0, acc1);
+    mv_compute<FMT, KBW, RL>(r, kw0, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     for (int base = kw0 + KBW; base < kw1; base += KBW) {
-        mv_load<FMT, KBW>(r, w, tile, base, kw1);
-        mv_compute<FMT, KBW>(r, base, kw1, kb0, L.xs, L.sxs, acc0, acc1);
+        mv_load<FMT, KBW, RL>(r, w, tile, rbase, base, kw1);
+        mv_compute<FMT, KBW, RL>(r, base, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     }
     // 5. reduce the four waves
     GH_MARK(3);
     L.red[wave * TILE_ROWS + lane] = acc0;
-    L.red[wave * TILE_ROWS + 64 + lane] = acc1;
+    if (RL == 2) L.red[wave * TILE_ROWS + 64 + lane] = acc1;
     __syncthreads();
     GH_MARK(4);
     float y = 0.0f;
     const int t = threadIdx.x;
-    if (t < TILE_ROWS) y = (L.red[t] + L.red[TILE_ROWS + t]) + (L.red[2 * TILE_ROWS + t] + L.red[3 * TILE_ROWS + t]);
-    epi(L, tile, s, t, y);
+    const bool valid = t < 64 * RL;
+    if (valid) y = (L.red[t] + L.red[TILE_ROWS + t]) + (L.red[2 * TILE_ROWS + t] + L.red[3 * TILE_ROWS + t]);
+    epi(L, rt, tile * TILE_ROWS + rbase + t, s, valid, y);
     GH_MARK(5);
 }
 
 // ------------------------------------------------------------------
-// prologues: load() issues the global loads of the input, finish() builds
-// xs[0 .. n) = input[c0 .. c0+n) in LDS
+// prologues: load() issues the global loads of the input, finish<FMT>()
+// builds xs[0 .. n) = input[c0 .. c0+n) in LDS through emit_x4
 // ------------------------------------------------------------------
 __device__ __forceinline__ float4 fma4(float w, float4 o, float4 acc) {
     return make_float4(acc.x + w * o.x, acc.y + w * o.y, acc.z + w * o.z, acc.w + w * o.w);
 }
 __device__ __forceinline__ float4 f4z() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// Store float4 group gi (< ng) of the input slice.  For Q4_0 the 8 groups of
+// a 32-element block sit in 8 consecutive lanes, which sum the block (sxs,
+// for the -8 * sum(x) term) and scale elements 16..31 by 1/16 (exact) for
+// the high-nibble products of dot_q4_word.  Called by every thread of the
+// workgroup with gi = base + threadIdx.x (base uniform, a multiple of NT).
+template <int FMT>
+__device__ __forceinline__ void emit_x4(const MvLds& L, int gi, int ng, float4 v) {
+    if constexpr (FMT == FMT_Q4) {
+        const float bs = group_sum<8>((v.x + v.y) + (v.z + v.w));
+        if ((gi & 7) >= 4) v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
+        if (gi < ng) {
+            ((float4*)L.xs)[gi] = v;
+            if ((gi & 7) == 0) L.sxs[gi >> 3] = bs;
+        }
+    } else {
+        if (gi < ng) ((float4*)L.xs)[gi] = v;
+    }
+}
 
 // sum over s < S of the float4 group g of part[s][ld]: all loads issued
 // before the first add, so the sum costs one round trip.
@@ -457,14 +460,15 @@ struct ProPlain {
             r.v[k] = gi < (n >> 2) ? x4[gi] : f4z();
         }
     }
+    template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int ng = n >> 2;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int gi = threadIdx.x + k * NT;
-            if (gi < ng) ((float4*)L.xs)[gi] = r.v[k];
+        for (int k = 0; k < 2; ++k) emit_x4<FMT>(L, threadIdx.x + k * NT, ng, r.v[k]);
+        for (int base = 2 * NT; base < ng; base += NT) {
+            const int gi = base + threadIdx.x;
+            emit_x4<FMT>(L, gi, ng, gi < ng ? ((const float4*)(x + c0))[gi] : f4z());
         }
-        for (int gi = threadIdx.x + 2 * NT; gi < ng; gi += NT) ((float4*)L.xs)[gi] = ((const float4*)(x + c0))[gi];
     }
 };
 
@@ -492,11 +496,11 @@ struct ProResid {
     struct Regs {
         float4 pv[MAXS][MG];
         float4 bv[MG], wp[MG];
-        float wn;
+        float4 wn;  // norm weights of this thread's first group of the slice
     };
     __device__ void load(Regs& r, int c0, int n) const {
         const int NG = H >> 2, tid = threadIdx.x;
-        r.wn = tid < n ? w_norm[c0 + tid] : 0.0f;
+        r.wn = tid < (n >> 2) ? ((const float4*)(w_norm + c0))[tid] : f4z();
         if (from_embedding) return;
 #pragma unroll
         for (int k = 0; k < MG; ++k) {
@@ -509,6 +513,7 @@ struct ProResid {
             }
         }
     }
+    template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int NG = H >> 2, tid = threadIdx.x;
         float4 xv[MG];
@@ -536,6 +541,7 @@ struct ProResid {
             }
             float rms = 1.0f;
             if (w_post) rms = sqrtf(block_sum(ss, L.misc) / (float)H + eps);
+            GH_MARK(6);
 #pragma unroll
             for (int k = 0; k < MG; ++k)
                 if (tid + k * NT < NG) xv[k] = r.bv[k] + (w_post ? norm4(dv[k], rms, r.wp[k], zc) : dv[k]);
@@ -554,8 +560,14 @@ struct ProResid {
             }
         }
         const float rms = sqrtf(block_sum(ss, L.misc + 4) / (float)H + eps);  // barrier: tmp complete
-        if (tid < n) L.xs[tid] = norm_apply(L.tmp[c0 + tid], rms, r.wn, zc);
-        for (int i = tid + NT; i < n; i += NT) L.xs[i] = norm_apply(L.tmp[c0 + i], rms, w_norm[c0 + i], zc);
+        GH_MARK(7);
+        const int ng = n >> 2;
+        const float4* t4 = (const float4*)(L.tmp + c0);
+        emit_x4<FMT>(L, tid, ng, tid < ng ? norm4(t4[tid], rms, r.wn, zc) : f4z());
+        for (int b = NT; b < ng; b += NT) {
+            const int gi = b + tid;
+            emit_x4<FMT>(L, gi, ng, gi < ng ? norm4(t4[gi], rms, ((const float4*)(w_norm + c0))[gi], zc) : f4z());
+        }
     }
 };
 
@@ -621,6 +633,7 @@ struct ProAttnCombine {
             r.lj = bj[G + hg % G];
         }
     }
+    template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int stride = G * (HD + 2), tid = threadIdx.x;
         const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
@@ -641,20 +654,23 @@ struct ProAttnCombine {
         }
         __syncthreads();
         const int ng = n >> 2;
-        for (int gi = tid; gi < ng; gi += NT) {
-            const int c = c0 + 4 * gi, h = c / HD, d = c % HD;
-            const float* pbase = part + (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
-            const float* wv = wts + (h - h0) * ATTN_MAX_NC;
+        for (int base = 0; base < ng; base += NT) {
+            const int gi = base + tid;
             float4 acc = f4z();
-            int j = 0;
-            if (gi == tid) {  // chunks 0..PRE-1 were loaded by load()
+            if (gi < ng) {
+                const int c = c0 + 4 * gi, h = c / HD, d = c % HD;
+                const float* pbase = part + (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
+                const float* wv = wts + (h - h0) * ATTN_MAX_NC;
+                int j = 0;
+                if (base == 0) {  // chunks 0..PRE-1 were loaded by load()
 #pragma unroll
-                for (int jj = 0; jj < PRE; ++jj)
-                    if (jj < n_used) acc = fma4(wv[jj], r.ov[jj], acc);
-                j = PRE;
+                    for (int jj = 0; jj < PRE; ++jj)
+                        if (jj < n_used) acc = fma4(wv[jj], r.ov[jj], acc);
+                    j = PRE;
+                }
+                for (; j < n_used; ++j) acc = fma4(wv[j], *(const float4*)(pbase + (size_t)j * stride), acc);
             }
-            for (; j < n_used; ++j) acc = fma4(wv[j], *(const float4*)(pbase + (size_t)j * stride), acc);
-            ((float4*)L.xs)[gi] = acc;
+            emit_x4<FMT>(L, gi, ng, acc);
         }
     }
 };
@@ -675,29 +691,35 @@ struct ProGeglu {
             r.u[s] = ok && s < Sg ? ((const float4*)(part_gu + (size_t)s * ld_g + up_off))[g] : f4z();
         }
     }
+    template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int ng = n >> 2;
-        for (int gi = threadIdx.x; gi < ng; gi += NT) {
-            float4 gs, us;
-            if (gi == (int)threadIdx.x) {
-                gs = r.g[0];
-                us = r.u[0];
+        for (int base = 0; base < ng; base += NT) {
+            const int gi = base + threadIdx.x;
+            float4 h = f4z();
+            if (gi < ng) {
+                float4 gs, us;
+                if (base == 0) {
+                    gs = r.g[0];
+                    us = r.u[0];
 #pragma unroll
-                for (int s = 1; s < MAXS; ++s)
-                    if (s < Sg) {
-                        gs = gs + r.g[s];
-                        us = us + r.u[s];
+                    for (int s = 1; s < MAXS; ++s)
+                        if (s < Sg) {
+                            gs = gs + r.g[s];
+                            us = us + r.u[s];
+                        }
+                } else {
+                    const int g = (c0 >> 2) + gi;
+                    gs = us = f4z();
+                    for (int s = 0; s < Sg; ++s) {
+                        gs = gs + ((const float4*)(part_gu + (size_t)s * ld_g))[g];
+                        us = us + ((const float4*)(part_gu + (size_t)s * ld_g + up_off))[g];
                     }
-            } else {
-                const int g = (c0 >> 2) + gi;
-                gs = us = f4z();
-                for (int s = 0; s < Sg; ++s) {
-                    gs = gs + ((const float4*)(part_gu + (size_t)s * ld_g))[g];
-                    us = us + ((const float4*)(part_gu + (size_t)s * ld_g + up_off))[g];
                 }
+                h = make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y, gelu_tanh(gs.z) * us.z,
+                                gelu_tanh(gs.w) * us.w);
             }
-            ((float4*)L.xs)[gi] = make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y,
-                                              gelu_tanh(gs.z) * us.z, gelu_tanh(gs.w) * us.w);
+            emit_x4<FMT>(L, gi, ng, h);
         }
     }
 };
@@ -708,8 +730,8 @@ struct ProGeglu {
 struct EpiPartial {
     float* part;
     int ld;
-    __device__ void operator()(const MvLds&, int tile, int s, int t, float y) const {
-        if (t < TILE_ROWS) part[(size_t)s * ld + tile * TILE_ROWS + t] = y;
+    __device__ void operator()(const MvLds&, int, int row, int s, bool valid, float y) const {
+        if (valid) part[(size_t)s * ld + row] = y;
     }
 };
 
@@ -717,29 +739,28 @@ struct EpiOut {
     float* y;
     int rows, softcap;
     float cap;
-    __device__ void operator()(const MvLds&, int tile, int, int t, float v) const {
-        const int row = tile * TILE_ROWS + t;
-        if (t < TILE_ROWS && row < rows) y[row] = softcap ? cap * tanhf(v / cap) : v;
+    __device__ void operator()(const MvLds&, int, int row, int, bool valid, float v) const {
+        if (valid && row < rows) y[row] = softcap ? cap * tanhf(v / cap) : v;
     }
 };
 
-// Logits + this tile's greedy argmax key (first maximum); the finish kernel
-// reduces the per-tile keys (no same-address atomics on the step path).
+// Logits + this workgroup's greedy argmax key (first maximum); the finish
+// kernel reduces the per-workgroup keys (no same-address atomics on the step
+// path).
 struct EpiLogits {
     float* logits;  // nullable
     int V;
     unsigned long long* cand;
     StepState* st;
-    __device__ void operator()(const MvLds& L, int tile, int, int t, float y) const {
-        const int row = tile * TILE_ROWS + t;
+    __device__ void operator()(const MvLds& L, int rt, int row, int, bool valid, float y) const {
         unsigned long long key = 0ull;
-        if (t < TILE_ROWS && row < V) {
+        if (valid && row < V) {
             if (logits) logits[row] = y;
             key = argmax_key(y, row);
             if (isnan(y)) atomicOr(&st->nan_flag, 1);
         }
         const unsigned long long b = block_max_key(key, (unsigned long long*)(L.misc + 32));
-        if (t == 0) cand[tile] = b;
+        if (threadIdx.x == 0) cand[rt] = b;
     }
 };
 
@@ -820,23 +841,27 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
                      const Epi& epi, int tmp_floats) {
     const int per_split = (w.nblk + p.S - 1) / p.S;
     const size_t lds = mv_lds_bytes(w.fmt, per_split, tmp_floats);
-    const dim3 grid(w.tiles * p.S), block(NT);
+    const dim3 grid(p.row_tiles(w.tiles) * p.S), block(NT);
     // POS_ARG counts kernel arguments (DMat, S, Pro, Epi): the prologue is 2
     auto go = [&](void (*fn)(DMat, int, Pro, Epi)) {
         return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, w, p.S, pro, epi);
     };
-    if (w.fmt == FMT_Q4) {
-        switch (p.kbw) {
-            case 1: return go(k_matvec<FMT_Q4, 1, Pro, Epi>);
-            case 2: return go(k_matvec<FMT_Q4, 2, Pro, Epi>);
-            case 3: return go(k_matvec<FMT_Q4, 3, Pro, Epi>);
-            case 4: return go(k_matvec<FMT_Q4, 4, Pro, Epi>);
-            case 6: return go(k_matvec<FMT_Q4, 6, Pro, Epi>);
-            case 9: return go(k_matvec<FMT_Q4, 9, Pro, Epi>);
-            default: return set_error(GH_ERR_INVALID, "unsupported register batch %d", p.kbw);
-        }
+    auto by_rl = [&](auto kbw) -> int {
+        constexpr int KBW = decltype(kbw)::value;
+        if (w.fmt != FMT_Q4) return p.rl == 2 ? go(k_matvec<FMT_F32, 8, 2, Pro, Epi>) : go(k_matvec<FMT_F32, 8, 1, Pro, Epi>);
+        return p.rl == 2 ? go(k_matvec<FMT_Q4, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4, KBW, 1, Pro, Epi>);
+    };
+    if (p.rl != 1 && p.rl != 2) return set_error(GH_ERR_INVALID, "unsupported rows per lane %d", p.rl);
+    if (w.fmt != FMT_Q4) return by_rl(std::integral_constant<int, 8>{});
+    switch (p.kbw) {
+        case 1: return by_rl(std::integral_constant<int, 1>{});
+        case 2: return by_rl(std::integral_constant<int, 2>{});
+        case 3: return by_rl(std::integral_constant<int, 3>{});
+        case 4: return by_rl(std::integral_constant<int, 4>{});
+        case 6: return by_rl(std::integral_constant<int, 6>{});
+        case 9: return by_rl(std::integral_constant<int, 9>{});
+        default: return set_error(GH_ERR_INVALID, "unsupported register batch %d", p.kbw);
     }
-    return go(k_matvec<FMT_F32, 8, Pro, Epi>);
 }
 
 // float4 groups per thread of the residual prologue: ceil(H / 1024)
@@ -863,7 +888,7 @@ __global__ __launch_bounds__(NT) void k_final_norm(ProResid<MG> pro, float* xn) 
     L.tmp = L.sxs;
     typename ProResid<MG>::Regs r;
     pro.load(r, 0, pro.H);
-    pro.finish(L, r, 0, pro.H);
+    pro.template finish<FMT_F32>(L, r, 0, pro.H);
     __syncthreads();
     for (int i = threadIdx.x; i < pro.H; i += NT) xn[i] = L.xs[i];
 }
@@ -1385,7 +1410,7 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
         GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(m->embd), m->embd, m->plm, pro, epi, 0));
     }
     return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
-                          (const unsigned long long*)m->lm_cand, (int)m->embd.tiles, (const int32_t*)kv->d_prompt,
+                          (const unsigned long long*)m->lm_cand, m->plm.row_tiles(m->embd.tiles), (const int32_t*)kv->d_prompt,
                           kv->d_ids);
 }
 

@@ -136,11 +136,15 @@ int env_int(const char* name, int def) {
 // Work-split plans, overridable for tuning sweeps with GH_PLAN_{A,C,D,E}_S.
 void make_plans(gh_model* m) {
     const LayerDev& L = m->layers[0];
+    // Measured on MI355X (gemma3-1b shapes): the short per-layer matvecs and
+    // the LM head run fastest as 64-row workgroups (RL 1) with up to 8
+    // column splits; gate/up (13824 rows) as 128-row workgroups with 4.
     m->pa = choose_plan(m->fmt, L.qkv.tiles, L.qkv.nblk, 256);
     m->pc = choose_plan(m->fmt, L.o.tiles, L.o.nblk, 256);
-    m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, 320);
+    m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, 4 * L.gu.tiles);
     m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 128);
     m->plm = choose_plan(m->fmt, m->embd.tiles, m->embd.nblk, 1);
+    m->pa.rl = m->pc.rl = m->pe.rl = m->plm.rl = 1;
     auto over = [&](Plan& p, const char* env, const DMat& d) {
         int s = env_int(env, 0);
         if (s > 0) {
@@ -154,6 +158,13 @@ void make_plans(gh_model* m) {
     over(m->pc, "GH_PLAN_C_S", L.o);
     over(m->pd, "GH_PLAN_D_S", L.gu);
     over(m->pe, "GH_PLAN_E_S", L.down);
+    // rows per lane (2: 128-row workgroups, 1: 64-row workgroups)
+    m->pa.rl = env_int("GH_PLAN_A_RL", m->pa.rl);
+    m->pc.rl = env_int("GH_PLAN_C_RL", m->pc.rl);
+    m->pd.rl = env_int("GH_PLAN_D_RL", m->pd.rl);
+    m->pe.rl = env_int("GH_PLAN_E_RL", m->pe.rl);
+    m->plm.rl = env_int("GH_PLAN_LM_RL", m->plm.rl);
+    for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe, &m->plm}) p->rl = p->rl == 1 ? 1 : 2;
     for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe}) {
         capped(*p);
         const DMat& d = p == &m->pa ? L.qkv : p == &m->pc ? L.o : p == &m->pd ? L.gu : L.down;
@@ -178,7 +189,7 @@ int ensure_scratch(gh_model* m) {
     GH_CHECK(dev_alloc(m, &m->logits, (size_t)m->embd.tiles * TILE_ROWS));
     GH_CHECK(dev_alloc(m, &m->layer_out, (size_t)c.n_layers * c.hidden));
     GH_CHECK(dev_alloc(m, &m->xn_final, c.hidden));
-    GH_CHECK(dev_alloc(m, &m->lm_cand, (size_t)m->embd.tiles));
+    GH_CHECK(dev_alloc(m, &m->lm_cand, (size_t)m->plm.row_tiles(m->embd.tiles)));
     return GH_OK;
 }
 
@@ -362,6 +373,7 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     GH_CHECK(upload(ctx, t->codes, codes.data(), codes.size()));
     GH_CHECK(upload(ctx, t->scales, sc.data(), sc.size() * 2));
     t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, 512);
+    t->plan.rl = env_int("GH_Q4_RL", 2) == 1 ? 1 : 2;
     if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
     *out = t.release();
     return GH_OK;

@@ -101,11 +101,14 @@ def test_step_and_generate_agree_and_cache_grows(ctx):
     np.testing.assert_array_equal(gh.generate(m, kv1, prompt, 10), ids)
 
 
-@pytest.mark.parametrize("mode", [gh.MODE_GEMMA3, gh.MODE_REF])
-def test_small_q4_gqa_model_local_global_live_oracle(ctx, mode):
+@pytest.mark.parametrize("mode,rl", [(gh.MODE_GEMMA3, 2), (gh.MODE_REF, 2), (gh.MODE_GEMMA3, 1)])
+def test_small_q4_gqa_model_local_global_live_oracle(ctx, mode, rl, monkeypatch):
     """A 4B-shaped miniature: Q4_0, 8 q heads / 4 kv heads (group 2),
     head_dim 256, local window 5 with global every 2nd layer, per-type theta;
-    the live oracle checks every layer at every step (window binds)."""
+    the live oracle checks every layer at every step (window binds).  rl=1
+    runs every matvec phase with 64-row workgroups."""
+    for v in ("A", "C", "D", "E", "LM"):
+        monkeypatch.setenv(f"GH_PLAN_{v}_RL", str(rl))
     cfg = gh.preset("gemma3-4b")
     cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 4, 1024
     cfg.sliding_window, cfg.global_every, cfg.max_seq, cfg.mode = 5, 2, 64, mode

@@ -57,9 +57,12 @@ def test_q4_0_dequant_all_scale_patterns(ctx):
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
+@pytest.mark.parametrize("rl", [2, 1])
 @pytest.mark.parametrize("rows,cols", [(6912, 1152), (1152, 6912), (262144, 1152), (1536, 1152),
                                        (1152, 1024), (4, 64), (130, 96)])
-def test_q4_0_matvec_shapes(ctx, rows, cols):
+def test_q4_0_matvec_shapes(ctx, rows, cols, rl, monkeypatch):
+    """Both workgroup shapes: 128 rows (2 per lane) and 64 rows (1 per lane)."""
+    monkeypatch.setenv("GH_Q4_RL", str(rl))
     raw = _random_q4(rows, cols, rows + cols, subnormal_frac=0.005)
     x = np.random.default_rng(rows).normal(size=cols).astype(np.float32)
     t = gh.Q4Tensor(ctx, raw, rows, cols)
