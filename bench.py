@@ -65,6 +65,101 @@ def cpu_baseline(cfg, seconds: float, threads: int) -> dict:
                       f"cost is the 562 MB weight pass, position-independent at these lengths"}
 
 
+def extras_c2_matvec(gh, ctx) -> dict:
+    """C2: one Q4_0 matvec at the three Gemma-3-1B shapes, x ~ N(0, 1),
+    rotating over >= 2 GiB of device copies of the weights so the 256 MB
+    Infinity Cache cannot serve repeated reads.  Each call is
+    gh_q4_0_matvec (the op-level runLinearQ4 path: split-K matvec plus its
+    partial-sum kernel when the plan splits columns), captured into one
+    graph with a call per copy and replayed; the time is per call."""
+    import numpy as np
+    out = {}
+    for rows, cols, name in ((6912, 1152, "gate"), (1152, 6912, "down"), (262144, 1152, "lm_head")):
+        raw = gh.synth_q4_0(7, f"c2.{name}", 0.01, rows, cols)
+        wbytes = rows * cols // 32 * 18
+        copies = -(-(2 << 30) // wbytes)
+        ts = [gh.Q4Tensor(ctx, raw, rows, cols) for _ in range(copies)]
+        x = gh.DeviceBuffer.from_numpy(ctx, np.random.default_rng(3).normal(size=cols).astype(np.float32))
+        y = gh.DeviceBuffer(ctx, 4 * rows)
+        for t in ts:
+            gh._lib.check(gh.lib().gh_q4_0_matvec(t.h, x.ptr, y.ptr, 0, 0.0))
+        # one graph holding one call per copy, replayed (no per-call launch cost)
+        ctx.capture_begin()
+        for t in ts:
+            gh._lib.check(gh.lib().gh_q4_0_matvec(t.h, x.ptr, y.ptr, 0, 0.0))
+        reps = max(1, 256 // copies)
+        us = ctx.capture_replay(reps) * 1e3 / copies
+        algo = wbytes + 4 * cols + 4 * rows
+        out[f"{rows}x{cols}"] = {"avg_us": round(us, 3), "bytes": algo, "gbps": round(algo / us / 1e3, 1),
+                                 "frac": round(algo / us / 1e3 / HBM_PEAK_GBPS, 4), "copies": copies}
+        for t in ts:
+            t.close()
+        x.free()
+        y.free()
+        log(f"  C2 {rows}x{cols}: {us:.2f} us, {algo / us / 1e3:.0f} GB/s ({copies} copies)")
+    return out
+
+
+def extras_c4_attention(gh, ctx) -> dict:
+    """C4: one decode query (4 q heads, 1 kv head, head_dim 256) over a
+    K/V cache of 8192 or 32768 N(0, 1) positions, global (whole cache) and
+    local (last 512), scale 1/16: gh_attention_decode (split-K attention
+    plus its merge kernel), 20 calls captured into a graph and replayed."""
+    import numpy as np
+    out = {}
+    rng = np.random.default_rng(4)
+    hd, nq, nkv = 256, 4, 1
+    q = gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=nq * hd).astype(np.float32))
+    o = gh.DeviceBuffer(ctx, 4 * nq * hd)
+    for L in (8192, 32768):
+        k = gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
+        v = gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
+        for kind, pb in (("global", 0), ("local", L - 512)):
+            n = 20
+            call = lambda: gh._lib.check(gh.lib().gh_attention_decode(ctx.h, q.ptr, k.ptr, v.ptr, nq, nkv, hd,
+                                                                      pb, L, 0, o.ptr))
+            call()
+            ctx.capture_begin()
+            for _ in range(n):
+                call()
+            us = ctx.capture_replay(5) * 1e3 / n
+            algo = 2 * (L - pb) * nkv * hd * 4 + 8 * nq * hd
+            out[f"L{L}_{kind}"] = {"avg_us": round(us, 3), "bytes": algo, "gbps": round(algo / us / 1e3, 1),
+                                   "frac": round(algo / us / 1e3 / HBM_PEAK_GBPS, 4)}
+            log(f"  C4 L={L} {kind}: {us:.2f} us, {algo / us / 1e3:.0f} GB/s")
+        k.free()
+        v.free()
+    q.free()
+    o.free()
+    return out
+
+
+def extras_c5_gemma3_4b(gh, ctx, steps: int = 64, warmup: int = 8) -> dict:
+    """C5: Gemma-3-4B-shaped Q4_0 decode (34 layers, hidden 2560, 8 q / 4 kv
+    heads, window 1024) with seeded synthetic weights; the KV cache holds
+    4096 positions of seeded N(0, 1) K/V (gh_kv_synth, in place of running
+    a prefill), then greedy steps from position 4096."""
+    cfg = gh.preset("gemma3-4b")
+    n0 = 4096
+    cfg.max_seq = n0 + warmup + steps + 8
+    model = gh.GemmaModel(ctx, cfg)
+    model.synth(WEIGHT_SEED, q4=True)
+    kv = gh.KVCache(model, cfg.max_seq)
+    kv.synth(5, n0)
+    prompt = gh.synth_tokens(PROMPT_SEED, "c5", 1, cfg.vocab)
+    ms, _ = gh.bench_decode(model, kv, prompt, warmup, steps)
+    tok_s = steps / (ms / 1e3)
+    timings = {name: gh.time_kernel(model, kv, name, 10) for name in gh.STEP_KERNELS}
+    step_bytes = sum(t.bytes_per_launch * t.launches_per_step for t in timings.values())
+    log(f"  C5 gemma3-4b @ {n0}: {tok_s:.1f} tok/s")
+    out = {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4), "steps": steps,
+           "start_position": n0 + 1 + warmup, "step_algorithmic_bytes": int(step_bytes),
+           "step_frac_of_hbm_peak": round(step_bytes / (ms / steps * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+           "lm_head_gbps": round(timings["lm_head"].gbps, 1)}
+    del kv, model
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,6 +167,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the C2/C4/C5 measurements")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only; multi-GPU runs (--gpus > 1) are not "
@@ -122,6 +218,10 @@ def main(argv=None) -> int:
                              "step_us": round(t.avg_us * t.launches_per_step, 1)}
                     for t in timings.values()},
     }
+    if not a.no_extras:
+        out["extras"] = {"c2_matvec_rotating_2GiB": extras_c2_matvec(gh, ctx),
+                         "c4_attention": extras_c4_attention(gh, ctx),
+                         "c5_gemma3_4b_prefilled_4096": extras_c5_gemma3_4b(gh, ctx)}
     if not a.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds, threads)

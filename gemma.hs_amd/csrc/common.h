@@ -108,6 +108,9 @@ struct gh_ctx {
     hipStream_t stream = nullptr;
     std::recursive_mutex mu;
     std::vector<void*> bufs;  // gh_buf_alloc allocations
+    hipEvent_t t0 = nullptr, t1 = nullptr;  // gh_timer_start / gh_timer_stop
+    void* scratch = nullptr;                // op-level temporaries
+    size_t scratch_bytes = 0;
 };
 
 struct gh_q4 {
@@ -233,6 +236,8 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
                      int p_begin, int p_end, int n_splits, float* part, float* out, hipStream_t s);
 int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t s);
 int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
+int launch_synth_normal(float* out, size_t n, uint64_t key, float sigma, hipStream_t s);
+constexpr int GH_ATTN_OP_MAX_NC = 256;  // chunks per kv head of the op-level attention
 
 // repack.cpp
 void repack_q4_0(const uint8_t* raw, int64_t rows, int64_t cols, bool ftz, uint8_t* codes,

@@ -1210,7 +1210,8 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
 
 template <bool STEP>
 static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
-    if (a.nc > ATTN_MAX_NC) return set_error(GH_ERR_INVALID, "attention: more than %d splits", ATTN_MAX_NC);
+    const int max_nc = STEP ? ATTN_MAX_NC : GH_ATTN_OP_MAX_NC;
+    if (a.nc > max_nc || a.nc < 1) return set_error(GH_ERR_INVALID, "attention: %d splits (1..%d)", a.nc, max_nc);
     const dim3 grid(nkv * a.nc), block(NT);
 #define GH_ATTN_CASE(HD_, G_) \
     if (hd == HD_ && G == G_) return sink_launch<STEP ? 0 : -1>(k, "attention", bytes, k_attn<HD_, G_, STEP>, grid, block, 0, a);
@@ -1221,23 +1222,35 @@ static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a
     return set_error(GH_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
 
-// Merge of the split-K partials for the op-level entry point.
-__global__ void k_attn_combine(const float* part, int nc, int n_used, int G, int HD, int nq, float* out) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= nq * HD) return;
-    const int h = idx / HD, d = idx % HD, g = h / G, hl = h % G;
+// Merge of the split-K partials for the op-level entry point: one workgroup
+// per q head; the chunk states (m_j, l_j) are loaded in parallel, then every
+// thread sums its dims over the chunks with independent loads.
+__global__ __launch_bounds__(NT) void k_attn_combine(const float* part, int nc, int n_used, int G, int HD, float* out) {
+    __shared__ float wj[GH_ATTN_OP_MAX_NC];
+    __shared__ float slot[8];
+    const int h = blockIdx.x, g = h / G, hl = h % G, tid = threadIdx.x;
     const int stride = G * (HD + 2);
     const float* base = part + (size_t)g * nc * stride;
-    float M = -INFINITY;
-    for (int j = 0; j < n_used; ++j) M = fmaxf(M, base[(size_t)j * stride + hl]);
-    float den = 0.0f, num = 0.0f;
-    for (int j = 0; j < n_used; ++j) {
-        const float* p = base + (size_t)j * stride;
-        const float wgt = expf(p[hl] - M);
-        den += p[G + hl] * wgt;
-        num += p[2 * G + hl * HD + d] * wgt;
+    float m = -INFINITY, l = 0.0f;
+    if (tid < n_used) {
+        m = base[(size_t)tid * stride + hl];
+        l = base[(size_t)tid * stride + G + hl];
     }
-    out[idx] = num / den;
+    // block max of m over the chunks (n_used <= NT)
+    float mx = wave_max(m);
+    if ((tid & 63) == 0) slot[tid >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(slot[0], slot[1]), fmaxf(slot[2], slot[3]));
+    const float w = tid < n_used ? expf(m - M) : 0.0f;
+    if (tid < n_used) wj[tid] = w;
+    const float den = block_sum(l * w, slot + 4);  // barrier: wj complete
+    for (int d = tid; d < HD; d += NT) {
+        const float* o = base + 2 * G + hl * HD + d;
+        float num = 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < n_used; ++j) num += o[(size_t)j * stride] * wj[j];
+        out[(size_t)h * HD + d] = num / den;
+    }
 }
 
 // ------------------------------------------------------------------
@@ -1525,8 +1538,33 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     Sink k;
     k.s = s;
     GH_CHECK(launch_attn_t<false>(k, 0.0, hd, nq / nkv, a, nkv));
-    hipLaunchKernelGGL(k_attn_combine, dim3((nq * hd + 255) / 256), dim3(256), 0, s, part, n_splits, a.n_used, nq / nkv,
-                       hd, nq, out);
+    hipLaunchKernelGGL(k_attn_combine, dim3(nq), dim3(NT), 0, s, part, n_splits, a.n_used, nq / nkv, hd, out);
+    GH_HIP(hipGetLastError());
+    return GH_OK;
+}
+
+// Seeded N(0, sigma) values, counter-based: element i hashes (key, i) with
+// SplitMix64 and maps the 64 bits to two uniforms for Box-Muller.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void k_synth_normal(float* out, size_t n, uint64_t key, float sigma) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const uint64_t h = splitmix64(key ^ splitmix64(i));
+        const float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+        const float u2 = (float)((h >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+        out[i] = sigma * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307f * u2);
+    }
+}
+
+int launch_synth_normal(float* out, size_t n, uint64_t key, float sigma, hipStream_t s) {
+    if (n == 0) return GH_OK;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, s, out, n, key, sigma);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }

@@ -296,8 +296,70 @@ extern "C" int gh_ctx_destroy(gh_ctx* ctx) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     for (void* p : ctx->bufs) hipFree(p);
+    if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->t0) hipEventDestroy(ctx->t0);
+    if (ctx->t1) hipEventDestroy(ctx->t1);
     hipStreamDestroy(ctx->stream);
     delete ctx;
+    return GH_OK;
+}
+
+extern "C" int gh_timer_start(gh_ctx* ctx) {
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    if (!ctx->t0) GH_HIP(hipEventCreate(&ctx->t0));
+    if (!ctx->t1) GH_HIP(hipEventCreate(&ctx->t1));
+    GH_HIP(hipEventRecord(ctx->t0, ctx->stream));
+    return GH_OK;
+}
+
+extern "C" int gh_timer_stop(gh_ctx* ctx, float* ms_out) {
+    if (!ms_out) return set_error(GH_ERR_INVALID, "null output");
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    if (!ctx->t0 || !ctx->t1) return set_error(GH_ERR_STATE, "gh_timer_stop without gh_timer_start");
+    GH_HIP(hipEventRecord(ctx->t1, ctx->stream));
+    GH_HIP(hipEventSynchronize(ctx->t1));
+    GH_HIP(hipEventElapsedTime(ms_out, ctx->t0, ctx->t1));
+    return GH_OK;
+}
+
+extern "C" int gh_capture_begin(gh_ctx* ctx) {
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    GH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return GH_OK;
+}
+
+extern "C" int gh_capture_replay(gh_ctx* ctx, int32_t n_replays, float* ms_per_replay_out) {
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    hipGraph_t g = nullptr;
+    GH_HIP(hipStreamEndCapture(ctx->stream, &g));
+    if (n_replays <= 0 || !ms_per_replay_out) {
+        hipGraphDestroy(g);
+        return set_error(GH_ERR_INVALID, "bad arguments");
+    }
+    hipGraphExec_t ge = nullptr;
+    int rc = GH_OK;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipGraphInstantiate failed");
+    if (rc == GH_OK && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess))
+        rc = set_error(GH_ERR_HIP, "hipEventCreate failed");
+    if (rc == GH_OK && hipGraphLaunch(ge, ctx->stream) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipGraphLaunch failed");
+    if (rc == GH_OK && hipEventRecord(a, ctx->stream) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
+    for (int i = 0; i < n_replays && rc == GH_OK; ++i)
+        if (hipGraphLaunch(ge, ctx->stream) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipGraphLaunch failed");
+    float ms = 0.0f;
+    if (rc == GH_OK && hipEventRecord(b, ctx->stream) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
+    if (rc == GH_OK && hipEventSynchronize(b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventSynchronize failed");
+    if (rc == GH_OK && hipEventElapsedTime(&ms, a, b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventElapsedTime failed");
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    if (ge) hipGraphExecDestroy(ge);
+    hipGraphDestroy(g);
+    GH_CHECK(rc);
+    *ms_per_replay_out = ms / n_replays;
     return GH_OK;
 }
 
@@ -390,12 +452,39 @@ extern "C" int gh_q4_0_free(gh_q4* t) {
     return GH_OK;
 }
 
+// Op-level calls are synchronous, except while the context stream is being
+// captured (gh_capture_begin): then they only enqueue.
+static int op_sync(gh_ctx* ctx) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    GH_HIP(hipStreamIsCapturing(ctx->stream, &st));
+    if (st == hipStreamCaptureStatusNone) GH_HIP(hipStreamSynchronize(ctx->stream));
+    return GH_OK;
+}
+
+// Per-context device scratch for op-level temporaries; grows outside capture.
+static int ctx_scratch(gh_ctx* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->scratch_bytes) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        GH_HIP(hipStreamIsCapturing(ctx->stream, &st));
+        if (st != hipStreamCaptureStatusNone)
+            return set_error(GH_ERR_STATE, "op needs %zu B of scratch while capturing; run it once before capture", bytes);
+        GH_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->scratch) GH_HIP(hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        GH_HIP(hipMalloc(&ctx->scratch, bytes));
+        ctx->scratch_bytes = bytes;
+    }
+    *out = ctx->scratch;
+    return GH_OK;
+}
+
 extern "C" int gh_q4_0_dequant(gh_q4* t, float* out) {
     if (!t || !out) return set_error(GH_ERR_INVALID, "null argument");
     GH_CHECK(ctx_bind(t->ctx));
     Lock lk(t->ctx->mu);
     GH_CHECK(launch_q4_dequant(t->m, out, t->ctx->stream));
-    GH_HIP(hipStreamSynchronize(t->ctx->stream));
+    GH_CHECK(op_sync(t->ctx));
     return GH_OK;
 }
 
@@ -405,7 +494,7 @@ extern "C" int gh_q4_0_matvec(gh_q4* t, const float* x, float* y, int softcap, f
     GH_CHECK(ctx_bind(t->ctx));
     Lock lk(t->ctx->mu);
     GH_CHECK(launch_matvec_plain(t->m, t->plan, x, t->part, y, softcap, cap, t->ctx->stream));
-    GH_HIP(hipStreamSynchronize(t->ctx->stream));
+    GH_CHECK(op_sync(t->ctx));
     return GH_OK;
 }
 
@@ -444,7 +533,7 @@ extern "C" int gh_rmsnorm(gh_ctx* ctx, const float* x, const float* w, int n, fl
     OP_ENTER(ctx);
     if (!x || !w || !y || n <= 0) return set_error(GH_ERR_INVALID, "gh_rmsnorm: bad arguments");
     GH_CHECK(launch_rmsnorm(x, w, n, eps, zc, y, ctx->stream));
-    GH_HIP(hipStreamSynchronize(ctx->stream));
+    GH_CHECK(op_sync(ctx));
     return GH_OK;
 }
 
@@ -452,7 +541,7 @@ extern "C" int gh_qk_norm(gh_ctx* ctx, const float* x, const float* w, int n_hea
     OP_ENTER(ctx);
     if (!x || !w || !y || n_heads <= 0) return set_error(GH_ERR_INVALID, "gh_qk_norm: bad arguments");
     GH_CHECK(launch_qk_norm(x, w, n_heads, hd, eps, zc, y, ctx->stream));
-    GH_HIP(hipStreamSynchronize(ctx->stream));
+    GH_CHECK(op_sync(ctx));
     return GH_OK;
 }
 
@@ -467,7 +556,7 @@ extern "C" int gh_rope(gh_ctx* ctx, float* x, int n_heads, int hd, float theta, 
     GH_HIP(hipMalloc((void**)&d, tab.size() * sizeof(float)));
     int rc = upload(ctx, d, tab.data(), tab.size() * sizeof(float));
     if (rc == GH_OK) rc = launch_rope(x, n_heads, hd, d, ctx->stream);
-    if (hipStreamSynchronize(ctx->stream) != hipSuccess && rc == GH_OK) rc = set_error(GH_ERR_HIP, "gh_rope: sync failed");
+    if (rc == GH_OK) rc = op_sync(ctx);
     hipFree(d);
     return rc;
 }
@@ -478,22 +567,21 @@ extern "C" int gh_attention_decode(gh_ctx* ctx, const float* q, const float* kc,
     if (!q || !kc || !vc || !out || nkv <= 0 || nq % nkv || p_begin < 0 || p_end <= p_begin)
         return set_error(GH_ERR_INVALID, "gh_attention_decode: bad arguments");
     const int n_pos = p_end - p_begin;
-    if (n_splits <= 0) n_splits = std::max(1, std::min(n_pos / 64, 64));
-    n_splits = std::min(std::min(n_splits, n_pos), 64);
-    float* part = nullptr;
+    // default: about 128 positions per chunk, up to GH_ATTN_OP_MAX_NC chunks per kv head
+    if (n_splits <= 0) n_splits = std::max(1, std::min((n_pos + 127) / 128, GH_ATTN_OP_MAX_NC));
+    n_splits = std::min(std::min(n_splits, n_pos), GH_ATTN_OP_MAX_NC);
+    void* part = nullptr;
     const int G = nq / nkv;
-    GH_HIP(hipMallocAsync((void**)&part, sizeof(float) * nkv * n_splits * G * (hd + 2), ctx->stream));
-    int rc = launch_attention(q, kc, vc, nq, nkv, hd, p_begin, p_end, n_splits, part, out, ctx->stream);
-    hipFreeAsync(part, ctx->stream);
-    GH_HIP(hipStreamSynchronize(ctx->stream));
-    return rc;
+    GH_CHECK(ctx_scratch(ctx, sizeof(float) * nkv * n_splits * G * (hd + 2), &part));
+    GH_CHECK(launch_attention(q, kc, vc, nq, nkv, hd, p_begin, p_end, n_splits, (float*)part, out, ctx->stream));
+    return op_sync(ctx);
 }
 
 extern "C" int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, float* h) {
     OP_ENTER(ctx);
     if (!g || !u || !h || n <= 0) return set_error(GH_ERR_INVALID, "gh_gelu_mul: bad arguments");
     GH_CHECK(launch_gelu_mul(g, u, n, h, ctx->stream));
-    GH_HIP(hipStreamSynchronize(ctx->stream));
+    GH_CHECK(op_sync(ctx));
     return GH_OK;
 }
 
@@ -508,7 +596,7 @@ extern "C" int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx) {
         GH_HIP(hipMemcpyAsync(&h, key, 8, hipMemcpyDeviceToHost, ctx->stream));
     }
     hipFreeAsync(key, ctx->stream);
-    GH_HIP(hipStreamSynchronize(ctx->stream));
+    GH_CHECK(op_sync(ctx));
     if (rc == GH_OK) *idx = (int32_t)(0xFFFFFFFFu - (uint32_t)(h & 0xFFFFFFFFull));
     return rc;
 }
@@ -773,6 +861,25 @@ extern "C" int gh_kv_reset(gh_kv* kv) {
 extern "C" int gh_kv_length(gh_kv* kv, int32_t* len) {
     if (!kv || !len) return set_error(GH_ERR_INVALID, "null argument");
     *len = kv->len;
+    return GH_OK;
+}
+
+extern "C" int gh_kv_synth(gh_kv* kv, uint64_t seed, int32_t n_pos, float sigma) {
+    if (!kv) return set_error(GH_ERR_INVALID, "null kv");
+    if (n_pos < 0 || n_pos > kv->max_seq) return set_error(GH_ERR_RANGE, "n_pos %d outside [0, %d]", n_pos, kv->max_seq);
+    gh_model* m = kv->m;
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    const gh_config& c = m->cfg;
+    const size_t per_layer = (size_t)kv->max_seq * c.n_kv_heads * c.head_dim;
+    const size_t n = (size_t)n_pos * c.n_kv_heads * c.head_dim;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const uint64_t key = seed * 0x9E3779B97F4A7C15ull + (uint64_t)l * 2;
+        GH_CHECK(launch_synth_normal(kv->k + l * per_layer, n, key, sigma, m->ctx->stream));
+        GH_CHECK(launch_synth_normal(kv->v + l * per_layer, n, key + 1, sigma, m->ctx->stream));
+    }
+    GH_HIP(hipStreamSynchronize(m->ctx->stream));
+    kv->len = n_pos;
     return GH_OK;
 }
 

@@ -66,6 +66,28 @@ class Context:
     def sync(self) -> None:
         check(lib().gh_ctx_sync(self.h))
 
+    def timer_start(self) -> None:
+        """Record the start event of gh_timer_start on the context stream."""
+        check(lib().gh_timer_start(self.h))
+
+    def timer_stop(self) -> float:
+        """ms since timer_start, measured with HIP events on the stream."""
+        ms = C.c_float()
+        check(lib().gh_timer_stop(self.h, C.byref(ms)))
+        return ms.value
+
+    def capture_begin(self) -> None:
+        """Start capturing the context stream: launch-only op calls enqueue
+        into a graph instead of running (gh_capture_begin)."""
+        check(lib().gh_capture_begin(self.h))
+
+    def capture_replay(self, n_replays: int) -> float:
+        """End the capture, replay the graph n_replays times between two
+        HIP events; returns ms per replay (gh_capture_replay)."""
+        ms = C.c_float()
+        check(lib().gh_capture_replay(self.h, n_replays, C.byref(ms)))
+        return ms.value
+
     def close(self) -> None:
         if self.h:
             lib().gh_ctx_destroy(self.h)
@@ -360,6 +382,11 @@ class KVCache:
         return n.value
 
     __len__ = cacheLength
+
+    def synth(self, seed: int, n_pos: int, sigma: float = 1.0) -> None:
+        """Fill positions [0, n_pos) with seeded N(0, sigma) K/V (a stand-in
+        for a prefilled context; gh_kv_synth) and set the length to n_pos."""
+        check(lib().gh_kv_synth(self.h, seed, n_pos, sigma))
 
     def reset(self) -> None:
         check(lib().gh_kv_reset(self.h))

@@ -67,6 +67,19 @@ int gh_ctx_create(int device, gh_ctx** out);
 int gh_ctx_destroy(gh_ctx* ctx);
 /* waitAll (src/Gemma/Model.hs:1432) */
 int gh_ctx_sync(gh_ctx* ctx);
+/* Event timer on the context stream (replaces the wall-clock timing of
+ * examples/BenchmarkKVCache.hs:186-210): start records an event, stop
+ * records a second one, waits for it and returns the elapsed ms. */
+int gh_timer_start(gh_ctx* ctx);
+int gh_timer_stop(gh_ctx* ctx, float* ms_out);
+/* Graph timing of op-level calls (no reference counterpart; used by the
+ * matvec and attention microbenchmarks): after gh_capture_begin the
+ * launch-only op calls (gh_q4_0_matvec, gh_attention_decode, gh_rmsnorm,
+ * gh_qk_norm, gh_gelu_mul, gh_q4_0_dequant) enqueue without
+ * synchronising; gh_capture_replay ends the capture, replays the graph
+ * n_replays times between two events and returns the ms per replay. */
+int gh_capture_begin(gh_ctx* ctx);
+int gh_capture_replay(gh_ctx* ctx, int32_t n_replays, float* ms_per_replay_out);
 
 /* ================================================================
  * Buffers: replace createTensor / createTensorWithData / fromGPU
@@ -169,6 +182,11 @@ int gh_kv_create(gh_model* m, int32_t max_seq, gh_kv** out);
 int gh_kv_destroy(gh_kv* kv);
 int gh_kv_reset(gh_kv* kv);
 int gh_kv_length(gh_kv* kv, int32_t* len_out);
+/* Benchmark set-up with no reference counterpart: fill positions
+ * [0, n_pos) of every layer's K and V with seeded N(0, sigma) values
+ * (counter-based generator on the device) and set the cache length to
+ * n_pos, standing in for a prefilled context. */
+int gh_kv_synth(gh_kv* kv, uint64_t seed, int32_t n_pos, float sigma);
 
 /* runGemmaInferenceCached (src/Gemma/Model.hs:1313-1437) and its layer-0
  * variant runGemmaInferenceCachedWithLayer0 (src/Gemma/Model.hs:1441):

@@ -170,3 +170,60 @@ def test_time_kernel_leaves_state_unchanged(ctx):
     np.testing.assert_array_equal(np.concatenate([first, rest]), ref)
     with pytest.raises(gh.GemmaHipError):
         gh.time_kernel(m, kv_b, "finish", 1)
+
+
+@pytest.mark.parametrize("preset", ["tiny", "mini4b"])
+def test_gguf_loaded_model_matches_synth_model(ctx, tmp_path, preset):
+    """loadGemmaModelFromGGUF (src/Gemma/Model.hs:908) through
+    gh_model_load_gguf: a GGUF file holding the seeded synthetic tensors
+    gives the same config and bit-identical logits and ids as the model
+    built from the same tensors with gh_model_set_tensor."""
+    import sys
+    sys.path.insert(0, str(GOLDEN.parent))
+    from gguf_writer import synth_gguf
+    if preset == "tiny":
+        cfg = gh.preset("tiny")
+    else:
+        cfg = gh.preset("gemma3-4b")
+        cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 3, 1024
+        cfg.sliding_window, cfg.global_every = 5, 6
+    path = tmp_path / f"{preset}.gguf"
+    synth_gguf(path, cfg, 21, q4=True)
+    mg = gh.GemmaModel.load_gguf(ctx, str(path), max_seq=64)
+    got = mg.config()
+    for f in ("vocab", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "ffn", "sliding_window"):
+        assert getattr(got, f) == getattr(cfg, f), f
+    cfg.max_seq = 64
+    ms = _gpu_model(ctx, cfg, 21, True)
+    prompt = gh.synth_tokens(4, "prompt", 7, cfg.vocab)
+    kg, ks = gh.KVCache(mg, 64), gh.KVCache(ms, 64)
+    for t in prompt:
+        lg, _, _ = gh.runGemmaInferenceCached(mg, int(t), kg)
+        ls, _, _ = gh.runGemmaInferenceCached(ms, int(t), ks)
+        np.testing.assert_array_equal(lg, ls)
+    np.testing.assert_array_equal(gh.generate(mg, kg, [int(prompt[-1])], 10), gh.generate(ms, ks, [int(prompt[-1])], 10))
+
+
+def test_kv_synth_prefill_and_timer(ctx):
+    """gh_kv_synth fills a cache deterministically and sets its length;
+    decoding then continues from that position; the event timer measures
+    a positive duration."""
+    cfg = gh.preset("tiny")
+    m = _gpu_model(ctx, cfg, 3, True)
+    outs = []
+    for _ in range(2):
+        kv = gh.KVCache(m, 96)
+        kv.synth(11, 40)
+        assert len(kv) == 40
+        logits, _, _ = gh.runGemmaInferenceCached(m, 5, kv)
+        assert len(kv) == 41 and np.all(np.isfinite(logits))
+        outs.append(logits)
+    np.testing.assert_array_equal(outs[0], outs[1])
+    kv = gh.KVCache(m, 96)
+    kv.synth(12, 40)
+    assert not np.array_equal(gh.runGemmaInferenceCached(m, 5, kv)[0], outs[0])
+    with pytest.raises(gh.GemmaHipError):
+        kv.synth(1, 97)
+    ctx.timer_start()
+    gh.generate(m, kv, [5], 4)
+    assert ctx.timer_stop() > 0.0

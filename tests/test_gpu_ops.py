@@ -143,3 +143,36 @@ def test_attention_decode_global_and_local(ctx, nq, nkv, hd, L):
     a = gh.attention_decode(ctx, q, K, V, nq, nkv, hd, 0, L, n_splits=1)
     b = gh.attention_decode(ctx, q, K, V, nq, nkv, hd, 0, L, n_splits=min(L, 64))
     assert rel_err(a, b) < 1e-5
+
+
+def test_capture_replay_matches_eager_calls(ctx):
+    """gh_capture_begin / gh_capture_replay: op calls captured into a graph
+    and replayed give the eager results; an op that would need new scratch
+    during capture is refused."""
+    rows, cols = 1152, 6912
+    raw = _random_q4(rows, cols, 5)
+    t = gh.Q4Tensor(ctx, raw, rows, cols)
+    xv = np.random.default_rng(5).normal(size=cols).astype(np.float32)
+    want = t.matvec(xv)
+    x = gh.DeviceBuffer.from_numpy(ctx, xv)
+    y = gh.DeviceBuffer(ctx, 4 * rows)
+    ctx.capture_begin()
+    gh._lib.check(gh.lib().gh_q4_0_matvec(t.h, x.ptr, y.ptr, 0, 0.0))
+    assert ctx.capture_replay(3) > 0.0
+    np.testing.assert_array_equal(y.numpy(), want)
+    for b in (x, y):
+        b.free()
+    t.close()
+    # a fresh context has no op scratch yet: attention may not allocate it during capture
+    c2 = gh.Context(0)
+    q = gh.DeviceBuffer.from_numpy(c2, np.ones(8 * 256, np.float32))
+    kv = gh.DeviceBuffer.from_numpy(c2, np.ones(300 * 256 * 4, np.float32))
+    o = gh.DeviceBuffer(c2, 4 * 8 * 256)
+    c2.capture_begin()
+    with pytest.raises(gh.GemmaHipError) as e:
+        gh._lib.check(gh.lib().gh_attention_decode(c2.h, q.ptr, kv.ptr, kv.ptr, 8, 4, 256, 0, 300, 3, o.ptr))
+    assert e.value.name == "GH_ERR_STATE"
+    c2.capture_replay(1)
+    for b in (q, kv, o):
+        b.free()
+    c2.close()
