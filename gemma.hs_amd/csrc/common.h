@@ -70,6 +70,9 @@ struct StepState {
     int32_t nan_flag;   // set when a logit is NaN
     int32_t gen_count;  // generated ids written so far
     int32_t gen_cap;    // capacity of the ids buffer
+    float inv_temp;     // 1/temperature; 0 = greedy
+    uint32_t seed_lo, seed_hi;  // Philox key of the sampler
+    int32_t pad;
     unsigned long long keys[2];  // argmax keys, slot pos & 1
 };
 
@@ -185,7 +188,9 @@ struct gh_model {
     float* logits = nullptr;
     float* layer_out = nullptr;
     float* xn_final = nullptr;               // final-norm output, input of the LM head
-    unsigned long long* lm_cand = nullptr;   // per-tile argmax keys of the LM head
+    unsigned long long* lm_cand = nullptr;   // per-workgroup argmax keys of the LM head
+    float* lm_m = nullptr;                   // per-workgroup max logit (sampling)
+    float* lm_s = nullptr;                   // per-workgroup sum of exp((l - max) / T) (sampling)
     // presence tracking
     bool has_embd = false, has_out_norm = false;
     std::vector<uint32_t> present;  // per layer bitmask of tensor kinds
@@ -202,6 +207,8 @@ struct gh_kv {
     float* rope = nullptr;        // [2 (local, global)][max_seq][head_dim/2] (cos, sin) pairs
     int32_t* d_prompt = nullptr;  // [max_seq]
     int32_t* d_ids = nullptr;     // [max_seq]
+    float inv_temp = 0.0f;        // sampler: 1/temperature (0 = greedy)
+    uint64_t seed = 0;            // sampler: Philox key
     gh::StepState* h_st = nullptr;  // pinned staging
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -238,6 +245,8 @@ int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t
 int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
 int launch_synth_normal(float* out, size_t n, uint64_t key, float sigma, hipStream_t s);
 constexpr int GH_ATTN_OP_MAX_NC = 256;  // chunks per kv head of the op-level attention
+int launch_sample_logits(const float* logits, int n, float inv_temp, uint64_t seed, uint64_t counter, float* scratch,
+                         int32_t* token_dev, hipStream_t s);
 
 // repack.cpp
 void repack_q4_0(const uint8_t* raw, int64_t rows, int64_t cols, bool ftz, uint8_t* codes,

@@ -134,6 +134,14 @@ __device__ __forceinline__ float block_sum(float v, float* slot) {
     return (slot[0] + slot[1]) + (slot[2] + slot[3]);
 }
 
+// Max over the 256 threads, one barrier (same slot rules as block_sum).
+__device__ __forceinline__ float block_max(float v, float* slot) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(slot[0], slot[1]), fmaxf(slot[2], slot[3]));
+}
+
 // Order-preserving argmax key: larger value wins, then lower index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
     unsigned b = __float_as_uint(v);
@@ -752,15 +760,27 @@ struct EpiLogits {
     int V;
     unsigned long long* cand;
     StepState* st;
+    float* bm;  // per-workgroup max logit (written when sampling)
+    float* bs;  // per-workgroup sum of exp((l - max) / T)
     __device__ void operator()(const MvLds& L, int rt, int row, int, bool valid, float y) const {
+        const bool in = valid && row < V;
         unsigned long long key = 0ull;
-        if (valid && row < V) {
+        if (in) {
             if (logits) logits[row] = y;
             key = argmax_key(y, row);
             if (isnan(y)) atomicOr(&st->nan_flag, 1);
         }
         const unsigned long long b = block_max_key(key, (unsigned long long*)(L.misc + 32));
         if (threadIdx.x == 0) cand[rt] = b;
+        const float inv_t = st->inv_temp;
+        if (inv_t > 0.0f) {  // temperature sampling: softmax statistics of this workgroup's rows
+            const float mb = block_max(in ? y : -INFINITY, L.misc + 16);
+            const float sb = block_sum(in ? expf((y - mb) * inv_t) : 0.0f, L.misc + 20);
+            if (threadIdx.x == 0) {
+                bm[rt] = mb;
+                bs[rt] = sb;
+            }
+        }
     }
 };
 
@@ -1256,14 +1276,119 @@ __global__ __launch_bounds__(NT) void k_attn_combine(const float* part, int nc, 
 // ------------------------------------------------------------------
 // step epilogue: greedy token from the per-tile keys, next token, position
 // ------------------------------------------------------------------
+// Philox4x32-10 counter-based generator (Salmon, Moraes, Dror, Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3", SC'11): 10 rounds of the
+// 4x32 round function with the published multipliers and Weyl key bumps.
+struct PhiloxOut {
+    uint32_t x, y, z, w;
+};
+__host__ __device__ inline PhiloxOut philox4x32_10(PhiloxOut c, uint32_t k0, uint32_t k1) {
+    for (int r = 0; r < 10; ++r) {
+        if (r) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c.z;
+        c = PhiloxOut{(uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c.w ^ k1, (uint32_t)p0};
+    }
+    return c;
+}
+// u in [0, 1) from Philox(counter = (lo, hi, 0, 0), key = seed): the top 24
+// bits of the first output word.
+__host__ __device__ inline float philox_uniform(uint64_t seed, uint64_t counter) {
+    const PhiloxOut o = philox4x32_10(PhiloxOut{(uint32_t)counter, (uint32_t)(counter >> 32), 0u, 0u}, (uint32_t)seed,
+                                      (uint32_t)(seed >> 32));
+    return (float)(o.x >> 8) * (1.0f / 16777216.0f);
+}
+
+// Categorical draw from softmax(l / T) over n logits given per-block
+// statistics (block b = rows [b*R, b*R+R): max bm[b], sum bs[b] of
+// exp((l - bm[b]) / T)):  M = max bm, W_b = bs[b] exp((bm[b] - M) / T),
+// target = u * sum W; the block whose running sum of W passes the target,
+// then the row whose running sum of exp((l - M) / T) inside it passes the
+// remainder.  Called by all NT threads; returns the row in every thread.
+__device__ int sample_select(const float* bm, const float* bs, int nb, int R, const float* logits, int n, float inv_t,
+                             float u) {
+    __shared__ float part[NT];
+    __shared__ float slot[8];
+    __shared__ int chosen;
+    const int tid = threadIdx.x;
+    float m = -INFINITY;
+    for (int b = tid; b < nb; b += NT) m = fmaxf(m, bm[b]);
+    const float M = block_max(m, slot);
+    const int per = (nb + NT - 1) / NT, b0 = min(nb, tid * per), b1 = min(nb, b0 + per);
+    float w = 0.0f;
+    for (int b = b0; b < b1; ++b) w += bs[b] * expf((bm[b] - M) * inv_t);
+    part[tid] = w;
+    __syncthreads();
+    if (tid == 0) {
+        float z = 0.0f;
+        for (int t = 0; t < NT; ++t) z += part[t];
+        float target = u * z, acc = 0.0f;
+        int t = 0, last_t = -1;
+        for (; t < NT; ++t) {
+            if (part[t] > 0.0f) last_t = t;
+            if (acc + part[t] > target && part[t] > 0.0f) break;
+            acc += part[t];
+        }
+        if (t == NT) {  // rounding: the target landed past the total
+            t = last_t;
+            acc = z - part[t];
+        }
+        target -= acc;
+        const int c0 = min(nb, t * per), c1 = min(nb, c0 + per);
+        int bsel = -1, last_b = -1;
+        float acc_b = 0.0f;
+        for (int b = c0; b < c1; ++b) {
+            const float wb = bs[b] * expf((bm[b] - M) * inv_t);
+            if (wb > 0.0f) last_b = b;
+            if (acc_b + wb > target && wb > 0.0f) {
+                bsel = b;
+                break;
+            }
+            acc_b += wb;
+        }
+        if (bsel < 0) {
+            bsel = last_b;
+            acc_b = 0.0f;
+            for (int b = c0; b < bsel; ++b) acc_b += bs[b] * expf((bm[b] - M) * inv_t);
+        }
+        target -= acc_b;
+        const int r0 = bsel * R, r1 = min(n, r0 + R);
+        int row = -1, last_r = r0;
+        float acc_r = 0.0f;
+        for (int r = r0; r < r1; ++r) {
+            const float wr = expf((logits[r] - M) * inv_t);
+            if (wr > 0.0f) last_r = r;
+            if (acc_r + wr > target && wr > 0.0f) {
+                row = r;
+                break;
+            }
+            acc_r += wr;
+        }
+        chosen = row >= 0 ? row : last_r;
+    }
+    __syncthreads();
+    return chosen;
+}
+
 __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, const unsigned long long* cand, int n_cand,
-                                                    const int32_t* prompt, int32_t* ids) {
+                                                    const float* bm, const float* bs, int rows_per_cand,
+                                                    const float* logits, int V, const int32_t* prompt, int32_t* ids) {
     __shared__ unsigned long long slot[4];
-    unsigned long long best = 0ull;
-    for (int i = threadIdx.x; i < n_cand; i += NT) best = umax64(best, cand[i]);
-    best = block_max_key(best, slot);
+    const float inv_t = st->inv_temp;
+    int tok;
+    if (inv_t > 0.0f) {  // temperature sampling with a Philox draw keyed by the seed, counter = position
+        const uint64_t seed = ((uint64_t)st->seed_hi << 32) | st->seed_lo;
+        tok = sample_select(bm, bs, n_cand, rows_per_cand, logits, V, inv_t, philox_uniform(seed, (uint64_t)pos));
+    } else {  // greedy: first maximum (sampleGreedy, examples/BenchmarkKVCache.hs:223-224)
+        unsigned long long best = 0ull;
+        for (int i = threadIdx.x; i < n_cand; i += NT) best = umax64(best, cand[i]);
+        best = block_max_key(best, slot);
+        tok = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFull));
+    }
     if (threadIdx.x != 0) return;
-    const int tok = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFull));
     st->last = tok;
     const int rel = pos + 1 - st->start;
     int next = tok;
@@ -1419,12 +1544,13 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     // LM head (tied embedding) + per-tile argmax keys
     {
         ProPlain pro{m->xn_final};
-        EpiLogits epi{m->logits, c.vocab, m->lm_cand, kv->st};
+        EpiLogits epi{m->logits, c.vocab, m->lm_cand, kv->st, m->lm_m, m->lm_s};
         GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(m->embd), m->embd, m->plm, pro, epi, 0));
     }
     return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
-                          (const unsigned long long*)m->lm_cand, m->plm.row_tiles(m->embd.tiles), (const int32_t*)kv->d_prompt,
-                          kv->d_ids);
+                          (const unsigned long long*)m->lm_cand, m->plm.row_tiles(m->embd.tiles), (const float*)m->lm_m,
+                          (const float*)m->lm_s, 64 * m->plm.rl, (const float*)m->logits, c.vocab,
+                          (const int32_t*)kv->d_prompt, kv->d_ids);
 }
 
 // ------------------------------------------------------------------
@@ -1565,6 +1691,36 @@ int launch_synth_normal(float* out, size_t n, uint64_t key, float sigma, hipStre
     if (n == 0) return GH_OK;
     const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL(k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, s, out, n, key, sigma);
+    GH_HIP(hipGetLastError());
+    return GH_OK;
+}
+
+// Op-level sampling: per-64-row-block softmax statistics, then the draw.
+__global__ __launch_bounds__(64) void k_sample_blocks(const float* logits, int n, float inv_t, float* bm, float* bs) {
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    const bool in = r < n;
+    const float y = in ? logits[r] : -INFINITY;
+    const float m = wave_max(y);
+    const float s = wave_sum(in ? expf((y - m) * inv_t) : 0.0f);
+    if (threadIdx.x == 0) {
+        bm[blockIdx.x] = m;
+        bs[blockIdx.x] = s;
+    }
+}
+
+__global__ __launch_bounds__(NT) void k_sample_select(const float* bm, const float* bs, int nb, const float* logits, int n,
+                                                      float inv_t, uint64_t seed, uint64_t counter, int32_t* token) {
+    const int t = sample_select(bm, bs, nb, 64, logits, n, inv_t, philox_uniform(seed, counter));
+    if (threadIdx.x == 0) *token = t;
+}
+
+int launch_sample_logits(const float* logits, int n, float inv_t, uint64_t seed, uint64_t counter, float* scratch,
+                         int32_t* token, hipStream_t s) {
+    if (!(inv_t > 0.0f)) return set_error(GH_ERR_INVALID, "sampling needs a temperature > 0");
+    const int nb = (n + 63) / 64;
+    hipLaunchKernelGGL(k_sample_blocks, dim3(nb), dim3(64), 0, s, logits, n, inv_t, scratch, scratch + nb);
+    hipLaunchKernelGGL(k_sample_select, dim3(1), dim3(NT), 0, s, (const float*)scratch, (const float*)(scratch + nb), nb,
+                       logits, n, inv_t, seed, counter, token);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }

@@ -190,6 +190,8 @@ int ensure_scratch(gh_model* m) {
     GH_CHECK(dev_alloc(m, &m->layer_out, (size_t)c.n_layers * c.hidden));
     GH_CHECK(dev_alloc(m, &m->xn_final, c.hidden));
     GH_CHECK(dev_alloc(m, &m->lm_cand, (size_t)m->plm.row_tiles(m->embd.tiles)));
+    GH_CHECK(dev_alloc(m, &m->lm_m, (size_t)m->plm.row_tiles(m->embd.tiles)));
+    GH_CHECK(dev_alloc(m, &m->lm_s, (size_t)m->plm.row_tiles(m->embd.tiles)));
     return GH_OK;
 }
 
@@ -255,6 +257,10 @@ int put_state(gh_kv* kv, int pos, int token, int start, int n_prompt, int gen_ca
     h->nan_flag = 0;
     h->gen_count = 0;
     h->gen_cap = gen_cap;
+    h->inv_temp = kv->inv_temp;
+    h->seed_lo = (uint32_t)kv->seed;
+    h->seed_hi = (uint32_t)(kv->seed >> 32);
+    h->pad = 0;
     GH_HIP(hipMemcpyAsync(kv->st, h, offsetof(StepState, keys), hipMemcpyHostToDevice, kv->m->ctx->stream));
     return GH_OK;
 }
@@ -585,6 +591,27 @@ extern "C" int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, f
     return GH_OK;
 }
 
+extern "C" int gh_sample_logits(gh_ctx* ctx, const float* logits, int n, float temperature, uint64_t seed,
+                                uint64_t counter, int32_t* token_out) {
+    OP_ENTER(ctx);
+    if (!logits || !token_out || n <= 0) return set_error(GH_ERR_INVALID, "gh_sample_logits: bad arguments");
+    if (!(temperature >= 0.0f) || std::isinf(temperature))
+        return set_error(GH_ERR_INVALID, "temperature must be finite and >= 0");
+    if (temperature == 0.0f) return gh_argmax(ctx, logits, n, token_out);
+    const int nblk = (n + 63) / 64;
+    void* scratch = nullptr;
+    GH_CHECK(ctx_scratch(ctx, sizeof(float) * (2 * (size_t)nblk + 4), &scratch));
+    float* sc = (float*)scratch;
+    int32_t* tok_dev = (int32_t*)(sc + 2 * (size_t)nblk);
+    GH_CHECK(launch_sample_logits(logits, n, temperature > 0.0f ? 1.0f / temperature : 0.0f, seed, counter, sc, tok_dev,
+                                  ctx->stream));
+    int32_t tok = -1;
+    GH_HIP(hipMemcpyAsync(&tok, tok_dev, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+    GH_CHECK(op_sync(ctx));
+    *token_out = tok;
+    return GH_OK;
+}
+
 extern "C" int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx) {
     OP_ENTER(ctx);
     if (!v || !idx || n <= 0) return set_error(GH_ERR_INVALID, "gh_argmax: bad arguments");
@@ -861,6 +888,15 @@ extern "C" int gh_kv_reset(gh_kv* kv) {
 extern "C" int gh_kv_length(gh_kv* kv, int32_t* len) {
     if (!kv || !len) return set_error(GH_ERR_INVALID, "null argument");
     *len = kv->len;
+    return GH_OK;
+}
+
+extern "C" int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed) {
+    if (!kv) return set_error(GH_ERR_INVALID, "null kv");
+    if (!(temperature >= 0.0f) || std::isinf(temperature))
+        return set_error(GH_ERR_INVALID, "temperature must be finite and >= 0");
+    kv->inv_temp = temperature > 0.0f ? 1.0f / temperature : 0.0f;
+    kv->seed = seed;
     return GH_OK;
 }
 

@@ -30,7 +30,7 @@ GemmaConfig = GhConfig
 __all__ = [
     "GemmaConfig", "GemmaHipError", "Context", "DeviceBuffer", "Q4Tensor", "GemmaModel", "KVCache",
     "preset", "runLinearQ4", "runGemmaInferenceCached", "runGemmaInferenceCachedWithLayer0",
-    "generate", "bench_decode", "profile_steps", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
+    "generate", "bench_decode", "profile_steps", "sample_logits", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
     "tensor_list", "synth_tensors", "device_count", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q4_0",
     "MODE_GEMMA3", "MODE_REF", "FLAG_QK_NORM", "FLAG_POST_ATTN_NORM", "FLAG_POST_FFN_NORM",
     "FLAG_ZERO_CENTERED", "FLAG_IEEE_SCALES",
@@ -245,6 +245,19 @@ def attention_decode(ctx: Context, q, k_cache, v_cache, nq: int, nkv: int, head_
             b.free()
 
 
+def sample_logits(ctx: Context, logits, temperature: float, seed: int, counter: int) -> int:
+    """Draw from softmax(logits / T) with Philox4x32-10 (key seed, counter);
+    temperature 0 is the argmax (gh_sample_logits)."""
+    lb = _dev(ctx, logits)
+    t = C.c_int32()
+    try:
+        check(lib().gh_sample_logits(ctx.h, lb.ptr, len(logits), float(temperature), int(seed), int(counter),
+                                     C.byref(t)))
+        return t.value
+    finally:
+        lb.free()
+
+
 def gelu_mul(ctx: Context, g, u) -> np.ndarray:
     gb, ub, hb = _dev(ctx, g), _dev(ctx, u), DeviceBuffer(ctx, 4 * len(g))
     check(lib().gh_gelu_mul(ctx.h, gb.ptr, ub.ptr, len(g), hb.ptr))
@@ -387,6 +400,12 @@ class KVCache:
         """Fill positions [0, n_pos) with seeded N(0, sigma) K/V (a stand-in
         for a prefilled context; gh_kv_synth) and set the length to n_pos."""
         check(lib().gh_kv_synth(self.h, seed, n_pos, sigma))
+
+    def set_sampling(self, temperature: float, seed: int = 0) -> None:
+        """Next-token rule of this cache's steps: temperature 0 = greedy
+        (sampleToken, app/Main.hs:488-507); > 0 = draw from softmax(l / T)
+        with Philox keyed by seed, counter = position (gh_kv_set_sampling)."""
+        check(lib().gh_kv_set_sampling(self.h, float(temperature), int(seed)))
 
     def reset(self) -> None:
         check(lib().gh_kv_reset(self.h))

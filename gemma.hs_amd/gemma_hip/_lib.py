@@ -103,6 +103,8 @@ SIGNATURES = {
     "gh_timer_start": (C.c_int, [_P]),
     "gh_timer_stop": (C.c_int, [_P, C.POINTER(C.c_float)]),
     "gh_kv_synth": (C.c_int, [_P, C.c_uint64, C.c_int32, C.c_float]),
+    "gh_kv_set_sampling": (C.c_int, [_P, C.c_float, C.c_uint64]),
+    "gh_sample_logits": (C.c_int, [_P, _P, C.c_int, C.c_float, C.c_uint64, C.c_uint64, _I32]),
     "gh_time_kernel": (C.c_int, [_P, _P, C.c_char_p, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double), _I32]),
     "gh_synth_f32": (C.c_int, [C.c_uint64, C.c_char_p, C.c_float, _P, C.c_size_t]),
     "gh_synth_q4_0": (C.c_int, [C.c_uint64, C.c_char_p, C.c_float, C.c_int64, C.c_int64, _P]),

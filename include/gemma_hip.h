@@ -133,6 +133,12 @@ int gh_attention_decode(gh_ctx* ctx, const float* q, const float* k_cache, const
 int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, float* h);
 /* sampleToken / sampleWithTemperature, app/Main.hs:488-507 (first max) */
 int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx_out);
+/* Op-level draw from softmax(logits[n] / temperature) with Philox4x32-10
+ * (key = seed, counter = counter); temperature 0 is gh_argmax.  Same
+ * device code as the step's sampler. */
+int gh_sample_logits(gh_ctx* ctx, const float* logits, int n, float temperature, uint64_t seed, uint64_t counter,
+                     int32_t* token_out);
+
 
 /* ================================================================
  * Model: replaces GemmaConfig / loadGemmaModel / loadGemmaModelFromGGUF
@@ -187,6 +193,12 @@ int gh_kv_length(gh_kv* kv, int32_t* len_out);
  * (counter-based generator on the device) and set the cache length to
  * n_pos, standing in for a prefilled context. */
 int gh_kv_synth(gh_kv* kv, uint64_t seed, int32_t n_pos, float sigma);
+/* Sampling of the next token for this cache's steps: temperature 0 is
+ * greedy (the reference's sampleToken / sampleWithTemperature, which is an
+ * argmax at any temperature: app/Main.hs:488-507); temperature > 0 draws
+ * from softmax(logits / T) with Philox4x32-10 keyed by `seed`, counter =
+ * the step's position, so a generation is reproducible. */
+int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed);
 
 /* runGemmaInferenceCached (src/Gemma/Model.hs:1313-1437) and its layer-0
  * variant runGemmaInferenceCachedWithLayer0 (src/Gemma/Model.hs:1441):

@@ -27,6 +27,13 @@
  *   orc_argmax                          : numpy.argmax (first max) -- pinned.
  *   orc_softcap                         : parity unpinned (the reference's
  *       runMatmulQ4_0DSL body is absent; Gemma-2 form cap*tanh(y/cap)).
+ *   orc_philox4x32_10                   : the published Random123
+ *       known-answer vectors for philox4x32-10 -- pinned.
+ *   orc_sample                          : inversion sampling; pinned by the
+ *       closed forms of equal logits (index = floor(u n)) and of a single
+ *       dominant logit, and by frequencies against softmax on small n.
+ *       There is no reference counterpart: the reference's temperature
+ *       path is an argmax (app/Main.hs:505-507).
  *   orc_step / orc_generate             : composition of the above; checked
  *       against an independent float64 numpy restatement in the tests.
  */
@@ -533,4 +540,59 @@ int orc_generate(orc_model* m, const int32_t* prompt, int n_prompt, int n_gen, i
     }
     free(lg);
     return rc;
+}
+
+/* Philox4x32-10 (J. Salmon, M. Moraes, R. Dror, D. Shaw, "Parallel random
+ * numbers: as easy as 1, 2, 3", SC'11): ten rounds of
+ *   (c0..c3) -> (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0))
+ * with the key bumped by the Weyl constants between rounds. */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; ++r) {
+        if (r) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1, n3 = (uint32_t)p0;
+        c0 = n0;
+        c1 = n1;
+        c2 = n2;
+        c3 = n3;
+    }
+    out[0] = c0;
+    out[1] = c1;
+    out[2] = c2;
+    out[3] = c3;
+}
+
+float orc_philox_uniform(uint64_t seed, uint64_t counter) {
+    const uint32_t ctr[4] = {(uint32_t)counter, (uint32_t)(counter >> 32), 0u, 0u};
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t o[4];
+    orc_philox4x32_10(ctr, key, o);
+    return (float)(o[0] >> 8) * (1.0f / 16777216.0f);
+}
+
+int32_t orc_sample(const float* logits, int n, float temperature, float u, double* margin_out) {
+    double m = -INFINITY;
+    for (int i = 0; i < n; ++i)
+        if (logits[i] > m) m = logits[i];
+    double z = 0.0;
+    for (int i = 0; i < n; ++i) z += exp(((double)logits[i] - m) / temperature);
+    const double target = (double)u * z;
+    double acc = 0.0, margin = INFINITY;
+    int32_t pick = -1, last = 0;
+    for (int i = 0; i < n; ++i) {
+        const double w = exp(((double)logits[i] - m) / temperature);
+        if (w > 0.0) last = i;
+        if (fabs(acc - target) < margin) margin = fabs(acc - target);
+        if (pick < 0 && acc + w > target && w > 0.0) pick = i;
+        acc += w;
+    }
+    if (fabs(acc - target) < margin) margin = fabs(acc - target);
+    if (margin_out) *margin_out = margin / z;
+    return pick >= 0 ? pick : last;
 }

@@ -65,6 +65,15 @@ float orc_gelu_tanh(float x);
 void orc_geglu(const float* g, const float* u, int n, float* h);
 int32_t orc_argmax(const float* v, int n);
 void orc_softcap(float* y, int n, float cap);
+/* Philox4x32-10 (Salmon et al., SC'11) and the sampler's uniform: top 24
+ * bits of the first output word for counter (lo, hi, 0, 0), key = seed. */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+float orc_philox_uniform(uint64_t seed, uint64_t counter);
+/* Draw from softmax(logits / temperature) by inversion of u in double
+ * precision: the first index whose running sum of exp((l - max) / T)
+ * exceeds u * total.  margin_out (may be NULL): distance of u * total to
+ * the nearest running-sum boundary, relative to the total. */
+int32_t orc_sample(const float* logits, int n, float temperature, float u, double* margin_out);
 
 /* ---- whole model ---- */
 typedef struct orc_model orc_model;

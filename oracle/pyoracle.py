@@ -51,6 +51,9 @@ _SIG = {
     "orc_step": (C.c_int, [_P, C.c_int32, C.c_int32, _P, _P]),
     "orc_generate": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P]),
     "orc_set_threads": (None, [C.c_int]),
+    "orc_philox4x32_10": (None, [_P, _P, _P]),
+    "orc_philox_uniform": (C.c_float, [C.c_uint64, C.c_uint64]),
+    "orc_sample": (C.c_int32, [_P, C.c_int, C.c_float, C.c_float, C.POINTER(C.c_double)]),
 }
 
 _lib = None
@@ -226,3 +229,24 @@ class OracleModel:
             self.close()
         except Exception:
             pass
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.empty(4, dtype=np.uint32)
+    lib().orc_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def philox_uniform(seed: int, counter: int) -> float:
+    return float(lib().orc_philox_uniform(seed, counter))
+
+
+def sample(logits, temperature: float, u: float):
+    """(index, margin): inversion draw of u from softmax(logits / T); margin
+    = distance of u * total to the nearest cumulative boundary / total."""
+    x = f32(logits)
+    m = C.c_double()
+    i = lib().orc_sample(_p(x), len(x), temperature, u, C.byref(m))
+    return int(i), m.value

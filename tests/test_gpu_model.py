@@ -227,3 +227,37 @@ def test_kv_synth_prefill_and_timer(ctx):
     ctx.timer_start()
     gh.generate(m, kv, [5], 4)
     assert ctx.timer_stop() > 0.0
+
+
+def test_temperature_sampling_in_the_step(ctx):
+    """gh_kv_set_sampling: temperature 0 keeps the greedy ids; T > 0 draws
+    each step's token from softmax(logits / T) with Philox(seed, counter =
+    position) -- checked against the oracle's draw on the step's own logits
+    -- and the same seed reproduces the same generation."""
+    cfg = gh.preset("tiny")
+    m = _gpu_model(ctx, cfg, 7, True)
+    prompt = gh.synth_tokens(3, "prompt", 6, cfg.vocab)
+    kv = gh.KVCache(m, 64)
+    greedy = gh.generate(m, kv, prompt, 10)
+    kv = gh.KVCache(m, 64)
+    kv.set_sampling(0.0, 5)
+    np.testing.assert_array_equal(gh.generate(m, kv, prompt, 10), greedy)
+    T, seed = 1.3, 1234
+    runs = []
+    for _ in range(2):
+        kv = gh.KVCache(m, 64)
+        kv.set_sampling(T, seed)
+        runs.append(gh.generate(m, kv, prompt, 12))
+    np.testing.assert_array_equal(runs[0], runs[1])
+    assert not np.array_equal(runs[0], greedy[:12] if len(greedy) >= 12 else runs[0] + 1)
+    kv = gh.KVCache(m, 64)
+    kv.set_sampling(T, seed)
+    toks = list(prompt)
+    for pos in range(len(prompt) + 8):
+        logits, _, nxt = gh.runGemmaInferenceCached(m, int(toks[pos]), kv)
+        want, margin = orc.sample(logits, T, orc.philox_uniform(seed, pos))
+        assert nxt == want or margin < 1e-4, (pos, nxt, want, margin)
+        if pos >= len(prompt) - 1:
+            toks.append(nxt)
+    with pytest.raises(gh.GemmaHipError):
+        kv.set_sampling(-1.0, 0)

@@ -176,3 +176,22 @@ def test_capture_replay_matches_eager_calls(ctx):
     for b in (q, kv, o):
         b.free()
     c2.close()
+
+
+def test_sample_logits_matches_oracle(ctx):
+    """Device Philox + two-level inversion against the oracle: equal logits
+    give floor(u n) exactly (pins the device uniform); random logits give
+    the oracle's draw except where u * total sits within 1e-4 of a boundary
+    (float vs double running sums); temperature 0 is the argmax."""
+    n = 1000
+    for c in range(20):
+        u = orc.philox_uniform(11, c)
+        assert gh.sample_logits(ctx, np.zeros(n, np.float32), 0.9, 11, c) == int(np.floor(u * n))
+    rng = np.random.default_rng(2)
+    for n, T in ((262144, 1.0), (5000, 0.3), (130, 2.0)):
+        logits = (3 * rng.normal(size=n)).astype(np.float32)
+        for c in range(10):
+            got = gh.sample_logits(ctx, logits, T, 99, c)
+            want, margin = orc.sample(logits, T, orc.philox_uniform(99, c))
+            assert got == want or margin < 1e-4, (n, T, c, got, want, margin)
+        assert gh.sample_logits(ctx, logits, 0.0, 99, 0) == int(np.argmax(logits))

@@ -219,6 +219,38 @@ def test_argmax_first_maximum():
     assert orc.argmax(w) == int(np.argmax(w))
 
 
+def test_philox_known_answer_vectors():
+    """Random123's published philox4x32-10 known-answer vectors."""
+    kat = [((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+           ((0xffffffff,) * 4, (0xffffffff,) * 2, (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+           ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+            (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1))]
+    for ctr, key, want in kat:
+        assert tuple(int(v) for v in orc.philox4x32_10(ctr, key)) == want
+    u = [orc.philox_uniform(7, c) for c in range(2000)]
+    assert all(0.0 <= x < 1.0 for x in u)
+    assert abs(np.mean(u) - 0.5) < 0.02 and abs(np.var(u) - 1 / 12) < 0.01
+
+
+def test_sampler_closed_forms_and_frequencies():
+    """Equal logits: index floor(u n); one dominant logit: always it; small
+    vocabulary: empirical frequencies match softmax(l / T)."""
+    n = 37
+    for u in (0.0, 0.2, 0.5, 0.999):
+        assert orc.sample(np.zeros(n, np.float32), 0.7, u)[0] == int(np.floor(u * n))
+    l = np.full(50, -40.0, np.float32)
+    l[13] = 40.0
+    assert all(orc.sample(l, 1.0, u)[0] == 13 for u in (1e-6, 0.5, 0.9999))
+    rng = np.random.default_rng(1)
+    logits = rng.normal(size=8).astype(np.float32)
+    T = 0.8
+    p = np.exp(logits / T - np.max(logits / T))
+    p /= p.sum()
+    draws = [orc.sample(logits, T, orc.philox_uniform(3, c))[0] for c in range(20000)]
+    freq = np.bincount(draws, minlength=8) / len(draws)
+    assert np.max(np.abs(freq - p)) < 0.015
+
+
 def test_softcap_form():
     y = np.array([0.0, 10.0, -100.0, 1000.0], np.float32)
     np.testing.assert_allclose(orc.softcap(y, 30.0), 30.0 * np.tanh(y.astype(np.float64) / 30.0), rtol=1e-6)
