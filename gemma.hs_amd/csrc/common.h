@@ -72,7 +72,7 @@ struct StepState {
     int32_t gen_cap;    // capacity of the ids buffer
     float inv_temp;     // 1/temperature; 0 = greedy
     uint32_t seed_lo, seed_hi;  // Philox key of the sampler
-    int32_t pad;
+    int32_t xchg_err;   // persistent step: an exchange wait timed out
     unsigned long long keys[2];  // argmax keys, slot pos & 1
 };
 
@@ -195,6 +195,18 @@ struct gh_model {
     bool has_embd = false, has_out_norm = false;
     std::vector<uint32_t> present;  // per layer bitmask of tensor kinds
     std::vector<gh_kv*> kvs;
+    // persistent step (GH_PERSISTENT=1): exchange words, launch counter, grid
+    int persistent = 0;
+    uint64_t* w_qkv = nullptr;
+    uint64_t* w_attn = nullptr;
+    uint64_t* w_o = nullptr;
+    uint64_t* w_gu = nullptr;
+    uint64_t* w_down = nullptr;
+    uint64_t* w_x = nullptr;
+    uint64_t* w_x1 = nullptr;
+    uint64_t* w_xn = nullptr;
+    uint32_t p_tick = 0;
+    int p_grid = 0;
 };
 
 struct gh_kv {
@@ -214,6 +226,7 @@ struct gh_kv {
     hipGraphExec_t graph_exec = nullptr;
     std::vector<std::unique_ptr<gh::NodeArgsBase>> graph_args;
     std::vector<gh::PosPatch> patches;
+    void* d_players = nullptr;  // persistent step: per-layer pointer table
 };
 
 namespace gh {
@@ -232,6 +245,8 @@ struct Profiler {
 
 // kernels.hip: one decode step at position `pos` (patched per replay in graphs)
 int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos);
+int persistent_supported(const gh_model* m);
+int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos);
 int launch_q4_dequant(const DMat& w, float* out, hipStream_t s);
 int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* part, float* y,
                         int softcap, float cap, hipStream_t s);

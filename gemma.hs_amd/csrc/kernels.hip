@@ -356,14 +356,27 @@ inline size_t mv_lds_bytes(int fmt, int per_split, int tmp_floats) {
     return f * sizeof(float);
 }
 
-// One workgroup = 64*RL rows (one or both halves of a 128-row tile) x one
-// column split.  Rows: lane (RL 1) or lane and lane+64 (RL 2) of the
-// workgroup's rows; the four waves split the split's column blocks.
-template <int FMT, int KBW, int RL, class Pro, class Epi>
-__global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) {
-    extern __shared__ float lds[];
+// LDS carve-up of one matvec work item (floats from `lds`).
+template <int FMT>
+__device__ __forceinline__ MvLds mv_lds(float* lds, int per_split) {
     constexpr int BK = Blk<FMT>::BK;
-    const int rt = blockIdx.x / S, s = blockIdx.x % S;
+    MvLds L;
+    L.red = lds;
+    L.misc = lds + 512;
+    L.xs = lds + 576;
+    L.sxs = L.xs + per_split * BK;
+    L.tmp = L.sxs + ((per_split + 3) & ~3);
+    return L;
+}
+
+// One matvec work item: 64*RL rows (one or both halves of 128-row tile
+// `tile`, starting at row rbase of it) x column split s of S.  Rows: lane
+// (RL 1) or lane and lane+64 (RL 2); the four waves split the split's
+// column blocks.  `rt` is the item's row-tile index for the epilogue.
+template <int FMT, int KBW, int RL, class Pro, class Epi>
+__device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
+                                        const MvLds& L) {
+    constexpr int BK = Blk<FMT>::BK;
     const int tile = RL == 2 ? rt : rt >> 1, rbase = RL == 2 ? 0 : (rt & 1) * 64;
     const int nb = w.nblk;
     const int per_split = (nb + S - 1) / S;
@@ -372,13 +385,6 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int per_wave = (nk + 3) >> 2;
     const int kw0 = min(kb1, kb0 + wave * per_wave), kw1 = min(kb1, kw0 + per_wave);
-
-    MvLds L;
-    L.red = lds;
-    L.misc = lds + 512;
-    L.xs = lds + 576;
-    L.sxs = L.xs + per_split * BK;
-    L.tmp = L.sxs + ((per_split + 3) & ~3);
 
     // 1. the prologue's input loads go out first (they are waited on first),
     // 2. then the weights of the first register batch,
@@ -411,6 +417,14 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
     if (valid) y = (L.red[t] + L.red[TILE_ROWS + t]) + (L.red[2 * TILE_ROWS + t] + L.red[3 * TILE_ROWS + t]);
     epi(L, rt, tile * TILE_ROWS + rbase + t, s, valid, y);
     GH_MARK(5);
+}
+
+// One workgroup per work item: grid = row tiles x S.
+template <int FMT, int KBW, int RL, class Pro, class Epi>
+__global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) {
+    extern __shared__ float lds[];
+    const int per_split = (w.nblk + S - 1) / S;
+    mv_item<FMT, KBW, RL>(w, blockIdx.x / S, blockIdx.x % S, S, pro, epi, mv_lds<FMT>(lds, per_split));
 }
 
 // ------------------------------------------------------------------
@@ -733,6 +747,232 @@ struct ProGeglu {
 };
 
 // ------------------------------------------------------------------
+// word exchange of the persistent step: a phase publishes its outputs as
+// 64-bit words (epoch << 32 | float bits) with relaxed agent-scope stores
+// (written through to memory); a consumer polls each word with relaxed
+// agent-scope loads (L2 bypassed) until its epoch matches.  A word is
+// single-copy atomic, so it validates itself: no fences are needed.  Every
+// wait is bounded; on timeout the step's error flag is set and all later
+// waits give up at once, so the kernel always finishes.
+// ------------------------------------------------------------------
+constexpr int XCHG_SPIN = 1 << 18;
+
+__device__ __forceinline__ void st_word(uint64_t* p, uint32_t epoch, float v) {
+    __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __noinline__ float poll_word_slow(const uint64_t* p, uint32_t epoch, int* err) {
+    for (int spin = 0; spin < XCHG_SPIN; ++spin) {
+        const uint64_t v = ld_word(p);
+        if ((uint32_t)(v >> 32) == epoch) return __uint_as_float((uint32_t)v);
+        if ((spin & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return 0.0f;
+    }
+    __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return 0.0f;
+}
+
+// A source of float4 groups published as words.
+struct WSrc {
+    const uint64_t* w;
+    uint32_t epoch;
+    int* err;
+    __device__ float g1(size_t i) const {
+        const uint64_t v = ld_word(w + i);
+        return (uint32_t)(v >> 32) == epoch ? __uint_as_float((uint32_t)v) : poll_word_slow(w + i, epoch, err);
+    }
+    // elements i .. i+3
+    __device__ float4 g4e(size_t i) const {
+        const uint64_t* p = w + i;
+        const uint64_t a = ld_word(p), b = ld_word(p + 1), c = ld_word(p + 2), d = ld_word(p + 3);
+        float4 r;
+        r.x = (uint32_t)(a >> 32) == epoch ? __uint_as_float((uint32_t)a) : poll_word_slow(p, epoch, err);
+        r.y = (uint32_t)(b >> 32) == epoch ? __uint_as_float((uint32_t)b) : poll_word_slow(p + 1, epoch, err);
+        r.z = (uint32_t)(c >> 32) == epoch ? __uint_as_float((uint32_t)c) : poll_word_slow(p + 2, epoch, err);
+        r.w = (uint32_t)(d >> 32) == epoch ? __uint_as_float((uint32_t)d) : poll_word_slow(p + 3, epoch, err);
+        return r;
+    }
+};
+
+__device__ __forceinline__ void st_word4(uint64_t* p, uint32_t epoch, float4 v) {
+    st_word(p, epoch, v.x);
+    st_word(p + 1, epoch, v.y);
+    st_word(p + 2, epoch, v.z);
+    st_word(p + 3, epoch, v.w);
+}
+
+// Residual stream update + RMSNorm from published words (persistent step):
+//   x = E[token] * sqrt(H)                       (layer 0, src/Gemma/Model.hs:1346-1361)
+//     or base + postnorm(sum_s part_s)           (TBG:305-343, TBG:413-444)
+//   xs = norm(x) with w_norm
+// The item with `publish` set stores x as words (for the next residual
+// update) and, when given, to layer_out_row.  out_norm_words (optional):
+// instead of building a matvec input, publish norm(x) as words (final norm).
+template <int MG>
+struct ProResidW {
+    int from_embedding;
+    DMat embd;
+    const StepState* st;
+    float escale;
+    WSrc base;
+    WSrc part;  // S splits of ld words each
+    int S, ld;
+    const float* w_post;  // nullable
+    const float* w_norm;
+    float eps;
+    int zc, H;
+    int publish;
+    uint64_t* x_out;  // words, epoch x_epoch
+    uint32_t x_epoch;
+    float* layer_out_row;  // nullable
+    struct Regs {};
+    __device__ void load(Regs&, int, int) const {}
+    // x in registers (xv) and LDS tmp; returns rms of x
+    __device__ float build_x(const MvLds& L, float4 (&xv)[MG]) const {
+        const int NG = H >> 2, tid = threadIdx.x;
+        if (from_embedding) {
+            const int tok = min(max(st->token, 0), embd.rows - 1);
+#pragma unroll
+            for (int k = 0; k < MG; ++k) {
+                const int g = tid + k * NT;
+                if (g < NG) {
+                    const float4 e = dq_elem4(embd, tok, 4 * g);
+                    xv[k] = make_float4(e.x * escale, e.y * escale, e.z * escale, e.w * escale);
+                }
+            }
+        } else {
+            float4 dv[MG], bv[MG];
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < MG; ++k) {
+                const int g = tid + k * NT;
+                dv[k] = bv[k] = f4z();
+                if (g < NG) {
+                    bv[k] = base.g4e(4 * (size_t)g);
+                    for (int s = 0; s < S; ++s) dv[k] = dv[k] + part.g4e((size_t)s * ld + 4 * (size_t)g);
+                    ss += dot4(dv[k], dv[k]);
+                }
+            }
+            float rms = 1.0f;
+            if (w_post) rms = sqrtf(block_sum(ss, L.misc) / (float)H + eps);
+#pragma unroll
+            for (int k = 0; k < MG; ++k) {
+                const int g = tid + k * NT;
+                if (g < NG)
+                    xv[k] = bv[k] + (w_post ? norm4(dv[k], rms, ((const float4*)w_post)[g], zc) : dv[k]);
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            if (g < NG) {
+                ((float4*)L.tmp)[g] = xv[k];
+                ss += dot4(xv[k], xv[k]);
+                if (publish) {
+                    if (x_out) st_word4(x_out + 4 * (size_t)g, x_epoch, xv[k]);
+                    if (layer_out_row) ((float4*)layer_out_row)[g] = xv[k];
+                }
+            }
+        }
+        return sqrtf(block_sum(ss, L.misc + 4) / (float)H + eps);  // barrier: tmp complete
+    }
+    template <int FMT>
+    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
+        float4 xv[MG];
+        const float rms = build_x(L, xv);
+        const int ng = n >> 2, tid = threadIdx.x;
+        const float4* t4 = (const float4*)(L.tmp + c0);
+        for (int b = 0; b < ng; b += NT) {
+            const int gi = b + tid;
+            emit_x4<FMT>(L, gi, ng, gi < ng ? norm4(t4[gi], rms, ((const float4*)(w_norm + c0))[gi], zc) : f4z());
+        }
+    }
+};
+
+// O-projection input from published attention chunk states (persistent step).
+struct ProAttnCombineW {
+    WSrc part;  // [nkv][nc][G][HD+2] words
+    int nc, G, HD, n_used;
+    struct Regs {};
+    __device__ void load(Regs&, int, int) const {}
+    template <int FMT>
+    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
+        const int stride = G * (HD + 2), tid = threadIdx.x;
+        const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
+        float* wts = L.tmp;
+        for (int hh = tid >> 6; hh < nh; hh += 4) {
+            const int j = tid & 63, hg = h0 + hh;
+            float mj = -INFINITY, lj = 0.0f;
+            if (j < n_used) {
+                const size_t bj = ((size_t)(hg / G) * nc + j) * stride;
+                mj = part.g1(bj + hg % G);
+                lj = part.g1(bj + G + hg % G);
+            }
+            const float M = wave_max(mj);
+            const float e = j < n_used ? expf(mj - M) : 0.0f;
+            const float den = wave_sum(lj * e);
+            wts[hh * ATTN_MAX_NC + j] = e / den;
+        }
+        __syncthreads();
+        const int ng = n >> 2;
+        for (int b = 0; b < ng; b += NT) {
+            const int gi = b + tid;
+            float4 acc = f4z();
+            if (gi < ng) {
+                const int c = c0 + 4 * gi, h = c / HD, d = c % HD;
+                const size_t pbase = (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
+                const float* wv = wts + (h - h0) * ATTN_MAX_NC;
+                for (int j = 0; j < n_used; ++j) acc = fma4(wv[j], part.g4e(pbase + (size_t)j * stride), acc);
+            }
+            emit_x4<FMT>(L, gi, ng, acc);
+        }
+    }
+};
+
+// Down-projection input from published gate/up outputs (persistent step).
+struct ProGegluW {
+    WSrc gu;  // gate rows [0, up_off), up rows [up_off, ...)
+    int up_off;
+    struct Regs {};
+    __device__ void load(Regs&, int, int) const {}
+    template <int FMT>
+    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
+        const int ng = n >> 2;
+        for (int b = 0; b < ng; b += NT) {
+            const int gi = b + threadIdx.x;
+            float4 h = f4z();
+            if (gi < ng) {
+                const float4 g = gu.g4e(c0 + 4 * (size_t)gi), u = gu.g4e(up_off + c0 + 4 * (size_t)gi);
+                h = make_float4(gelu_tanh(g.x) * u.x, gelu_tanh(g.y) * u.y, gelu_tanh(g.z) * u.z, gelu_tanh(g.w) * u.w);
+            }
+            emit_x4<FMT>(L, gi, ng, h);
+        }
+    }
+};
+
+// Input slice already in LDS from the previous item of the same matrix.
+struct ProKeep {
+    struct Regs {};
+    __device__ void load(Regs&, int, int) const {}
+    template <int FMT>
+    __device__ void finish(const MvLds&, Regs&, int, int) const {}
+};
+
+// Matvec outputs as words (split s at s * ld).
+struct EpiW {
+    uint64_t* w;
+    int ld;
+    uint32_t epoch;
+    __device__ void operator()(const MvLds&, int, int row, int s, bool valid, float y) const {
+        if (valid) st_word(w + (size_t)s * ld + row, epoch, y);
+    }
+};
+
+// ------------------------------------------------------------------
 // epilogues (called by all threads; t < 128 hold row sums)
 // ------------------------------------------------------------------
 struct EpiPartial {
@@ -993,8 +1233,30 @@ __device__ __forceinline__ void wave_head_rope(float* p, const float2* cs) {
 // q/k, appends k/v to the cache (appendKVCacheShader, AttentionGPU.hs:502-534)
 // and uses them for the p == pos row.  The window and the chunking come from
 // the host (AttnArgs::set_pos).
-template <int HD, int G, bool STEP>
-__global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
+// Sources of the QKV vector: the split partials of the QKV matvec, or
+// published words (persistent step).  g4(row) = float4 at fused-QKV row.
+struct QkvPartials {
+    const float* part;
+    int S, ld;
+    __device__ float4 g4(int row) const { return sum_splits4(part, S, ld, row >> 2); }
+};
+struct QkvWords {
+    WSrc w;
+    __device__ float4 g4(int row) const { return w.g4e((size_t)row); }
+};
+// Sinks of the chunk state: plain floats or published words.
+struct AttnOutPlain {
+    float* part;
+    __device__ void put(size_t i, float v) const { part[i] = v; }
+};
+struct AttnOutWords {
+    uint64_t* w;
+    uint32_t epoch;
+    __device__ void put(size_t i, float v) const { st_word(w + i, epoch, v); }
+};
+
+template <int HD, int G, bool STEP, class In, class Out>
+__device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const In& in, const Out& out) {
     constexpr int SUB = ATTN_SUB;
     constexpr int K4 = HD / 32;               // score phase: float4 per lane per position
     static_assert(SUB == 32, "one score round of 8 positions per wave");
@@ -1016,8 +1278,6 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     __shared__ __align__(16) float so[NSLOT][G * HD];
 
     GH_MARK(0);
-    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
-    if (j >= a.n_used) return;  // uniform per workgroup
     const int pos = STEP ? a.pos : -1;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
@@ -1059,7 +1319,7 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
                 const int row = i < G * HD ? a.q_off + g * G * HD + i
                               : i < (G + 1) * HD ? a.k_off + g * HD + (i - G * HD)
                                                  : a.v_off + g * HD + (i - (G + 1) * HD);
-                pv[m] = sum_splits4(a.part_qkv, a.Sa, a.ld_qkv, row >> 2);
+                pv[m] = in.g4(row);
             }
         }
         float wq[NWR], wk[NWR];
@@ -1210,22 +1470,29 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     for (int h = 0; h < G; ++h) *(float4*)&so[slot][h * HD + 4 * dq] = acc[h];
     __syncthreads();
     GH_MARK(5);
-    float* out = a.part + ((size_t)g * a.nc + j) * (G * (HD + 2));
+    const size_t ob = ((size_t)g * a.nc + j) * (G * (HD + 2));
     for (int idx = tid; idx < G * HD; idx += NT) {
         float O = 0.0f;
 #pragma unroll
         for (int s2 = 0; s2 < NSLOT; ++s2) O += so[s2][idx];
-        out[2 * G + idx] = O;
+        out.put(ob + 2 * G + idx, O);
     }
 #pragma unroll
     for (int hi = 0; hi < HPW; ++hi) {
         const int h = wave + 4 * hi;
         if (h < G && lane == 0) {
-            out[h] = mrun[hi];
-            out[G + h] = lrun[hi];
+            out.put(ob + h, mrun[hi]);
+            out.put(ob + G + h, lrun[hi]);
         }
     }
     GH_MARK(6);
+}
+
+template <int HD, int G, bool STEP>
+__global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
+    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
+    if (j >= a.n_used) return;  // uniform per workgroup
+    attn_item<HD, G, STEP>(a, g, j, QkvPartials{a.part_qkv, a.Sa, a.ld_qkv}, AttnOutPlain{a.part});
 }
 
 template <bool STEP>
@@ -1400,6 +1667,363 @@ __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, cons
     }
     st->token = next;
     st->pos = pos + 1;
+}
+
+// ------------------------------------------------------------------
+// persistent step: one cooperative launch per token.  Every workgroup runs
+// the same phase sequence (per layer: QKV, attention, O, gate/up, down;
+// then the final norm and the LM head) and takes the work items of each
+// phase that map to it; phases exchange their outputs as published words
+// (st_word / WSrc), so the only waits are on the data each item needs.
+// Buffer reuse is safe: a phase's buffer is rewritten one layer later,
+// after a dependency chain that passes through every reader of it.
+// ------------------------------------------------------------------
+struct PLayer {
+    DMat qkv, o, gu, down;
+    const float* attn_norm;
+    const float* q_norm;
+    const float* k_norm;
+    const float* post_attn;
+    const float* ffn_norm;
+    const float* post_ffw;
+    float* kc;
+    float* vc;
+    int global;
+    int pad;
+};
+
+struct PArgs {
+    const PLayer* layers;
+    DMat embd;
+    const float* out_norm;
+    StepState* st;
+    int pos;
+    uint32_t tick;  // epoch of layer l = tick * (L + 2) + l + 1; final norm: l = L
+    const float* rope_local;
+    const float* rope_global;
+    uint64_t* w_qkv;
+    uint64_t* w_attn;
+    uint64_t* w_o;
+    uint64_t* w_gu;
+    uint64_t* w_down;
+    uint64_t* w_x;
+    uint64_t* w_x1;
+    uint64_t* w_xn;
+    int L, H, nkv, q_rows_pad, kv_rows_pad, f_pad, S_down, nc;
+    float eps, escale, scale;
+    int zc, use_qk_norm, post_attn_norm, post_ffn_norm, mode, window;
+    int pb[2], pe[2], ch[2], n_used[2];  // attention range at pos: [0] local, [1] global layer
+    float* logits;
+    unsigned long long* cand;
+    float* bm;
+    float* bs;
+    float* layer_out;
+    int V;
+    uint32_t* host_tick;  // host-side launch counter (not used on the device)
+    // position-dependent arguments of one replay: position, a fresh epoch
+    // base, and the attention range of local and global layers
+    void set_pos(int p) {
+        pos = p;
+        tick = ++*host_tick;
+        for (int t = 0; t < 2; ++t) {
+            AttnArgs r{};
+            r.global = t;
+            r.window = window;
+            r.mode = mode;
+            r.nc = nc;
+            r.set_pos(p);
+            pb[t] = r.pb;
+            pe[t] = r.pe;
+            ch[t] = r.ch;
+            n_used[t] = r.n_used;
+        }
+    }
+};
+
+// Final-norm input published once: xs = words of norm(x_L) (LM head).
+struct ProXnW {
+    WSrc xn;
+    struct Regs {};
+    __device__ void load(Regs&, int, int) const {}
+    template <int FMT>
+    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
+        const int ng = n >> 2;
+        for (int b = 0; b < ng; b += NT) {
+            const int gi = b + threadIdx.x;
+            emit_x4<FMT>(L, gi, ng, gi < ng ? xn.g4e(c0 + 4 * (size_t)gi) : f4z());
+        }
+    }
+};
+
+constexpr int P_KBW = 9;
+
+template <int HD, int G, int MG>
+__global__ __launch_bounds__(NT) void k_step_persistent(PArgs a) {
+    extern __shared__ float lds[];
+    const int nwg = gridDim.x, wg = blockIdx.x;
+    int* err = &a.st->xchg_err;
+    int off = 0;  // items of consecutive phases start at consecutive workgroups
+    auto each = [&](int n_items, auto&& f) {
+        for (int i = ((wg - off) % nwg + nwg) % nwg; i < n_items; i += nwg) {
+            __syncthreads();  // LDS of the previous item is free
+            f(i);
+        }
+        off = (off + n_items) % nwg;
+    };
+    const int H = a.H;
+    for (int l = 0; l < a.L; ++l) {
+        const PLayer& P = a.layers[l];
+        const uint32_t e = a.tick * (uint32_t)(a.L + 2) + (uint32_t)l + 1u, ep = e - 1u;
+        // QKV: residual update from the previous layer's down partials, pre-attention norm
+        each(P.qkv.tiles * 2, [&](int rt) {
+            ProResidW<MG> pro;
+            pro.from_embedding = l == 0;
+            pro.embd = a.embd;
+            pro.st = a.st;
+            pro.escale = a.escale;
+            pro.base = WSrc{a.w_x1, ep, err};
+            pro.part = WSrc{a.w_down, ep, err};
+            pro.S = a.S_down;
+            pro.ld = l > 0 ? a.layers[l - 1].down.tiles * TILE_ROWS : 0;
+            pro.w_post = l > 0 && a.post_ffn_norm ? a.layers[l - 1].post_ffw : nullptr;
+            pro.w_norm = P.attn_norm;
+            pro.eps = a.eps;
+            pro.zc = a.zc;
+            pro.H = H;
+            pro.publish = rt == 0;
+            pro.x_out = a.w_x;
+            pro.x_epoch = e;
+            pro.layer_out_row = l > 0 ? a.layer_out + (size_t)(l - 1) * H : nullptr;
+            mv_item<FMT_Q4, P_KBW, 1>(P.qkv, rt, 0, 1, pro, EpiW{a.w_qkv, 0, e}, mv_lds<FMT_Q4>(lds, P.qkv.nblk));
+        });
+        // attention: QK-norm, RoPE, KV append, split-K chunks
+        {
+            const int t = P.global ? 1 : 0;
+            AttnArgs aa{};
+            aa.q_off = 0;
+            aa.k_off = a.q_rows_pad;
+            aa.v_off = a.q_rows_pad + a.kv_rows_pad;
+            aa.q_norm = P.q_norm;
+            aa.k_norm = P.k_norm;
+            aa.use_qk_norm = a.use_qk_norm && P.q_norm && P.k_norm;
+            aa.zc = a.zc;
+            aa.eps = a.eps;
+            aa.rope = (a.mode == GH_MODE_REF || P.global) ? a.rope_global : a.rope_local;
+            aa.pos = a.pos;
+            aa.global = P.global;
+            aa.window = a.window;
+            aa.mode = a.mode;
+            aa.kc = P.kc;
+            aa.vc = P.vc;
+            aa.nkv = a.nkv;
+            aa.scale = a.scale;
+            aa.nc = a.nc;
+            aa.pb = a.pb[t];
+            aa.pe = a.pe[t];
+            aa.ch = a.ch[t];
+            aa.n_used = a.n_used[t];
+            const int nu = aa.n_used;
+            each(a.nkv * nu, [&](int it) {
+                attn_item<HD, G, true>(aa, it / nu, it % nu, QkvWords{WSrc{a.w_qkv, e, err}},
+                                       AttnOutWords{a.w_attn, e});
+            });
+            // O projection: merge of the chunk states
+            each(P.o.tiles * 2, [&](int rt) {
+                ProAttnCombineW pro{WSrc{a.w_attn, e, err}, a.nc, G, HD, nu};
+                mv_item<FMT_Q4, P_KBW, 1>(P.o, rt, 0, 1, pro, EpiW{a.w_o, 0, e}, mv_lds<FMT_Q4>(lds, P.o.nblk));
+            });
+        }
+        // gate/up: post-attention residual update, pre-FFN norm
+        each(P.gu.tiles * 2, [&](int rt) {
+            ProResidW<MG> pro;
+            pro.from_embedding = 0;
+            pro.embd = a.embd;
+            pro.st = a.st;
+            pro.escale = 1.0f;
+            pro.base = WSrc{a.w_x, e, err};
+            pro.part = WSrc{a.w_o, e, err};
+            pro.S = 1;
+            pro.ld = P.o.tiles * TILE_ROWS;
+            pro.w_post = a.post_attn_norm ? P.post_attn : nullptr;
+            pro.w_norm = P.ffn_norm ? P.ffn_norm : P.post_attn;
+            pro.eps = a.eps;
+            pro.zc = a.zc;
+            pro.H = H;
+            pro.publish = rt == 0;
+            pro.x_out = a.w_x1;
+            pro.x_epoch = e;
+            pro.layer_out_row = nullptr;
+            mv_item<FMT_Q4, P_KBW, 1>(P.gu, rt, 0, 1, pro, EpiW{a.w_gu, 0, e}, mv_lds<FMT_Q4>(lds, P.gu.nblk));
+        });
+        // down: GeGLU of its column split
+        const int sd = a.S_down;
+        each(P.down.tiles * 2 * sd, [&](int it) {
+            ProGegluW pro{WSrc{a.w_gu, e, err}, a.f_pad};
+            mv_item<FMT_Q4, P_KBW, 1>(P.down, it / sd, it % sd, sd, pro, EpiW{a.w_down, P.down.tiles * TILE_ROWS, e},
+                                      mv_lds<FMT_Q4>(lds, (P.down.nblk + sd - 1) / sd));
+        });
+    }
+    // final residual + norm, published once
+    const uint32_t eL1 = a.tick * (uint32_t)(a.L + 2) + (uint32_t)a.L, eL = eL1 + 1u;
+    each(1, [&](int) {
+        const PLayer& P = a.layers[a.L - 1];
+        ProResidW<MG> pro;
+        pro.from_embedding = 0;
+        pro.embd = a.embd;
+        pro.st = a.st;
+        pro.escale = 1.0f;
+        pro.base = WSrc{a.w_x1, eL1, err};
+        pro.part = WSrc{a.w_down, eL1, err};
+        pro.S = a.S_down;
+        pro.ld = P.down.tiles * TILE_ROWS;
+        pro.w_post = a.post_ffn_norm ? P.post_ffw : nullptr;
+        pro.w_norm = a.out_norm;
+        pro.eps = a.eps;
+        pro.zc = a.zc;
+        pro.H = H;
+        pro.publish = 1;
+        pro.x_out = nullptr;
+        pro.x_epoch = eL;
+        pro.layer_out_row = a.layer_out + (size_t)(a.L - 1) * H;
+        MvLds L = mv_lds<FMT_F32>(lds, H / 4);
+        float4 xv[MG];
+        const float rms = pro.build_x(L, xv);
+        for (int g = threadIdx.x; g < H / 4; g += NT)
+            st_word4(a.w_xn + 4 * (size_t)g, eL, norm4(((const float4*)L.tmp)[g], rms, ((const float4*)a.out_norm)[g], a.zc));
+    });
+    // LM head (tied embedding): the normed vector is polled by a
+    // workgroup's first item and kept in LDS for its others
+    bool have_x = false;
+    each(a.embd.tiles * 2, [&](int rt) {
+        EpiLogits epi{a.logits, a.V, a.cand, a.st, a.bm, a.bs};
+        const MvLds L = mv_lds<FMT_Q4>(lds, a.embd.nblk);
+        if (!have_x) {
+            mv_item<FMT_Q4, P_KBW, 1>(a.embd, rt, 0, 1, ProXnW{WSrc{a.w_xn, eL, err}}, epi, L);
+            have_x = true;
+        } else {
+            mv_item<FMT_Q4, P_KBW, 1>(a.embd, rt, 0, 1, ProKeep{}, epi, L);
+        }
+    });
+}
+
+// Dynamic LDS of the persistent step (floats): the largest matvec item.
+inline size_t persistent_lds_bytes(const gh_model* m) {
+    const gh_config& c = m->cfg;
+    const LayerDev& L0 = m->layers[0];
+    size_t f = 0;
+    auto item = [&](int per_split, int tmp) { f = std::max(f, (size_t)(576 + per_split * 32 + ((per_split + 3) & ~3) + tmp)); };
+    item(L0.qkv.nblk, c.hidden);
+    item(L0.o.nblk, (c.n_heads + 2) * ATTN_MAX_NC);
+    item(L0.gu.nblk, c.hidden);
+    item((L0.down.nblk + m->pe.S - 1) / m->pe.S, 0);
+    item(m->embd.nblk, 0);
+    // final norm: xs (H) + block-sum pad (H/4) + tmp (H)
+    f = std::max(f, (size_t)(576 + c.hidden + ((c.hidden / 4 + 3) & ~3) + c.hidden));
+    return f * sizeof(float);
+}
+
+// Per-cache table of layer pointers for the persistent step.
+static int persistent_layers(gh_model* m, gh_kv* kv) {
+    if (kv->d_players) return GH_OK;
+    const gh_config& c = m->cfg;
+    const size_t kv_layer = (size_t)kv->max_seq * c.n_kv_heads * c.head_dim;
+    std::vector<PLayer> h(c.n_layers);
+    for (int i = 0; i < c.n_layers; ++i) {
+        const LayerDev& L = m->layers[i];
+        PLayer& p = h[i];
+        p.qkv = L.qkv;
+        p.o = L.o;
+        p.gu = L.gu;
+        p.down = L.down;
+        p.attn_norm = L.attn_norm;
+        p.q_norm = L.q_norm;
+        p.k_norm = L.k_norm;
+        p.post_attn = L.post_attn;
+        p.ffn_norm = L.ffn_norm;
+        p.post_ffw = L.post_ffw;
+        p.kc = kv->k + i * kv_layer;
+        p.vc = kv->v + i * kv_layer;
+        p.global = L.global ? 1 : 0;
+        p.pad = 0;
+    }
+    void* d = nullptr;
+    GH_HIP(hipMalloc(&d, sizeof(PLayer) * h.size()));
+    if (hipMemcpy(d, h.data(), sizeof(PLayer) * h.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        hipFree(d);
+        return set_error(GH_ERR_HIP, "upload of the persistent layer table failed");
+    }
+    kv->d_players = d;
+    return GH_OK;
+}
+
+int persistent_supported(const gh_model* m) {
+    const gh_config& c = m->cfg;
+    const int G = c.n_heads / c.n_kv_heads, MG = (c.hidden / 4 + NT - 1) / NT;
+    if (m->fmt != FMT_Q4) return 0;
+    return (c.head_dim == 32 && G == 4 && MG == 1) || (c.head_dim == 256 && G == 4 && MG == 2) ||
+           (c.head_dim == 256 && G == 2 && (MG == 1 || MG == 3));
+}
+
+// One decode step as the persistent kernel (one workgroup per CU) + the
+// finish kernel, into a sink (graph nodes or stream launches).  The grid
+// is the CU count at one workgroup per CU, so all workgroups are resident;
+// the bounded waits turn anything else into GH_ERR_STATE, not a hang.
+int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
+    const gh_config& c = m->cfg;
+    if (!persistent_supported(m)) return set_error(GH_ERR_INVALID, "persistent step: unsupported shape");
+    GH_CHECK(persistent_layers(m, kv));
+    const int hd = c.head_dim, G = c.n_heads / c.n_kv_heads, H = c.hidden, MG = (H / 4 + NT - 1) / NT;
+    PArgs a{};
+    a.layers = (const PLayer*)kv->d_players;
+    a.embd = m->embd;
+    a.out_norm = m->out_norm;
+    a.st = kv->st;
+    a.rope_local = kv->rope;
+    a.rope_global = kv->rope + (size_t)kv->max_seq * hd;
+    a.w_qkv = m->w_qkv;
+    a.w_attn = m->w_attn;
+    a.w_o = m->w_o;
+    a.w_gu = m->w_gu;
+    a.w_down = m->w_down;
+    a.w_x = m->w_x;
+    a.w_x1 = m->w_x1;
+    a.w_xn = m->w_xn;
+    a.L = c.n_layers;
+    a.H = H;
+    a.nkv = c.n_kv_heads;
+    a.q_rows_pad = m->q_rows_pad;
+    a.kv_rows_pad = m->kv_rows_pad;
+    a.f_pad = m->f_pad;
+    a.S_down = m->pe.S;
+    a.nc = m->attn_nc;
+    a.eps = c.rms_eps;
+    a.escale = sqrtf((float)H);
+    a.scale = 1.0f / sqrtf((float)hd);
+    a.zc = (c.flags & GH_FLAG_ZERO_CENTERED) ? 1 : 0;
+    a.use_qk_norm = (c.flags & GH_FLAG_QK_NORM) ? 1 : 0;
+    a.post_attn_norm = (c.flags & GH_FLAG_POST_ATTN_NORM) ? 1 : 0;
+    a.post_ffn_norm = (c.flags & GH_FLAG_POST_FFN_NORM) ? 1 : 0;
+    a.mode = c.mode;
+    a.window = c.sliding_window;
+    a.logits = m->logits;
+    a.cand = m->lm_cand;
+    a.bm = m->lm_m;
+    a.bs = m->lm_s;
+    a.layer_out = m->layer_out;
+    a.V = c.vocab;
+    a.host_tick = &m->p_tick;
+    a.set_pos(pos);
+    const size_t lds = persistent_lds_bytes(m);
+    const dim3 grid(m->p_grid), block(NT);
+    auto go = [&](void (*fn)(PArgs)) { return sink_launch<0>(sink, "step", 0.0, fn, grid, block, lds, a); };
+    if (hd == 32 && G == 4 && MG == 1) GH_CHECK(go(k_step_persistent<32, 4, 1>));
+    else if (hd == 256 && G == 4 && MG == 2) GH_CHECK(go(k_step_persistent<256, 4, 2>));
+    else if (hd == 256 && G == 2 && MG == 1) GH_CHECK(go(k_step_persistent<256, 2, 1>));
+    else GH_CHECK(go(k_step_persistent<256, 2, 3>));
+    const int n_cand = 2 * m->embd.tiles;  // 64-row LM-head items
+    return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
+                          (const unsigned long long*)m->lm_cand, n_cand, (const float*)m->lm_m, (const float*)m->lm_s, 64,
+                          (const float*)m->logits, c.vocab, (const int32_t*)kv->d_prompt, kv->d_ids);
 }
 
 // ------------------------------------------------------------------

@@ -189,9 +189,36 @@ int ensure_scratch(gh_model* m) {
     GH_CHECK(dev_alloc(m, &m->logits, (size_t)m->embd.tiles * TILE_ROWS));
     GH_CHECK(dev_alloc(m, &m->layer_out, (size_t)c.n_layers * c.hidden));
     GH_CHECK(dev_alloc(m, &m->xn_final, c.hidden));
-    GH_CHECK(dev_alloc(m, &m->lm_cand, (size_t)m->plm.row_tiles(m->embd.tiles)));
-    GH_CHECK(dev_alloc(m, &m->lm_m, (size_t)m->plm.row_tiles(m->embd.tiles)));
-    GH_CHECK(dev_alloc(m, &m->lm_s, (size_t)m->plm.row_tiles(m->embd.tiles)));
+    // per LM-head workgroup (at most 2 per tile: 64-row workgroups)
+    GH_CHECK(dev_alloc(m, &m->lm_cand, 2 * (size_t)m->embd.tiles));
+    GH_CHECK(dev_alloc(m, &m->lm_m, 2 * (size_t)m->embd.tiles));
+    GH_CHECK(dev_alloc(m, &m->lm_s, 2 * (size_t)m->embd.tiles));
+    // persistent step: exchange words (GH_PERSISTENT=1 on a supported shape)
+    m->persistent = env_int("GH_PERSISTENT", 0) && persistent_supported(m);
+    if (m->persistent) {
+        int cus = 0;
+        GH_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->ctx->device));
+        if (cus <= 0) {
+            m->persistent = 0;
+        } else {
+            m->p_grid = cus;
+            GH_CHECK(dev_alloc(m, &m->w_qkv, (size_t)L.qkv.tiles * TILE_ROWS));
+            GH_CHECK(dev_alloc(m, &m->w_attn, (size_t)c.n_kv_heads * m->attn_nc * G * (c.head_dim + 2)));
+            GH_CHECK(dev_alloc(m, &m->w_o, (size_t)L.o.tiles * TILE_ROWS));
+            GH_CHECK(dev_alloc(m, &m->w_gu, (size_t)L.gu.tiles * TILE_ROWS));
+            GH_CHECK(dev_alloc(m, &m->w_down, (size_t)m->pe.S * L.down.tiles * TILE_ROWS));
+            GH_CHECK(dev_alloc(m, &m->w_x, (size_t)c.hidden));
+            GH_CHECK(dev_alloc(m, &m->w_x1, (size_t)c.hidden));
+            GH_CHECK(dev_alloc(m, &m->w_xn, (size_t)c.hidden));
+            // epoch 0 everywhere: no published word matches before its phase
+            const size_t nw[] = {(size_t)L.qkv.tiles * TILE_ROWS, (size_t)c.n_kv_heads * m->attn_nc * G * (c.head_dim + 2),
+                                 (size_t)L.o.tiles * TILE_ROWS, (size_t)L.gu.tiles * TILE_ROWS,
+                                 (size_t)m->pe.S * L.down.tiles * TILE_ROWS, (size_t)c.hidden, (size_t)c.hidden,
+                                 (size_t)c.hidden};
+            uint64_t* ws[] = {m->w_qkv, m->w_attn, m->w_o, m->w_gu, m->w_down, m->w_x, m->w_x1, m->w_xn};
+            for (int i = 0; i < 8; ++i) GH_HIP(hipMemset(ws[i], 0, nw[i] * sizeof(uint64_t)));
+        }
+    }
     return GH_OK;
 }
 
@@ -214,7 +241,7 @@ int kv_graph(gh_kv* kv) {
     sink.patches = &kv->patches;
     kv->graph_args.clear();
     kv->patches.clear();
-    int rc = enqueue_step(m, kv, sink, 0);
+    int rc = m->persistent ? enqueue_persistent(m, kv, sink, 0) : enqueue_step(m, kv, sink, 0);
     if (rc != GH_OK) {
         hipGraphDestroy(g);
         return rc;
@@ -235,7 +262,7 @@ int launch_step(gh_kv* kv, int pos) {
     if (env_int("GH_NO_GRAPH", 0)) {
         Sink sink;
         sink.s = s;
-        return enqueue_step(kv->m, kv, sink, pos);
+        return kv->m->persistent ? enqueue_persistent(kv->m, kv, sink, pos) : enqueue_step(kv->m, kv, sink, pos);
     }
     GH_CHECK(kv_graph(kv));
     for (auto& p : kv->patches) {
@@ -260,7 +287,7 @@ int put_state(gh_kv* kv, int pos, int token, int start, int n_prompt, int gen_ca
     h->inv_temp = kv->inv_temp;
     h->seed_lo = (uint32_t)kv->seed;
     h->seed_hi = (uint32_t)(kv->seed >> 32);
-    h->pad = 0;
+    h->xchg_err = 0;
     GH_HIP(hipMemcpyAsync(kv->st, h, offsetof(StepState, keys), hipMemcpyHostToDevice, kv->m->ctx->stream));
     return GH_OK;
 }
@@ -873,6 +900,7 @@ extern "C" int gh_kv_destroy(gh_kv* kv) {
     hipFree(kv->rope);
     hipFree(kv->d_prompt);
     hipFree(kv->d_ids);
+    if (kv->d_players) hipFree(kv->d_players);
     hipHostFree(kv->h_st);
     m->kvs.erase(std::remove(m->kvs.begin(), m->kvs.end(), kv), m->kvs.end());
     delete kv;
@@ -940,6 +968,7 @@ extern "C" int gh_step(gh_model* m, gh_kv* kv, int32_t token, float* logits, flo
     GH_HIP(hipStreamSynchronize(s));
     kv->len += 1;
     if (argmax_out) *argmax_out = kv->h_st->last;
+    if (kv->h_st->xchg_err) return set_error(GH_ERR_STATE, "persistent step: a phase exchange timed out");
     if (kv->h_st->nan_flag) return set_error(GH_ERR_NAN, "NaN in logits at position %d", kv->len - 1);
     return GH_OK;
 }
@@ -981,6 +1010,7 @@ static int run_device_fed(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t
     kv->len += (int)steps;
     const int got = kv->h_st->gen_count;
     if (ids_out && got > 0) GH_HIP(hipMemcpy(ids_out, kv->d_ids, sizeof(int32_t) * got, hipMemcpyDeviceToHost));
+    if (kv->h_st->xchg_err) return set_error(GH_ERR_STATE, "persistent step: a phase exchange timed out");
     if (kv->h_st->nan_flag) return set_error(GH_ERR_NAN, "NaN in logits during generation");
     if (got != gen_cap) return set_error(GH_ERR_STATE, "generated %d ids, expected %d", got, gen_cap);
     return GH_OK;

@@ -261,3 +261,19 @@ def test_temperature_sampling_in_the_step(ctx):
             toks.append(nxt)
     with pytest.raises(gh.GemmaHipError):
         kv.set_sampling(-1.0, 0)
+
+
+@pytest.mark.skip(reason="persistent step (GH_PERSISTENT=1): the model tests pass on MI355X but the test "
+                         "process aborted at exit (std::bad_variant_access raised inside the HIP runtime "
+                         "during teardown) in two runs; the cause is not found yet, so the mode stays off "
+                         "and this test stays skipped until it is")
+def test_persistent_step_matches_graph_step(ctx, monkeypatch):
+    """The persistent step kernel (one workgroup per CU, phases exchanging
+    epoch-tagged words) gives the graph step's ids and per-layer states."""
+    cfg = gh.preset("gemma3-1b")
+    ref = _gpu_model(ctx, cfg, 1234, True)
+    prompt = gh.synth_tokens(1, "prompt", 16, cfg.vocab)
+    want = gh.generate(ref, gh.KVCache(ref, 256), prompt, 24)
+    monkeypatch.setenv("GH_PERSISTENT", "1")
+    m = _gpu_model(ctx, cfg, 1234, True)
+    np.testing.assert_array_equal(gh.generate(m, gh.KVCache(m, 256), prompt, 24), want)
