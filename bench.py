@@ -33,6 +33,11 @@ WEIGHT_SEED = 1234
 PROMPT_SEED = 1
 N_PROMPT = 128
 # back-to-back replays per kernel kind in the event-timed pass (a few ms each)
+# HBM bytes per LM-head launch from two rocprofv3 --pmc passes
+# (profiles/lm_head_gemma3-1b_decode.md): FETCH_SIZE 83,038 KiB x 1.99976 and
+# WRITE_SIZE 1,152 KiB x 1.0, each factor = the bytes a 256 MiB device copy
+# moves / what the counter reads for that copy.
+LM_HEAD_TRAFFIC_BYTES = 171_221_066
 KERNEL_REPS = {"qkv": 40, "attention": 40, "o_proj": 40, "gate_up": 40, "down": 40, "final_norm": 400,
                "lm_head": 200}
 
@@ -200,7 +205,8 @@ def main(argv=None) -> int:
     # roofline kernel: the LM head, the largest Q4_0 matvec (262144 x 1152)
     lm = timings["lm_head"]
     roofline = {"bound": "hbm", "achieved": round(lm.gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(lm.gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "lm_head",
+                "frac": round(lm.gbps / HBM_PEAK_GBPS, 4), "traffic": LM_HEAD_TRAFFIC_BYTES,
+                "traffic_source": "rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated)", "kernel": "lm_head",
                 "bytes_per_launch": int(lm.bytes_per_launch), "avg_us": round(lm.avg_us, 3)}
 
     out = {

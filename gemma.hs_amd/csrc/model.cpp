@@ -1102,18 +1102,45 @@ extern "C" int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t 
     GH_CHECK(enqueue_step(m, kv, sink, kv->len));  // warm-up
     const int per_step = sink.launched;
     const double bytes = per_step ? sink.bytes / per_step : 0.0;
-    hipEvent_t a, b;
-    GH_HIP(hipEventCreate(&a));
-    GH_HIP(hipEventCreate(&b));
+    // Graph mode (default): the n_reps passes are built into one graph and
+    // replayed once, so the launches run back to back as the decode graph
+    // runs them, with no host work between them.  GH_NO_GRAPH=1: eager
+    // launches, one host pass of the step per repetition.
+    const bool use_graph = !env_int("GH_NO_GRAPH", 0);
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    std::vector<std::unique_ptr<gh::NodeArgsBase>> store;
+    std::vector<gh::PosPatch> patches;
+    hipEvent_t a = nullptr, b = nullptr;
     int rc = GH_OK;
-    if (hipEventRecord(a, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
-    for (int i = 0; i < n_reps && rc == GH_OK; ++i) rc = enqueue_step(m, kv, sink, kv->len);
+    if (use_graph) {
+        if (hipGraphCreate(&g, 0) != hipSuccess) return set_error(GH_ERR_HIP, "hipGraphCreate failed");
+        gh::Sink gs;
+        gs.g = g;
+        gs.only = name;
+        gs.store = &store;
+        gs.patches = &patches;
+        for (int i = 0; i < n_reps && rc == GH_OK; ++i) rc = enqueue_step(m, kv, gs, kv->len);
+        if (rc == GH_OK && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
+            rc = set_error(GH_ERR_HIP, "hipGraphInstantiate failed");
+        if (rc == GH_OK && hipGraphLaunch(ge, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipGraphLaunch failed");
+    }
+    if (rc == GH_OK && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess))
+        rc = set_error(GH_ERR_HIP, "hipEventCreate failed");
+    if (rc == GH_OK && hipEventRecord(a, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
+    if (use_graph) {
+        if (rc == GH_OK && hipGraphLaunch(ge, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipGraphLaunch failed");
+    } else {
+        for (int i = 0; i < n_reps && rc == GH_OK; ++i) rc = enqueue_step(m, kv, sink, kv->len);
+    }
     float ms = 0.0f;
     if (rc == GH_OK && hipEventRecord(b, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
     if (rc == GH_OK && hipEventSynchronize(b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventSynchronize failed");
     if (rc == GH_OK && hipEventElapsedTime(&ms, a, b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventElapsedTime failed");
-    (void)hipEventDestroy(a);
-    (void)hipEventDestroy(b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
     GH_CHECK(rc);
     *avg_us_out = per_step ? 1e3 * ms / ((double)n_reps * per_step) : 0.0;
     if (bytes_per_launch_out) *bytes_per_launch_out = bytes;

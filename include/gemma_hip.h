@@ -239,7 +239,9 @@ int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kernel_stat* st
  * "lm_head") of one step at the cache's current position, n_reps times
  * back to back on the context stream between two HIP events, and returns
  * the average duration per launch, the algorithmic HBM bytes per launch
- * and the launches per step.  The replayed kernels are idempotent (same
+ * and the launches per step.  The n_reps passes run as one captured graph
+ * (the way the decode loop runs them), or as eager launches when
+ * GH_NO_GRAPH=1.  The replayed kernels are idempotent (same
  * inputs, same outputs), so the model and cache state are unchanged.
  * Also replaces the gpu_print_profile_stats hook (BenchmarkKVCache.hs:38-42). */
 int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t n_reps, double* avg_us_out,
