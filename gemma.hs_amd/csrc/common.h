@@ -106,6 +106,9 @@ struct DevBuf {
 
 }  // namespace gh
 
+struct gh_model;
+struct gh_q4;
+
 struct gh_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -114,6 +117,9 @@ struct gh_ctx {
     hipEvent_t t0 = nullptr, t1 = nullptr;  // gh_timer_start / gh_timer_stop
     void* scratch = nullptr;                // op-level temporaries
     size_t scratch_bytes = 0;
+    // handles created on this context; gh_ctx_destroy destroys what is left
+    std::vector<gh_model*> models;
+    std::vector<gh_q4*> q4s;
 };
 
 struct gh_q4 {
@@ -123,6 +129,7 @@ struct gh_q4 {
     uint16_t* scales = nullptr;
     gh::Plan plan;
     float* part = nullptr;  // [S][rows_pad] partial sums
+    ~gh_q4();               // frees the device buffers
 };
 
 struct gh_kv;
@@ -158,6 +165,19 @@ struct Sink {
     const char* only = nullptr;  // launch only the kernels of this name (timing)
     int launched = 0;            // kernels enqueued
     double bytes = 0.0;          // their algorithmic bytes
+};
+
+// Buffers of the batched prompt prefill (per model, grown on demand).
+struct PfBufs {
+    int cap = 0;                 // token rows (multiple of 64) the row buffers hold
+    float* x = nullptr;          // [cap][H] residual after attention / after the layer
+    float* x1 = nullptr;         // [cap][H] residual after attention
+    void* a = nullptr;           // [3][cap][Kmax] bf16 (Q4_0 weights) or [cap][Kmax] f32: GEMM operand
+    float* q = nullptr;          // [cap][nq * hd] normed + roped queries
+    float* st = nullptr;         // [cap][nq][hd + 2] attention state (o, m, l) per token
+    int32_t* tok = nullptr;      // [cap] token ids of the chunk
+    float* part = nullptr;       // split-K GEMM partials
+    size_t part_floats = 0;
 };
 
 }  // namespace gh
@@ -207,6 +227,8 @@ struct gh_model {
     uint64_t* w_xn = nullptr;
     uint32_t p_tick = 0;
     int p_grid = 0;
+    // batched prompt prefill
+    gh::PfBufs pf;
 };
 
 struct gh_kv {
@@ -247,6 +269,12 @@ struct Profiler {
 int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos);
 int persistent_supported(const gh_model* m);
 int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos);
+// kernels.hip: batched prefill of n tokens (ids in m->pf.tok) at positions
+// pos0 .. pos0+n-1; with `head`, also the final norm, LM head and next-token
+// selection of the last of them (position pos0+n-1).
+constexpr int PF_MAX_TOKENS = 512;  // tokens per prefill pass
+int pf_splits(const DMat& w, int Pp, int* kb_per);
+int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool head);
 int launch_q4_dequant(const DMat& w, float* out, hipStream_t s);
 int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* part, float* y,
                         int softcap, float cap, hipStream_t s);

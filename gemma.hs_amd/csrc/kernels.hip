@@ -2043,6 +2043,21 @@ double mat_bytes(const DMat& w) {
 }
 }  // namespace
 
+// LM head (tied embedding) on m->xn_final with per-workgroup argmax keys
+// and softmax statistics, then the next-token selection of position pos.
+static int enqueue_head(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
+    const gh_config& c = m->cfg;
+    {
+        ProPlain pro{m->xn_final};
+        EpiLogits epi{m->logits, c.vocab, m->lm_cand, kv->st, m->lm_m, m->lm_s};
+        GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(m->embd), m->embd, m->plm, pro, epi, 0));
+    }
+    return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
+                          (const unsigned long long*)m->lm_cand, m->plm.row_tiles(m->embd.tiles), (const float*)m->lm_m,
+                          (const float*)m->lm_s, 64 * m->plm.rl, (const float*)m->logits, c.vocab,
+                          (const int32_t*)kv->d_prompt, kv->d_ids);
+}
+
 int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     const gh_config& c = m->cfg;
     const int H = c.hidden, nkv = c.n_kv_heads, hd = c.head_dim;
@@ -2165,16 +2180,506 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             return sink_launch(sink, "final_norm", 0.0, k_final_norm<MG>, dim3(1), dim3(NT), lds, pro, m->xn_final);
         }));
     }
-    // LM head (tied embedding) + per-tile argmax keys
-    {
-        ProPlain pro{m->xn_final};
-        EpiLogits epi{m->logits, c.vocab, m->lm_cand, kv->st, m->lm_m, m->lm_s};
-        GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(m->embd), m->embd, m->plm, pro, epi, 0));
+    return enqueue_head(m, kv, sink, pos);
+}
+
+// ------------------------------------------------------------------
+// batched prompt prefill: n prompt tokens in one pass per layer, instead of
+// the token-by-token prompt loop of app/Main.hs:426-436.  Per layer:
+//   rows   residual update + norm of every token row -> GEMM operand A
+//   GEMM   A [n x K] times the Q4_0 (or f32) weight rows on MFMA -> split-K partials
+//   qkv    QK-norm + RoPE of each token's q/k, K/V append at its position
+//   attn   causal attention of each token over the cache (attn_item, one chunk)
+//   a_out  o / l per head -> GEMM operand A
+//   geglu  gelu_tanh(g) * u -> GEMM operand A
+// The arithmetic per token is the decode step's (TBG:92-461); only the
+// matvecs become GEMMs.
+// ------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// bf16 bits of x, rounded to nearest even (activations are finite).
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// GEMM operand A, [Pp][K] per part.  With Q4_0 weights (split = 1): three
+// bf16 parts hi + mid + lo with x - hi - mid - lo below 2^-24 |x|, and the
+// columns of every 32-column block permuted so that lane group g of an MFMA
+// reads columns {4g..4g+3, 16+4g..16+4g+3} as one 16-byte vector: the low
+// and high nibbles of code bytes 4g..4g+3.  With f32 weights: plain f32.
+struct PfA {
+    void* p;
+    int Pp, K;
+    int split;
+    // columns k..k+3 (k a multiple of 4) of token row t
+    __device__ void put4(int t, int k, float4 v) const {
+        if (!split) {
+            *(float4*)((float*)p + (size_t)t * K + k) = v;
+            return;
+        }
+        const int kk = k & 31;
+        const size_t at = (size_t)t * K + (k & ~31) + (kk < 16 ? 2 * kk : 2 * kk - 28);
+        float r[4] = {v.x, v.y, v.z, v.w};
+        uint16_t* base = (uint16_t*)p + at;
+#pragma unroll
+        for (int part = 0; part < 3; ++part) {
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[e] = bf16_rne(r[e]);
+                r[e] -= __uint_as_float(h[e] << 16);  // exact
+            }
+            *(uint2*)(base + (size_t)part * Pp * K) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        }
     }
-    return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
-                          (const unsigned long long*)m->lm_cand, m->plm.row_tiles(m->embd.tiles), (const float*)m->lm_m,
-                          (const float*)m->lm_s, 64 * m->plm.rl, (const float*)m->logits, c.vocab,
-                          (const int32_t*)kv->d_prompt, kv->d_ids);
+};
+
+// Residual update + norm of token rows t0 + blockIdx.x (ProResid semantics):
+//   x = E[token] * sqrt(H)                      (layer 0)
+//     or base + postnorm(sum_s part_s)          (TBG:305-343, TBG:413-444)
+//   A row = norm(x) with w_norm   (or xn_out = norm(x) for the final norm)
+struct PfRows {
+    const int32_t* tok;   // layer 0: token ids
+    DMat embd;
+    float escale;
+    const float* base;    // else: residual rows [Pp][H]
+    const float* part;    // split-K partials [S][Pp][ld]
+    int S, ld, Pp;
+    const float* w_post;  // nullable
+    const float* w_norm;
+    float eps;
+    int zc, H;
+    float* x_out;         // nullable: new residual rows [Pp][H]
+    float* layer_out;     // nullable: receives row t_layer of x
+    int t_layer;
+    PfA a;
+    float* xn_out;        // nullable: plain normed row (final norm of one row)
+    int t0;
+};
+
+template <int MG>
+__global__ __launch_bounds__(NT) void k_pf_rows(PfRows r) {
+    __shared__ float slot[8];
+    const int t = r.t0 + blockIdx.x, tid = threadIdx.x, NG = r.H >> 2;
+    float4 xv[MG];
+    if (r.tok) {
+        const int tk = min(max(r.tok[t], 0), r.embd.rows - 1);
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            xv[k] = f4z();
+            if (g < NG) {
+                const float4 e = dq_elem4(r.embd, tk, 4 * g);
+                xv[k] = make_float4(e.x * r.escale, e.y * r.escale, e.z * r.escale, e.w * r.escale);
+            }
+        }
+    } else {
+        float4 dv[MG];
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            dv[k] = f4z();
+            if (g < NG) {
+                for (int s = 0; s < r.S; ++s) dv[k] = dv[k] + ((const float4*)(r.part + ((size_t)s * r.Pp + t) * r.ld))[g];
+                ss += dot4(dv[k], dv[k]);
+            }
+        }
+        float rms = 1.0f;
+        if (r.w_post) rms = sqrtf(block_sum(ss, slot) / (float)r.H + r.eps);
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            xv[k] = f4z();
+            if (g < NG) {
+                const float4 b = ((const float4*)(r.base + (size_t)t * r.H))[g];
+                xv[k] = b + (r.w_post ? norm4(dv[k], rms, ((const float4*)r.w_post)[g], r.zc) : dv[k]);
+            }
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MG; ++k) {
+        const int g = tid + k * NT;
+        if (g < NG) {
+            ss += dot4(xv[k], xv[k]);
+            if (r.x_out) ((float4*)(r.x_out + (size_t)t * r.H))[g] = xv[k];
+            if (r.layer_out && t == r.t_layer) ((float4*)r.layer_out)[g] = xv[k];
+        }
+    }
+    const float rms = sqrtf(block_sum(ss, slot + 4) / (float)r.H + r.eps);
+#pragma unroll
+    for (int k = 0; k < MG; ++k) {
+        const int g = tid + k * NT;
+        if (g < NG) {
+            const float4 y = norm4(xv[k], rms, ((const float4*)r.w_norm)[g], r.zc);
+            if (r.xn_out) ((float4*)r.xn_out)[g] = y;
+            else r.a.put4(t, 4 * g, y);
+        }
+    }
+}
+
+// GEMM of the prefill: out[s][t][row] = sum over split s's column blocks of
+// A[t][k] * W[row][k].  Workgroup = 64 token rows x 64 weight rows (one wave
+// per 16 weight rows, 4 token subtiles of 16 per wave) x one split.
+struct PfGemm {
+    PfA a;
+    DMat w;
+    int kb_per;  // column blocks per split
+    float* out;  // [S][Pp][ldo]
+    int ldo;
+};
+
+// bf16 bits of (q0 - 8) | (q1 - 8) << 16 for 4-bit codes: the integer is
+// exact in f32 (8388608 + q - 8388616) and in bf16.
+__device__ __forceinline__ uint32_t q4_bf16_pair(uint32_t q0, uint32_t q1) {
+    const float f0 = __uint_as_float(0x4B000000u | q0) - 8388616.0f;
+    const float f1 = __uint_as_float(0x4B000000u | q1) - 8388616.0f;
+    return (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+}
+
+// Q4_0 weights on v_mfma_f32_16x16x32_bf16: one 32-column block per MFMA
+// (A = 16 tokens x 32 columns, B = 32 columns x 16 weight rows), three MFMAs
+// per block (hi, mid, lo parts of A) into a fresh accumulator that is then
+// scaled by the block's d: the products (q - 8) * part are exact.
+__global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tile = blockIdx.x >> 1;
+    const int lr = (blockIdx.x & 1) * 64 + wave * 16 + (lane & 15);
+    const int t0 = blockIdx.y * 64;
+    const int kb0 = blockIdx.z * g.kb_per, kb1 = min(g.w.nblk, kb0 + g.kb_per);
+    const int gq = lane >> 4;
+    const int K = g.a.K;
+    const size_t pstride = (size_t)g.a.Pp * K;
+    const uint16_t* ab = (const uint16_t*)g.a.p + (size_t)(t0 + (lane & 15)) * K + 8 * gq;
+    const uint32_t* codes = (const uint32_t*)g.w.codes;
+    f32x4_t acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb = kb0; kb < kb1; ++kb) {
+        const size_t idx = ((size_t)tile * g.w.nblk + kb) * TILE_ROWS + lr;
+        const uint32_t wd = codes[idx * 4 + gq];
+        const float d = h2f(g.w.scales[idx]);
+        uint4 u;
+        u.x = q4_bf16_pair(wd & 15u, (wd >> 8) & 15u);
+        u.y = q4_bf16_pair((wd >> 16) & 15u, (wd >> 24) & 15u);
+        u.z = q4_bf16_pair((wd >> 4) & 15u, (wd >> 12) & 15u);
+        u.w = q4_bf16_pair((wd >> 20) & 15u, wd >> 28);
+        const bf16x8_t b = __builtin_bit_cast(bf16x8_t, u);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint16_t* ap = ab + (size_t)(16 * m) * K + (size_t)kb * 32;
+            const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, *(const uint4*)ap);
+            const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, *(const uint4*)(ap + pstride));
+            const bf16x8_t a2 = __builtin_bit_cast(bf16x8_t, *(const uint4*)(ap + 2 * pstride));
+            f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b, c, 0, 0, 0);
+            acc[m] += d * c;
+        }
+    }
+    // lane holds rows 4*gq .. 4*gq+3 of each 16-token subtile, column lane & 15
+    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + t0 + 4 * gq) * g.ldo + (size_t)tile * TILE_ROWS + lr;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[(size_t)(16 * m + r) * g.ldo] = acc[m][r];
+}
+
+// f32 weights on v_mfma_f32_16x16x4_f32: one 4-column block per MFMA.
+__global__ __launch_bounds__(NT) void k_pf_gemm_f32(PfGemm g) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tile = blockIdx.x >> 1;
+    const int lr = (blockIdx.x & 1) * 64 + wave * 16 + (lane & 15);
+    const int t0 = blockIdx.y * 64;
+    const int kb0 = blockIdx.z * g.kb_per, kb1 = min(g.w.nblk, kb0 + g.kb_per);
+    const int kq = lane >> 4;
+    const int K = g.a.K;
+    const float* ab = (const float*)g.a.p + (size_t)(t0 + (lane & 15)) * K + kq;
+    const float* wc = (const float*)g.w.codes;
+    f32x4_t acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb = kb0; kb < kb1; ++kb) {
+        const float bw = wc[(((size_t)tile * g.w.nblk + kb) * TILE_ROWS + lr) * 4 + kq];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(ab[(size_t)(16 * m) * K + 4 * kb], bw, acc[m], 0, 0, 0);
+    }
+    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + t0 + 4 * kq) * g.ldo + (size_t)tile * TILE_ROWS + lr;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[(size_t)(16 * m + r) * g.ldo] = acc[m][r];
+}
+
+// q/k/v of token t, kv head g: sum of the QKV split partials, QK-norm
+// (TBG:171-179), RoPE at the token's position, K/V append
+// (appendKVCacheShader, AttentionGPU.hs:502-534); q goes to the query rows.
+struct PfQkv {
+    const float* part;
+    int S, ld, Pp;
+    int q_off, k_off, v_off;
+    const float* q_norm;
+    const float* k_norm;
+    int use_qk_norm, zc;
+    float eps;
+    const float* rope;  // [max_seq][HD/2] (cos, sin) of this layer type
+    int pos0, nkv;
+    float* q;           // [Pp][nq * HD]
+    float* kc;
+    float* vc;
+};
+
+template <int HD, int G>
+__global__ __launch_bounds__(NT) void k_pf_qkv(PfQkv p) {
+    __shared__ __align__(16) float buf[(G + 2) * HD];
+    const int t = blockIdx.x / p.nkv, g = blockIdx.x % p.nkv, tid = threadIdx.x;
+    const int pos = p.pos0 + t;
+    for (int i = 4 * tid; i < (G + 2) * HD; i += 4 * NT) {
+        const int row = i < G * HD ? p.q_off + g * G * HD + i
+                      : i < (G + 1) * HD ? p.k_off + g * HD + (i - G * HD)
+                                         : p.v_off + g * HD + (i - (G + 1) * HD);
+        float4 s = f4z();
+        for (int sp = 0; sp < p.S; ++sp) s = s + *(const float4*)(p.part + ((size_t)sp * p.Pp + t) * p.ld + row);
+        *(float4*)&buf[i] = s;
+    }
+    __syncthreads();
+    const float2* cs = (const float2*)p.rope + (size_t)pos * (HD / 2);
+    for (int vec = tid >> 6; vec < G + 1; vec += 4) {
+        float* v = buf + vec * HD;
+        if (p.use_qk_norm) wave_head_norm<HD>(v, vec < G ? p.q_norm : p.k_norm, p.eps, p.zc);
+        wave_head_rope<HD>(v, cs);
+    }
+    __syncthreads();
+    for (int i = tid; i < G * HD; i += NT) p.q[(size_t)t * p.nkv * G * HD + (size_t)g * G * HD + i] = buf[i];
+    for (int i = tid; i < HD; i += NT) {
+        p.kc[((size_t)pos * p.nkv + g) * HD + i] = buf[G * HD + i];
+        p.vc[((size_t)pos * p.nkv + g) * HD + i] = buf[(G + 1) * HD + i];
+    }
+}
+
+// Attention of token t (kv head g) over its window of the cache, as one
+// chunk of the decode kernel's flash-decoding item; state per token.
+template <int HD, int G>
+__global__ __launch_bounds__(NT) void k_pf_attn(AttnArgs a, const float* q, int pos0, float* state) {
+    const int t = blockIdx.x / a.nkv, g = blockIdx.x % a.nkv;
+    AttnArgs b = a;
+    b.q = q + (size_t)t * a.nkv * G * HD;
+    b.nc = 1;
+    b.set_pos(pos0 + t);
+    attn_item<HD, G, false>(b, g, 0, QkvPartials{nullptr, 0, 0},
+                            AttnOutPlain{state + (size_t)t * a.nkv * G * (HD + 2)});
+}
+
+// o = o_unnormalised / l per head (the one-chunk merge) -> GEMM operand A.
+template <int HD, int G>
+__global__ __launch_bounds__(NT) void k_pf_attn_out(const float* state, int nkv, PfA a) {
+    const int t = blockIdx.x;
+    const float* st = state + (size_t)t * nkv * G * (HD + 2);
+    for (int i = 4 * threadIdx.x; i < nkv * G * HD; i += 4 * NT) {
+        const int h = i / HD, d = i % HD, g = h / G, hl = h % G;
+        const float* sg = st + (size_t)g * G * (HD + 2);
+        const float l = sg[G + hl];
+        const float* o = sg + 2 * G + hl * HD + d;
+        a.put4(t, i, make_float4(o[0] / l, o[1] / l, o[2] / l, o[3] / l));
+    }
+}
+
+// h = gelu_tanh(sum_s g_s) * sum_s u_s (MLP.hs:384-447) -> GEMM operand A.
+__global__ __launch_bounds__(NT) void k_pf_geglu(const float* part, int S, int ld, int Pp, int F, int up_off, PfA a) {
+    const int t = blockIdx.x;
+    for (int i = 4 * threadIdx.x; i < F; i += 4 * NT) {
+        float4 gs = f4z(), us = f4z();
+        for (int s = 0; s < S; ++s) {
+            const float* row = part + ((size_t)s * Pp + t) * ld;
+            gs = gs + *(const float4*)(row + i);
+            us = us + *(const float4*)(row + up_off + i);
+        }
+        a.put4(t, i, make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y, gelu_tanh(gs.z) * us.z,
+                                 gelu_tanh(gs.w) * us.w));
+    }
+}
+
+// Split count of a prefill GEMM over Pp token rows: enough workgroups for
+// two per CU, at most 8 splits.
+int pf_splits(const DMat& w, int Pp, int* kb_per) {
+    const int wgs = w.tiles * 2 * (Pp / 64);
+    int S = std::max(1, std::min(8, (512 + wgs - 1) / wgs));
+    S = std::min(S, w.nblk);
+    const int per = (w.nblk + S - 1) / S;
+    if (kb_per) *kb_per = per;
+    return (w.nblk + per - 1) / per;
+}
+
+static double pf_gemm_bytes(const DMat& w, int n) {
+    return mat_bytes(w) + 4.0 * (double)n * (w.cols + w.rows) - 4.0 * (w.cols + w.rows);
+}
+
+int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool head) {
+    const gh_config& c = m->cfg;
+    const PfBufs& B = m->pf;
+    const int H = c.hidden, hd = c.head_dim, nkv = c.n_kv_heads, G = c.n_heads / nkv, F = c.ffn;
+    const int Pp = (n + 63) / 64 * 64;
+    if (n <= 0 || Pp > B.cap) return set_error(GH_ERR_INVALID, "internal: prefill of %d rows, buffers hold %d", n, B.cap);
+    const int zc = (c.flags & GH_FLAG_ZERO_CENTERED) ? 1 : 0;
+    const float eps = c.rms_eps;
+    const size_t kv_layer = (size_t)kv->max_seq * nkv * hd;
+    const int split = m->fmt == FMT_Q4 ? 1 : 0;
+    auto A = [&](int K) { return PfA{B.a, Pp, K, split}; };
+    // GEMM of operand A (K columns) with w into the partials; returns S
+    auto gemm = [&](const char* name, const DMat& w, int* S_out) -> int {
+        int per = 0;
+        const int S = pf_splits(w, Pp, &per);
+        if ((size_t)S * Pp * w.tiles * TILE_ROWS > B.part_floats)
+            return set_error(GH_ERR_INVALID, "internal: prefill partials too small");
+        *S_out = S;
+        PfGemm g{A(w.cols), w, per, B.part, w.tiles * TILE_ROWS};
+        const dim3 grid(w.tiles * 2, Pp / 64, S), block(NT);
+        return w.fmt == FMT_Q4 ? sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4, grid, block, 0, g)
+                               : sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_f32, grid, block, 0, g);
+    };
+    auto rows = [&](const char* name, PfRows r, int n_rows) {
+        return with_mg(H, [&](auto mg) {
+            return sink_launch(sink, name, 0.0, k_pf_rows<decltype(mg)::value>, dim3(n_rows), dim3(NT), 0, r);
+        });
+    };
+    int S = 0;
+    for (int li = 0; li < c.n_layers; ++li) {
+        const LayerDev& L = m->layers[li];
+        const LayerDev* P = li > 0 ? &m->layers[li - 1] : nullptr;
+        // residual (embedding at layer 0) + pre-attention norm
+        {
+            PfRows r{};
+            r.tok = li == 0 ? B.tok : nullptr;
+            r.embd = m->embd;
+            r.escale = sqrtf((float)H);
+            r.base = B.x1;
+            r.part = B.part;
+            r.S = S;
+            r.ld = P ? P->down.tiles * TILE_ROWS : 0;
+            r.Pp = Pp;
+            r.w_post = P && (c.flags & GH_FLAG_POST_FFN_NORM) ? P->post_ffw : nullptr;
+            r.w_norm = L.attn_norm;
+            r.eps = eps;
+            r.zc = zc;
+            r.H = H;
+            r.x_out = B.x;
+            r.layer_out = li > 0 ? m->layer_out + (size_t)(li - 1) * H : nullptr;
+            r.t_layer = n - 1;
+            r.a = A(H);
+            GH_CHECK(rows("pf_rows", r, n));
+        }
+        GH_CHECK(gemm("pf_qkv", L.qkv, &S));
+        // QK-norm, RoPE, K/V append
+        {
+            PfQkv q{};
+            q.part = B.part;
+            q.S = S;
+            q.ld = L.qkv.tiles * TILE_ROWS;
+            q.Pp = Pp;
+            q.q_off = 0;
+            q.k_off = m->q_rows_pad;
+            q.v_off = m->q_rows_pad + m->kv_rows_pad;
+            q.q_norm = L.q_norm;
+            q.k_norm = L.k_norm;
+            q.use_qk_norm = (c.flags & GH_FLAG_QK_NORM) && L.q_norm && L.k_norm;
+            q.zc = zc;
+            q.eps = eps;
+            const bool global_theta = c.mode == GH_MODE_REF ? true : L.global;
+            q.rope = kv->rope + (global_theta ? (size_t)kv->max_seq * hd : 0);
+            q.pos0 = pos0;
+            q.nkv = nkv;
+            q.q = B.q;
+            q.kc = kv->k + li * kv_layer;
+            q.vc = kv->v + li * kv_layer;
+#define GH_PF_QKV(HD_, G_) \
+    if (hd == HD_ && G == G_) GH_CHECK(sink_launch(sink, "pf_qkv_post", 0.0, k_pf_qkv<HD_, G_>, dim3(n * nkv), dim3(NT), 0, q)); else
+            GH_PF_QKV(256, 1) GH_PF_QKV(256, 2) GH_PF_QKV(256, 4) GH_PF_QKV(256, 8)
+            GH_PF_QKV(128, 1) GH_PF_QKV(128, 2) GH_PF_QKV(128, 4) GH_PF_QKV(128, 8)
+            GH_PF_QKV(32, 1) GH_PF_QKV(32, 2) GH_PF_QKV(32, 4) GH_PF_QKV(32, 8)
+            return set_error(GH_ERR_INVALID, "prefill: unsupported head_dim %d / group %d", hd, G);
+#undef GH_PF_QKV
+        }
+        // causal attention per token, then o / l into operand A
+        {
+            AttnArgs a{};
+            a.global = L.global;
+            a.window = c.sliding_window;
+            a.mode = c.mode;
+            a.kc = kv->k + li * kv_layer;
+            a.vc = kv->v + li * kv_layer;
+            a.nkv = nkv;
+            a.scale = 1.0f / sqrtf((float)hd);
+            a.nc = 1;
+            const PfA ao = A(c.n_heads * hd);
+#define GH_PF_ATTN(HD_, G_)                                                                                      \
+    if (hd == HD_ && G == G_) {                                                                                  \
+        GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_attn<HD_, G_>, dim3(n * nkv), dim3(NT), 0, a,            \
+                             (const float*)B.q, pos0, B.st));                                                   \
+        GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT), 0,            \
+                             (const float*)B.st, nkv, ao));                                                     \
+    } else
+            GH_PF_ATTN(256, 1) GH_PF_ATTN(256, 2) GH_PF_ATTN(256, 4) GH_PF_ATTN(256, 8)
+            GH_PF_ATTN(128, 1) GH_PF_ATTN(128, 2) GH_PF_ATTN(128, 4) GH_PF_ATTN(128, 8)
+            GH_PF_ATTN(32, 1) GH_PF_ATTN(32, 2) GH_PF_ATTN(32, 4) GH_PF_ATTN(32, 8)
+            return set_error(GH_ERR_INVALID, "prefill: unsupported head_dim %d / group %d", hd, G);
+#undef GH_PF_ATTN
+        }
+        GH_CHECK(gemm("pf_o", L.o, &S));
+        // post-attention norm + residual + pre-FFN norm
+        {
+            PfRows r{};
+            r.embd = m->embd;
+            r.base = B.x;
+            r.part = B.part;
+            r.S = S;
+            r.ld = L.o.tiles * TILE_ROWS;
+            r.Pp = Pp;
+            r.w_post = (c.flags & GH_FLAG_POST_ATTN_NORM) ? L.post_attn : nullptr;
+            r.w_norm = L.ffn_norm ? L.ffn_norm : L.post_attn;
+            r.eps = eps;
+            r.zc = zc;
+            r.H = H;
+            r.x_out = B.x1;
+            r.a = A(H);
+            GH_CHECK(rows("pf_rows", r, n));
+        }
+        GH_CHECK(gemm("pf_gate_up", L.gu, &S));
+        GH_CHECK(sink_launch(sink, "pf_geglu", 0.0, k_pf_geglu, dim3(n), dim3(NT), 0, (const float*)B.part, S,
+                             L.gu.tiles * TILE_ROWS, Pp, F, m->f_pad, A(F)));
+        GH_CHECK(gemm("pf_down", L.down, &S));
+    }
+    if (!head) {
+        // the next chunk's layer 0 starts from the embedding; nothing carries over
+        return GH_OK;
+    }
+    // last token: final residual + norm into the LM head's input, then the
+    // decode step's LM head and next-token selection at its position
+    {
+        const LayerDev& P = m->layers[c.n_layers - 1];
+        PfRows r{};
+        r.embd = m->embd;
+        r.base = B.x1;
+        r.part = B.part;
+        r.S = S;
+        r.ld = P.down.tiles * TILE_ROWS;
+        r.Pp = Pp;
+        r.w_post = (c.flags & GH_FLAG_POST_FFN_NORM) ? P.post_ffw : nullptr;
+        r.w_norm = m->out_norm;
+        r.eps = eps;
+        r.zc = zc;
+        r.H = H;
+        r.layer_out = m->layer_out + (size_t)(c.n_layers - 1) * H;
+        r.t_layer = n - 1;
+        r.a = A(H);
+        r.xn_out = m->xn_final;
+        r.t0 = n - 1;
+        GH_CHECK(rows("pf_final_norm", r, 1));
+    }
+    return enqueue_head(m, kv, sink, pos0 + n - 1);
 }
 
 // ------------------------------------------------------------------

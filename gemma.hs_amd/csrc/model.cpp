@@ -222,6 +222,49 @@ int ensure_scratch(gh_model* m) {
     return GH_OK;
 }
 
+void free_prefill(gh_model* m) {
+    PfBufs& B = m->pf;
+    for (void* p : {(void*)B.x, (void*)B.x1, B.a, (void*)B.q, (void*)B.st, (void*)B.tok, (void*)B.part})
+        if (p) hipFree(p);
+    B = PfBufs{};
+}
+
+// Prefill buffers for passes of up to n tokens (rows rounded up to 64).
+int prefill_reserve(gh_model* m, int n) {
+    const gh_config& c = m->cfg;
+    const int cap = (n + 63) / 64 * 64;
+    if (cap > PF_MAX_TOKENS) return set_error(GH_ERR_INVALID, "internal: prefill pass of %d tokens", n);
+    if (m->pf.cap >= cap) return GH_OK;
+    GH_HIP(hipStreamSynchronize(m->ctx->stream));
+    free_prefill(m);
+    const LayerDev& L = m->layers[0];
+    const int H = c.hidden, nq = c.n_heads, hd = c.head_dim;
+    const size_t kmax = std::max({(size_t)H, (size_t)nq * hd, (size_t)c.ffn});
+    size_t part = 0;
+    for (const DMat* w : {&L.qkv, &L.o, &L.gu, &L.down})
+        for (int pp = 64; pp <= cap; pp += 64)
+            part = std::max(part, (size_t)pf_splits(*w, pp, nullptr) * pp * w->tiles * TILE_ROWS);
+    PfBufs& B = m->pf;
+    auto get = [&](void** p, size_t bytes) -> int {
+        hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 16));
+        if (e != hipSuccess) {
+            free_prefill(m);
+            return set_error(GH_ERR_OOM, "prefill: hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+        }
+        return GH_OK;
+    };
+    GH_CHECK(get((void**)&B.x, sizeof(float) * cap * H));
+    GH_CHECK(get((void**)&B.x1, sizeof(float) * cap * H));
+    GH_CHECK(get(&B.a, (m->fmt == FMT_Q4 ? 6 : 4) * (size_t)cap * kmax));
+    GH_CHECK(get((void**)&B.q, sizeof(float) * cap * nq * hd));
+    GH_CHECK(get((void**)&B.st, sizeof(float) * cap * nq * (hd + 2)));
+    GH_CHECK(get((void**)&B.tok, sizeof(int32_t) * cap));
+    GH_CHECK(get((void**)&B.part, sizeof(float) * part));
+    B.part_floats = part;
+    B.cap = cap;
+    return GH_OK;
+}
+
 int model_ready(gh_model* m) {
     if (!m) return set_error(GH_ERR_INVALID, "null model");
     GH_CHECK(gh_model_check(m));
@@ -328,6 +371,9 @@ extern "C" int gh_ctx_destroy(gh_ctx* ctx) {
     if (!ctx) return GH_OK;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
+    // handles still open on the context go first: they use its stream
+    for (gh_model* m : std::vector<gh_model*>(ctx->models)) gh_model_destroy(m);
+    for (gh_q4* t : std::vector<gh_q4*>(ctx->q4s)) gh_q4_0_free(t);
     for (void* p : ctx->bufs) hipFree(p);
     if (ctx->scratch) hipFree(ctx->scratch);
     if (ctx->t0) hipEventDestroy(ctx->t0);
@@ -470,17 +516,26 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, 512);
     t->plan.rl = env_int("GH_Q4_RL", 2) == 1 ? 1 : 2;
     if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
+    ctx->q4s.push_back(t.get());
     *out = t.release();
     return GH_OK;
+}
+
+gh_q4::~gh_q4() {
+    if (codes) hipFree(codes);
+    if (scales) hipFree(scales);
+    if (part) hipFree(part);
 }
 
 extern "C" int gh_q4_0_free(gh_q4* t) {
     if (!t) return GH_OK;
     hipSetDevice(t->ctx->device);
     hipStreamSynchronize(t->ctx->stream);
-    hipFree(t->codes);
-    hipFree(t->scales);
-    if (t->part) hipFree(t->part);
+    {
+        Lock lk(t->ctx->mu);
+        auto& v = t->ctx->q4s;
+        v.erase(std::remove(v.begin(), v.end(), t), v.end());
+    }
     delete t;
     return GH_OK;
 }
@@ -716,6 +771,7 @@ extern "C" int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out
         m->inv_freq[i] = 1.0f / powf(c.rope_theta_local, e);
         m->inv_freq[c.head_dim / 2 + i] = 1.0f / powf(c.rope_theta_global, e);
     }
+    ctx->models.push_back(m.get());
     *out = m.release();
     return GH_OK;
 }
@@ -725,6 +781,12 @@ extern "C" int gh_model_destroy(gh_model* m) {
     hipSetDevice(m->ctx->device);
     hipStreamSynchronize(m->ctx->stream);
     for (gh_kv* kv : std::vector<gh_kv*>(m->kvs)) gh_kv_destroy(kv);
+    free_prefill(m);
+    {
+        Lock lk(m->ctx->mu);
+        auto& v = m->ctx->models;
+        v.erase(std::remove(v.begin(), v.end(), m), v.end());
+    }
     for (auto& b : m->owned) hipFree(b.p);
     delete m;
     return GH_OK;
@@ -1035,6 +1097,66 @@ extern "C" int gh_bench_decode(gh_model* m, gh_kv* kv, const int32_t* prompt, in
     GH_CHECK(model_ready(m));
     return run_device_fed(m, kv, prompt, n_prompt, n_prompt + n_warmup, n_steps, n_warmup + n_steps + 1, ms_out,
                           ids_out);
+}
+
+// Batched prefill of n tokens at the cache's next positions, in passes of
+// up to PF_MAX_TOKENS; the last token's logits, layer outputs and next token
+// are those of gh_step at that position.
+static int prefill_run(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, float* logits, float* layer_out,
+                       int32_t* next_out) {
+    const gh_config& c = m->cfg;
+    if (!tokens || n <= 0) return set_error(GH_ERR_INVALID, "prefill: empty token list");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.vocab)
+            return set_error(GH_ERR_INVALID, "prefill: token %d outside [0, %d)", tokens[i], c.vocab);
+    if ((long long)kv->len + n > kv->max_seq)
+        return set_error(GH_ERR_RANGE, "prefill of %d tokens from position %d; KV holds %d", n, kv->len, kv->max_seq);
+    hipStream_t s = m->ctx->stream;
+    GH_CHECK(prefill_reserve(m, std::min(n, PF_MAX_TOKENS)));
+    GH_CHECK(put_state(kv, kv->len + n - 1, tokens[n - 1], kv->len, 0, 0));
+    Sink sink;
+    sink.s = s;
+    for (int done = 0; done < n;) {
+        const int k = std::min(PF_MAX_TOKENS, n - done);
+        GH_HIP(hipMemcpyAsync(m->pf.tok, tokens + done, sizeof(int32_t) * k, hipMemcpyHostToDevice, s));
+        GH_CHECK(enqueue_prefill(m, kv, sink, k, kv->len + done, done + k == n));
+        done += k;
+    }
+    GH_CHECK(get_state(kv));
+    if (logits) GH_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * c.vocab, hipMemcpyDeviceToHost, s));
+    if (layer_out)
+        GH_HIP(hipMemcpyAsync(layer_out, m->layer_out, sizeof(float) * c.n_layers * c.hidden, hipMemcpyDeviceToHost, s));
+    GH_HIP(hipStreamSynchronize(s));
+    kv->len += n;
+    if (next_out) *next_out = kv->h_st->last;
+    if (kv->h_st->nan_flag) return set_error(GH_ERR_NAN, "NaN in logits at position %d", kv->len - 1);
+    return GH_OK;
+}
+
+extern "C" int gh_prefill(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, float* logits, float* layer_out,
+                          int32_t* next_out) {
+    if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    return prefill_run(m, kv, tokens, n, logits, layer_out, next_out);
+}
+
+extern "C" int gh_generate_prefill(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
+                                   int32_t* ids_out) {
+    if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
+    if (n_gen <= 0 || !ids_out) return set_error(GH_ERR_INVALID, "n_gen must be > 0 with an output buffer");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    if (prompt && n_prompt > 0 && (long long)kv->len + n_prompt + n_gen - 1 > kv->max_seq)
+        return set_error(GH_ERR_RANGE, "generation needs %d positions from %d; KV holds %d", n_prompt + n_gen - 1,
+                         kv->len, kv->max_seq);
+    int32_t next = 0;
+    GH_CHECK(prefill_run(m, kv, prompt, n_prompt, nullptr, nullptr, &next));
+    ids_out[0] = next;
+    if (n_gen == 1) return GH_OK;
+    return run_device_fed(m, kv, &next, 1, n_gen - 1, 0, n_gen - 1, nullptr, ids_out + 1);
 }
 
 extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kernel_stat* stats, int32_t max_stats,

@@ -17,6 +17,7 @@ fallback: without libgemma_hip.so (or without a GPU) the calls raise.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -30,7 +31,7 @@ GemmaConfig = GhConfig
 __all__ = [
     "GemmaConfig", "GemmaHipError", "Context", "DeviceBuffer", "Q4Tensor", "GemmaModel", "KVCache",
     "preset", "runLinearQ4", "runGemmaInferenceCached", "runGemmaInferenceCachedWithLayer0",
-    "generate", "bench_decode", "profile_steps", "sample_logits", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
+    "generate", "prefill", "bench_decode", "profile_steps", "sample_logits", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
     "tensor_list", "synth_tensors", "device_count", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q4_0",
     "MODE_GEMMA3", "MODE_REF", "FLAG_QK_NORM", "FLAG_POST_ATTN_NORM", "FLAG_POST_FFN_NORM",
     "FLAG_ZERO_CENTERED", "FLAG_IEEE_SCALES",
@@ -62,6 +63,8 @@ class Context:
         h = C.c_void_p()
         check(lib().gh_ctx_create(device, C.byref(h)))
         self.h = h
+        # models and Q4_0 tensors created on this context: closed before it
+        self._children = weakref.WeakSet()
 
     def sync(self) -> None:
         check(lib().gh_ctx_sync(self.h))
@@ -89,7 +92,11 @@ class Context:
         return ms.value
 
     def close(self) -> None:
+        """Destroy the context; models (with their caches) and Q4_0 tensors
+        still open on it are closed first and their handles become None."""
         if self.h:
+            for child in list(self._children):
+                child.close()
             lib().gh_ctx_destroy(self.h)
             self.h = None
 
@@ -153,6 +160,7 @@ class Q4Tensor:
         check(lib().gh_q4_0_upload(ctx.h, _ptr(raw), rows, cols, FLAG_IEEE_SCALES if ieee_scales else 0,
                                    C.byref(h)))
         self.ctx, self.h, self.rows, self.cols = ctx, h, rows, cols
+        ctx._children.add(self)
 
     def dequant(self) -> np.ndarray:
         out = DeviceBuffer(self.ctx, 4 * self.rows * self.cols)
@@ -344,6 +352,7 @@ class GemmaModel:
             check(lib().gh_model_create(ctx.h, C.byref(cfg), C.byref(h)))
             handle = h
         self.h = handle
+        ctx._children.add(self)
         self.cfg = self.config()
 
     @classmethod
@@ -448,11 +457,31 @@ def runGemmaInferenceCachedWithLayer0(model: GemmaModel, token: int, cache: KVCa
     return logits, cache, layers, nxt.value
 
 
-def generate(model: GemmaModel, cache: KVCache, prompt, n_gen: int) -> np.ndarray:
-    """Greedy generation loop on device (app/Main.hs:372-463)."""
+def prefill(model: GemmaModel, cache: KVCache, tokens, want_logits: bool = True, want_layers: bool = False):
+    """Batched prefill: the prompt tokens at the cache's next positions in one
+    pass per layer (Q4_0 GEMMs on MFMA) instead of one decode step per token
+    (the prompt loop of app/Main.hs:426-436).  Returns (logits, layers[L, H],
+    next token) of the last token, as runGemmaInferenceCachedWithLayer0 would
+    after stepping the tokens one by one; logits / layers are None unless
+    asked for."""
+    t = np.ascontiguousarray(tokens, dtype=np.int32)
+    c = model.cfg
+    logits = np.empty(c.vocab, np.float32) if want_logits else None
+    layers = np.empty((c.n_layers, c.hidden), np.float32) if want_layers else None
+    nxt = C.c_int32()
+    check(lib().gh_prefill(model.h, cache.h, _ptr(t), len(t), _ptr(logits) if want_logits else None,
+                           _ptr(layers) if want_layers else None, C.byref(nxt)))
+    return logits, layers, nxt.value
+
+
+def generate(model: GemmaModel, cache: KVCache, prompt, n_gen: int, prefill: bool = False) -> np.ndarray:
+    """Generation loop on device (app/Main.hs:372-463): greedy, or sampled per
+    KVCache.set_sampling.  prefill=True feeds the prompt as one batched
+    prefill instead of token by token."""
     p = np.ascontiguousarray(prompt, dtype=np.int32)
     ids = np.empty(n_gen, np.int32)
-    check(lib().gh_generate(model.h, cache.h, _ptr(p), len(p), n_gen, _ptr(ids)))
+    fn = lib().gh_generate_prefill if prefill else lib().gh_generate
+    check(fn(model.h, cache.h, _ptr(p), len(p), n_gen, _ptr(ids)))
     return ids
 
 

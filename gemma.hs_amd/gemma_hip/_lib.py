@@ -96,6 +96,8 @@ SIGNATURES = {
     "gh_kv_length": (C.c_int, [_P, _I32]),
     "gh_step": (C.c_int, [_P, _P, C.c_int32, _P, _P, _I32]),
     "gh_generate": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
+    "gh_prefill": (C.c_int, [_P, _P, _P, C.c_int32, _P, _P, _I32]),
+    "gh_generate_prefill": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     "gh_bench_decode": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, C.c_int32, _F, _P]),
     "gh_profile_steps": (C.c_int, [_P, _P, C.c_int32, C.POINTER(GhKernelStat), C.c_int32, _I32]),
     "gh_capture_begin": (C.c_int, [_P]),

@@ -64,6 +64,8 @@ const char* gh_version(void);
 typedef struct gh_ctx gh_ctx;
 int gh_device_count(int* n_out);
 int gh_ctx_create(int device, gh_ctx** out);
+/* Also destroys the models (with their KV caches) and Q4_0 tensors still
+ * open on the context: their handles are invalid afterwards. */
 int gh_ctx_destroy(gh_ctx* ctx);
 /* waitAll (src/Gemma/Model.hs:1432) */
 int gh_ctx_sync(gh_ctx* ctx);
@@ -213,6 +215,25 @@ int gh_step(gh_model* m, gh_kv* kv, int32_t token, float* logits, float* layer_o
  * host round trip per token: ids_out[n_gen]. */
 int gh_generate(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
                 int32_t* ids_out);
+
+/* Batched prompt prefill.  It replaces the token-by-token prompt loop
+ * `goPrompt` (app/Main.hs:426-436), which calls runGemmaInferenceCached
+ * once per token; the reference itself rejects more than one token per
+ * call (src/Gemma/Model.hs:1321-1324).
+ * The n tokens run at the cache's next positions in one pass per layer:
+ * the projections are Q4_0 (or f32) GEMMs on MFMA, attention is causal
+ * over the cache, and K/V are appended.  Passes hold up to 512 tokens.
+ * The cache then holds n more positions.  logits[vocab], layer_out
+ * [n_layers*hidden] (may be NULL) and next_out (greedy, or sampled per
+ * gh_kv_set_sampling) are those of the last token: what gh_step on that
+ * token would return after the others. */
+int gh_prefill(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, float* logits, float* layer_out,
+               int32_t* next_out);
+
+/* gh_generate with the prompt fed by gh_prefill: ids_out[0] is the
+ * prefill's next token, then n_gen - 1 decode steps on device. */
+int gh_generate_prefill(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
+                        int32_t* ids_out);
 
 /* Decode benchmark (examples/BenchmarkKVCache.hs:56-165): feeds the prompt,
  * runs n_warmup greedy steps, then times n_steps greedy steps with HIP

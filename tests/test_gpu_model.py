@@ -151,6 +151,25 @@ def test_errors_kv_full_bad_token_incomplete_model(ctx):
         bare.set_tensor("blk.0.nonsense.weight", np.zeros(4, np.float32), gh.DTYPE_F32)
 
 
+def test_context_close_closes_its_models_and_tensors():
+    """Closing a context first closes the models (and their caches) and Q4_0
+    tensors made on it; their later close / finalisation is a no-op instead
+    of a call through the destroyed context."""
+    c2 = gh.Context(0)
+    cfg = gh.preset("tiny")
+    m = _gpu_model(c2, cfg, 2, False)
+    kv = gh.KVCache(m, 8)
+    gh.runGemmaInferenceCached(m, 1, kv, want_logits=False)
+    raw = np.zeros(64 * 18, np.uint8)
+    t = gh.Q4Tensor(c2, raw, 64, 32)
+    c2.close()
+    assert m.h is None and t.h is None and c2.h is None
+    m.close()
+    kv.close()
+    t.close()
+    del m, kv, t
+
+
 @pytest.mark.gpu
 def test_time_kernel_leaves_state_unchanged(ctx):
     """gh_time_kernel replays step kernels at the current position; the
