@@ -165,6 +165,56 @@ def extras_c5_gemma3_4b(gh, ctx, steps: int = 64, warmup: int = 8) -> dict:
     return out
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA
+
+
+def extras_f2_prefill(gh, ctx, model, sizes=(128, 512), reps: int = 5) -> dict:
+    """f2: batched prefill of a seeded prompt on the C3 model (gh_prefill):
+    wall time between two HIP events on the context stream (host launches
+    included), median of `reps`, and the per-kernel profile of one more run.
+    GEMM flops = 2 * tokens * rows * cols of the fused matrix; each Q4_0
+    GEMM issues 3 bf16 MFMAs per product (hi, mid and lo parts of the
+    activations), so its MFMA utilisation is 3x the flop rate / peak."""
+    cfg = model.cfg
+    H, F, hd = cfg.hidden, cfg.ffn, cfg.head_dim
+    shapes = {"pf_qkv": ((cfg.n_heads + 2 * cfg.n_kv_heads) * hd, H), "pf_o": (H, cfg.n_heads * hd),
+              "pf_gate_up": (2 * F, H), "pf_down": (H, F)}
+    out = {}
+    for n in sizes:
+        prompt = gh.synth_tokens(PROMPT_SEED, "prefill", n, cfg.vocab)
+        kv = gh.KVCache(model, n + 8)
+        gh.prefill(model, kv, prompt, want_logits=False)  # warm-up (buffers, code)
+        times = []
+        for _ in range(reps):
+            kv.reset()
+            ctx.timer_start()
+            gh.prefill(model, kv, prompt, want_logits=False)
+            times.append(ctx.timer_stop())
+        ms = sorted(times)[len(times) // 2]
+        kv.reset()
+        stats = gh.profile_prefill(model, kv, prompt)
+        kern = {}
+        gemm_ms = 0.0
+        for st in stats:
+            e = {"launches": st.launches, "total_us": round(st.total_ms * 1e3, 1)}
+            if st.name in shapes:
+                r, c = shapes[st.name]
+                fl = 2.0 * n * r * c * st.launches
+                tf = fl / (st.total_ms * 1e-3) / 1e12
+                e["tflops"] = round(tf, 1)
+                e["mfma_util"] = round(3 * tf / MFMA_BF16_PEAK_TFLOPS, 4)
+                gemm_ms += st.total_ms
+            kern[st.name] = e
+        layer_flops = 2.0 * n * sum(r * c for r, c in shapes.values())
+        tok_s = n / (ms * 1e-3)
+        log(f"  f2 prefill {n} tokens: {ms:.3f} ms -> {tok_s:.0f} tok/s (GEMMs {gemm_ms:.3f} ms of events)")
+        out[str(n)] = {"ms": round(ms, 4), "tok_s": round(tok_s, 1),
+                       "gemm_tflops": round(layer_flops * cfg.n_layers / (gemm_ms * 1e-3) / 1e12, 1),
+                       "kernels": kern}
+        del kv
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -227,7 +277,8 @@ def main(argv=None) -> int:
     if not a.no_extras:
         out["extras"] = {"c2_matvec_rotating_2GiB": extras_c2_matvec(gh, ctx),
                          "c4_attention": extras_c4_attention(gh, ctx),
-                         "c5_gemma3_4b_prefilled_4096": extras_c5_gemma3_4b(gh, ctx)}
+                         "c5_gemma3_4b_prefilled_4096": extras_c5_gemma3_4b(gh, ctx),
+                         "f2_prefill_gemma3_1b": extras_f2_prefill(gh, ctx, model)}
     if not a.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds, threads)

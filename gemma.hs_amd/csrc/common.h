@@ -172,7 +172,8 @@ struct PfBufs {
     int cap = 0;                 // token rows (multiple of 64) the row buffers hold
     float* x = nullptr;          // [cap][H] residual after attention / after the layer
     float* x1 = nullptr;         // [cap][H] residual after attention
-    void* a = nullptr;           // [3][cap][Kmax] bf16 (Q4_0 weights) or [cap][Kmax] f32: GEMM operand
+    void* a = nullptr;           // [2][cap][Kmax] fp16 (Q4_0 weights) or [cap][Kmax] f32: GEMM operand
+    float* ascale = nullptr;     // [cap] inverse row scales of the fp16 operand
     float* q = nullptr;          // [cap][nq * hd] normed + roped queries
     float* st = nullptr;         // [cap][nq][hd + 2] attention state (o, m, l) per token
     int32_t* tok = nullptr;      // [cap] token ids of the chunk

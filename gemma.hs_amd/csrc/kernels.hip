@@ -2195,46 +2195,58 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
 // The arithmetic per token is the decode step's (TBG:92-461); only the
 // matvecs become GEMMs.
 // ------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// bf16 bits of x, rounded to nearest even (activations are finite).
-__device__ __forceinline__ uint32_t bf16_rne(float x) {
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
-// GEMM operand A, [Pp][K] per part.  With Q4_0 weights (split = 1): three
-// bf16 parts hi + mid + lo with x - hi - mid - lo below 2^-24 |x|, and the
-// columns of every 32-column block permuted so that lane group g of an MFMA
-// reads columns {4g..4g+3, 16+4g..16+4g+3} as one 16-byte vector: the low
-// and high nibbles of code bytes 4g..4g+3.  With f32 weights: plain f32.
+// GEMM operand A, [Pp][K] per part.
+// With Q4_0 weights (split = 1), each token row t is first scaled by a power
+// of two, so that its largest |x| lies in [2^14, 2^15); inv_scale[t] undoes it.
+// The row is then stored as two fp16 parts hi + lo.  Per element the error
+// |x - (hi + lo) / scale| is at most 2^-23 |x| + 2^-40 max|x|, which is below
+// f32 rounding.  (q - 8) * part is exact in the MFMA's f32 products.
+// The columns of every 32-column block are permuted to match the weight
+// fragments: lane group g of an MFMA holds columns
+// {4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1, 16+4g+3}, the low and
+// high nibbles of code bytes 4g..4g+3 as q4_f16_pair unpacks them.
+// With f32 weights (split = 0): plain f32, unscaled.
 struct PfA {
     void* p;
     int Pp, K;
     int split;
-    // columns k..k+3 (k a multiple of 4) of token row t
-    __device__ void put4(int t, int k, float4 v) const {
+    float* inv_scale;  // [Pp] (split only)
+    // columns k..k+3 (k a multiple of 4) of token row t, scaled by sc
+    __device__ void put4(int t, int k, float4 v, float sc) const {
         if (!split) {
             *(float4*)((float*)p + (size_t)t * K + k) = v;
             return;
         }
         const int kk = k & 31;
         const size_t at = (size_t)t * K + (k & ~31) + (kk < 16 ? 2 * kk : 2 * kk - 28);
-        float r[4] = {v.x, v.y, v.z, v.w};
-        uint16_t* base = (uint16_t*)p + at;
+        const float x[4] = {v.x * sc, v.z * sc, v.y * sc, v.w * sc};  // stored order 0, 2, 1, 3
+        uint32_t hi[4], lo[4];
 #pragma unroll
-        for (int part = 0; part < 3; ++part) {
-            uint32_t h[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                h[e] = bf16_rne(r[e]);
-                r[e] -= __uint_as_float(h[e] << 16);  // exact
-            }
-            *(uint2*)(base + (size_t)part * Pp * K) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        for (int e = 0; e < 4; ++e) {
+            const _Float16 h = (_Float16)x[e];
+            hi[e] = __builtin_bit_cast(uint16_t, h);
+            lo[e] = __builtin_bit_cast(uint16_t, (_Float16)(x[e] - (float)h));
         }
+        uint16_t* base = (uint16_t*)p + at;
+        *(uint2*)base = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
+        *(uint2*)(base + (size_t)Pp * K) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+    }
+    // scale of a row whose largest |x| is m; thread 0 records its inverse
+    __device__ float row_scale(int t, float m) const {
+        if (!split) return 1.0f;
+        int ex = 0;
+        if (m > 0.0f && m < INFINITY) frexpf(m, &ex);
+        ex = min(max(ex, -100), 100);
+        if (threadIdx.x == 0) inv_scale[t] = ldexpf(1.0f, ex - 15);
+        return ldexpf(1.0f, 15 - ex);
     }
 };
+
+__device__ __forceinline__ float amax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
 
 // Residual update + norm of token rows t0 + blockIdx.x (ProResid semantics):
 //   x = E[token] * sqrt(H)                      (layer 0)
@@ -2261,7 +2273,7 @@ struct PfRows {
 
 template <int MG>
 __global__ __launch_bounds__(NT) void k_pf_rows(PfRows r) {
-    __shared__ float slot[8];
+    __shared__ float slot[12];
     const int t = r.t0 + blockIdx.x, tid = threadIdx.x, NG = r.H >> 2;
     float4 xv[MG];
     if (r.tok) {
@@ -2310,20 +2322,32 @@ __global__ __launch_bounds__(NT) void k_pf_rows(PfRows r) {
         }
     }
     const float rms = sqrtf(block_sum(ss, slot + 4) / (float)r.H + r.eps);
+    float4 y[MG];
+    float mx = 0.0f;
 #pragma unroll
     for (int k = 0; k < MG; ++k) {
         const int g = tid + k * NT;
-        if (g < NG) {
-            const float4 y = norm4(xv[k], rms, ((const float4*)r.w_norm)[g], r.zc);
-            if (r.xn_out) ((float4*)r.xn_out)[g] = y;
-            else r.a.put4(t, 4 * g, y);
+        y[k] = g < NG ? norm4(xv[k], rms, ((const float4*)r.w_norm)[g], r.zc) : f4z();
+        mx = fmaxf(mx, amax4(y[k]));
+    }
+    if (r.xn_out) {
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            if (g < NG) ((float4*)r.xn_out)[g] = y[k];
         }
+        return;
+    }
+    const float sc = r.a.row_scale(t, r.a.split ? block_max(mx, slot + 8) : 0.0f);
+#pragma unroll
+    for (int k = 0; k < MG; ++k) {
+        const int g = tid + k * NT;
+        if (g < NG) r.a.put4(t, 4 * g, y[k], sc);
     }
 }
 
 // GEMM of the prefill: out[s][t][row] = sum over split s's column blocks of
-// A[t][k] * W[row][k].  Workgroup = 64 token rows x 64 weight rows (one wave
-// per 16 weight rows, 4 token subtiles of 16 per wave) x one split.
+// A[t][k] * W[row][k].
 struct PfGemm {
     PfA a;
     DMat w;
@@ -2332,60 +2356,102 @@ struct PfGemm {
     int ldo;
 };
 
-// bf16 bits of (q0 - 8) | (q1 - 8) << 16 for 4-bit codes: the integer is
-// exact in f32 (8388608 + q - 8388616) and in bf16.
-__device__ __forceinline__ uint32_t q4_bf16_pair(uint32_t q0, uint32_t q1) {
-    const float f0 = __uint_as_float(0x4B000000u | q0) - 8388616.0f;
-    const float f1 = __uint_as_float(0x4B000000u | q1) - 8388616.0f;
-    return (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+// (q - 8) as fp16 for the two nibbles of w at bits [s, s+4) and [s+16, s+20):
+// 1024 + q is 0x6400 | q in fp16, and 1024 + q - 1032 is exact.
+__device__ __forceinline__ uint32_t q4_f16_pair(uint32_t w, int s) {
+    const uint32_t v = ((w >> s) & 0x000F000Fu) | 0x64006400u;
+    const f16x2_t h = __builtin_bit_cast(f16x2_t, v) - f16x2_t{(_Float16)1032.0f, (_Float16)1032.0f};
+    return __builtin_bit_cast(uint32_t, h);
 }
 
-// Q4_0 weights on v_mfma_f32_16x16x32_bf16: one 32-column block per MFMA
-// (A = 16 tokens x 32 columns, B = 32 columns x 16 weight rows), three MFMAs
-// per block (hi, mid, lo parts of A) into a fresh accumulator that is then
-// scaled by the block's d: the products (q - 8) * part are exact.
+// The 8 fp16 weights of code dword w (bytes 4g..4g+3 of a row's block), in
+// the order of the A column permutation.
+__device__ __forceinline__ uint4 q4_f16_frag(uint32_t w) {
+    return make_uint4(q4_f16_pair(w, 0), q4_f16_pair(w, 8), q4_f16_pair(w, 4), q4_f16_pair(w, 12));
+}
+
+constexpr int PF_DEPTH = 4;  // column blocks in flight per workgroup
+
+// Q4_0 weights on v_mfma_f32_16x16x32_f16.  Workgroup = 64 token rows x one
+// 128-row weight tile x one split; wave w owns token rows 16w..16w+15 and
+// all 8 row subtiles.
+// Per 32-column block (one MFMA K step):
+//   1. the workgroup unpacks the block's codes of its 128 rows once into
+//      LDS as fp16 fragments, and its scales as f32;
+//   2. each wave runs 2 MFMAs (hi, lo parts of A) per row subtile into a
+//      fresh accumulator, then adds d * that to the running sum.
+// Codes, scales and A fragments are loaded PF_DEPTH blocks ahead.  The LDS
+// fragments are double-buffered, with one barrier per block.
 __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int tile = blockIdx.x >> 1;
-    const int lr = (blockIdx.x & 1) * 64 + wave * 16 + (lane & 15);
-    const int t0 = blockIdx.y * 64;
-    const int kb0 = blockIdx.z * g.kb_per, kb1 = min(g.w.nblk, kb0 + g.kb_per);
-    const int gq = lane >> 4;
+    __shared__ __align__(16) uint4 bs[2][8][64];
+    __shared__ float ss[2][TILE_ROWS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tile = blockIdx.x;
+    const int t0 = blockIdx.y * 64 + 16 * wave;
+    const int kb0 = blockIdx.z * g.kb_per, nk = min(g.w.nblk, kb0 + g.kb_per) - kb0;
     const int K = g.a.K;
     const size_t pstride = (size_t)g.a.Pp * K;
-    const uint16_t* ab = (const uint16_t*)g.a.p + (size_t)(t0 + (lane & 15)) * K + 8 * gq;
-    const uint32_t* codes = (const uint32_t*)g.w.codes;
-    f32x4_t acc[4];
+    const uint16_t* abase = (const uint16_t*)g.a.p + (size_t)(t0 + (lane & 15)) * K + 8 * (lane >> 4);
+    const uint32_t* codes = (const uint32_t*)g.w.codes + ((size_t)tile * g.w.nblk + kb0) * TILE_ROWS * 4;
+    const uint16_t* scales = g.w.scales + ((size_t)tile * g.w.nblk + kb0) * TILE_ROWS;
+    // this thread's two code dwords of a block: items tid and tid + 256 of
+    // 512 = 128 rows x 4; item -> (row = item >> 2, g = item & 3) -> LDS
+    // fragment (subtile row >> 4, lane (row & 15) + 16 g)
+    const int r1 = tid >> 2, r2 = (tid + 256) >> 2, gq = tid & 3;
+    uint4* const frag1 = &bs[0][r1 >> 4][(r1 & 15) + 16 * gq];
+    uint4* const frag2 = &bs[0][r2 >> 4][(r2 & 15) + 16 * gq];
+    uint32_t rb1[PF_DEPTH], rb2[PF_DEPTH];
+    uint16_t rs[PF_DEPTH];
+    uint4 ra0[PF_DEPTH], ra1[PF_DEPTH];
+    auto load = [&](int j, int i) {
+        const uint32_t* cb = codes + (size_t)i * TILE_ROWS * 4;
+        rb1[j] = __builtin_nontemporal_load(cb + tid);
+        rb2[j] = __builtin_nontemporal_load(cb + tid + 256);
+        rs[j] = tid < TILE_ROWS ? scales[(size_t)i * TILE_ROWS + tid] : (uint16_t)0;
+        const uint16_t* ap = abase + (size_t)(kb0 + i) * 32;
+        ra0[j] = *(const uint4*)ap;
+        ra1[j] = *(const uint4*)(ap + pstride);
+    };
+    f32x4_t acc[8];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc[m] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kb = kb0; kb < kb1; ++kb) {
-        const size_t idx = ((size_t)tile * g.w.nblk + kb) * TILE_ROWS + lr;
-        const uint32_t wd = codes[idx * 4 + gq];
-        const float d = h2f(g.w.scales[idx]);
-        uint4 u;
-        u.x = q4_bf16_pair(wd & 15u, (wd >> 8) & 15u);
-        u.y = q4_bf16_pair((wd >> 16) & 15u, (wd >> 24) & 15u);
-        u.z = q4_bf16_pair((wd >> 4) & 15u, (wd >> 12) & 15u);
-        u.w = q4_bf16_pair((wd >> 20) & 15u, wd >> 28);
-        const bf16x8_t b = __builtin_bit_cast(bf16x8_t, u);
+    for (int n = 0; n < 8; ++n) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const uint16_t* ap = ab + (size_t)(16 * m) * K + (size_t)kb * 32;
-            const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, *(const uint4*)ap);
-            const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, *(const uint4*)(ap + pstride));
-            const bf16x8_t a2 = __builtin_bit_cast(bf16x8_t, *(const uint4*)(ap + 2 * pstride));
-            f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b, c, 0, 0, 0);
-            acc[m] += d * c;
+    for (int j = 0; j < PF_DEPTH; ++j)
+        if (j < nk) load(j, j);
+    for (int base = 0; base < nk; base += PF_DEPTH) {
+#pragma unroll
+        for (int j = 0; j < PF_DEPTH; ++j) {
+            const int i = base + j;
+            if (i >= nk) break;
+            const int buf = j & 1;  // == i & 1: PF_DEPTH is even
+            frag1[buf * 8 * 64] = q4_f16_frag(rb1[j]);
+            frag2[buf * 8 * 64] = q4_f16_frag(rb2[j]);
+            if (tid < TILE_ROWS) ss[buf][tid] = h2f(rs[j]);
+            const f16x8_t a0 = __builtin_bit_cast(f16x8_t, ra0[j]);
+            const f16x8_t a1 = __builtin_bit_cast(f16x8_t, ra1[j]);
+            __syncthreads();
+            if (i + PF_DEPTH < nk) load(j, i + PF_DEPTH);
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                const f16x8_t b = __builtin_bit_cast(f16x8_t, bs[buf][n][lane]);
+                const float d = ss[buf][16 * n + (lane & 15)];
+                f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, c, 0, 0, 0);
+                acc[n] += d * c;
+            }
         }
     }
-    // lane holds rows 4*gq .. 4*gq+3 of each 16-token subtile, column lane & 15
-    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + t0 + 4 * gq) * g.ldo + (size_t)tile * TILE_ROWS + lr;
+    // lane holds token rows 4*(lane>>4) .. +3 of the wave's 16, weight row
+    // 16 n + (lane & 15) of the tile
+    const int tr = t0 + 4 * (lane >> 4);
+    float inv[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int r = 0; r < 4; ++r) inv[r] = g.a.inv_scale[tr + r];
+    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + tr) * g.ldo + (size_t)tile * TILE_ROWS + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[(size_t)(16 * m + r) * g.ldo] = acc[m][r];
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[(size_t)r * g.ldo + 16 * n] = acc[n][r] * inv[r];
 }
 
 // f32 weights on v_mfma_f32_16x16x4_f32: one 4-column block per MFMA.
@@ -2475,22 +2541,34 @@ __global__ __launch_bounds__(NT) void k_pf_attn(AttnArgs a, const float* q, int 
 }
 
 // o = o_unnormalised / l per head (the one-chunk merge) -> GEMM operand A.
+// The row (all heads) is staged in dynamic LDS for its scale.
 template <int HD, int G>
 __global__ __launch_bounds__(NT) void k_pf_attn_out(const float* state, int nkv, PfA a) {
-    const int t = blockIdx.x;
+    extern __shared__ __align__(16) float rowbuf[];
+    __shared__ float slot[4];
+    const int t = blockIdx.x, n = nkv * G * HD;
     const float* st = state + (size_t)t * nkv * G * (HD + 2);
-    for (int i = 4 * threadIdx.x; i < nkv * G * HD; i += 4 * NT) {
+    float mx = 0.0f;
+    for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) {
         const int h = i / HD, d = i % HD, g = h / G, hl = h % G;
         const float* sg = st + (size_t)g * G * (HD + 2);
         const float l = sg[G + hl];
         const float* o = sg + 2 * G + hl * HD + d;
-        a.put4(t, i, make_float4(o[0] / l, o[1] / l, o[2] / l, o[3] / l));
+        const float4 v = make_float4(o[0] / l, o[1] / l, o[2] / l, o[3] / l);
+        *(float4*)&rowbuf[i] = v;
+        mx = fmaxf(mx, amax4(v));
     }
+    const float sc = a.row_scale(t, block_max(mx, slot));  // barrier: rowbuf complete
+    for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) a.put4(t, i, *(const float4*)&rowbuf[i], sc);
 }
 
 // h = gelu_tanh(sum_s g_s) * sum_s u_s (MLP.hs:384-447) -> GEMM operand A.
+// The row is staged in dynamic LDS (F floats) for its scale.
 __global__ __launch_bounds__(NT) void k_pf_geglu(const float* part, int S, int ld, int Pp, int F, int up_off, PfA a) {
+    extern __shared__ __align__(16) float rowbuf[];
+    __shared__ float slot[4];
     const int t = blockIdx.x;
+    float mx = 0.0f;
     for (int i = 4 * threadIdx.x; i < F; i += 4 * NT) {
         float4 gs = f4z(), us = f4z();
         for (int s = 0; s < S; ++s) {
@@ -2498,16 +2576,21 @@ __global__ __launch_bounds__(NT) void k_pf_geglu(const float* part, int S, int l
             gs = gs + *(const float4*)(row + i);
             us = us + *(const float4*)(row + up_off + i);
         }
-        a.put4(t, i, make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y, gelu_tanh(gs.z) * us.z,
-                                 gelu_tanh(gs.w) * us.w));
+        const float4 h = make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y, gelu_tanh(gs.z) * us.z,
+                                     gelu_tanh(gs.w) * us.w);
+        *(float4*)&rowbuf[i] = h;
+        mx = fmaxf(mx, amax4(h));
     }
+    const float sc = a.row_scale(t, block_max(mx, slot));  // barrier: rowbuf complete
+    for (int i = 4 * threadIdx.x; i < F; i += 4 * NT) a.put4(t, i, *(const float4*)&rowbuf[i], sc);
 }
 
-// Split count of a prefill GEMM over Pp token rows: enough workgroups for
-// two per CU, at most 8 splits.
+// Split count of a prefill GEMM over Pp token rows: none when the grid has
+// 192 workgroups or more (the partials would cost more HBM traffic than the
+// idle CUs), else enough for two per CU, at most 8.
 int pf_splits(const DMat& w, int Pp, int* kb_per) {
-    const int wgs = w.tiles * 2 * (Pp / 64);
-    int S = std::max(1, std::min(8, (512 + wgs - 1) / wgs));
+    const int wgs = (w.fmt == FMT_Q4 ? w.tiles : 2 * w.tiles) * (Pp / 64);
+    int S = wgs >= 192 ? 1 : std::max(1, std::min(8, (512 + wgs - 1) / wgs));
     S = std::min(S, w.nblk);
     const int per = (w.nblk + S - 1) / S;
     if (kb_per) *kb_per = per;
@@ -2528,7 +2611,9 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
     const float eps = c.rms_eps;
     const size_t kv_layer = (size_t)kv->max_seq * nkv * hd;
     const int split = m->fmt == FMT_Q4 ? 1 : 0;
-    auto A = [&](int K) { return PfA{B.a, Pp, K, split}; };
+    auto A = [&](int K) { return PfA{B.a, Pp, K, split, B.ascale}; };
+    if ((size_t)F * sizeof(float) > 65536 || (size_t)c.n_heads * hd * sizeof(float) > 65536)
+        return set_error(GH_ERR_INVALID, "prefill: ffn %d / heads x head_dim %d above 16384", F, c.n_heads * hd);
     // GEMM of operand A (K columns) with w into the partials; returns S
     auto gemm = [&](const char* name, const DMat& w, int* S_out) -> int {
         int per = 0;
@@ -2537,9 +2622,9 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
             return set_error(GH_ERR_INVALID, "internal: prefill partials too small");
         *S_out = S;
         PfGemm g{A(w.cols), w, per, B.part, w.tiles * TILE_ROWS};
-        const dim3 grid(w.tiles * 2, Pp / 64, S), block(NT);
-        return w.fmt == FMT_Q4 ? sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4, grid, block, 0, g)
-                               : sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_f32, grid, block, 0, g);
+        if (w.fmt == FMT_Q4)
+            return sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4, dim3(w.tiles, Pp / 64, S), dim3(NT), 0, g);
+        return sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_f32, dim3(w.tiles * 2, Pp / 64, S), dim3(NT), 0, g);
     };
     auto rows = [&](const char* name, PfRows r, int n_rows) {
         return with_mg(H, [&](auto mg) {
@@ -2619,8 +2704,8 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
     if (hd == HD_ && G == G_) {                                                                                  \
         GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_attn<HD_, G_>, dim3(n * nkv), dim3(NT), 0, a,            \
                              (const float*)B.q, pos0, B.st));                                                   \
-        GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT), 0,            \
-                             (const float*)B.st, nkv, ao));                                                     \
+        GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT),                \
+                             sizeof(float) * c.n_heads * hd, (const float*)B.st, nkv, ao));                     \
     } else
             GH_PF_ATTN(256, 1) GH_PF_ATTN(256, 2) GH_PF_ATTN(256, 4) GH_PF_ATTN(256, 8)
             GH_PF_ATTN(128, 1) GH_PF_ATTN(128, 2) GH_PF_ATTN(128, 4) GH_PF_ATTN(128, 8)
@@ -2648,7 +2733,7 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
             GH_CHECK(rows("pf_rows", r, n));
         }
         GH_CHECK(gemm("pf_gate_up", L.gu, &S));
-        GH_CHECK(sink_launch(sink, "pf_geglu", 0.0, k_pf_geglu, dim3(n), dim3(NT), 0, (const float*)B.part, S,
+        GH_CHECK(sink_launch(sink, "pf_geglu", 0.0, k_pf_geglu, dim3(n), dim3(NT), sizeof(float) * F, (const float*)B.part, S,
                              L.gu.tiles * TILE_ROWS, Pp, F, m->f_pad, A(F)));
         GH_CHECK(gemm("pf_down", L.down, &S));
     }

@@ -224,7 +224,7 @@ int ensure_scratch(gh_model* m) {
 
 void free_prefill(gh_model* m) {
     PfBufs& B = m->pf;
-    for (void* p : {(void*)B.x, (void*)B.x1, B.a, (void*)B.q, (void*)B.st, (void*)B.tok, (void*)B.part})
+    for (void* p : {(void*)B.x, (void*)B.x1, B.a, (void*)B.ascale, (void*)B.q, (void*)B.st, (void*)B.tok, (void*)B.part})
         if (p) hipFree(p);
     B = PfBufs{};
 }
@@ -255,7 +255,8 @@ int prefill_reserve(gh_model* m, int n) {
     };
     GH_CHECK(get((void**)&B.x, sizeof(float) * cap * H));
     GH_CHECK(get((void**)&B.x1, sizeof(float) * cap * H));
-    GH_CHECK(get(&B.a, (m->fmt == FMT_Q4 ? 6 : 4) * (size_t)cap * kmax));
+    GH_CHECK(get(&B.a, sizeof(float) * cap * kmax));  // 2 fp16 parts or 1 f32
+    GH_CHECK(get((void**)&B.ascale, sizeof(float) * cap));
     GH_CHECK(get((void**)&B.q, sizeof(float) * cap * nq * hd));
     GH_CHECK(get((void**)&B.st, sizeof(float) * cap * nq * (hd + 2)));
     GH_CHECK(get((void**)&B.tok, sizeof(int32_t) * cap));
@@ -1099,11 +1100,37 @@ extern "C" int gh_bench_decode(gh_model* m, gh_kv* kv, const int32_t* prompt, in
                           ids_out);
 }
 
+// Per-kernel-kind totals of a profiled run; releases the events.
+static int collect_stats(Profiler& prof, gh_kernel_stat* stats, int32_t max_stats, int32_t* n_stats) {
+    std::vector<double> tot(prof.names.size(), 0.0), bytes(prof.names.size(), 0.0);
+    std::vector<int> cnt(prof.names.size(), 0);
+    for (auto& r : prof.recs) {
+        float ms = 0.0f;
+        hipEventElapsedTime(&ms, r.a, r.b);
+        tot[r.kind] += ms;
+        bytes[r.kind] += r.bytes;
+        cnt[r.kind] += 1;
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+    }
+    prof.recs.clear();
+    const int n = std::min<int>((int)prof.names.size(), max_stats);
+    for (int i = 0; i < n; ++i) {
+        std::memset(&stats[i], 0, sizeof(gh_kernel_stat));
+        std::snprintf(stats[i].name, sizeof(stats[i].name), "%s", prof.names[i].c_str());
+        stats[i].launches = cnt[i];
+        stats[i].total_ms = tot[i];
+        stats[i].bytes = cnt[i] ? bytes[i] / cnt[i] : 0.0;
+    }
+    *n_stats = n;
+    return GH_OK;
+}
+
 // Batched prefill of n tokens at the cache's next positions, in passes of
 // up to PF_MAX_TOKENS; the last token's logits, layer outputs and next token
 // are those of gh_step at that position.
 static int prefill_run(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, float* logits, float* layer_out,
-                       int32_t* next_out) {
+                       int32_t* next_out, Profiler* prof = nullptr) {
     const gh_config& c = m->cfg;
     if (!tokens || n <= 0) return set_error(GH_ERR_INVALID, "prefill: empty token list");
     for (int i = 0; i < n; ++i)
@@ -1116,6 +1143,7 @@ static int prefill_run(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n,
     GH_CHECK(put_state(kv, kv->len + n - 1, tokens[n - 1], kv->len, 0, 0));
     Sink sink;
     sink.s = s;
+    sink.prof = prof;
     for (int done = 0; done < n;) {
         const int k = std::min(PF_MAX_TOKENS, n - done);
         GH_HIP(hipMemcpyAsync(m->pf.tok, tokens + done, sizeof(int32_t) * k, hipMemcpyHostToDevice, s));
@@ -1181,28 +1209,21 @@ extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kern
     }
     GH_CHECK(get_state(kv));
     GH_HIP(hipStreamSynchronize(s));
-    std::vector<double> tot(prof.names.size(), 0.0), bytes(prof.names.size(), 0.0);
-    std::vector<int> cnt(prof.names.size(), 0);
-    for (auto& r : prof.recs) {
-        float ms = 0.0f;
-        hipEventElapsedTime(&ms, r.a, r.b);
-        tot[r.kind] += ms;
-        bytes[r.kind] += r.bytes;
-        cnt[r.kind] += 1;
-        hipEventDestroy(r.a);
-        hipEventDestroy(r.b);
-    }
-    if (rc != GH_OK) return rc;
-    const int n = std::min<int>((int)prof.names.size(), max_stats);
-    for (int i = 0; i < n; ++i) {
-        std::memset(&stats[i], 0, sizeof(gh_kernel_stat));
-        std::snprintf(stats[i].name, sizeof(stats[i].name), "%s", prof.names[i].c_str());
-        stats[i].launches = cnt[i];
-        stats[i].total_ms = tot[i];
-        stats[i].bytes = cnt[i] ? bytes[i] / cnt[i] : 0.0;
-    }
-    *n_stats = n;
-    return GH_OK;
+    const int rc2 = collect_stats(prof, stats, max_stats, n_stats);
+    return rc != GH_OK ? rc : rc2;
+}
+
+extern "C" int gh_prefill_profile(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, gh_kernel_stat* stats,
+                                  int32_t max_stats, int32_t* n_stats) {
+    if (!m || !kv || kv->m != m || !stats || !n_stats) return set_error(GH_ERR_INVALID, "bad arguments");
+    GH_CHECK(ctx_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_ready(m));
+    Profiler prof;
+    const int rc = prefill_run(m, kv, tokens, n, nullptr, nullptr, nullptr, &prof);
+    GH_HIP(hipStreamSynchronize(m->ctx->stream));
+    const int rc2 = collect_stats(prof, stats, max_stats, n_stats);
+    return rc != GH_OK ? rc : rc2;
 }
 
 extern "C" int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t n_reps, double* avg_us_out,

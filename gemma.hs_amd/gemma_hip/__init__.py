@@ -31,7 +31,7 @@ GemmaConfig = GhConfig
 __all__ = [
     "GemmaConfig", "GemmaHipError", "Context", "DeviceBuffer", "Q4Tensor", "GemmaModel", "KVCache",
     "preset", "runLinearQ4", "runGemmaInferenceCached", "runGemmaInferenceCachedWithLayer0",
-    "generate", "prefill", "bench_decode", "profile_steps", "sample_logits", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
+    "generate", "prefill", "bench_decode", "profile_steps", "profile_prefill", "sample_logits", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
     "tensor_list", "synth_tensors", "device_count", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q4_0",
     "MODE_GEMMA3", "MODE_REF", "FLAG_QK_NORM", "FLAG_POST_ATTN_NORM", "FLAG_POST_FFN_NORM",
     "FLAG_ZERO_CENTERED", "FLAG_IEEE_SCALES",
@@ -517,6 +517,17 @@ def profile_steps(model: GemmaModel, cache: KVCache, n_steps: int) -> list[Kerne
     arr = (GhKernelStat * 32)()
     n = C.c_int32()
     check(lib().gh_profile_steps(model.h, cache.h, n_steps, arr, 32, C.byref(n)))
+    return [KernelStat(arr[i].name.decode(), arr[i].launches, arr[i].total_ms, arr[i].bytes)
+            for i in range(n.value)]
+
+
+def profile_prefill(model: GemmaModel, cache: KVCache, tokens) -> list[KernelStat]:
+    """gh_prefill of the tokens with per-kernel event timing (the cache
+    advances as with prefill)."""
+    t = np.ascontiguousarray(tokens, dtype=np.int32)
+    arr = (GhKernelStat * 32)()
+    n = C.c_int32()
+    check(lib().gh_prefill_profile(model.h, cache.h, _ptr(t), len(t), arr, 32, C.byref(n)))
     return [KernelStat(arr[i].name.decode(), arr[i].launches, arr[i].total_ms, arr[i].bytes)
             for i in range(n.value)]
 

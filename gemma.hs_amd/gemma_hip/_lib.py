@@ -100,6 +100,7 @@ SIGNATURES = {
     "gh_generate_prefill": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     "gh_bench_decode": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, C.c_int32, _F, _P]),
     "gh_profile_steps": (C.c_int, [_P, _P, C.c_int32, C.POINTER(GhKernelStat), C.c_int32, _I32]),
+    "gh_prefill_profile": (C.c_int, [_P, _P, _P, C.c_int32, C.POINTER(GhKernelStat), C.c_int32, _I32]),
     "gh_capture_begin": (C.c_int, [_P]),
     "gh_capture_replay": (C.c_int, [_P, C.c_int32, C.POINTER(C.c_float)]),
     "gh_timer_start": (C.c_int, [_P]),

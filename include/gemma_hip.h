@@ -255,6 +255,11 @@ typedef struct gh_kernel_stat {
 } gh_kernel_stat;
 int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kernel_stat* stats,
                      int32_t max_stats, int32_t* n_stats_out);
+/* gh_prefill of n tokens with HIP events around every kernel: the same
+ * per-kernel-kind statistics (no reference counterpart: the reference has
+ * no prefill).  The cache advances by n as with gh_prefill. */
+int gh_prefill_profile(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, gh_kernel_stat* stats,
+                       int32_t max_stats, int32_t* n_stats_out);
 /* Kernel timing for the roofline: replays only the step kernels named
  * `name` ("qkv", "attention", "o_proj", "gate_up", "down", "final_norm",
  * "lm_head") of one step at the cache's current position, n_reps times
