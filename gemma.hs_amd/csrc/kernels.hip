@@ -2372,49 +2372,55 @@ __device__ __forceinline__ uint4 q4_f16_frag(uint32_t w) {
 
 constexpr int PF_DEPTH = 4;  // column blocks in flight per workgroup
 
-// Q4_0 weights on v_mfma_f32_16x16x32_f16.  Workgroup = 64 token rows x one
-// 128-row weight tile x one split; wave w owns token rows 16w..16w+15 and
-// all 8 row subtiles.
+// Q4_0 weights on v_mfma_f32_16x16x32_f16.  Workgroup = 64 token rows x
+// 16*NS weight rows (NS = 8: one 128-row tile, NS = 4: half a tile) x one
+// split; wave w owns token rows 16w..16w+15 and all NS row subtiles.
 // Per 32-column block (one MFMA K step):
-//   1. the workgroup unpacks the block's codes of its 128 rows once into
-//      LDS as fp16 fragments, and its scales as f32;
+//   1. the workgroup unpacks the block's codes of its rows once into LDS as
+//      fp16 fragments, and its scales as f32;
 //   2. each wave runs 2 MFMAs (hi, lo parts of A) per row subtile into a
 //      fresh accumulator, then adds d * that to the running sum.
 // Codes, scales and A fragments are loaded PF_DEPTH blocks ahead.  The LDS
 // fragments are double-buffered, with one barrier per block.
+template <int NS>
 __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
-    __shared__ __align__(16) uint4 bs[2][8][64];
-    __shared__ float ss[2][TILE_ROWS];
+    constexpr int R = 16 * NS;       // weight rows per workgroup
+    constexpr int NI = R * 4 / NT;   // code dwords per thread per block
+    static_assert(NI >= 1 && NI * NT == R * 4, "NS must be 4 or 8");
+    __shared__ __align__(16) uint4 bs[2][NS][64];
+    __shared__ float ss[2][R];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.x / (8 / NS), r0 = (blockIdx.x % (8 / NS)) * R;
     const int t0 = blockIdx.y * 64 + 16 * wave;
     const int kb0 = blockIdx.z * g.kb_per, nk = min(g.w.nblk, kb0 + g.kb_per) - kb0;
     const int K = g.a.K;
     const size_t pstride = (size_t)g.a.Pp * K;
     const uint16_t* abase = (const uint16_t*)g.a.p + (size_t)(t0 + (lane & 15)) * K + 8 * (lane >> 4);
-    const uint32_t* codes = (const uint32_t*)g.w.codes + ((size_t)tile * g.w.nblk + kb0) * TILE_ROWS * 4;
-    const uint16_t* scales = g.w.scales + ((size_t)tile * g.w.nblk + kb0) * TILE_ROWS;
-    // this thread's two code dwords of a block: items tid and tid + 256 of
-    // 512 = 128 rows x 4; item -> (row = item >> 2, g = item & 3) -> LDS
-    // fragment (subtile row >> 4, lane (row & 15) + 16 g)
-    const int r1 = tid >> 2, r2 = (tid + 256) >> 2, gq = tid & 3;
-    uint4* const frag1 = &bs[0][r1 >> 4][(r1 & 15) + 16 * gq];
-    uint4* const frag2 = &bs[0][r2 >> 4][(r2 & 15) + 16 * gq];
-    uint32_t rb1[PF_DEPTH], rb2[PF_DEPTH];
+    const uint32_t* codes = (const uint32_t*)g.w.codes + ((size_t)tile * g.w.nblk + kb0) * TILE_ROWS * 4 + r0 * 4;
+    const uint16_t* scales = g.w.scales + ((size_t)tile * g.w.nblk + kb0) * TILE_ROWS + r0;
+    // code dword item = tid + NT*q of the block's R x 4 -> (row = item >> 2,
+    // g = item & 3) -> LDS fragment (subtile row >> 4, lane (row & 15) + 16 g)
+    uint4* frag[NI];
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+        const int item = tid + NT * q, row = item >> 2;
+        frag[q] = &bs[0][row >> 4][(row & 15) + 16 * (item & 3)];
+    }
+    uint32_t rb[PF_DEPTH][NI];
     uint16_t rs[PF_DEPTH];
     uint4 ra0[PF_DEPTH], ra1[PF_DEPTH];
     auto load = [&](int j, int i) {
         const uint32_t* cb = codes + (size_t)i * TILE_ROWS * 4;
-        rb1[j] = __builtin_nontemporal_load(cb + tid);
-        rb2[j] = __builtin_nontemporal_load(cb + tid + 256);
-        rs[j] = tid < TILE_ROWS ? scales[(size_t)i * TILE_ROWS + tid] : (uint16_t)0;
+#pragma unroll
+        for (int q = 0; q < NI; ++q) rb[j][q] = __builtin_nontemporal_load(cb + tid + NT * q);
+        rs[j] = tid < R ? scales[(size_t)i * TILE_ROWS + tid] : (uint16_t)0;
         const uint16_t* ap = abase + (size_t)(kb0 + i) * 32;
         ra0[j] = *(const uint4*)ap;
         ra1[j] = *(const uint4*)(ap + pstride);
     };
-    f32x4_t acc[8];
+    f32x4_t acc[NS];
 #pragma unroll
-    for (int n = 0; n < 8; ++n) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int n = 0; n < NS; ++n) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < PF_DEPTH; ++j)
         if (j < nk) load(j, j);
@@ -2424,15 +2430,15 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
             const int i = base + j;
             if (i >= nk) break;
             const int buf = j & 1;  // == i & 1: PF_DEPTH is even
-            frag1[buf * 8 * 64] = q4_f16_frag(rb1[j]);
-            frag2[buf * 8 * 64] = q4_f16_frag(rb2[j]);
-            if (tid < TILE_ROWS) ss[buf][tid] = h2f(rs[j]);
+#pragma unroll
+            for (int q = 0; q < NI; ++q) frag[q][buf * NS * 64] = q4_f16_frag(rb[j][q]);
+            if (tid < R) ss[buf][tid] = h2f(rs[j]);
             const f16x8_t a0 = __builtin_bit_cast(f16x8_t, ra0[j]);
             const f16x8_t a1 = __builtin_bit_cast(f16x8_t, ra1[j]);
             __syncthreads();
             if (i + PF_DEPTH < nk) load(j, i + PF_DEPTH);
 #pragma unroll
-            for (int n = 0; n < 8; ++n) {
+            for (int n = 0; n < NS; ++n) {
                 const f16x8_t b = __builtin_bit_cast(f16x8_t, bs[buf][n][lane]);
                 const float d = ss[buf][16 * n + (lane & 15)];
                 f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
@@ -2442,17 +2448,21 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
         }
     }
     // lane holds token rows 4*(lane>>4) .. +3 of the wave's 16, weight row
-    // 16 n + (lane & 15) of the tile
+    // r0 + 16 n + (lane & 15) of the tile
     const int tr = t0 + 4 * (lane >> 4);
     float inv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) inv[r] = g.a.inv_scale[tr + r];
-    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + tr) * g.ldo + (size_t)tile * TILE_ROWS + (lane & 15);
+    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + tr) * g.ldo + (size_t)tile * TILE_ROWS + r0 + (lane & 15);
 #pragma unroll
-    for (int n = 0; n < 8; ++n)
+    for (int n = 0; n < NS; ++n)
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[(size_t)r * g.ldo + 16 * n] = acc[n][r] * inv[r];
 }
+
+// Row-subtiles per workgroup of a Q4_0 prefill GEMM: whole tiles, unless
+// even 8 splits leave fewer than 512 workgroups; then half tiles.
+static int pf_ns(const DMat& w, int Pp) { return w.tiles * (Pp / 64) * 8 >= 512 ? 8 : 4; }
 
 // f32 weights on v_mfma_f32_16x16x4_f32: one 4-column block per MFMA.
 __global__ __launch_bounds__(NT) void k_pf_gemm_f32(PfGemm g) {
@@ -2585,12 +2595,12 @@ __global__ __launch_bounds__(NT) void k_pf_geglu(const float* part, int S, int l
     for (int i = 4 * threadIdx.x; i < F; i += 4 * NT) a.put4(t, i, *(const float4*)&rowbuf[i], sc);
 }
 
-// Split count of a prefill GEMM over Pp token rows: none when the grid has
-// 192 workgroups or more (the partials would cost more HBM traffic than the
-// idle CUs), else enough for two per CU, at most 8.
+// Split count of a prefill GEMM over Pp token rows: enough for two
+// workgroups per CU, at most 8 (the workgroups' own latency chain, not the
+// partials' traffic, is what bounds these GEMMs at prompt sizes).
 int pf_splits(const DMat& w, int Pp, int* kb_per) {
-    const int wgs = (w.fmt == FMT_Q4 ? w.tiles : 2 * w.tiles) * (Pp / 64);
-    int S = wgs >= 192 ? 1 : std::max(1, std::min(8, (512 + wgs - 1) / wgs));
+    const int wgs = (w.fmt == FMT_Q4 ? w.tiles * (8 / pf_ns(w, Pp)) : 2 * w.tiles) * (Pp / 64);
+    int S = std::max(1, std::min(8, (512 + wgs - 1) / wgs));
     S = std::min(S, w.nblk);
     const int per = (w.nblk + S - 1) / S;
     if (kb_per) *kb_per = per;
@@ -2622,8 +2632,12 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
             return set_error(GH_ERR_INVALID, "internal: prefill partials too small");
         *S_out = S;
         PfGemm g{A(w.cols), w, per, B.part, w.tiles * TILE_ROWS};
-        if (w.fmt == FMT_Q4)
-            return sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4, dim3(w.tiles, Pp / 64, S), dim3(NT), 0, g);
+        if (w.fmt == FMT_Q4) {
+            const int ns = pf_ns(w, Pp);
+            const dim3 grid(w.tiles * (8 / ns), Pp / 64, S);
+            return ns == 8 ? sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4<8>, grid, dim3(NT), 0, g)
+                           : sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4<4>, grid, dim3(NT), 0, g);
+        }
         return sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_f32, dim3(w.tiles * 2, Pp / 64, S), dim3(NT), 0, g);
     };
     auto rows = [&](const char* name, PfRows r, int n_rows) {
