@@ -175,7 +175,7 @@ struct PfBufs {
     void* a = nullptr;           // [2][cap][Kmax] fp16 (Q4_0 weights) or [cap][Kmax] f32: GEMM operand
     float* ascale = nullptr;     // [cap] inverse row scales of the fp16 operand
     float* q = nullptr;          // [cap][nq * hd] normed + roped queries
-    float* st = nullptr;         // [cap][nq][hd + 2] attention state (o, m, l) per token
+    float* st = nullptr;         // [cap][nkv][PF_ATTN_NC][G][hd + 2] attention chunk states per token
     int32_t* tok = nullptr;      // [cap] token ids of the chunk
     float* part = nullptr;       // split-K GEMM partials
     size_t part_floats = 0;
@@ -274,6 +274,7 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos);
 // pos0 .. pos0+n-1; with `head`, also the final norm, LM head and next-token
 // selection of the last of them (position pos0+n-1).
 constexpr int PF_MAX_TOKENS = 512;  // tokens per prefill pass
+constexpr int PF_ATTN_NC = 16;      // attention chunks per token and kv head in the prefill
 int pf_splits(const DMat& w, int Pp, int* kb_per);
 int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool head);
 int launch_q4_dequant(const DMat& w, float* out, hipStream_t s);

@@ -2295,7 +2295,7 @@ __global__ __launch_bounds__(NT) void k_pf_rows(PfRows r) {
             const int g = tid + k * NT;
             dv[k] = f4z();
             if (g < NG) {
-                for (int s = 0; s < r.S; ++s) dv[k] = dv[k] + ((const float4*)(r.part + ((size_t)s * r.Pp + t) * r.ld))[g];
+                dv[k] = sum_splits4(r.part + (size_t)t * r.ld, r.S, r.Pp * r.ld, g);
                 ss += dot4(dv[k], dv[k]);
             }
         }
@@ -2518,9 +2518,7 @@ __global__ __launch_bounds__(NT) void k_pf_qkv(PfQkv p) {
         const int row = i < G * HD ? p.q_off + g * G * HD + i
                       : i < (G + 1) * HD ? p.k_off + g * HD + (i - G * HD)
                                          : p.v_off + g * HD + (i - (G + 1) * HD);
-        float4 s = f4z();
-        for (int sp = 0; sp < p.S; ++sp) s = s + *(const float4*)(p.part + ((size_t)sp * p.Pp + t) * p.ld + row);
-        *(float4*)&buf[i] = s;
+        *(float4*)&buf[i] = sum_splits4(p.part + (size_t)t * p.ld, p.S, p.Pp * p.ld, row >> 2);
     }
     __syncthreads();
     const float2* cs = (const float2*)p.rope + (size_t)pos * (HD / 2);
@@ -2537,39 +2535,70 @@ __global__ __launch_bounds__(NT) void k_pf_qkv(PfQkv p) {
     }
 }
 
-// Attention of token t (kv head g) over its window of the cache, as one
-// chunk of the decode kernel's flash-decoding item; state per token.
+// Attention of token t (kv head g) over its window of the cache: the
+// window is split into up to a.nc (<= PF_ATTN_NC, from the host: one per 128
+// positions of the longest window) chunks of ATTN_SUB-multiple length, each
+// a workgroup running the decode kernel's flash-decoding item; the chunk
+// states {m, l, o} go to the token's slot of `state`.
 template <int HD, int G>
 __global__ __launch_bounds__(NT) void k_pf_attn(AttnArgs a, const float* q, int pos0, float* state) {
-    const int t = blockIdx.x / a.nkv, g = blockIdx.x % a.nkv;
+    const int j = blockIdx.x % a.nc, tg = blockIdx.x / a.nc;
+    const int t = tg / a.nkv, g = tg % a.nkv;
     AttnArgs b = a;
     b.q = q + (size_t)t * a.nkv * G * HD;
-    b.nc = 1;
     b.set_pos(pos0 + t);
-    attn_item<HD, G, false>(b, g, 0, QkvPartials{nullptr, 0, 0},
-                            AttnOutPlain{state + (size_t)t * a.nkv * G * (HD + 2)});
+    if (j >= b.n_used) return;  // uniform per workgroup
+    attn_item<HD, G, false>(b, g, j, QkvPartials{nullptr, 0, 0},
+                            AttnOutPlain{state + (size_t)t * a.nkv * PF_ATTN_NC * G * (HD + 2)});
 }
 
-// o = o_unnormalised / l per head (the one-chunk merge) -> GEMM operand A.
-// The row (all heads) is staged in dynamic LDS for its scale.
+// Merge of token t's chunk states per head, o = sum_j w_j o_j / sum_j w_j l_j
+// with w_j = exp(m_j - max_j m_j), into GEMM operand A.  The row (all heads)
+// is staged in dynamic LDS for its scale.
 template <int HD, int G>
-__global__ __launch_bounds__(NT) void k_pf_attn_out(const float* state, int nkv, PfA a) {
+__global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const float* state, PfA out) {
     extern __shared__ __align__(16) float rowbuf[];
+    __shared__ float wj[8 * G][PF_ATTN_NC];
+    __shared__ float den[8 * G];
     __shared__ float slot[4];
-    const int t = blockIdx.x, n = nkv * G * HD;
-    const float* st = state + (size_t)t * nkv * G * (HD + 2);
+    const int t = blockIdx.x, nq = a.nkv * G, n = nq * HD, tid = threadIdx.x;
+    AttnArgs b = a;
+    b.set_pos(pos0 + t);
+    const int nu = b.n_used;
+    const size_t cstride = (size_t)G * (HD + 2);  // one chunk state
+    const float* st = state + (size_t)t * a.nkv * PF_ATTN_NC * cstride;
+    // chunk weights per head (nq <= 8 G heads, one thread per head)
+    if (tid < nq) {
+        const int g = tid / G, hl = tid % G;
+        const float* sg = st + (size_t)g * a.nc * cstride;  // attn_item's layout: (g * nc + chunk)
+        float M = -INFINITY;
+        for (int c = 0; c < nu; ++c) M = fmaxf(M, sg[c * cstride + hl]);
+        float dsum = 0.0f;
+        for (int c = 0; c < nu; ++c) {
+            const float w = expf(sg[c * cstride + hl] - M);
+            wj[tid][c] = w;
+            dsum += w * sg[c * cstride + G + hl];
+        }
+        den[tid] = dsum;
+    }
+    __syncthreads();
     float mx = 0.0f;
-    for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) {
+    for (int i = 4 * tid; i < n; i += 4 * NT) {
         const int h = i / HD, d = i % HD, g = h / G, hl = h % G;
-        const float* sg = st + (size_t)g * G * (HD + 2);
-        const float l = sg[G + hl];
-        const float* o = sg + 2 * G + hl * HD + d;
-        const float4 v = make_float4(o[0] / l, o[1] / l, o[2] / l, o[3] / l);
+        const float* o = st + (size_t)g * a.nc * cstride + 2 * G + hl * HD + d;
+        float4 v = f4z();
+        for (int c = 0; c < nu; ++c) {
+            const float w = wj[h][c];
+            const float* oc = o + c * cstride;
+            v = make_float4(v.x + w * oc[0], v.y + w * oc[1], v.z + w * oc[2], v.w + w * oc[3]);
+        }
+        const float l = den[h];
+        v = make_float4(v.x / l, v.y / l, v.z / l, v.w / l);
         *(float4*)&rowbuf[i] = v;
         mx = fmaxf(mx, amax4(v));
     }
-    const float sc = a.row_scale(t, block_max(mx, slot));  // barrier: rowbuf complete
-    for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) a.put4(t, i, *(const float4*)&rowbuf[i], sc);
+    const float sc = out.row_scale(t, block_max(mx, slot));  // barrier: rowbuf complete
+    for (int i = 4 * tid; i < n; i += 4 * NT) out.put4(t, i, *(const float4*)&rowbuf[i], sc);
 }
 
 // h = gelu_tanh(sum_s g_s) * sum_s u_s (MLP.hs:384-447) -> GEMM operand A.
@@ -2622,8 +2651,9 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
     const size_t kv_layer = (size_t)kv->max_seq * nkv * hd;
     const int split = m->fmt == FMT_Q4 ? 1 : 0;
     auto A = [&](int K) { return PfA{B.a, Pp, K, split, B.ascale}; };
-    if ((size_t)F * sizeof(float) > 65536 || (size_t)c.n_heads * hd * sizeof(float) > 65536)
-        return set_error(GH_ERR_INVALID, "prefill: ffn %d / heads x head_dim %d above 16384", F, c.n_heads * hd);
+    if ((size_t)F * sizeof(float) > 65536 || (size_t)c.n_heads * hd * sizeof(float) > 65536 || nkv > 8)
+        return set_error(GH_ERR_INVALID, "prefill: ffn %d / heads x head_dim %d above 16384 or %d kv heads above 8", F,
+                         c.n_heads * hd, nkv);
     // GEMM of operand A (K columns) with w into the partials; returns S
     auto gemm = [&](const char* name, const DMat& w, int* S_out) -> int {
         int per = 0;
@@ -2712,14 +2742,15 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
             a.vc = kv->v + li * kv_layer;
             a.nkv = nkv;
             a.scale = 1.0f / sqrtf((float)hd);
-            a.nc = 1;
+            // chunks per token: one per 128 positions of the longest window
+            a.nc = std::max(1, std::min(PF_ATTN_NC, (pos0 + n + 127) / 128));
             const PfA ao = A(c.n_heads * hd);
 #define GH_PF_ATTN(HD_, G_)                                                                                      \
     if (hd == HD_ && G == G_) {                                                                                  \
-        GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_attn<HD_, G_>, dim3(n * nkv), dim3(NT), 0, a,            \
-                             (const float*)B.q, pos0, B.st));                                                   \
+        GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_attn<HD_, G_>, dim3(n * nkv * a.nc), dim3(NT), 0,        \
+                             a, (const float*)B.q, pos0, B.st));                                                \
         GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT),                \
-                             sizeof(float) * c.n_heads * hd, (const float*)B.st, nkv, ao));                     \
+                             sizeof(float) * c.n_heads * hd, a, pos0, (const float*)B.st, ao));                 \
     } else
             GH_PF_ATTN(256, 1) GH_PF_ATTN(256, 2) GH_PF_ATTN(256, 4) GH_PF_ATTN(256, 8)
             GH_PF_ATTN(128, 1) GH_PF_ATTN(128, 2) GH_PF_ATTN(128, 4) GH_PF_ATTN(128, 8)

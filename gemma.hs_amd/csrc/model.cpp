@@ -258,7 +258,7 @@ int prefill_reserve(gh_model* m, int n) {
     GH_CHECK(get(&B.a, sizeof(float) * cap * kmax));  // 2 fp16 parts or 1 f32
     GH_CHECK(get((void**)&B.ascale, sizeof(float) * cap));
     GH_CHECK(get((void**)&B.q, sizeof(float) * cap * nq * hd));
-    GH_CHECK(get((void**)&B.st, sizeof(float) * cap * nq * (hd + 2)));
+    GH_CHECK(get((void**)&B.st, sizeof(float) * cap * nq * PF_ATTN_NC * (hd + 2)));
     GH_CHECK(get((void**)&B.tok, sizeof(int32_t) * cap));
     GH_CHECK(get((void**)&B.part, sizeof(float) * part));
     B.part_floats = part;

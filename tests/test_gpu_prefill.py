@@ -99,6 +99,28 @@ def test_prefill_gqa_window_then_decode_live_oracle(ctx, mode):
         assert rel_err(logits, olog) < ACT_TOL, pos
 
 
+def test_prefill_gqa_long_window_chunks_live_oracle(ctx):
+    """GQA miniature (4 kv heads, group 2) with a 300-token prefill: the
+    attention of each token is split over several chunks (one per 128
+    positions), global layers attend to all 300 positions and local layers
+    to a 160-token window; the last token's layers and logits against the
+    oracle stepping the same tokens."""
+    cfg = _mini4b(gh.MODE_GEMMA3, window=160, layers=2)
+    cfg.max_seq = 320
+    m = _gpu_model(ctx, cfg, 17, True)
+    om = _oracle_model(cfg, 17, True)
+    toks = gh.synth_tokens(9, "long", 300, cfg.vocab)
+    for pos in range(len(toks) - 1):
+        om.step(int(toks[pos]), pos)
+    olog, olay, obest = om.step(int(toks[-1]), len(toks) - 1, want_layers=True)
+    kv = gh.KVCache(m, 320)
+    logits, layers, nxt = gh.prefill(m, kv, toks, want_layers=True)
+    for l in range(cfg.n_layers):
+        assert rel_err(layers[l], olay[l]) < ACT_TOL, l
+    assert rel_err(logits, olog) < ACT_TOL
+    assert nxt == obest
+
+
 def test_prefill_passes_chunks_and_ragged_sizes(ctx):
     """f32 tiny model, 600 tokens: one prefill call (two passes of 512 + 88
     rows), the same tokens as prefills of 1, 63, 65, 7 and 464 tokens, and
