@@ -2354,7 +2354,29 @@ struct PfGemm {
     int kb_per;  // column blocks per split
     float* out;  // [S][Pp][ldo]
     int ldo;
+    int X, Y, S;  // row groups, 64-token tiles, splits (the grid is 1-D, see pf_tile)
 };
+
+// XCD-aware workgroup order of the 1-D prefill GEMM grid.  Workgroups go to
+// the 8 XCDs round-robin (XCD = id % 8), each XCD with its own L2.  Key =
+// (row group x, split z) names the weight slice a workgroup reads; key k
+// runs on XCD k % 8, and its Y token tiles run back to back there, so the
+// slice is fetched from HBM once.  With 8 splits, split z lives on XCD z
+// only, so its column slice of A is fetched by one L2 as well.  Ids past
+// the last key return (fewer than 8 Y of them).
+struct PfTile {
+    int x, y, z;
+};
+__device__ __forceinline__ bool pf_tile(const PfGemm& g, PfTile& t) {
+    const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
+    t.y = j % g.Y;
+    const int key = (j / g.Y) * 8 + xcd;
+    if (key >= g.X * g.S) return false;
+    t.x = key / g.S;
+    t.z = key % g.S;
+    return true;
+}
+inline int pf_grid(int X, int Y, int S) { return (X * S + 7) / 8 * 8 * Y; }
 
 // (q - 8) as fp16 for the two nibbles of w at bits [s, s+4) and [s+16, s+20):
 // 1024 + q is 0x6400 | q in fp16, and 1024 + q - 1032 is exact.
@@ -2389,10 +2411,12 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
     static_assert(NI >= 1 && NI * NT == R * 4, "NS must be 4 or 8");
     __shared__ __align__(16) uint4 bs[2][NS][64];
     __shared__ float ss[2][R];
+    PfTile pt;
+    if (!pf_tile(g, pt)) return;  // uniform per workgroup
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = blockIdx.x / (8 / NS), r0 = (blockIdx.x % (8 / NS)) * R;
-    const int t0 = blockIdx.y * 64 + 16 * wave;
-    const int kb0 = blockIdx.z * g.kb_per, nk = min(g.w.nblk, kb0 + g.kb_per) - kb0;
+    const int tile = pt.x / (8 / NS), r0 = (pt.x % (8 / NS)) * R;
+    const int t0 = pt.y * 64 + 16 * wave;
+    const int kb0 = pt.z * g.kb_per, nk = min(g.w.nblk, kb0 + g.kb_per) - kb0;
     const int K = g.a.K;
     const size_t pstride = (size_t)g.a.Pp * K;
     const uint16_t* abase = (const uint16_t*)g.a.p + (size_t)(t0 + (lane & 15)) * K + 8 * (lane >> 4);
@@ -2409,12 +2433,16 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
     uint32_t rb[PF_DEPTH][NI];
     uint16_t rs[PF_DEPTH];
     uint4 ra0[PF_DEPTH], ra1[PF_DEPTH];
+    // Block i's loads into ring slot j.  Every call issues the same loads
+    // (indices clamped into range, no branches), so the wait counts stay
+    // static and the PF_DEPTH blocks in flight are not drained early.
     auto load = [&](int j, int i) {
-        const uint32_t* cb = codes + (size_t)i * TILE_ROWS * 4;
+        const int ic = min(i, nk - 1);
+        const uint32_t* cb = codes + (size_t)ic * TILE_ROWS * 4;
 #pragma unroll
-        for (int q = 0; q < NI; ++q) rb[j][q] = __builtin_nontemporal_load(cb + tid + NT * q);
-        rs[j] = tid < R ? scales[(size_t)i * TILE_ROWS + tid] : (uint16_t)0;
-        const uint16_t* ap = abase + (size_t)(kb0 + i) * 32;
+        for (int q = 0; q < NI; ++q) rb[j][q] = cb[tid + NT * q];
+        rs[j] = scales[(size_t)ic * TILE_ROWS + min(tid, R - 1)];
+        const uint16_t* ap = abase + (size_t)(kb0 + ic) * 32;
         ra0[j] = *(const uint4*)ap;
         ra1[j] = *(const uint4*)(ap + pstride);
     };
@@ -2422,8 +2450,7 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
 #pragma unroll
     for (int n = 0; n < NS; ++n) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < PF_DEPTH; ++j)
-        if (j < nk) load(j, j);
+    for (int j = 0; j < PF_DEPTH; ++j) load(j, j);
     for (int base = 0; base < nk; base += PF_DEPTH) {
 #pragma unroll
         for (int j = 0; j < PF_DEPTH; ++j) {
@@ -2436,7 +2463,7 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
             const f16x8_t a0 = __builtin_bit_cast(f16x8_t, ra0[j]);
             const f16x8_t a1 = __builtin_bit_cast(f16x8_t, ra1[j]);
             __syncthreads();
-            if (i + PF_DEPTH < nk) load(j, i + PF_DEPTH);
+            load(j, i + PF_DEPTH);
 #pragma unroll
             for (int n = 0; n < NS; ++n) {
                 const f16x8_t b = __builtin_bit_cast(f16x8_t, bs[buf][n][lane]);
@@ -2453,7 +2480,7 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
     float inv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) inv[r] = g.a.inv_scale[tr + r];
-    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + tr) * g.ldo + (size_t)tile * TILE_ROWS + r0 + (lane & 15);
+    float* o = g.out + ((size_t)pt.z * g.a.Pp + tr) * g.ldo + (size_t)tile * TILE_ROWS + r0 + (lane & 15);
 #pragma unroll
     for (int n = 0; n < NS; ++n)
 #pragma unroll
@@ -2466,11 +2493,13 @@ static int pf_ns(const DMat& w, int Pp) { return w.tiles * (Pp / 64) * 8 >= 512 
 
 // f32 weights on v_mfma_f32_16x16x4_f32: one 4-column block per MFMA.
 __global__ __launch_bounds__(NT) void k_pf_gemm_f32(PfGemm g) {
+    PfTile pt;
+    if (!pf_tile(g, pt)) return;  // uniform per workgroup
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int tile = blockIdx.x >> 1;
-    const int lr = (blockIdx.x & 1) * 64 + wave * 16 + (lane & 15);
-    const int t0 = blockIdx.y * 64;
-    const int kb0 = blockIdx.z * g.kb_per, kb1 = min(g.w.nblk, kb0 + g.kb_per);
+    const int tile = pt.x >> 1;
+    const int lr = (pt.x & 1) * 64 + wave * 16 + (lane & 15);
+    const int t0 = pt.y * 64;
+    const int kb0 = pt.z * g.kb_per, kb1 = min(g.w.nblk, kb0 + g.kb_per);
     const int kq = lane >> 4;
     const int K = g.a.K;
     const float* ab = (const float*)g.a.p + (size_t)(t0 + (lane & 15)) * K + kq;
@@ -2484,7 +2513,7 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_f32(PfGemm g) {
         for (int m = 0; m < 4; ++m)
             acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(ab[(size_t)(16 * m) * K + 4 * kb], bw, acc[m], 0, 0, 0);
     }
-    float* o = g.out + ((size_t)blockIdx.z * g.a.Pp + t0 + 4 * kq) * g.ldo + (size_t)tile * TILE_ROWS + lr;
+    float* o = g.out + ((size_t)pt.z * g.a.Pp + t0 + 4 * kq) * g.ldo + (size_t)tile * TILE_ROWS + lr;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -2661,14 +2690,13 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
         if ((size_t)S * Pp * w.tiles * TILE_ROWS > B.part_floats)
             return set_error(GH_ERR_INVALID, "internal: prefill partials too small");
         *S_out = S;
-        PfGemm g{A(w.cols), w, per, B.part, w.tiles * TILE_ROWS};
-        if (w.fmt == FMT_Q4) {
-            const int ns = pf_ns(w, Pp);
-            const dim3 grid(w.tiles * (8 / ns), Pp / 64, S);
+        const int ns = w.fmt == FMT_Q4 ? pf_ns(w, Pp) : 4;  // f32: 64-row groups
+        PfGemm g{A(w.cols), w, per, B.part, w.tiles * TILE_ROWS, w.tiles * (8 / ns), Pp / 64, S};
+        const dim3 grid(pf_grid(g.X, g.Y, g.S));
+        if (w.fmt == FMT_Q4)
             return ns == 8 ? sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4<8>, grid, dim3(NT), 0, g)
                            : sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_q4<4>, grid, dim3(NT), 0, g);
-        }
-        return sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_f32, dim3(w.tiles * 2, Pp / 64, S), dim3(NT), 0, g);
+        return sink_launch(sink, name, pf_gemm_bytes(w, n), k_pf_gemm_f32, grid, dim3(NT), 0, g);
     };
     auto rows = [&](const char* name, PfRows r, int n_rows) {
         return with_mg(H, [&](auto mg) {
