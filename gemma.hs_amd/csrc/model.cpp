@@ -657,7 +657,11 @@ extern "C" int gh_attention_decode(gh_ctx* ctx, const float* q, const float* kc,
         return set_error(GH_ERR_INVALID, "gh_attention_decode: bad arguments");
     const int n_pos = p_end - p_begin;
     // default: about 128 positions per chunk, up to GH_ATTN_OP_MAX_NC chunks per kv head
-    if (n_splits <= 0) n_splits = std::max(1, std::min((n_pos + 127) / 128, GH_ATTN_OP_MAX_NC));
+    // default: 32-position chunks up to 128 workgroups (latency-bound short
+    // ranges), then 128-position chunks (long ranges), at most 256 (an
+    // MI355X sweep at 512, 8192 and 32768 positions)
+    if (n_splits <= 0)
+        n_splits = std::max(1, std::min({(n_pos + 31) / 32, std::max(128, (n_pos + 127) / 128), GH_ATTN_OP_MAX_NC}));
     n_splits = std::min(std::min(n_splits, n_pos), GH_ATTN_OP_MAX_NC);
     void* part = nullptr;
     const int G = nq / nkv;
