@@ -1495,6 +1495,121 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     attn_item<HD, G, STEP>(a, g, j, QkvPartials{a.part_qkv, a.Sa, a.ld_qkv}, AttnOutPlain{a.part});
 }
 
+// Long-range attention of one query token (op-level, head_dim 256): each
+// wave streams its own rounds of 8 positions with its own online softmax,
+// with K/V loaded two rounds ahead and no workgroup barrier inside the loop.
+// The four wave states are merged once at the end into the chunk state
+// {m[G], l[G], o[G][HD]} that k_attn_combine reads.
+//   scores: 8 lanes per position; lane kq holds 32 of the position's 256 K
+//           values (one 16 B piece of each 128 B line, as in attn_item), one
+//           3-step DPP sum per score;
+//   P.V:    lane = 4 dims; the 8 positions' weights come by readlane.
+template <int G>
+__global__ __launch_bounds__(NT) void k_attn_wave(AttnArgs a) {
+    constexpr int HD = 256, K4 = HD / 32, RP = 8;  // RP positions per round
+    __shared__ __align__(16) float qs[G * HD];
+    __shared__ float ms[4][G], ls[4][G];
+    __shared__ __align__(16) float os[4][G * HD];
+    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
+    if (j >= a.n_used) return;  // uniform per workgroup
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
+    const size_t pstride = (size_t)a.nkv * HD;
+    for (int i = tid; i < G * HD; i += NT) qs[i] = a.q[(size_t)g * G * HD + i];
+    const int kq = lane & 7, kp = lane >> 3;
+    const float* kbase = a.kc + (size_t)g * HD + 4 * kq;
+    const float* vbase = a.vc + (size_t)g * HD + 4 * lane;
+    const int nr = (c1 - c0 + RP - 1) / RP;  // rounds of the chunk; wave w takes w, w + 4, ...
+    // Chunks start at multiples of the chunk length, so without a rotation
+    // every workgroup would read the same offset of its chunk at the same
+    // time (the same HBM channels); round r of chunk j reads round
+    // (r + rot) % nr instead, a permutation, so the result is unchanged.
+    const int rot = (j * 5) % nr;
+    auto round_pos = [&](int r) { return c0 + RP * ((r + rot) % nr); };
+    float4 kr[2][K4], vr[2][RP];
+    // round r's K/V into slot u; positions clamped into the chunk so every
+    // call issues the same loads
+    auto load = [&](int u, int r) {
+        const int p0 = round_pos(min(r, nr - 1));
+        const float* ks = kbase + (size_t)min(p0 + kp, c1 - 1) * pstride;
+#pragma unroll
+        for (int i = 0; i < K4; ++i) kr[u][i] = *(const float4*)(ks + 32 * i);
+#pragma unroll
+        for (int k = 0; k < RP; ++k) vr[u][k] = *(const float4*)(vbase + (size_t)min(p0 + k, c1 - 1) * pstride);
+    };
+    float m[G], l[G];
+    float4 acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+        acc[h] = f4z();
+    }
+    load(0, wave);
+    load(1, wave + 4);
+    __syncthreads();  // qs complete
+    for (int r = wave; r < nr; r += 8) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int rr = r + 4 * u;
+            if (rr >= nr) break;  // uniform per wave
+            const int p0 = round_pos(rr);
+            const bool valid = p0 + kp < c1;
+            float pw[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float sv = 0.0f;
+#pragma unroll
+                for (int i = 0; i < K4; ++i) sv += dot4(*(const float4*)&qs[h * HD + 32 * i + 4 * kq], kr[u][i]);
+                sv = group_sum<8>(sv) * a.scale;
+                sv = valid ? sv : -INFINITY;
+                const float mn = fmaxf(m[h], wave_max(sv));  // round has a valid position: mn finite
+                const float corr = __expf(m[h] - mn);         // m = -inf -> 0
+                pw[h] = valid ? __expf(sv - mn) : 0.0f;
+                l[h] = l[h] * corr + wave_sum(kq == 0 ? pw[h] : 0.0f);
+                m[h] = mn;
+                acc[h] = make_float4(acc[h].x * corr, acc[h].y * corr, acc[h].z * corr, acc[h].w * corr);
+            }
+#pragma unroll
+            for (int k = 0; k < RP; ++k) {
+                if (p0 + k < c1) {  // uniform per wave
+#pragma unroll
+                    for (int h = 0; h < G; ++h) acc[h] = fma4(readlane(pw[h], 8 * k), vr[u][k], acc[h]);
+                }
+            }
+            load(u, rr + 8);
+        }
+    }
+    // merge the four wave states
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            ms[wave][h] = m[h];
+            ls[wave][h] = l[h];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) *(float4*)&os[wave][h * HD + 4 * lane] = acc[h];
+    __syncthreads();
+    const size_t ob = ((size_t)g * a.nc + j) * (G * (HD + 2));
+    for (int idx = tid; idx < G * HD; idx += NT) {
+        const int h = idx / HD;
+        const float M = fmaxf(fmaxf(ms[0][h], ms[1][h]), fmaxf(ms[2][h], ms[3][h]));
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) o += __expf(ms[w][h] - M) * os[w][idx];
+        a.part[ob + 2 * G + idx] = o;
+    }
+    if (tid < G) {
+        const float M = fmaxf(fmaxf(ms[0][tid], ms[1][tid]), fmaxf(ms[2][tid], ms[3][tid]));
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) L += __expf(ms[w][tid] - M) * ls[w][tid];
+        a.part[ob + tid] = M;
+        a.part[ob + G + tid] = L;
+    }
+}
+
 template <bool STEP>
 static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
     const int max_nc = STEP ? ATTN_MAX_NC : GH_ATTN_OP_MAX_NC;
@@ -1509,13 +1624,18 @@ static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a
     return set_error(GH_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
 
-// Merge of the split-K partials for the op-level entry point: one workgroup
-// per q head; the chunk states (m_j, l_j) are loaded in parallel, then every
-// thread sums its dims over the chunks with independent loads.
+// Merge of the split-K partials for the op-level entry point: workgroup
+// (q head h, 64-dim slice) loads the chunk states (m_j, l_j) in parallel,
+// then thread (c, d) sums dim d over chunks c, c + 4, ... (independent,
+// coalesced loads) and the four chunk groups are added in LDS.
+constexpr int COMB_DIMS = 64;
 __global__ __launch_bounds__(NT) void k_attn_combine(const float* part, int nc, int n_used, int G, int HD, float* out) {
     __shared__ float wj[GH_ATTN_OP_MAX_NC];
     __shared__ float slot[8];
-    const int h = blockIdx.x, g = h / G, hl = h % G, tid = threadIdx.x;
+    __shared__ float red[4][COMB_DIMS];
+    const int nds = (HD + COMB_DIMS - 1) / COMB_DIMS;
+    const int h = blockIdx.x / nds, d = (blockIdx.x % nds) * COMB_DIMS + (threadIdx.x & (COMB_DIMS - 1));
+    const int g = h / G, hl = h % G, tid = threadIdx.x, cg = tid / COMB_DIMS;
     const int stride = G * (HD + 2);
     const float* base = part + (size_t)g * nc * stride;
     float m = -INFINITY, l = 0.0f;
@@ -1531,12 +1651,17 @@ __global__ __launch_bounds__(NT) void k_attn_combine(const float* part, int nc, 
     const float w = tid < n_used ? expf(m - M) : 0.0f;
     if (tid < n_used) wj[tid] = w;
     const float den = block_sum(l * w, slot + 4);  // barrier: wj complete
-    for (int d = tid; d < HD; d += NT) {
+    float num = 0.0f;
+    if (d < HD) {
         const float* o = base + 2 * G + hl * HD + d;
-        float num = 0.0f;
 #pragma unroll 8
-        for (int j = 0; j < n_used; ++j) num += o[(size_t)j * stride] * wj[j];
-        out[(size_t)h * HD + d] = num / den;
+        for (int j = cg; j < n_used; j += 4) num += o[(size_t)j * stride] * wj[j];
+    }
+    red[cg][tid & (COMB_DIMS - 1)] = num;
+    __syncthreads();
+    if (cg == 0 && d < HD) {
+        const int dl = tid & (COMB_DIMS - 1);
+        out[(size_t)h * HD + d] = ((red[0][dl] + red[1][dl]) + (red[2][dl] + red[3][dl])) / den;
     }
 }
 
@@ -2950,8 +3075,24 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     a.set_range(p_begin, p_end);
     Sink k;
     k.s = s;
-    GH_CHECK(launch_attn_t<false>(k, 0.0, hd, nq / nkv, a, nkv));
-    hipLaunchKernelGGL(k_attn_combine, dim3(nq), dim3(NT), 0, s, part, n_splits, a.n_used, nq / nkv, hd, out);
+    const int G = nq / nkv;
+    // chunks of at least GH_ATTN_WAVE_MIN (default 64) positions: the
+    // wave-streaming kernel (head_dim 256)
+    static const int wave_min = [] {
+        const char* e = std::getenv("GH_ATTN_WAVE_MIN");
+        return e ? std::atoi(e) : 64;
+    }();
+    if (hd == 256 && a.ch >= wave_min && wave_min > 0 && (G == 1 || G == 2 || G == 4 || G == 8)) {
+        const dim3 grid(nkv * a.nc);
+        if (G == 1) hipLaunchKernelGGL(k_attn_wave<1>, grid, dim3(NT), 0, s, a);
+        else if (G == 2) hipLaunchKernelGGL(k_attn_wave<2>, grid, dim3(NT), 0, s, a);
+        else if (G == 4) hipLaunchKernelGGL(k_attn_wave<4>, grid, dim3(NT), 0, s, a);
+        else hipLaunchKernelGGL(k_attn_wave<8>, grid, dim3(NT), 0, s, a);
+    } else {
+        GH_CHECK(launch_attn_t<false>(k, 0.0, hd, G, a, nkv));
+    }
+    hipLaunchKernelGGL(k_attn_combine, dim3(nq * ((hd + COMB_DIMS - 1) / COMB_DIMS)), dim3(NT), 0, s, part, n_splits,
+                       a.n_used, G, hd, out);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }

@@ -128,9 +128,12 @@ def test_gelu_mul_and_argmax(ctx):
 
 
 @pytest.mark.parametrize("nq,nkv,hd,L", [(4, 1, 256, 8192), (4, 1, 256, 32768), (8, 4, 256, 4352),
-                                         (4, 1, 32, 300), (4, 2, 128, 1000)])
+                                         (8, 1, 256, 2050), (2, 2, 256, 3001), (4, 1, 32, 300), (4, 2, 128, 1000)])
 def test_attention_decode_global_and_local(ctx, nq, nkv, hd, L):
-    """Config C4 shapes: global layer over all L, local layer over the last 512."""
+    """Config C4 shapes: global layer over all L, local layer over the last 512.
+    Chunks of 64 positions or more (head_dim 256) run the wave-streaming
+    kernel, shorter ones the 32-position sub-chunk kernel; groups 1, 2, 4, 8
+    and ragged lengths are covered."""
     rng = np.random.default_rng(L)
     q = rng.normal(size=nq * hd).astype(np.float32)
     K = rng.normal(size=(L, nkv, hd)).astype(np.float32)
