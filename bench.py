@@ -160,7 +160,9 @@ def extras_c5_gemma3_4b(gh, ctx, steps: int = 64, warmup: int = 8) -> dict:
     out = {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4), "steps": steps,
            "start_position": n0 + 1 + warmup, "step_algorithmic_bytes": int(step_bytes),
            "step_frac_of_hbm_peak": round(step_bytes / (ms / steps * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-           "lm_head_gbps": round(timings["lm_head"].gbps, 1)}
+           "lm_head_gbps": round(timings["lm_head"].gbps, 1),
+           "kernels": {t.name: {"avg_us": round(t.avg_us, 3), "gbps": round(t.gbps, 1), "per_step": t.launches_per_step,
+                                "step_us": round(t.avg_us * t.launches_per_step, 1)} for t in timings.values()}}
     del kv, model
     return out
 

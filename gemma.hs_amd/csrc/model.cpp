@@ -136,15 +136,19 @@ int env_int(const char* name, int def) {
 // Work-split plans, overridable for tuning sweeps with GH_PLAN_{A,C,D,E}_S.
 void make_plans(gh_model* m) {
     const LayerDev& L = m->layers[0];
-    // Measured on MI355X (gemma3-1b shapes): the short per-layer matvecs and
-    // the LM head run fastest as 64-row workgroups (RL 1) with up to 8
-    // column splits; gate/up (13824 rows) as 128-row workgroups with 4.
+    // Measured on MI355X (sweeps of S x RL on the gemma3-1b and gemma3-4b
+    // shapes): o_proj, down and the LM head run fastest as 64-row
+    // workgroups (RL 1), down with 8 splits; qkv too up to 31 tiles, as
+    // 128-row workgroups with 8 splits from 32 tiles (4B: 6.3 vs 7.0 us);
+    // gate/up as 128-row workgroups with about 384 / tiles splits (1B: 4,
+    // 4B: 2).
     m->pa = choose_plan(m->fmt, L.qkv.tiles, L.qkv.nblk, 256);
     m->pc = choose_plan(m->fmt, L.o.tiles, L.o.nblk, 256);
-    m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, 4 * L.gu.tiles);
-    m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 128);
+    m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, std::max(1, (384 + L.gu.tiles / 2) / L.gu.tiles) * L.gu.tiles);
+    m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 8 * L.down.tiles);
     m->plm = choose_plan(m->fmt, m->embd.tiles, m->embd.nblk, 1);
-    m->pa.rl = m->pc.rl = m->pe.rl = m->plm.rl = 1;
+    m->pc.rl = m->pe.rl = m->plm.rl = 1;
+    m->pa.rl = L.qkv.tiles >= 32 ? 2 : 1;
     auto over = [&](Plan& p, const char* env, const DMat& d) {
         int s = env_int(env, 0);
         if (s > 0) {
