@@ -76,6 +76,24 @@ def build_lib(jobs: int = 8) -> Path:
     return LIB
 
 
+HOST_TEST_SRC = REPO / "tests" / "cpp" / "host_api_test.cpp"
+HOST_TEST_LIB = REPO / "tests" / "cpp" / "libhost_api_test.so"
+
+
+def build_host_tests() -> Path:
+    """The C++ host-API checks (tests/cpp/host_api_test.cpp) as a shared
+    library linked against libgemma_hip and the oracle; it finds both through
+    an $ORIGIN-relative runpath."""
+    tmp = HOST_TEST_LIB.with_suffix(".so.tmp")
+    _run([HOST_CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+          f"-I{REPO / 'include'}", f"-I{PKG / 'host'}", f"-I{ORACLE_DIR}", str(HOST_TEST_SRC), "-o", str(tmp),
+          f"-L{LIB.parent}", "-lgemma_hip", f"-L{ORACLE_LIB.parent}", "-loracle",
+          "-Wl,-rpath,$ORIGIN/../../gemma.hs_amd/gemma_hip", "-Wl,-rpath,$ORIGIN/../../oracle/build",
+          "-Wl,--allow-shlib-undefined"])
+    os.replace(tmp, HOST_TEST_LIB)
+    return HOST_TEST_LIB
+
+
 def build_oracle() -> Path:
     ORACLE_LIB.parent.mkdir(exist_ok=True)
     cc = shutil.which("gcc") or "cc"
@@ -88,13 +106,15 @@ def build_oracle() -> Path:
 
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--only", choices=["lib", "oracle"])
+    ap.add_argument("--only", choices=["lib", "oracle"])  # default: lib, oracle and the C++ host tests
     ap.add_argument("-j", type=int, default=8)
     a = ap.parse_args(argv)
     if a.only in (None, "oracle"):
         print("built", build_oracle())
     if a.only in (None, "lib"):
         print("built", build_lib(a.j))
+    if a.only is None:
+        print("built", build_host_tests())
 
 
 if __name__ == "__main__":

@@ -147,3 +147,26 @@ def test_tensor_list_matches_header_names():
     for n in names:
         stem = n.replace(".weight", "")
         assert stem in text, n
+
+
+def test_cpp_host_api_header_compiles_and_test_library_exports_its_entry(tmp_path):
+    """gemma.hs_amd/host/Gemma.hpp (the C++ mirror of the reference's Haskell
+    API over the C ABI) compiles on its own, and build() produced the host-API
+    test library with its entry point (run on the GPU by
+    tests/test_gpu_host_api.py)."""
+    import shutil
+    import subprocess
+    cxx = shutil.which("g++") or "c++"
+    src = tmp_path / "use.cpp"
+    src.write_text('#include "Gemma.hpp"\n'
+                   'int main() { gemma::GemmaConfig c = gemma::preset("tiny"); return c.vocab == 1024 ? 0 : 1; }\n')
+    exe = tmp_path / "use"
+    r = subprocess.run([cxx, "-std=c++17", "-Wall", "-Werror", f"-I{REPO / 'include'}",
+                        f"-I{REPO / 'gemma.hs_amd' / 'host'}", str(src), "-o", str(exe),
+                        f"-L{REPO / 'gemma.hs_amd' / 'gemma_hip'}", "-lgemma_hip",
+                        f"-Wl,-rpath,{REPO / 'gemma.hs_amd' / 'gemma_hip'}", "-Wl,--allow-shlib-undefined"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    import ctypes
+    t = ctypes.CDLL(str(REPO / "tests" / "cpp" / "libhost_api_test.so"))
+    assert hasattr(t, "gh_host_api_tests")
