@@ -2988,6 +2988,7 @@ __global__ void k_sum_partials(const float* part, int S, int ld, int rows, int s
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
     float a = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < S; ++s) a += part[(size_t)s * ld + r];
     y[r] = softcap ? cap * tanhf(a / cap) : a;
 }

@@ -518,8 +518,10 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     d.scales = t->scales;
     GH_CHECK(upload(ctx, t->codes, codes.data(), codes.size()));
     GH_CHECK(upload(ctx, t->scales, sc.data(), sc.size() * 2));
-    t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, 512);
-    t->plan.rl = env_int("GH_Q4_RL", 2) == 1 ? 1 : 2;
+    // 64-row workgroups, about 512 of them, up to 16 column splits (an
+    // MI355X sweep of the C2 shapes: 6912x1152 5.5 us, 1152x6912 6.1 us)
+    t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, env_int("GH_Q4_TARGET", 512), env_int("GH_Q4_MAXS", 16));
+    t->plan.rl = env_int("GH_Q4_RL", 1) == 2 ? 2 : 1;
     if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
     ctx->q4s.push_back(t.get());
     *out = t.release();
