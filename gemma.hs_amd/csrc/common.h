@@ -86,6 +86,14 @@ struct Plan {
     int row_tiles(int tiles) const { return rl == 2 ? tiles : 2 * tiles; }
 };
 
+// float4 groups per thread (256 threads) of the widest column split of a
+// matrix under plan p: the GeGLU prologue of the down projection holds
+// gm x (gate/up splits) partial groups, at most 8.
+inline int geglu_groups(const DMat& w, const Plan& p) {
+    const int cols = (w.nblk + p.S - 1) / p.S * block_cols(w.fmt);
+    return (cols / 4 + 255) / 256;
+}
+
 struct LayerDev {
     DMat qkv, o, gu, down;
     float* attn_norm = nullptr;

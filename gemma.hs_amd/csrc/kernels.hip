@@ -34,6 +34,9 @@
 #ifndef GH_MARK
 #define GH_MARK(slot)
 #endif
+#ifndef GH_MARK_END
+#define GH_MARK_END()
+#endif
 
 namespace gh {
 
@@ -171,6 +174,44 @@ __device__ __forceinline__ unsigned long long block_max_key(unsigned long long k
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
+// ------------------------------------------------------------------
+// Raw buffer views.  A load whose byte offset lies outside the view returns
+// zeros without touching memory (the buffer range check of CDNA), so
+// optional, ragged and split-count-dependent loads need neither a branch
+// nor a clamp: every load of a prologue or weight batch is straight-line
+// code, and the compiler's s_waitcnt counts stay exact (a prologue waits
+// for its own inputs, not for the weight loads issued after them).
+// ------------------------------------------------------------------
+constexpr uint32_t OOB = 0x80000000u;  // past the end of every view (views are < 2 GiB)
+constexpr int CP_NT = 2;               // cache policy of streamed weights: non-temporal
+
+struct BufView {
+    __amdgpu_buffer_rsrc_t r;
+    // bytes = 0 (or p = nullptr with bytes = 0): every load reads zeros
+    __device__ __forceinline__ BufView(const void* p, size_t bytes)
+        : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                              (int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu), 0x00020000)) {}
+    template <int CP = 0>
+    __device__ __forceinline__ float4 f4(uint32_t off) const {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP));
+    }
+    template <int CP = 0>
+    __device__ __forceinline__ u32x4 u4(uint32_t off) const {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP));
+    }
+    template <int CP = 0>
+    __device__ __forceinline__ float f1(uint32_t off) const {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP));
+    }
+    template <int CP = 0>
+    __device__ __forceinline__ uint16_t h1(uint32_t off) const {
+        return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, CP);
+    }
+};
+
+// wave index as a wave-uniform (scalar) value
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // GELU(tanh) with the +-10 clamp of src/Gemma/Layers/MLP.hs:384-447.
 __device__ __forceinline__ float gelu_tanh(float x) {
     float x3 = x * x * x;
@@ -242,28 +283,34 @@ struct WRegs {
     uint16_t s0[KBW], s1[KBW];
 };
 
+// Views of a tiled matrix: the codes (16 B per row and column block) and,
+// for Q4_0, the fp16 scales (2 B per row and block).
+struct MatViews {
+    BufView codes, scales;
+    __device__ __forceinline__ explicit MatViews(const DMat& w)
+        : codes(w.codes, (size_t)w.tiles * w.nblk * TILE_ROWS * 16),
+          scales(w.scales, w.fmt == FMT_Q4 ? (size_t)w.tiles * w.nblk * TILE_ROWS * 2 : 0) {}
+};
+
 // Loads of one register batch: rows rbase+lane (and rbase+lane+64 when a
-// lane holds RL = 2 rows) of column blocks [base, min(base+KBW, kw1)).
+// lane holds RL = 2 rows) of column blocks base .. base+KBW-1 of row tile
+// `tile`; blocks at or past kw1 (wave-uniform) read zeros from an
+// out-of-range offset, so the batch is straight-line code.
 template <int FMT, int KBW, int RL>
-__device__ __forceinline__ void mv_load(WRegs<FMT, KBW>& r, const DMat& w, int tile, int rbase, int base, int kw1) {
+__device__ __forceinline__ void mv_load(WRegs<FMT, KBW>& r, const DMat& w, const MatViews& v, int tile, int rbase,
+                                        int base, int kw1) {
     const int lane = threadIdx.x & 63;
-    const u32x4* cp = (const u32x4*)w.codes + (size_t)tile * w.nblk * TILE_ROWS + rbase;
-    const uint16_t* sp = w.scales + (size_t)tile * w.nblk * TILE_ROWS + rbase;
-    auto one = [&](int i, int kb) {
-        r.c0[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + lane);
-        if (RL == 2) r.c1[i] = __builtin_nontemporal_load(cp + (size_t)kb * TILE_ROWS + 64 + lane);
+    const uint32_t row0 = (uint32_t)tile * (uint32_t)w.nblk * TILE_ROWS + (uint32_t)(rbase + lane);
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+        const bool ok = base + i < kw1;
+        const uint32_t e = row0 + (uint32_t)(base + i) * TILE_ROWS;  // element (row, block) index
+        r.c0[i] = v.codes.template u4<CP_NT>(ok ? e * 16u : OOB);
+        if (RL == 2) r.c1[i] = v.codes.template u4<CP_NT>(ok ? (e + 64u) * 16u : OOB);
         if (FMT == FMT_Q4) {
-            r.s0[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + lane);
-            if (RL == 2) r.s1[i] = __builtin_nontemporal_load(sp + (size_t)kb * TILE_ROWS + 64 + lane);
+            r.s0[i] = v.scales.template h1<CP_NT>(ok ? e * 2u : OOB);
+            if (RL == 2) r.s1[i] = v.scales.template h1<CP_NT>(ok ? (e + 64u) * 2u : OOB);
         }
-    };
-    if (base + KBW <= kw1) {  // full batch (kw1 is wave-uniform)
-#pragma unroll
-        for (int i = 0; i < KBW; ++i) one(i, base + i);
-    } else {
-#pragma unroll
-        for (int i = 0; i < KBW; ++i)
-            if (base + i < kw1) one(i, base + i);
     }
 }
 
@@ -372,7 +419,8 @@ __device__ __forceinline__ MvLds mv_lds(float* lds, int per_split) {
 // One matvec work item: 64*RL rows (one or both halves of 128-row tile
 // `tile`, starting at row rbase of it) x column split s of S.  Rows: lane
 // (RL 1) or lane and lane+64 (RL 2); the four waves split the split's
-// column blocks.  `rt` is the item's row-tile index for the epilogue.
+// column blocks evenly.  `rt` is the item's row-tile index for the
+// epilogue, which wave 0 runs on the summed rows.
 template <int FMT, int KBW, int RL, class Pro, class Epi>
 __device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
                                         const MvLds& L) {
@@ -382,18 +430,24 @@ __device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, con
     const int per_split = (nb + S - 1) / S;
     const int kb0 = min(nb, s * per_split), kb1 = min(nb, kb0 + per_split);
     const int nk = kb1 - kb0;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int per_wave = (nk + 3) >> 2;
-    const int kw0 = min(kb1, kb0 + wave * per_wave), kw1 = min(kb1, kw0 + per_wave);
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int kw0 = kb0 + (nk * wave >> 2), kw1 = kb0 + (nk * (wave + 1) >> 2);
 
     // 1. the prologue's input loads go out first (they are waited on first),
-    // 2. then the weights of the first register batch,
+    // 2. then the epilogue's and the weights of the first register batch,
     // 3. the prologue builds the input slice [kb0*BK, kb1*BK) in LDS.
     GH_MARK(0);
     typename Pro::Regs pr;
     pro.load(pr, kb0 * BK, nk * BK);
+    typename Epi::Regs er;
+    epi.load(er);
+    // the scheduler may not interleave the three groups: a prologue add
+    // hoisted above a weight load would make that load wait for the inputs
+    __builtin_amdgcn_sched_barrier(0);
+    const MatViews mv(w);
     WRegs<FMT, KBW> r;
-    mv_load<FMT, KBW, RL>(r, w, tile, rbase, kw0, kw1);
+    mv_load<FMT, KBW, RL>(r, w, mv, tile, rbase, kw0, kw1);
+    __builtin_amdgcn_sched_barrier(0);
     pro.template finish<FMT>(L, pr, kb0 * BK, nk * BK);
     GH_MARK(1);
     __syncthreads();
@@ -402,21 +456,25 @@ __device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, con
     float acc0 = 0.0f, acc1 = 0.0f;
     mv_compute<FMT, KBW, RL>(r, kw0, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     for (int base = kw0 + KBW; base < kw1; base += KBW) {
-        mv_load<FMT, KBW, RL>(r, w, tile, rbase, base, kw1);
+        mv_load<FMT, KBW, RL>(r, w, mv, tile, rbase, base, kw1);
         mv_compute<FMT, KBW, RL>(r, base, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     }
-    // 5. reduce the four waves
+    // 5. reduce the four waves; wave 0 finishes the item
     GH_MARK(3);
     L.red[wave * TILE_ROWS + lane] = acc0;
     if (RL == 2) L.red[wave * TILE_ROWS + 64 + lane] = acc1;
     __syncthreads();
     GH_MARK(4);
-    float y = 0.0f;
-    const int t = threadIdx.x;
-    const bool valid = t < 64 * RL;
-    if (valid) y = (L.red[t] + L.red[TILE_ROWS + t]) + (L.red[2 * TILE_ROWS + t] + L.red[3 * TILE_ROWS + t]);
-    epi(L, rt, tile * TILE_ROWS + rbase + t, s, valid, y);
+    if (wave == 0) {
+        const float y0 = (L.red[lane] + L.red[TILE_ROWS + lane]) + (L.red[2 * TILE_ROWS + lane] + L.red[3 * TILE_ROWS + lane]);
+        float y1 = 0.0f;
+        if (RL == 2)
+            y1 = (L.red[64 + lane] + L.red[TILE_ROWS + 64 + lane]) +
+                 (L.red[2 * TILE_ROWS + 64 + lane] + L.red[3 * TILE_ROWS + 64 + lane]);
+        epi.template run<RL>(L, er, rt, tile * TILE_ROWS + rbase + lane, s, y0, y1);
+    }
     GH_MARK(5);
+    GH_MARK_END();
 }
 
 // One workgroup per work item: grid = row tiles x S.
@@ -475,18 +533,16 @@ struct ProPlain {
         float4 v[2];
     };
     __device__ void load(Regs& r, int c0, int n) const {
-        const float4* x4 = (const float4*)(x + c0);
+        const BufView X(x + c0, (size_t)n * 4);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int gi = threadIdx.x + k * NT;
-            r.v[k] = gi < (n >> 2) ? x4[gi] : f4z();
-        }
+        for (int k = 0; k < 2; ++k) r.v[k] = X.f4(16u * (threadIdx.x + k * NT));
     }
     template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int ng = n >> 2;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) emit_x4<FMT>(L, threadIdx.x + k * NT, ng, r.v[k]);
+        for (int k = 0; k < 2; ++k)
+            if (k * NT < ng) emit_x4<FMT>(L, threadIdx.x + k * NT, ng, r.v[k]);
         for (int base = 2 * NT; base < ng; base += NT) {
             const int gi = base + threadIdx.x;
             emit_x4<FMT>(L, gi, ng, gi < ng ? ((const float4*)(x + c0))[gi] : f4z());
@@ -499,10 +555,14 @@ struct ProPlain {
 //     or E[token] * sqrt(H) for layer 0        (src/Gemma/Model.hs:1346-1361)
 //   xs = norm(x) with w_norm                   (TBG:110, MLP.hs:507-622, RMSNorm.hs:343-386)
 // Block 0 stores x to x_out and, when asked, to layer_out_row.  All split
-// partials (S <= MAXS) are loaded in one round trip.
-template <int MG>
+// partials (S <= MAXS), the residual and both norm weights are loaded in one
+// round trip, as straight-line buffer loads (absent splits read zeros).
+// EMB: layer 0 (x is the token's embedding row); a separate instance, so
+// that in the other layers the compiler keeps every prologue load ahead of
+// the weight loads (a runtime branch lets it sink them into the branch).
+template <int MG, bool EMB = false>
 struct ProResid {
-    int from_embedding;
+    int from_embedding;  // must equal EMB
     DMat embd;
     const StepState* st;
     float escale;
@@ -518,20 +578,23 @@ struct ProResid {
     struct Regs {
         float4 pv[MAXS][MG];
         float4 bv[MG], wp[MG];
-        float4 wn;  // norm weights of this thread's first group of the slice
+        float4 wn[MG];  // norm weights of this thread's groups of the slice
     };
     __device__ void load(Regs& r, int c0, int n) const {
         const int NG = H >> 2, tid = threadIdx.x;
-        r.wn = tid < (n >> 2) ? ((const float4*)(w_norm + c0))[tid] : f4z();
-        if (from_embedding) return;
+        const BufView WN(w_norm + c0, (size_t)n * 4);
 #pragma unroll
-        for (int k = 0; k < MG; ++k) {
-            const int g = tid + k * NT;
-            if (g < NG) {
-                r.bv[k] = ((const float4*)base)[g];
-                r.wp[k] = w_post ? ((const float4*)w_post)[g] : f4z();
+        for (int k = 0; k < MG; ++k) r.wn[k] = WN.f4(16u * (tid + k * NT));
+        if constexpr (!EMB) {
+            const BufView P(part, (size_t)S * ld * 4), B(base, (size_t)H * 4), WP(w_post, w_post ? (size_t)H * 4 : 0);
 #pragma unroll
-                for (int s = 0; s < MAXS; ++s) r.pv[s][k] = s < S ? ((const float4*)(part + (size_t)s * ld))[g] : f4z();
+            for (int k = 0; k < MG; ++k) {
+                const int g = tid + k * NT;
+                const uint32_t o = g < NG ? 16u * g : OOB;
+                r.bv[k] = B.f4(o);
+                r.wp[k] = WP.f4(o);
+#pragma unroll
+                for (int s = 0; s < MAXS; ++s) r.pv[s][k] = P.f4(g < NG ? 4u * (uint32_t)(s * ld) + 16u * g : OOB);
             }
         }
     }
@@ -539,42 +602,42 @@ struct ProResid {
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int NG = H >> 2, tid = threadIdx.x;
         float4 xv[MG];
-        if (from_embedding) {
+        if constexpr (EMB) {
             // the host validates tokens; the clamp keeps a corrupted state in bounds
             const int tok = min(max(st->token, 0), embd.rows - 1);
 #pragma unroll
             for (int k = 0; k < MG; ++k) {
                 const int g = tid + k * NT;
+                xv[k] = f4z();
                 if (g < NG) {
                     const float4 e = dq_elem4(embd, tok, 4 * g);
                     xv[k] = make_float4(e.x * escale, e.y * escale, e.z * escale, e.w * escale);
                 }
             }
         } else {
+            // absent splits and groups past H were read as zeros
             float4 dv[MG];
             float ss = 0.0f;
 #pragma unroll
             for (int k = 0; k < MG; ++k) {
                 dv[k] = r.pv[0][k];
 #pragma unroll
-                for (int s = 1; s < MAXS; ++s)
-                    if (s < S) dv[k] = dv[k] + r.pv[s][k];
-                if (tid + k * NT < NG) ss += dot4(dv[k], dv[k]);
+                for (int s = 1; s < MAXS; ++s) dv[k] = dv[k] + r.pv[s][k];
+                ss += dot4(dv[k], dv[k]);
             }
             float rms = 1.0f;
             if (w_post) rms = sqrtf(block_sum(ss, L.misc) / (float)H + eps);
             GH_MARK(6);
 #pragma unroll
-            for (int k = 0; k < MG; ++k)
-                if (tid + k * NT < NG) xv[k] = r.bv[k] + (w_post ? norm4(dv[k], rms, r.wp[k], zc) : dv[k]);
+            for (int k = 0; k < MG; ++k) xv[k] = r.bv[k] + (w_post ? norm4(dv[k], rms, r.wp[k], zc) : dv[k]);
         }
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < MG; ++k) {
             const int g = tid + k * NT;
+            ss += dot4(xv[k], xv[k]);
             if (g < NG) {
                 ((float4*)L.tmp)[g] = xv[k];
-                ss += dot4(xv[k], xv[k]);
                 if (blockIdx.x == 0) {
                     if (x_out) ((float4*)x_out)[g] = xv[k];
                     if (layer_out_row) ((float4*)layer_out_row)[g] = xv[k];
@@ -585,10 +648,10 @@ struct ProResid {
         GH_MARK(7);
         const int ng = n >> 2;
         const float4* t4 = (const float4*)(L.tmp + c0);
-        emit_x4<FMT>(L, tid, ng, tid < ng ? norm4(t4[tid], rms, r.wn, zc) : f4z());
-        for (int b = NT; b < ng; b += NT) {
-            const int gi = b + tid;
-            emit_x4<FMT>(L, gi, ng, gi < ng ? norm4(t4[gi], rms, ((const float4*)(w_norm + c0))[gi], zc) : f4z());
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int gi = tid + k * NT;
+            if (k * NT < ng) emit_x4<FMT>(L, gi, ng, gi < ng ? norm4(t4[gi], rms, r.wn[k], zc) : f4z());
         }
     }
 };
@@ -625,6 +688,7 @@ struct ProAttnCombine {
     int nc, G, HD;
     int global, window, mode;
     int n_used;  // chunks of this position, derived on the host
+    int nkv;
     __host__ __device__ void set_pos(int p) {
         int pb, pe, ch;
         pos = p;
@@ -638,110 +702,119 @@ struct ProAttnCombine {
     };
     __device__ void load(Regs& r, int c0, int n) const {
         const int stride = G * (HD + 2), tid = threadIdx.x;
+        const BufView P(part, (size_t)nkv * nc * stride * 4);
         // this thread's column group (one per thread up to 1024 columns)
         const int c = c0 + 4 * tid, h = c / HD, d = c % HD;
-        const float* pbase = part + (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
+        const uint32_t ob = 4u * (uint32_t)((h / G) * nc * stride + 2 * G + (h % G) * HD + d);
+        const bool in = tid < (n >> 2);
 #pragma unroll
-        for (int j = 0; j < PRE; ++j) r.ov[j] = (tid < (n >> 2) && j < n_used) ? *(const float4*)(pbase + (size_t)j * stride) : f4z();
+        for (int j = 0; j < PRE; ++j) r.ov[j] = P.f4(in && j < n_used ? ob + 4u * (uint32_t)(j * stride) : OOB);
         // (m, l) of chunk j = lane for head h0 + wave
         const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
         const int hh = tid >> 6, j = tid & 63;
-        r.mj = -INFINITY;
-        r.lj = 0.0f;
-        if (hh < nh && j < n_used) {
-            const int hg = h0 + hh;
-            const float* bj = part + ((size_t)(hg / G) * nc + j) * stride;
-            r.mj = bj[hg % G];
-            r.lj = bj[G + hg % G];
-        }
+        const bool ok = hh < nh && j < n_used;
+        const int hg = h0 + hh;
+        const uint32_t bj = 4u * (uint32_t)(((hg / G) * nc + j) * stride + hg % G);
+        r.mj = ok ? P.f1(bj) : -INFINITY;
+        r.lj = P.f1(ok ? bj + 4u * G : OOB);
     }
     template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int stride = G * (HD + 2), tid = threadIdx.x;
         const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
         float* wts = L.tmp;  // [nh][ATTN_MAX_NC] merge weights exp(m_j - M) / sum_j l_j exp(m_j - M)
-        for (int hh = tid >> 6; hh < nh; hh += 4) {
-            const int j = tid & 63;
-            float mj = r.mj, lj = r.lj;
-            if (hh >= 4) {  // heads beyond the first four of the slice
-                const int hg = h0 + hh;
-                const float* bj = part + ((size_t)(hg / G) * nc + j) * stride;
-                mj = j < n_used ? bj[hg % G] : -INFINITY;
-                lj = j < n_used ? bj[G + hg % G] : 0.0f;
-            }
+        const int j = tid & 63;
+        auto weights = [&](int hh, float mj, float lj) {
             const float M = wave_max(mj);
             const float e = j < n_used ? expf(mj - M) : 0.0f;
             const float den = wave_sum(lj * e);
             wts[hh * ATTN_MAX_NC + j] = e / den;
+        };
+        // straight-line first pass on the prefetched (m, l); heads beyond the
+        // slice's first four (slices of more than 4 heads) load theirs here
+        const int w0 = wave_id();
+        if (w0 < nh) weights(w0, r.mj, r.lj);
+        for (int hh = w0 + 4; hh < nh; hh += 4) {
+            const int hg = h0 + hh;
+            const float* bj = part + ((size_t)(hg / G) * nc + j) * stride;
+            weights(hh, j < n_used ? bj[hg % G] : -INFINITY, j < n_used ? bj[G + hg % G] : 0.0f);
         }
         __syncthreads();
         const int ng = n >> 2;
-        for (int base = 0; base < ng; base += NT) {
-            const int gi = base + tid;
+        auto group = [&](int gi, const float4* pre) {
             float4 acc = f4z();
             if (gi < ng) {
                 const int c = c0 + 4 * gi, h = c / HD, d = c % HD;
                 const float* pbase = part + (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
                 const float* wv = wts + (h - h0) * ATTN_MAX_NC;
-                int j = 0;
-                if (base == 0) {  // chunks 0..PRE-1 were loaded by load()
+                int jj = 0;
+                if (pre) {  // chunks 0..PRE-1 were loaded by load() (zeros past n_used)
 #pragma unroll
-                    for (int jj = 0; jj < PRE; ++jj)
-                        if (jj < n_used) acc = fma4(wv[jj], r.ov[jj], acc);
-                    j = PRE;
+                    for (int q = 0; q < PRE; ++q)
+                        if (q < n_used) acc = fma4(wv[q], pre[q], acc);
+                    jj = PRE;
                 }
-                for (; j < n_used; ++j) acc = fma4(wv[j], *(const float4*)(pbase + (size_t)j * stride), acc);
+                for (; jj < n_used; ++jj) acc = fma4(wv[jj], *(const float4*)(pbase + (size_t)jj * stride), acc);
             }
             emit_x4<FMT>(L, gi, ng, acc);
-        }
+        };
+        group(tid, r.ov);
+        for (int base = NT; base < ng; base += NT) group(base + tid, nullptr);
     }
 };
 
 // Down-projection input: h = gelu_tanh(sum_s g_s) * sum_s u_s (MLP.hs:384-447).
+// The gate/up split partials of the slice are loaded in one round trip:
+// gm (1 or 2) float4 groups per thread, register slot i holding split
+// i / gm of group i % gm (the host keeps Sg * gm <= MAXS).
 struct ProGeglu {
     const float* part_gu;
     int Sg, ld_g, up_off;
+    int gm;
     struct Regs {
         float4 g[MAXS], u[MAXS];
     };
     __device__ void load(Regs& r, int c0, int n) const {
-        const int gi = threadIdx.x, g = (c0 >> 2) + gi;
-        const bool ok = gi < (n >> 2);
+        const BufView P(part_gu, (size_t)Sg * ld_g * 4);
+        const int ng = n >> 2;
 #pragma unroll
-        for (int s = 0; s < MAXS; ++s) {
-            r.g[s] = ok && s < Sg ? ((const float4*)(part_gu + (size_t)s * ld_g))[g] : f4z();
-            r.u[s] = ok && s < Sg ? ((const float4*)(part_gu + (size_t)s * ld_g + up_off))[g] : f4z();
+        for (int i = 0; i < MAXS; ++i) {
+            const int s = gm == 2 ? i >> 1 : i, gi = threadIdx.x + (gm == 2 ? (i & 1) * NT : 0);
+            const bool ok = s < Sg && gi < ng;
+            const uint32_t o = 4u * (uint32_t)(s * ld_g + c0 + 4 * gi);
+            r.g[i] = P.f4(ok ? o : OOB);
+            r.u[i] = P.f4(ok ? o + 4u * (uint32_t)up_off : OOB);
         }
     }
     template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int ng = n >> 2;
-        for (int base = 0; base < ng; base += NT) {
-            const int gi = base + threadIdx.x;
+        auto emit = [&](int gi, float4 gs, float4 us) {
             float4 h = f4z();
-            if (gi < ng) {
-                float4 gs, us;
-                if (base == 0) {
-                    gs = r.g[0];
-                    us = r.u[0];
-#pragma unroll
-                    for (int s = 1; s < MAXS; ++s)
-                        if (s < Sg) {
-                            gs = gs + r.g[s];
-                            us = us + r.u[s];
-                        }
-                } else {
-                    const int g = (c0 >> 2) + gi;
-                    gs = us = f4z();
-                    for (int s = 0; s < Sg; ++s) {
-                        gs = gs + ((const float4*)(part_gu + (size_t)s * ld_g))[g];
-                        us = us + ((const float4*)(part_gu + (size_t)s * ld_g + up_off))[g];
-                    }
-                }
+            if (gi < ng)
                 h = make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y, gelu_tanh(gs.z) * us.z,
                                 gelu_tanh(gs.w) * us.w);
-            }
             emit_x4<FMT>(L, gi, ng, h);
+        };
+        if (gm == 1) {
+            float4 gs = r.g[0], us = r.u[0];
+#pragma unroll
+            for (int s = 1; s < MAXS; ++s) {
+                gs = gs + r.g[s];
+                us = us + r.u[s];
+            }
+            emit(threadIdx.x, gs, us);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                float4 gs = r.g[k], us = r.u[k];
+#pragma unroll
+                for (int s = 1; s < MAXS / 2; ++s) {
+                    gs = gs + r.g[2 * s + k];
+                    us = us + r.u[2 * s + k];
+                }
+                if (k * NT < ng) emit(threadIdx.x + k * NT, gs, us);
+            }
         }
     }
 };
@@ -967,19 +1040,30 @@ struct EpiW {
     uint64_t* w;
     int ld;
     uint32_t epoch;
-    __device__ void operator()(const MvLds&, int, int row, int s, bool valid, float y) const {
-        if (valid) st_word(w + (size_t)s * ld + row, epoch, y);
+    struct Regs {};
+    __device__ void load(Regs&) const {}
+    template <int RL>
+    __device__ void run(const MvLds&, const Regs&, int, int row0, int s, float y0, float y1) const {
+        st_word(w + (size_t)s * ld + row0, epoch, y0);
+        if (RL == 2) st_word(w + (size_t)s * ld + row0 + 64, epoch, y1);
     }
 };
 
 // ------------------------------------------------------------------
-// epilogues (called by all threads; t < 128 hold row sums)
+// epilogues: load() runs at kernel start (its global loads go out with the
+// prologue's); run<RL>() is called by the 64 lanes of wave 0 with the sums
+// of rows row0 = (item's first row) + lane and, when RL = 2, row0 + 64.
+// No epilogue may use a workgroup barrier.
 // ------------------------------------------------------------------
 struct EpiPartial {
     float* part;
     int ld;
-    __device__ void operator()(const MvLds&, int, int row, int s, bool valid, float y) const {
-        if (valid) part[(size_t)s * ld + row] = y;
+    struct Regs {};
+    __device__ void load(Regs&) const {}
+    template <int RL>
+    __device__ void run(const MvLds&, const Regs&, int, int row0, int s, float y0, float y1) const {
+        part[(size_t)s * ld + row0] = y0;
+        if (RL == 2) part[(size_t)s * ld + row0 + 64] = y1;
     }
 };
 
@@ -987,37 +1071,54 @@ struct EpiOut {
     float* y;
     int rows, softcap;
     float cap;
-    __device__ void operator()(const MvLds&, int, int row, int, bool valid, float v) const {
-        if (valid && row < rows) y[row] = softcap ? cap * tanhf(v / cap) : v;
+    struct Regs {};
+    __device__ void load(Regs&) const {}
+    template <int RL>
+    __device__ void run(const MvLds&, const Regs&, int, int row0, int, float y0, float y1) const {
+        if (row0 < rows) y[row0] = softcap ? cap * tanhf(y0 / cap) : y0;
+        if (RL == 2 && row0 + 64 < rows) y[row0 + 64] = softcap ? cap * tanhf(y1 / cap) : y1;
     }
 };
 
-// Logits + this workgroup's greedy argmax key (first maximum); the finish
-// kernel reduces the per-workgroup keys (no same-address atomics on the step
-// path).
+// Logits + this item's greedy argmax key (first maximum); the finish kernel
+// reduces the per-item keys (no same-address atomics on the step path).
+// When sampling, also the item's max logit and sum of exp((l - max) / T).
 struct EpiLogits {
     float* logits;  // nullable
     int V;
     unsigned long long* cand;
     StepState* st;
-    float* bm;  // per-workgroup max logit (written when sampling)
-    float* bs;  // per-workgroup sum of exp((l - max) / T)
-    __device__ void operator()(const MvLds& L, int rt, int row, int, bool valid, float y) const {
-        const bool in = valid && row < V;
-        unsigned long long key = 0ull;
-        if (in) {
-            if (logits) logits[row] = y;
-            key = argmax_key(y, row);
-            if (isnan(y)) atomicOr(&st->nan_flag, 1);
+    float* bm;  // per-item max logit (written when sampling)
+    float* bs;  // per-item sum of exp((l - max) / T)
+    struct Regs {
+        float inv_t;
+    };
+    __device__ void load(Regs& r) const { r.inv_t = st->inv_temp; }
+    template <int RL>
+    __device__ void run(const MvLds&, const Regs& r, int rt, int row0, int, float y0, float y1) const {
+        const int lane = threadIdx.x & 63;
+        const bool in0 = row0 < V, in1 = RL == 2 && row0 + 64 < V;
+        if (logits) {
+            if (in0) logits[row0] = y0;
+            if (in1) logits[row0 + 64] = y1;
         }
-        const unsigned long long b = block_max_key(key, (unsigned long long*)(L.misc + 32));
-        if (threadIdx.x == 0) cand[rt] = b;
-        const float inv_t = st->inv_temp;
-        if (inv_t > 0.0f) {  // temperature sampling: softmax statistics of this workgroup's rows
-            const float mb = block_max(in ? y : -INFINITY, L.misc + 16);
-            const float sb = block_sum(in ? expf((y - mb) * inv_t) : 0.0f, L.misc + 20);
-            if (threadIdx.x == 0) {
-                bm[rt] = mb;
+        if ((in0 && isnan(y0)) || (in1 && isnan(y1))) atomicOr(&st->nan_flag, 1);
+        // first maximum: the wave's max value, then the lowest row holding it
+        // (every row of the lower half precedes every row of the upper half)
+        const float v0 = in0 ? y0 : -INFINITY, v1 = in1 ? y1 : -INFINITY;
+        const float M = wave_max(fmaxf(v0, v1));
+        const unsigned long long b0 = __ballot(in0 && v0 == M);
+        const unsigned long long b1 = __ballot(in1 && v1 == M);
+        const int first = row0 - lane;
+        unsigned long long key = 0ull;
+        if (b0) key = argmax_key(M, first + __builtin_ctzll(b0));
+        else if (b1) key = argmax_key(M, first + 64 + __builtin_ctzll(b1));
+        if (lane == 0) cand[rt] = key;
+        if (r.inv_t > 0.0f) {  // temperature sampling: softmax statistics of the item's rows
+            const float e = (in0 ? expf((y0 - M) * r.inv_t) : 0.0f) + (in1 ? expf((y1 - M) * r.inv_t) : 0.0f);
+            const float sb = wave_sum(e);
+            if (lane == 0) {
+                bm[rt] = M;
                 bs[rt] = sb;
             }
         }
@@ -1235,14 +1336,31 @@ __device__ __forceinline__ void wave_head_rope(float* p, const float2* cs) {
 // the host (AttnArgs::set_pos).
 // Sources of the QKV vector: the split partials of the QKV matvec, or
 // published words (persistent step).  g4(row) = float4 at fused-QKV row.
+// issue() starts the loads of the float4 at fused-QKV row `row` (ok: the
+// thread has one), get() returns it.
 struct QkvPartials {
     const float* part;
     int S, ld;
-    __device__ float4 g4(int row) const { return sum_splits4(part, S, ld, row >> 2); }
+    struct Pre {
+        float4 v[MAXS];
+    };
+    __device__ void issue(Pre& p, int row, bool ok) const {
+        const BufView P(part, (size_t)S * ld * 4);
+#pragma unroll
+        for (int s = 0; s < MAXS; ++s) p.v[s] = P.f4(ok ? 4u * (uint32_t)(s * ld + row) : OOB);
+    }
+    __device__ float4 get(const Pre& p, int) const {  // absent splits read zeros
+        float4 r = p.v[0];
+#pragma unroll
+        for (int s = 1; s < MAXS; ++s) r = r + p.v[s];
+        return r;
+    }
 };
 struct QkvWords {
     WSrc w;
-    __device__ float4 g4(int row) const { return w.g4e((size_t)row); }
+    struct Pre {};
+    __device__ void issue(Pre&, int, bool) const {}
+    __device__ float4 get(const Pre&, int row) const { return w.g4e((size_t)row); }
 };
 // Sinks of the chunk state: plain floats or published words.
 struct AttnOutPlain {
@@ -1303,14 +1421,36 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
             vr[k] = *(const float4*)(vbase + (size_t)min(s0 + pl, c1 - 1) * pstride);
         }
     };
-    // 1. K/V of the first sub-chunk in flight (row pos comes from LDS below)
-    load_k(c0);
-    load_v(c0);
-    GH_MARK(1);
-
-    // 2. q (and in step mode k, v of this token) into LDS
+    // 1. the QKV partials of this token (step mode), the QK-norm weights and
+    //    the RoPE row go out first; then the K/V of the first sub-chunk (row
+    //    pos comes from LDS below), so waiting for the prologue's inputs does
+    //    not wait for the cache rows.
     if (STEP) {
-        float4 pv[MG4];
+        typename In::Pre pv[MG4];
+#pragma unroll
+        for (int m = 0; m < MG4; ++m) {
+            const int gi = tid + m * NT, i = 4 * gi;
+            const int row = i < G * HD ? a.q_off + g * G * HD + i
+                          : i < (G + 1) * HD ? a.k_off + g * HD + (i - G * HD)
+                                             : a.v_off + g * HD + (i - (G + 1) * HD);
+            in.issue(pv[m], row, gi < NG4);
+        }
+        const BufView QN(a.q_norm, a.use_qk_norm ? HD * 4 : 0), KN(a.k_norm, a.use_qk_norm ? HD * 4 : 0);
+        float wq[NWR], wk[NWR];
+#pragma unroll
+        for (int r = 0; r < NWR; ++r) {
+            const uint32_t o = 4u * (lane + 64 * r);
+            wq[r] = QN.f1(o);
+            wk[r] = KN.f1(o);
+        }
+        const BufView CS(a.rope + (size_t)pos * HD, HD * 4);
+        const float2 csv = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(CS.r, tid < HD / 2 ? 8u * tid : OOB, 0, 0));
+        __builtin_amdgcn_sched_barrier(0);  // keep the cache-row loads behind the prologue's
+        load_k(c0);
+        load_v(c0);
+        __builtin_amdgcn_sched_barrier(0);
+        GH_MARK(1);
+        // 2. q, k, v of this token into LDS
 #pragma unroll
         for (int m = 0; m < MG4; ++m) {
             const int gi = tid + m * NT;
@@ -1319,26 +1459,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
                 const int row = i < G * HD ? a.q_off + g * G * HD + i
                               : i < (G + 1) * HD ? a.k_off + g * HD + (i - G * HD)
                                                  : a.v_off + g * HD + (i - (G + 1) * HD);
-                pv[m] = in.g4(row);
-            }
-        }
-        float wq[NWR], wk[NWR];
-#pragma unroll
-        for (int r = 0; r < NWR; ++r) {
-            const int i = lane + 64 * r;
-            wq[r] = (a.use_qk_norm && i < HD) ? a.q_norm[i] : 0.0f;
-            wk[r] = (a.use_qk_norm && i < HD) ? a.k_norm[i] : 0.0f;
-        }
-        if (tid < HD / 2) cs[tid] = ((const float2*)a.rope)[(size_t)pos * (HD / 2) + tid];
-#pragma unroll
-        for (int m = 0; m < MG4; ++m) {
-            const int gi = tid + m * NT;
-            if (gi < NG4) {
-                const int i = 4 * gi;
                 float* dst = i < G * HD ? &qs[i] : i < (G + 1) * HD ? &ks[i - G * HD] : &vs[i - (G + 1) * HD];
-                *(float4*)dst = pv[m];
+                *(float4*)dst = in.get(pv[m], row);
             }
         }
+        if (tid < HD / 2) cs[tid] = csv;
         __syncthreads();
         GH_MARK(2);
         // QK-norm (TBG:171-179), then RoPE, on the G q heads and the k head
@@ -1369,6 +1494,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
             }
         }
     } else {
+        load_k(c0);
+        load_v(c0);
+        GH_MARK(1);
         for (int i = tid; i < G * HD; i += NT) qs[i] = a.q[(size_t)g * G * HD + i];
         __syncthreads();
     }
@@ -1486,6 +1614,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
         }
     }
     GH_MARK(6);
+    GH_MARK_END();
 }
 
 template <int HD, int G, bool STEP>
@@ -2195,9 +2324,9 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
         LayerDev& L = m->layers[li];
         const LayerDev* P = li > 0 ? &m->layers[li - 1] : nullptr;
         // A: residual + pre-attention norm + fused QKV matvec
-        GH_CHECK(with_mg(H, [&](auto mg) {
-            ProResid<decltype(mg)::value> pro;
-            pro.from_embedding = li == 0;
+        auto qkv = [&](auto mg, auto emb) {
+            ProResid<decltype(mg)::value, decltype(emb)::value> pro;
+            pro.from_embedding = decltype(emb)::value;
             pro.embd = m->embd;
             pro.st = kv->st;
             pro.escale = sqrtf((float)H);
@@ -2214,6 +2343,9 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             pro.layer_out_row = li > 0 ? m->layer_out + (size_t)(li - 1) * H : nullptr;
             EpiPartial epi{m->part_qkv, L.qkv.tiles * TILE_ROWS};
             return launch_mv(sink, "qkv", mat_bytes(L.qkv), L.qkv, m->pa, pro, epi, H);
+        };
+        GH_CHECK(with_mg(H, [&](auto mg) {
+            return li == 0 ? qkv(mg, std::true_type{}) : qkv(mg, std::false_type{});
         }));
         // B: QK-norm + RoPE + KV append + split-K attention
         {
@@ -2245,7 +2377,7 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
         }
         // C: attention merge + O projection
         {
-            ProAttnCombine pro{m->attn_part, pos, m->attn_nc, G, hd, L.global ? 1 : 0, c.sliding_window, c.mode, 0};
+            ProAttnCombine pro{m->attn_part, pos, m->attn_nc, G, hd, L.global ? 1 : 0, c.sliding_window, c.mode, 0, nkv};
             pro.set_pos(pos);
             EpiPartial epi{m->part_o, L.o.tiles * TILE_ROWS};
             const int per_split = (L.o.nblk + m->pc.S - 1) / m->pc.S * block_cols(L.o.fmt);
@@ -2275,7 +2407,11 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
         }));
         // E: GeGLU + down projection
         {
-            ProGeglu pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad};
+            const int gm = geglu_groups(L.down, m->pe);
+            if (gm > 2 || gm * m->pd.S > MAXS)
+                return set_error(GH_ERR_INVALID, "down projection split of %d columns with %d gate/up splits",
+                                 (L.down.nblk + m->pe.S - 1) / m->pe.S * block_cols(L.down.fmt), m->pd.S);
+            ProGeglu pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad, gm};
             EpiPartial epi{m->part_d, L.down.tiles * TILE_ROWS};
             GH_CHECK(launch_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, pro, epi, 0));
         }

@@ -169,6 +169,10 @@ void make_plans(gh_model* m) {
     m->pe.rl = env_int("GH_PLAN_E_RL", m->pe.rl);
     m->plm.rl = env_int("GH_PLAN_LM_RL", m->plm.rl);
     for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe, &m->plm}) p->rl = p->rl == 1 ? 1 : 2;
+    capped(m->pe);
+    // the down projection's GeGLU prologue holds gm float4 groups of each
+    // gate/up split: gm * S <= 8 (gm <= 2 up to 2048 columns per split)
+    m->pd.S = std::max(1, std::min(m->pd.S, 8 / std::max(1, std::min(2, geglu_groups(L.down, m->pe)))));
     for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe}) {
         capped(*p);
         const DMat& d = p == &m->pa ? L.qkv : p == &m->pc ? L.o : p == &m->pd ? L.gu : L.down;
