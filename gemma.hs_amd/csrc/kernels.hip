@@ -25,6 +25,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "common.h"
@@ -183,7 +184,10 @@ __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_
 // for its own inputs, not for the weight loads issued after them).
 // ------------------------------------------------------------------
 constexpr uint32_t OOB = 0x80000000u;  // past the end of every view (views are < 2 GiB)
-constexpr int CP_NT = 2;               // cache policy of streamed weights: non-temporal
+#ifndef GH_CP_WEIGHTS
+#define GH_CP_WEIGHTS 2
+#endif
+constexpr int CP_NT = GH_CP_WEIGHTS;  // cache policy of streamed weights (2: non-temporal)
 
 struct BufView {
     __amdgpu_buffer_rsrc_t r;
@@ -228,6 +232,17 @@ __device__ __forceinline__ float4 operator+(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 __device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+// The step's norms scale by one reciprocal of the RMS per vector instead of
+// dividing every element: (x * (1/rms)) differs from x / rms by at most an
+// ulp or so, far inside the 1e-4 activation tolerance, and it takes the
+// divide sequence off the latency chain of every prologue.
+__device__ __forceinline__ float norm_apply_inv(float x, float inv, float w, int zc) {
+    return zc ? (x * inv) * (1.0f + w) : (x * inv) * w;
+}
+__device__ __forceinline__ float4 norm4i(float4 x, float inv, float4 w, int zc) {
+    return make_float4(norm_apply_inv(x.x, inv, w.x, zc), norm_apply_inv(x.y, inv, w.y, zc),
+                       norm_apply_inv(x.z, inv, w.z, zc), norm_apply_inv(x.w, inv, w.w, zc));
+}
 __device__ __forceinline__ float4 norm4(float4 x, float rms, float4 w, int zc) {
     return make_float4(norm_apply(x.x, rms, w.x, zc), norm_apply(x.y, rms, w.y, zc), norm_apply(x.z, rms, w.z, zc),
                        norm_apply(x.w, rms, w.w, zc));
@@ -625,11 +640,11 @@ struct ProResid {
                 for (int s = 1; s < MAXS; ++s) dv[k] = dv[k] + r.pv[s][k];
                 ss += dot4(dv[k], dv[k]);
             }
-            float rms = 1.0f;
-            if (w_post) rms = sqrtf(block_sum(ss, L.misc) / (float)H + eps);
+            float inv = 1.0f;
+            if (w_post) inv = 1.0f / sqrtf(block_sum(ss, L.misc) / (float)H + eps);
             GH_MARK(6);
 #pragma unroll
-            for (int k = 0; k < MG; ++k) xv[k] = r.bv[k] + (w_post ? norm4(dv[k], rms, r.wp[k], zc) : dv[k]);
+            for (int k = 0; k < MG; ++k) xv[k] = r.bv[k] + (w_post ? norm4i(dv[k], inv, r.wp[k], zc) : dv[k]);
         }
         float ss = 0.0f;
 #pragma unroll
@@ -644,14 +659,14 @@ struct ProResid {
                 }
             }
         }
-        const float rms = sqrtf(block_sum(ss, L.misc + 4) / (float)H + eps);  // barrier: tmp complete
+        const float inv = 1.0f / sqrtf(block_sum(ss, L.misc + 4) / (float)H + eps);  // barrier: tmp complete
         GH_MARK(7);
         const int ng = n >> 2;
         const float4* t4 = (const float4*)(L.tmp + c0);
 #pragma unroll
         for (int k = 0; k < MG; ++k) {
             const int gi = tid + k * NT;
-            if (k * NT < ng) emit_x4<FMT>(L, gi, ng, gi < ng ? norm4(t4[gi], rms, r.wn[k], zc) : f4z());
+            if (k * NT < ng) emit_x4<FMT>(L, gi, ng, gi < ng ? norm4i(t4[gi], inv, r.wn[k], zc) : f4z());
         }
     }
 };
@@ -1476,11 +1491,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
                     const int i = lane + 64 * r;
                     if (i < HD) ss += p[i] * p[i];
                 }
-                const float rms = sqrtf(wave_sum(ss) / (float)HD + a.eps);
+                const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)HD + a.eps);
 #pragma unroll
                 for (int r = 0; r < NWR; ++r) {
                     const int i = lane + 64 * r;
-                    if (i < HD) p[i] = norm_apply(p[i], rms, vec < G ? wq[r] : wk[r], a.zc);
+                    if (i < HD) p[i] = norm_apply_inv(p[i], inv, vec < G ? wq[r] : wk[r], a.zc);
                 }
             }
             wave_head_rope<HD>(p, cs);
