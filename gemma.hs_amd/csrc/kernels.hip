@@ -1555,6 +1555,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
             }
         }
         __syncthreads();
+        GH_MARK(8);
         // 4. softmax update of the heads this wave owns
         const bool valid = lane < SUB && s0 + lane < c1;
 #pragma unroll
@@ -1572,6 +1573,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
             }
         }
         __syncthreads();
+        GH_MARK(9);
         // 5. P.V over this slot's positions
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -1752,6 +1754,251 @@ __global__ __launch_bounds__(NT) void k_attn_wave(AttnArgs a) {
         a.part[ob + tid] = M;
         a.part[ob + G + tid] = L;
     }
+}
+
+// One query token of the decode step over cache positions [pb, pe): split-K
+// over chunks as attn_item (workgroup (g, j): kv head g, chunk j; the same
+// {m[G], l[G], o[G][HD]} chunk state), with a short dependency chain:
+//   prologue  the QKV split partials of this token are summed in registers,
+//             one float4 group per lane, each q/k head vector held by
+//             LPH = HD/4 consecutive lanes: QK-norm (TBG:171-179) is one
+//             lane-group reduction, split-half RoPE (ropeShader) swaps with
+//             the lane LPH/2 away; q, k, v go to LDS behind one barrier.
+//             Only workgroup 0 (the KV append, appendKVCacheShader) and the
+//             workgroup whose chunk holds `pos` load the k/v partials.
+//   stream    wave w takes the chunk's rounds of 8 positions w, w+4, ...
+//             with its own online softmax, K/V two rounds ahead, no
+//             workgroup barrier: scores 8 lanes per position (lane kq holds
+//             one 16 B piece of each 128 B line of the K row), one 3-step
+//             DPP sum per score; P.V lane = 4 dims, weights by readlane.
+//   merge     the four wave states, once, through LDS.
+// PF: K/V rounds per wave loaded ahead (1 for chunks of up to 4 rounds, where
+// each wave has at most one round; 2 otherwise).  The kernel picks the body
+// before issuing any load, so each body's s_waitcnt counts stay exact.
+template <int HD, int G>
+struct AttnStepLds {
+    float qs[G * HD];
+    float ks[HD];
+    float vs[HD];
+    float ms[4][G], ls[4][G];
+    float os[4][G * HD];
+};
+
+template <int HD, int G, int PF>
+__device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, AttnStepLds<HD, G>& S) {
+    constexpr int LPH = HD / 4;                  // lanes per head vector (one float4 each)
+    constexpr int NG4 = (G + 2) * LPH;           // float4 groups of q | k | v
+    constexpr int MG4 = (NG4 + NT - 1) / NT;     // groups per thread
+    constexpr int K4 = HD / 32, RP = 8;          // score float4 per lane and position; positions per round
+    static_assert(HD % 32 == 0 && LPH <= 64, "head_dim 32..256");
+    float* qs = S.qs;
+    float* ks = S.ks;
+    float* vs = S.vs;
+    auto& ms = S.ms;
+    auto& ls = S.ls;
+    auto& os = S.os;
+    GH_MARK(0);
+    const int pos = a.pos;
+    const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
+    const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
+    const bool own = pos >= c0 && pos < c1;  // this chunk scores the current position
+    const bool need_kv = own || j == 0;      // j == 0 appends k, v to the cache
+    const size_t pstride = (size_t)a.nkv * HD;
+
+    // 1. prologue loads: partials, QK-norm weights, RoPE row (straight-line)
+    const BufView P(a.part_qkv, (size_t)a.Sa * a.ld_qkv * 4);
+    const BufView QN(a.q_norm, a.use_qk_norm ? HD * 4 : 0), KN(a.k_norm, a.use_qk_norm ? HD * 4 : 0);
+    const BufView CS(a.rope + (size_t)pos * HD, HD * 4);
+    float4 pv[MG4][MAXS], wn[MG4], cs0[MG4], cs1[MG4];
+#pragma unroll
+    for (int m = 0; m < MG4; ++m) {
+        const int gi = tid + m * NT, vec = gi / LPH, d = 4 * (gi % LPH);  // vector (G q heads, k, v), first dim
+        const int row = vec < G ? a.q_off + (g * G + vec) * HD + d : vec == G ? a.k_off + g * HD + d : a.v_off + g * HD + d;
+        const bool ok = gi < NG4 && (vec < G || need_kv);
+#pragma unroll
+        for (int s = 0; s < MAXS; ++s) pv[m][s] = P.f4(ok ? 4u * (uint32_t)(s * a.ld_qkv + row) : OOB);
+        const float4 wq = QN.f4(vec < G ? 4u * d : OOB), wk = KN.f4(vec == G ? 4u * d : OOB);
+        wn[m] = vec < G ? wq : wk;
+        const int i = d % (HD / 2);  // RoPE pair index of the first dim
+        cs0[m] = CS.f4(vec <= G ? 8u * i : OOB);
+        cs1[m] = CS.f4(vec <= G ? 8u * i + 16u : OOB);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // K/V rounds as buffer loads: rounds past the chunk's and positions past
+    // its end read zeros without traffic (and are masked); row pos is
+    // replaced from LDS (it is being appended)
+    const int kq = lane & 7, kp = lane >> 3;
+    const BufView KC(a.kc, (size_t)a.pe * pstride * 4), VC(a.vc, (size_t)a.pe * pstride * 4);
+    const uint32_t kcol = 4u * (uint32_t)(g * HD + 4 * kq), vcol = 4u * (uint32_t)(g * HD + 4 * lane);
+    const int nr = (c1 - c0 + RP - 1) / RP;
+    const int rot = (j * 5) % nr;  // round order rotated per chunk (HBM channels), a permutation
+    auto round_pos = [&](int r) { return c0 + RP * ((r + rot) % nr); };
+    float4 kr[PF][K4], vr[PF][RP];
+    auto load = [&](int u, int r) {
+        const bool rok = r < nr;
+        const int p0 = round_pos(rok ? r : 0);
+        const uint32_t ko = rok && p0 + kp < c1 ? 4u * (uint32_t)(p0 + kp) * (uint32_t)pstride + kcol : OOB;
+#pragma unroll
+        for (int i = 0; i < K4; ++i) kr[u][i] = KC.f4(ko + 128u * i);
+#pragma unroll
+        for (int k = 0; k < RP; ++k)
+            vr[u][k] = VC.f4(rok && p0 + k < c1 && lane < LPH ? 4u * (uint32_t)(p0 + k) * (uint32_t)pstride + vcol : OOB);
+    };
+    load(0, wave);
+    if (PF == 2) load(PF - 1, wave + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    GH_MARK(1);
+
+    // 2. sums, QK-norm, RoPE in registers; q, k, v to LDS
+#pragma unroll
+    for (int m = 0; m < MG4; ++m) {
+        const int gi = tid + m * NT, vec = gi / LPH, d = 4 * (gi % LPH);
+        float4 v = pv[m][0];
+#pragma unroll
+        for (int s = 1; s < MAXS; ++s) v = v + pv[m][s];  // absent splits read zeros
+        if (m * NT < NG4) {  // uniform: some lane of the workgroup holds a group
+            const bool qk = vec <= G;
+            if (a.use_qk_norm) {
+                const float ss = group_sum<LPH>(qk ? dot4(v, v) : 0.0f);
+                const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+                if (qk) v = norm4i(v, inv, wn[m], a.zc);
+            }
+            // split-half RoPE: the partner dims d +- HD/2 sit LPH/2 lanes away
+            float4 pr;
+            pr.x = __shfl_xor(v.x, LPH / 2, 64);
+            pr.y = __shfl_xor(v.y, LPH / 2, 64);
+            pr.z = __shfl_xor(v.z, LPH / 2, 64);
+            pr.w = __shfl_xor(v.w, LPH / 2, 64);
+            if (qk) {
+                const float c[4] = {cs0[m].x, cs0[m].z, cs1[m].x, cs1[m].z}, sn[4] = {cs0[m].y, cs0[m].w, cs1[m].y, cs1[m].w};
+                const float x[4] = {v.x, v.y, v.z, v.w}, q[4] = {pr.x, pr.y, pr.z, pr.w};
+                float y[4];
+                const bool first = d < HD / 2;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = first ? x[e] * c[e] - q[e] * sn[e] : q[e] * sn[e] + x[e] * c[e];
+                v = make_float4(y[0], y[1], y[2], y[3]);
+            }
+            if (gi < NG4) {
+                float* dst = vec < G ? &qs[vec * HD + d] : vec == G ? &ks[d] : &vs[d];
+                *(float4*)dst = v;
+            }
+        }
+    }
+    __syncthreads();
+    GH_MARK(2);
+    if (j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
+        for (int i = tid; i < HD; i += NT) {
+            a.kc[((size_t)pos * a.nkv + g) * HD + i] = ks[i];
+            a.vc[((size_t)pos * a.nkv + g) * HD + i] = vs[i];
+        }
+    }
+
+    // 3. stream the wave's rounds
+    float mrun[G], lrun[G];
+    float4 acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        mrun[h] = -INFINITY;
+        lrun[h] = 0.0f;
+        acc[h] = f4z();
+    }
+    for (int r = wave; r < nr; r += 4 * PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int rr = r + 4 * u;
+            if (rr >= nr) break;  // uniform per wave
+            const int p0 = round_pos(rr);
+            if (own && pos >= p0 && pos < p0 + RP) {  // the current row comes from LDS
+                if (p0 + kp == pos) {
+#pragma unroll
+                    for (int i = 0; i < K4; ++i) kr[u][i] = *(const float4*)&ks[32 * i + 4 * kq];
+                }
+#pragma unroll
+                for (int k = 0; k < RP; ++k)
+                    if (p0 + k == pos && lane < LPH) vr[u][k] = *(const float4*)&vs[4 * lane];
+            }
+            const bool valid = p0 + kp < c1;
+            float pw[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float sv = 0.0f;
+#pragma unroll
+                for (int i = 0; i < K4; ++i) sv += dot4(*(const float4*)&qs[h * HD + 32 * i + 4 * kq], kr[u][i]);
+                sv = group_sum<8>(sv) * a.scale;
+                sv = valid ? sv : -INFINITY;
+                const float mn = fmaxf(mrun[h], wave_max(sv));  // the round has a valid position: mn finite
+                const float corr = __expf(mrun[h] - mn);          // mrun = -inf -> 0
+                pw[h] = valid ? __expf(sv - mn) : 0.0f;
+                lrun[h] = lrun[h] * corr + wave_sum(kq == 0 ? pw[h] : 0.0f);
+                mrun[h] = mn;
+                acc[h] = make_float4(acc[h].x * corr, acc[h].y * corr, acc[h].z * corr, acc[h].w * corr);
+            }
+#pragma unroll
+            for (int k = 0; k < RP; ++k) {
+                if (p0 + k < c1) {  // uniform per wave
+#pragma unroll
+                    for (int h = 0; h < G; ++h) acc[h] = fma4(readlane(pw[h], 8 * k), vr[u][k], acc[h]);
+                }
+            }
+            if (PF == 2) load(u, rr + 8);
+        }
+    }
+    GH_MARK(4);
+    // 4. merge the four wave states; write the chunk's state
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            ms[wave][h] = mrun[h];
+            ls[wave][h] = lrun[h];
+        }
+    }
+    if (lane < LPH) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) *(float4*)&os[wave][h * HD + 4 * lane] = acc[h];
+    }
+    __syncthreads();
+    GH_MARK(5);
+    const size_t ob = ((size_t)g * a.nc + j) * (G * (HD + 2));
+    for (int idx = tid; idx < G * HD; idx += NT) {
+        const int h = idx / HD;
+        const float M = fmaxf(fmaxf(ms[0][h], ms[1][h]), fmaxf(ms[2][h], ms[3][h]));
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) o += __expf(ms[w][h] - M) * os[w][idx];
+        a.part[ob + 2 * G + idx] = o;
+    }
+    if (tid < G) {
+        const float M = fmaxf(fmaxf(ms[0][tid], ms[1][tid]), fmaxf(ms[2][tid], ms[3][tid]));
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) L += __expf(ms[w][tid] - M) * ls[w][tid];
+        a.part[ob + tid] = M;
+        a.part[ob + G + tid] = L;
+    }
+    GH_MARK(6);
+    GH_MARK_END();
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
+    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
+    if (j >= a.n_used) return;  // uniform per workgroup
+    const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
+    __shared__ __align__(16) AttnStepLds<HD, G> lds;
+    if (c1 - c0 <= 32) attn_step_body<HD, G, 1>(a, g, j, lds);
+    else attn_step_body<HD, G, 2>(a, g, j, lds);
+}
+
+static int launch_attn_step(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
+    if (a.nc > ATTN_MAX_NC || a.nc < 1) return set_error(GH_ERR_INVALID, "attention: %d splits (1..%d)", a.nc, ATTN_MAX_NC);
+    const dim3 grid(nkv * a.nc), block(NT);
+#define GH_ATTN_CASE(HD_, G_) \
+    if (hd == HD_ && G == G_) return sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_>, grid, block, 0, a);
+    GH_ATTN_CASE(256, 1) GH_ATTN_CASE(256, 2) GH_ATTN_CASE(256, 4) GH_ATTN_CASE(256, 8)
+    GH_ATTN_CASE(128, 1) GH_ATTN_CASE(128, 2) GH_ATTN_CASE(128, 4) GH_ATTN_CASE(128, 8)
+    GH_ATTN_CASE(32, 1) GH_ATTN_CASE(32, 2) GH_ATTN_CASE(32, 4) GH_ATTN_CASE(32, 8)
+#undef GH_ATTN_CASE
+    return set_error(GH_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
 
 template <bool STEP>
@@ -2388,7 +2635,7 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             a.part = m->attn_part;
             a.nc = m->attn_nc;
             a.set_pos(pos);
-            GH_CHECK(launch_attn_t<true>(sink, 2.0 * 4.0 * hd * nkv * (a.pe - a.pb), hd, G, a, nkv));
+            GH_CHECK(launch_attn_step(sink, 2.0 * 4.0 * hd * nkv * (a.pe - a.pb), hd, G, a, nkv));
         }
         // C: attention merge + O projection
         {
