@@ -27,6 +27,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "common.h"
 
@@ -436,9 +437,39 @@ __device__ __forceinline__ MvLds mv_lds(float* lds, int per_split) {
 // (RL 1) or lane and lane+64 (RL 2); the four waves split the split's
 // column blocks evenly.  `rt` is the item's row-tile index for the
 // epilogue, which wave 0 runs on the summed rows.
+//
+// A prologue may define load_v<V>() and variant(): the waves whose share of
+// the input loads is all out of range (a partial last round of float4
+// groups, or no groups at all) take the variant V = 0 that does not issue
+// those loads, since each load instruction costs its CU's address unit the
+// same time whether or not its offset is in range.  The variant is chosen
+// before any load, so each variant's s_waitcnt counts stay exact.
+template <class P, class = void>
+struct HasLoadVariants : std::false_type {};
+template <class P>
+struct HasLoadVariants<P, std::void_t<decltype(&P::template load_v<0>)>> : std::true_type {};
+
+template <int FMT, int KBW, int RL, int V, class Pro, class Epi>
+__device__ __forceinline__ void mv_item_v(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
+                                          const MvLds& L);
+
 template <int FMT, int KBW, int RL, class Pro, class Epi>
 __device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
                                         const MvLds& L) {
+    if constexpr (HasLoadVariants<Pro>::value) {
+        constexpr int BK = Blk<FMT>::BK;
+        const int per_split = (w.nblk + S - 1) / S;
+        const int kb0 = min(w.nblk, s * per_split), nk = min(w.nblk, kb0 + per_split) - kb0;
+        if (pro.variant(kb0 * BK, nk * BK)) mv_item_v<FMT, KBW, RL, 1>(w, rt, s, S, pro, epi, L);
+        else mv_item_v<FMT, KBW, RL, 0>(w, rt, s, S, pro, epi, L);
+    } else {
+        mv_item_v<FMT, KBW, RL, 1>(w, rt, s, S, pro, epi, L);
+    }
+}
+
+template <int FMT, int KBW, int RL, int V, class Pro, class Epi>
+__device__ __forceinline__ void mv_item_v(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
+                                          const MvLds& L) {
     constexpr int BK = Blk<FMT>::BK;
     const int tile = RL == 2 ? rt : rt >> 1, rbase = RL == 2 ? 0 : (rt & 1) * 64;
     const int nb = w.nblk;
@@ -453,7 +484,8 @@ __device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, con
     // 3. the prologue builds the input slice [kb0*BK, kb1*BK) in LDS.
     GH_MARK(0);
     typename Pro::Regs pr;
-    pro.load(pr, kb0 * BK, nk * BK);
+    if constexpr (HasLoadVariants<Pro>::value) pro.template load_v<V>(pr, kb0 * BK, nk * BK);
+    else pro.load(pr, kb0 * BK, nk * BK);
     typename Epi::Regs er;
     epi.load(er);
     // the scheduler may not interleave the three groups: a prologue add
@@ -595,24 +627,30 @@ struct ProResid {
         float4 bv[MG], wp[MG];
         float4 wn[MG];  // norm weights of this thread's groups of the slice
     };
-    __device__ void load(Regs& r, int c0, int n) const {
+    // variant 1: this wave has groups in the last round of the H/4 groups
+    __device__ int variant(int, int) const { return wave_id() * 64 + (MG - 1) * NT < (H >> 2); }
+    template <int V>
+    __device__ void load_v(Regs& r, int c0, int n) const {
+        constexpr int RR = MG > 1 && V == 0 ? MG - 1 : MG;  // rounds this wave loads
         const int NG = H >> 2, tid = threadIdx.x;
         const BufView WN(w_norm + c0, (size_t)n * 4);
 #pragma unroll
-        for (int k = 0; k < MG; ++k) r.wn[k] = WN.f4(16u * (tid + k * NT));
+        for (int k = 0; k < MG; ++k) r.wn[k] = k < RR ? WN.f4(16u * (tid + k * NT)) : f4z();
         if constexpr (!EMB) {
             const BufView P(part, (size_t)S * ld * 4), B(base, (size_t)H * 4), WP(w_post, w_post ? (size_t)H * 4 : 0);
 #pragma unroll
             for (int k = 0; k < MG; ++k) {
                 const int g = tid + k * NT;
                 const uint32_t o = g < NG ? 16u * g : OOB;
-                r.bv[k] = B.f4(o);
-                r.wp[k] = WP.f4(o);
+                r.bv[k] = k < RR ? B.f4(o) : f4z();
+                r.wp[k] = k < RR ? WP.f4(o) : f4z();
 #pragma unroll
-                for (int s = 0; s < MAXS; ++s) r.pv[s][k] = P.f4(g < NG ? 4u * (uint32_t)(s * ld) + 16u * g : OOB);
+                for (int s = 0; s < MAXS; ++s)
+                    r.pv[s][k] = k < RR ? P.f4(g < NG ? 4u * (uint32_t)(s * ld) + 16u * g : OOB) : f4z();
             }
         }
     }
+    __device__ void load(Regs& r, int c0, int n) const { load_v<1>(r, c0, n); }
     template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int NG = H >> 2, tid = threadIdx.x;
@@ -715,7 +753,10 @@ struct ProAttnCombine {
         float4 ov[PRE];
         float mj, lj;
     };
-    __device__ void load(Regs& r, int c0, int n) const {
+    // variant 1: this wave holds column groups of the slice
+    __device__ int variant(int, int n) const { return wave_id() * 64 < (n >> 2); }
+    template <int V>
+    __device__ void load_v(Regs& r, int c0, int n) const {
         const int stride = G * (HD + 2), tid = threadIdx.x;
         const BufView P(part, (size_t)nkv * nc * stride * 4);
         // this thread's column group (one per thread up to 1024 columns)
@@ -723,7 +764,8 @@ struct ProAttnCombine {
         const uint32_t ob = 4u * (uint32_t)((h / G) * nc * stride + 2 * G + (h % G) * HD + d);
         const bool in = tid < (n >> 2);
 #pragma unroll
-        for (int j = 0; j < PRE; ++j) r.ov[j] = P.f4(in && j < n_used ? ob + 4u * (uint32_t)(j * stride) : OOB);
+        for (int j = 0; j < PRE; ++j)
+            r.ov[j] = V ? P.f4(in && j < n_used ? ob + 4u * (uint32_t)(j * stride) : OOB) : f4z();
         // (m, l) of chunk j = lane for head h0 + wave
         const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
         const int hh = tid >> 6, j = tid & 63;
@@ -733,6 +775,7 @@ struct ProAttnCombine {
         r.mj = ok ? P.f1(bj) : -INFINITY;
         r.lj = P.f1(ok ? bj + 4u * G : OOB);
     }
+    __device__ void load(Regs& r, int c0, int n) const { load_v<1>(r, c0, n); }
     template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
         const int stride = G * (HD + 2), tid = threadIdx.x;
@@ -780,20 +823,22 @@ struct ProAttnCombine {
 
 // Down-projection input: h = gelu_tanh(sum_s g_s) * sum_s u_s (MLP.hs:384-447).
 // The gate/up split partials of the slice are loaded in one round trip:
-// gm (1 or 2) float4 groups per thread, register slot i holding split
-// i / gm of group i % gm (the host keeps Sg * gm <= MAXS).
+// gm (1 or 2) float4 groups per thread, register slot i < NS holding split
+// i / gm of group i % gm (the host keeps Sg * gm <= NS; NS is 4 or 8, so
+// no load instruction is spent on absent splits beyond the next of those).
+template <int NS>
 struct ProGeglu {
     const float* part_gu;
     int Sg, ld_g, up_off;
     int gm;
     struct Regs {
-        float4 g[MAXS], u[MAXS];
+        float4 g[NS], u[NS];
     };
     __device__ void load(Regs& r, int c0, int n) const {
         const BufView P(part_gu, (size_t)Sg * ld_g * 4);
         const int ng = n >> 2;
 #pragma unroll
-        for (int i = 0; i < MAXS; ++i) {
+        for (int i = 0; i < NS; ++i) {
             const int s = gm == 2 ? i >> 1 : i, gi = threadIdx.x + (gm == 2 ? (i & 1) * NT : 0);
             const bool ok = s < Sg && gi < ng;
             const uint32_t o = 4u * (uint32_t)(s * ld_g + c0 + 4 * gi);
@@ -814,7 +859,7 @@ struct ProGeglu {
         if (gm == 1) {
             float4 gs = r.g[0], us = r.u[0];
 #pragma unroll
-            for (int s = 1; s < MAXS; ++s) {
+            for (int s = 1; s < NS; ++s) {
                 gs = gs + r.g[s];
                 us = us + r.u[s];
             }
@@ -824,7 +869,7 @@ struct ProGeglu {
             for (int k = 0; k < 2; ++k) {
                 float4 gs = r.g[k], us = r.u[k];
 #pragma unroll
-                for (int s = 1; s < MAXS / 2; ++s) {
+                for (int s = 1; s < NS / 2; ++s) {
                     gs = gs + r.g[2 * s + k];
                     us = us + r.u[2 * s + k];
                 }
@@ -1959,13 +2004,19 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     __syncthreads();
     GH_MARK(5);
     const size_t ob = ((size_t)g * a.nc + j) * (G * (HD + 2));
-    for (int idx = tid; idx < G * HD; idx += NT) {
-        const int h = idx / HD;
-        const float M = fmaxf(fmaxf(ms[0][h], ms[1][h]), fmaxf(ms[2][h], ms[3][h]));
-        float o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) o += __expf(ms[w][h] - M) * os[w][idx];
-        a.part[ob + 2 * G + idx] = o;
+    // four consecutive outputs per thread (one head each: HD % 4 == 0)
+    for (int q4 = tid; q4 < G * HD / 4; q4 += NT) {
+        const int h = 4 * q4 / HD;
+        const float m0 = ms[0][h], m1 = ms[1][h], m2 = ms[2][h], m3 = ms[3][h];
+        const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+        const float e0 = __expf(m0 - M), e1 = __expf(m1 - M), e2 = __expf(m2 - M), e3 = __expf(m3 - M);
+        const float4 o0 = *(const float4*)&os[0][4 * q4], o1 = *(const float4*)&os[1][4 * q4];
+        const float4 o2 = *(const float4*)&os[2][4 * q4], o3 = *(const float4*)&os[3][4 * q4];
+        float* dst = a.part + ob + 2 * G + 4 * q4;
+        dst[0] = ((e0 * o0.x + e1 * o1.x) + e2 * o2.x) + e3 * o3.x;
+        dst[1] = ((e0 * o0.y + e1 * o1.y) + e2 * o2.y) + e3 * o3.y;
+        dst[2] = ((e0 * o0.z + e1 * o1.z) + e2 * o2.z) + e3 * o3.z;
+        dst[3] = ((e0 * o0.w + e1 * o1.w) + e2 * o2.w) + e3 * o3.w;
     }
     if (tid < G) {
         const float M = fmaxf(fmaxf(ms[0][tid], ms[1][tid]), fmaxf(ms[2][tid], ms[3][tid]));
@@ -2673,9 +2724,14 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             if (gm > 2 || gm * m->pd.S > MAXS)
                 return set_error(GH_ERR_INVALID, "down projection split of %d columns with %d gate/up splits",
                                  (L.down.nblk + m->pe.S - 1) / m->pe.S * block_cols(L.down.fmt), m->pd.S);
-            ProGeglu pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad, gm};
             EpiPartial epi{m->part_d, L.down.tiles * TILE_ROWS};
-            GH_CHECK(launch_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, pro, epi, 0));
+            if (gm * m->pd.S <= 4) {
+                ProGeglu<4> pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad, gm};
+                GH_CHECK(launch_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, pro, epi, 0));
+            } else {
+                ProGeglu<MAXS> pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad, gm};
+                GH_CHECK(launch_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, pro, epi, 0));
+            }
         }
     }
     // final residual + norm, once
