@@ -26,6 +26,7 @@ ORACLE_DIR = REPO / "oracle"
 ORACLE_LIB = ORACLE_DIR / "build" / "liboracle.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+KERNEL_TUS = 4  # kernels.hip: step, persistent step, prefill, op level
 ARCH = "gfx950"
 # Packed FP32 (v_pk_*_f32) is disabled for every HIP translation unit.
 DEVICE_FLAGS = [
@@ -55,15 +56,19 @@ def build_lib(jobs: int = 8) -> Path:
     OBJ.mkdir(exist_ok=True)
     units = []
     for src in sorted(CSRC.iterdir()):
-        if src.suffix == ".hip":
-            units.append((src, [HIPCC, *DEVICE_FLAGS, "-x", "hip"]))
+        if src.name == "kernels.hip":
+            # compiled as KERNEL_TUS translation units in parallel (GH_TU in kernels.hip)
+            for tu in range(1, KERNEL_TUS + 1):
+                units.append((src, [HIPCC, *DEVICE_FLAGS, f"-DGH_TU={tu}", "-x", "hip"], f"{src.stem}_tu{tu}"))
+        elif src.suffix == ".hip":
+            units.append((src, [HIPCC, *DEVICE_FLAGS, "-x", "hip"], src.stem))
         elif src.suffix == ".cpp":
-            units.append((src, [HOST_CXX, *HOST_FLAGS]))
+            units.append((src, [HOST_CXX, *HOST_FLAGS], src.stem))
     objs = []
 
     def compile_one(item):
-        src, cmd = item
-        obj = OBJ / (src.stem + ".o")
+        src, cmd, stem = item
+        obj = OBJ / (stem + ".o")
         _run([*cmd, "-c", str(src), "-o", str(obj)])
         return obj
 

@@ -31,6 +31,16 @@
 
 #include "common.h"
 
+// The library compiles this file as several translation units in parallel
+// (GH_TU = 1 step, 2 persistent step, 3 prefill, 4 op level); each defines
+// its own host entry points and so instantiates only the kernels they
+// launch.  Kernels launched from several units are templates, whose
+// symbols are merged at link time.  GH_TU = 0 (the default) is everything.
+#ifndef GH_TU
+#define GH_TU 0
+#endif
+#define GH_IN_TU(n) (GH_TU == 0 || GH_TU == (n))
+
 // Phase timestamp hook for latency studies; compiles to nothing unless a
 // timing harness defines it before including this file.
 #ifndef GH_MARK
@@ -2040,6 +2050,7 @@ __global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
     else attn_step_body<HD, G, 2>(a, g, j, lds);
 }
 
+#if GH_IN_TU(1)
 static int launch_attn_step(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
     if (a.nc > ATTN_MAX_NC || a.nc < 1) return set_error(GH_ERR_INVALID, "attention: %d splits (1..%d)", a.nc, ATTN_MAX_NC);
     const dim3 grid(nkv * a.nc), block(NT);
@@ -2051,6 +2062,7 @@ static int launch_attn_step(Sink& k, double bytes, int hd, int G, const AttnArgs
 #undef GH_ATTN_CASE
     return set_error(GH_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
+#endif
 
 template <bool STEP>
 static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
@@ -2070,6 +2082,7 @@ static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a
 // (q head h, 64-dim slice) loads the chunk states (m_j, l_j) in parallel,
 // then thread (c, d) sums dim d over chunks c, c + 4, ... (independent,
 // coalesced loads) and the four chunk groups are added in LDS.
+#if GH_IN_TU(4)
 constexpr int COMB_DIMS = 64;
 __global__ __launch_bounds__(NT) void k_attn_combine(const float* part, int nc, int n_used, int G, int HD, float* out) {
     __shared__ float wj[GH_ATTN_OP_MAX_NC];
@@ -2106,6 +2119,7 @@ __global__ __launch_bounds__(NT) void k_attn_combine(const float* part, int nc, 
         out[(size_t)h * HD + d] = ((red[0][dl] + red[1][dl]) + (red[2][dl] + red[3][dl])) / den;
     }
 }
+#endif
 
 // ------------------------------------------------------------------
 // step epilogue: greedy token from the per-tile keys, next token, position
@@ -2207,6 +2221,8 @@ __device__ int sample_select(const float* bm, const float* bs, int nb, int R, co
     return chosen;
 }
 
+// (a template so that every translation unit that launches it has its copy)
+template <int = 0>
 __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, const unsigned long long* cand, int n_cand,
                                                     const float* bm, const float* bs, int rows_per_cand,
                                                     const float* logits, int V, const int32_t* prompt, int32_t* ids) {
@@ -2236,6 +2252,7 @@ __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, cons
     st->pos = pos + 1;
 }
 
+#if GH_IN_TU(2)
 // ------------------------------------------------------------------
 // persistent step: one cooperative launch per token.  Every workgroup runs
 // the same phase sequence (per layer: QKV, attention, O, gate/up, down;
@@ -2588,14 +2605,17 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     else if (hd == 256 && G == 2 && MG == 1) GH_CHECK(go(k_step_persistent<256, 2, 1>));
     else GH_CHECK(go(k_step_persistent<256, 2, 3>));
     const int n_cand = 2 * m->embd.tiles;  // 64-row LM-head items
-    return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
+    return sink_launch<1>(sink, "finish", 0.0, k_step_finish<0>, dim3(1), dim3(NT), 0, kv->st, pos,
                           (const unsigned long long*)m->lm_cand, n_cand, (const float*)m->lm_m, (const float*)m->lm_s, 64,
                           (const float*)m->logits, c.vocab, (const int32_t*)kv->d_prompt, kv->d_ids);
 }
 
+#endif  // GH_IN_TU(2)
+
 // ------------------------------------------------------------------
 // the decode step
 // ------------------------------------------------------------------
+#if GH_IN_TU(1)
 int Profiler::kind_of(const char* name) {
     for (size_t i = 0; i < names.size(); ++i)
         if (names[i] == name) return (int)i;
@@ -2603,8 +2623,10 @@ int Profiler::kind_of(const char* name) {
     return (int)names.size() - 1;
 }
 
+#endif
+
 namespace {
-double mat_bytes(const DMat& w) {
+[[maybe_unused]] double mat_bytes(const DMat& w) {
     const double wb = w.fmt == FMT_Q4 ? (double)w.rows * w.cols / 32.0 * 18.0 : (double)w.rows * w.cols * 4.0;
     return wb + 4.0 * w.cols + 4.0 * w.rows;
 }
@@ -2612,19 +2634,20 @@ double mat_bytes(const DMat& w) {
 
 // LM head (tied embedding) on m->xn_final with per-workgroup argmax keys
 // and softmax statistics, then the next-token selection of position pos.
-static int enqueue_head(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
+[[maybe_unused]] static int enqueue_head(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     const gh_config& c = m->cfg;
     {
         ProPlain pro{m->xn_final};
         EpiLogits epi{m->logits, c.vocab, m->lm_cand, kv->st, m->lm_m, m->lm_s};
         GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(m->embd), m->embd, m->plm, pro, epi, 0));
     }
-    return sink_launch<1>(sink, "finish", 0.0, k_step_finish, dim3(1), dim3(NT), 0, kv->st, pos,
+    return sink_launch<1>(sink, "finish", 0.0, k_step_finish<0>, dim3(1), dim3(NT), 0, kv->st, pos,
                           (const unsigned long long*)m->lm_cand, m->plm.row_tiles(m->embd.tiles), (const float*)m->lm_m,
                           (const float*)m->lm_s, 64 * m->plm.rl, (const float*)m->logits, c.vocab,
                           (const int32_t*)kv->d_prompt, kv->d_ids);
 }
 
+#if GH_IN_TU(1)
 int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     const gh_config& c = m->cfg;
     const int H = c.hidden, nkv = c.n_kv_heads, hd = c.head_dim;
@@ -2761,7 +2784,9 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     }
     return enqueue_head(m, kv, sink, pos);
 }
+#endif  // GH_IN_TU(1)
 
+#if GH_IN_TU(3)
 // ------------------------------------------------------------------
 // batched prompt prefill: n prompt tokens in one pass per layer, instead of
 // the token-by-token prompt loop of app/Main.hs:426-436.  Per layer:
@@ -3418,7 +3443,9 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
     }
     return enqueue_head(m, kv, sink, pos0 + n - 1);
 }
+#endif  // GH_IN_TU(3)
 
+#if GH_IN_TU(4)
 // ------------------------------------------------------------------
 // op-level kernels
 // ------------------------------------------------------------------
@@ -3644,5 +3671,7 @@ int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s)
     GH_HIP(hipGetLastError());
     return GH_OK;
 }
+
+#endif  // GH_IN_TU(4)
 
 }  // namespace gh
