@@ -1828,8 +1828,12 @@ __global__ __launch_bounds__(NT) void k_attn_wave(AttnArgs a) {
 //             DPP sum per score; P.V lane = 4 dims, weights by readlane.
 //   merge     the four wave states, once, through LDS.
 // PF: K/V rounds per wave loaded ahead (1 for chunks of up to 4 rounds, where
-// each wave has at most one round; 2 otherwise).  The kernel picks the body
-// before issuing any load, so each body's s_waitcnt counts stay exact.
+// each wave has at most one round; 2 otherwise).  SKIP: this wave's groups
+// in the last prologue round are all k/v that its workgroup does not need,
+// or past q|k|v, so it issues none of that round's loads (every load
+// instruction costs its CU's address unit the same time, in range or not).
+// The kernel picks the body before issuing any load, so each body's
+// s_waitcnt counts stay exact.
 template <int HD, int G>
 struct AttnStepLds {
     float qs[G * HD];
@@ -1839,7 +1843,7 @@ struct AttnStepLds {
     float os[4][G * HD];
 };
 
-template <int HD, int G, int PF>
+template <int HD, int G, int PF, bool SKIP>
 __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, AttnStepLds<HD, G>& S) {
     constexpr int LPH = HD / 4;                  // lanes per head vector (one float4 each)
     constexpr int NG4 = (G + 2) * LPH;           // float4 groups of q | k | v
@@ -1867,6 +1871,12 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     float4 pv[MG4][MAXS], wn[MG4], cs0[MG4], cs1[MG4];
 #pragma unroll
     for (int m = 0; m < MG4; ++m) {
+        if (SKIP && m == MG4 - 1) {
+#pragma unroll
+            for (int s = 0; s < MAXS; ++s) pv[m][s] = f4z();
+            wn[m] = cs0[m] = cs1[m] = f4z();
+            continue;
+        }
         const int gi = tid + m * NT, vec = gi / LPH, d = 4 * (gi % LPH);  // vector (G q heads, k, v), first dim
         const int row = vec < G ? a.q_off + (g * G + vec) * HD + d : vec == G ? a.k_off + g * HD + d : a.v_off + g * HD + d;
         const bool ok = gi < NG4 && (vec < G || need_kv);
@@ -2046,8 +2056,19 @@ __global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
     if (j >= a.n_used) return;  // uniform per workgroup
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
     __shared__ __align__(16) AttnStepLds<HD, G> lds;
-    if (c1 - c0 <= 32) attn_step_body<HD, G, 1>(a, g, j, lds);
-    else attn_step_body<HD, G, 2>(a, g, j, lds);
+    // the first vector of this wave's groups in the last prologue round
+    constexpr int LPH = HD / 4, NG4 = (G + 2) * LPH, MG4 = (NG4 + NT - 1) / NT;
+    const int vec_lo = ((MG4 - 1) * NT + wave_id() * 64) / LPH;
+    const int pos = a.pos;
+    const bool need_kv = (pos >= c0 && pos < c1) || j == 0;
+    const bool skip = vec_lo >= G + 2 || (vec_lo >= G && !need_kv);
+    if (c1 - c0 <= 32) {
+        if (skip) attn_step_body<HD, G, 1, true>(a, g, j, lds);
+        else attn_step_body<HD, G, 1, false>(a, g, j, lds);
+    } else {
+        if (skip) attn_step_body<HD, G, 2, true>(a, g, j, lds);
+        else attn_step_body<HD, G, 2, false>(a, g, j, lds);
+    }
 }
 
 #if GH_IN_TU(1)
