@@ -2248,26 +2248,44 @@ __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, cons
                                                     const float* bm, const float* bs, int rows_per_cand,
                                                     const float* logits, int V, const int32_t* prompt, int32_t* ids) {
     __shared__ unsigned long long slot[4];
+    // the step state and the prompt token at pos + 1 are read up front, so
+    // their round trips overlap the key reduction
     const float inv_t = st->inv_temp;
+    const int start = st->start, n_prompt = st->n_prompt, gen_count = st->gen_count, gen_cap = st->gen_cap;
+    const int rel = pos + 1 - start;
+    const bool from_prompt = prompt && rel >= 0 && rel < n_prompt;
+    const int ptok = from_prompt ? prompt[rel] : 0;
     int tok;
     if (inv_t > 0.0f) {  // temperature sampling with a Philox draw keyed by the seed, counter = position
         const uint64_t seed = ((uint64_t)st->seed_hi << 32) | st->seed_lo;
         tok = sample_select(bm, bs, n_cand, rows_per_cand, logits, V, inv_t, philox_uniform(seed, (uint64_t)pos));
     } else {  // greedy: first maximum (sampleGreedy, examples/BenchmarkKVCache.hs:223-224)
+        // the per-item keys as one batch of straight-line buffer loads (keys
+        // past n_cand read zero, which no real key loses to)
+        constexpr int KPT = 16;  // keys per thread in one round trip: 4096 items
+        const BufView C(cand, (size_t)n_cand * 8);
+        unsigned long long k[KPT];
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(C.r, 8u * (threadIdx.x + i * NT), 0, 0));
+            k[i] = ((unsigned long long)v.y << 32) | v.x;
+        }
         unsigned long long best = 0ull;
-        for (int i = threadIdx.x; i < n_cand; i += NT) best = umax64(best, cand[i]);
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) best = umax64(best, k[i]);
+        for (int i = threadIdx.x + KPT * NT; i < n_cand; i += NT) best = umax64(best, cand[i]);
         best = block_max_key(best, slot);
         tok = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFull));
     }
     if (threadIdx.x != 0) return;
     st->last = tok;
-    const int rel = pos + 1 - st->start;
     int next = tok;
-    if (prompt && rel < st->n_prompt) {
-        next = prompt[rel];
-    } else if (ids && st->gen_count < st->gen_cap) {
-        ids[st->gen_count] = tok;
-        st->gen_count = st->gen_count + 1;
+    if (from_prompt) {
+        next = ptok;
+    } else if (ids && gen_count < gen_cap) {
+        ids[gen_count] = tok;
+        st->gen_count = gen_count + 1;
     }
     st->token = next;
     st->pos = pos + 1;
