@@ -32,16 +32,16 @@ HBM_PEAK_GBPS = 8000.0
 WEIGHT_SEED = 1234
 PROMPT_SEED = 1
 N_PROMPT = 128
-# back-to-back replays per kernel kind in the event-timed pass (a few ms each)
 # HBM bytes per LM-head launch from two rocprofv3 --pmc passes
-# (profiles/lm_head_gemma3-1b_decode.md): FETCH_SIZE 83,038 KiB x 1.99976 and
-# WRITE_SIZE 1,152 KiB x 1.0, each factor = the bytes a 256 MiB device copy
+# (profiles/lm_head_gemma3-1b_decode.md): FETCH_SIZE 83,043.1 KiB x 1.99981 and
+# WRITE_SIZE 1,152.0 KiB x 1.0, each factor = the bytes a 256 MiB device copy
 # moves / what the counter reads for that copy.
-LM_HEAD_TRAFFIC_BYTES = 171_221_066
-# The LM head gets 40 replays (1.1 ms of streaming): inside the decode loop it
+LM_HEAD_TRAFFIC_BYTES = 171_232_107
+# Back-to-back replays per kernel kind in the event-timed pass (a few ms
+# each).  The LM head gets 40 (1.1 ms of streaming): inside the decode loop it
 # runs once per ~700 us of latency-bound kernels, and a longer back-to-back
 # run slows it down (traced: 26.8 us for the first 10 of 200 launches, 33.6 us
-# for the last 50, 28.2 us for the decode loop's own LM heads).
+# for the last 50, 28.7 us for the decode loop's own LM heads).
 KERNEL_REPS = {"qkv": 40, "attention": 40, "o_proj": 40, "gate_up": 40, "down": 40, "final_norm": 400,
                "lm_head": 40}
 
