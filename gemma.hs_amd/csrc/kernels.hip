@@ -157,6 +157,21 @@ __device__ __forceinline__ float block_max(float v, float* slot) {
     return fmaxf(fmaxf(slot[0], slot[1]), fmaxf(slot[2], slot[3]));
 }
 
+// Four sums over the 256 threads with one barrier (`slot`: 16 floats of LDS,
+// same reuse rule as block_sum).
+__device__ __forceinline__ float4 block_sum4(float4 v, float* slot) {
+    v.x = wave_sum(v.x);
+    v.y = wave_sum(v.y);
+    v.z = wave_sum(v.z);
+    v.w = wave_sum(v.w);
+    if ((threadIdx.x & 63) == 0) ((float4*)slot)[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float4 a = ((const float4*)slot)[0], b = ((const float4*)slot)[1];
+    const float4 c = ((const float4*)slot)[2], d = ((const float4*)slot)[3];
+    return make_float4((a.x + b.x) + (c.x + d.x), (a.y + b.y) + (c.y + d.y), (a.z + b.z) + (c.z + d.z),
+                       (a.w + b.w) + (c.w + d.w));
+}
+
 // Order-preserving argmax key: larger value wins, then lower index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
     unsigned b = __float_as_uint(v);
@@ -611,6 +626,12 @@ struct ProPlain {
 //   x  = base + postnorm(sum_s part_s)        (residual add, TBG:305-343 / TBG:413-444)
 //     or E[token] * sqrt(H) for layer 0        (src/Gemma/Model.hs:1346-1361)
 //   xs = norm(x) with w_norm                   (TBG:110, MLP.hs:507-622, RMSNorm.hs:343-386)
+// Thread t, round k holds float4 group (c0/4 + t + k*256) mod H/4 of the
+// vector: the groups are rotated so that each thread's first groups are the
+// workgroup's own slice, which it then lays out from registers.  Both RMS
+// values come from one block reduction of four sums: with d the split sum,
+// e = d * (1 + w_post) and c = 1/rms(d), x = b + c * e, so
+//   sum x^2 = sum b^2 + 2 c sum b e + c^2 sum e^2.
 // Block 0 stores x to x_out and, when asked, to layer_out_row.  All split
 // partials (S <= MAXS), the residual and both norm weights are loaded in one
 // round trip, as straight-line buffer loads (absent splits read zeros).
@@ -637,12 +658,17 @@ struct ProResid {
         float4 bv[MG], wp[MG];
         float4 wn[MG];  // norm weights of this thread's groups of the slice
     };
+    // group of thread t in round k, rotated to start at the slice's first group
+    __device__ static int group(int g0, int t, int k, int NG) {
+        const int g = g0 + t + k * NT;
+        return g >= NG ? g - NG : g;
+    }
     // variant 1: this wave has groups in the last round of the H/4 groups
     __device__ int variant(int, int) const { return wave_id() * 64 + (MG - 1) * NT < (H >> 2); }
     template <int V>
     __device__ void load_v(Regs& r, int c0, int n) const {
         constexpr int RR = MG > 1 && V == 0 ? MG - 1 : MG;  // rounds this wave loads
-        const int NG = H >> 2, tid = threadIdx.x;
+        const int NG = H >> 2, tid = threadIdx.x, g0 = c0 >> 2;
         const BufView WN(w_norm + c0, (size_t)n * 4);
 #pragma unroll
         for (int k = 0; k < MG; ++k) r.wn[k] = k < RR ? WN.f4(16u * (tid + k * NT)) : f4z();
@@ -650,71 +676,79 @@ struct ProResid {
             const BufView P(part, (size_t)S * ld * 4), B(base, (size_t)H * 4), WP(w_post, w_post ? (size_t)H * 4 : 0);
 #pragma unroll
             for (int k = 0; k < MG; ++k) {
-                const int g = tid + k * NT;
-                const uint32_t o = g < NG ? 16u * g : OOB;
+                const int g = group(g0, tid, k, NG);
+                const bool in = tid + k * NT < NG;
+                const uint32_t o = in ? 16u * g : OOB;
                 r.bv[k] = k < RR ? B.f4(o) : f4z();
                 r.wp[k] = k < RR ? WP.f4(o) : f4z();
 #pragma unroll
                 for (int s = 0; s < MAXS; ++s)
-                    r.pv[s][k] = k < RR ? P.f4(g < NG ? 4u * (uint32_t)(s * ld) + 16u * g : OOB) : f4z();
+                    r.pv[s][k] = k < RR ? P.f4(in ? 4u * (uint32_t)(s * ld) + 16u * g : OOB) : f4z();
             }
         }
     }
     __device__ void load(Regs& r, int c0, int n) const { load_v<1>(r, c0, n); }
     template <int FMT>
     __device__ void finish(const MvLds& L, Regs& r, int c0, int n) const {
-        const int NG = H >> 2, tid = threadIdx.x;
+        const int NG = H >> 2, tid = threadIdx.x, g0 = c0 >> 2;
         float4 xv[MG];
+        float inv;  // 1 / rms(x)
         if constexpr (EMB) {
             // the host validates tokens; the clamp keeps a corrupted state in bounds
             const int tok = min(max(st->token, 0), embd.rows - 1);
+            float ss = 0.0f;
 #pragma unroll
             for (int k = 0; k < MG; ++k) {
-                const int g = tid + k * NT;
                 xv[k] = f4z();
-                if (g < NG) {
-                    const float4 e = dq_elem4(embd, tok, 4 * g);
+                if (tid + k * NT < NG) {
+                    const float4 e = dq_elem4(embd, tok, 4 * group(g0, tid, k, NG));
                     xv[k] = make_float4(e.x * escale, e.y * escale, e.z * escale, e.w * escale);
                 }
+                ss += dot4(xv[k], xv[k]);
             }
+            inv = 1.0f / sqrtf(block_sum(ss, L.misc) / (float)H + eps);
         } else {
             // absent splits and groups past H were read as zeros
-            float4 dv[MG];
-            float ss = 0.0f;
+            float4 dv[MG], ev[MG];
+            float dd = 0.0f, bb = 0.0f, be = 0.0f, ee = 0.0f;
 #pragma unroll
             for (int k = 0; k < MG; ++k) {
                 dv[k] = r.pv[0][k];
 #pragma unroll
                 for (int s = 1; s < MAXS; ++s) dv[k] = dv[k] + r.pv[s][k];
-                ss += dot4(dv[k], dv[k]);
+                const float4 w1 = zc ? make_float4(1.0f + r.wp[k].x, 1.0f + r.wp[k].y, 1.0f + r.wp[k].z, 1.0f + r.wp[k].w)
+                                     : r.wp[k];
+                ev[k] = w_post ? make_float4(dv[k].x * w1.x, dv[k].y * w1.y, dv[k].z * w1.z, dv[k].w * w1.w) : dv[k];
+                dd += dot4(dv[k], dv[k]);
+                bb += dot4(r.bv[k], r.bv[k]);
+                be += dot4(r.bv[k], ev[k]);
+                ee += dot4(ev[k], ev[k]);
             }
-            float inv = 1.0f;
-            if (w_post) inv = 1.0f / sqrtf(block_sum(ss, L.misc) / (float)H + eps);
+            const float4 t = block_sum4(make_float4(dd, bb, be, ee), L.misc + 16);
+            const float c = w_post ? 1.0f / sqrtf(t.x / (float)H + eps) : 1.0f;
             GH_MARK(6);
 #pragma unroll
-            for (int k = 0; k < MG; ++k) xv[k] = r.bv[k] + (w_post ? norm4i(dv[k], inv, r.wp[k], zc) : dv[k]);
+            for (int k = 0; k < MG; ++k) xv[k] = r.bv[k] + (w_post ? norm4i(dv[k], c, r.wp[k], zc) : dv[k]);
+            const float sxx = fmaxf(t.y + 2.0f * c * t.z + c * c * t.w, 0.0f);
+            inv = 1.0f / sqrtf(sxx / (float)H + eps);
         }
-        float ss = 0.0f;
+        if (blockIdx.x == 0 && (x_out || layer_out_row)) {
 #pragma unroll
-        for (int k = 0; k < MG; ++k) {
-            const int g = tid + k * NT;
-            ss += dot4(xv[k], xv[k]);
-            if (g < NG) {
-                ((float4*)L.tmp)[g] = xv[k];
-                if (blockIdx.x == 0) {
+            for (int k = 0; k < MG; ++k) {
+                if (tid + k * NT < NG) {
+                    const int g = group(g0, tid, k, NG);
                     if (x_out) ((float4*)x_out)[g] = xv[k];
                     if (layer_out_row) ((float4*)layer_out_row)[g] = xv[k];
                 }
             }
         }
-        const float inv = 1.0f / sqrtf(block_sum(ss, L.misc + 4) / (float)H + eps);  // barrier: tmp complete
         GH_MARK(7);
+        // this thread's groups of the slice are its first ones (rotation)
         const int ng = n >> 2;
-        const float4* t4 = (const float4*)(L.tmp + c0);
 #pragma unroll
         for (int k = 0; k < MG; ++k) {
             const int gi = tid + k * NT;
-            if (k * NT < ng) emit_x4<FMT>(L, gi, ng, gi < ng ? norm4i(t4[gi], inv, r.wn[k], zc) : f4z());
+            if (k * NT < ng) emit_x4<FMT>(L, gi, ng, gi < ng ? norm4i(xv[k], inv, r.wn[k], zc) : f4z());
         }
     }
 };
