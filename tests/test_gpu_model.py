@@ -127,6 +127,31 @@ def test_small_q4_gqa_model_local_global_live_oracle(ctx, mode, rl, monkeypatch)
             assert nxt == obest
 
 
+@pytest.mark.parametrize("nq,nkv", [(8, 4), (4, 1)])
+def test_long_attention_chunks_live_oracle(ctx, nq, nkv, monkeypatch):
+    """Two attention chunks per kv head (GH_ATTN_NC=2), so past ~64 positions
+    every chunk spans several 8-position rounds per wave and the step kernel
+    loads K/V two rounds ahead, with partial last rounds; local layers with a
+    window of 80 slide.  Head dim 256, group 2 and 4; the live oracle checks
+    every layer and the logits along 150 steps."""
+    monkeypatch.setenv("GH_ATTN_NC", "2")
+    cfg = gh.preset("gemma3-4b")
+    cfg.n_heads, cfg.n_kv_heads = nq, nkv
+    cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 4, 1024
+    cfg.sliding_window, cfg.global_every, cfg.max_seq = 80, 2, 256
+    m = _gpu_model(ctx, cfg, 21, True)
+    om = _oracle_model(cfg, 21, True)
+    kv = gh.KVCache(m, 256)
+    toks = gh.synth_tokens(9, "t", 150, cfg.vocab)
+    for pos, t in enumerate(toks):
+        logits, _, layers, nxt = gh.runGemmaInferenceCachedWithLayer0(m, int(t), kv)
+        olog, olay, obest = om.step(int(t), pos, want_layers=True)
+        if pos % 7 == 0 or pos >= 140:
+            for l in range(cfg.n_layers):
+                assert rel_err(layers[l], olay[l]) < ACT_TOL, (pos, l)
+            assert rel_err(logits, olog) < ACT_TOL, pos
+
+
 def test_errors_kv_full_bad_token_incomplete_model(ctx):
     cfg = gh.preset("tiny")
     m = _gpu_model(ctx, cfg, 1, False)
