@@ -264,6 +264,11 @@ def main(argv=None) -> int:
                 "frac": round(lm.gbps / HBM_PEAK_GBPS, 4), "traffic": LM_HEAD_TRAFFIC_BYTES,
                 "traffic_source": "rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated)", "kernel": "lm_head",
                 "bytes_per_launch": int(lm.bytes_per_launch), "avg_us": round(lm.avg_us, 3)}
+    # the box's practical ceiling: 1 GiB read once per launch (non-temporal 16 B loads)
+    sr_gbps, sr_us = gh.stream_read_gbps(ctx, 1 << 30, 20)
+    log(f"  stream read 1 GiB: {sr_us:.1f} us -> {sr_gbps:.1f} GB/s")
+    roofline["measured_stream_read"] = {"gbps": round(sr_gbps, 1), "bytes": 1 << 30, "avg_us": round(sr_us, 2),
+                                        "lm_head_frac": round(lm.gbps / sr_gbps, 4)}
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,

@@ -35,8 +35,10 @@ int set_error(int code, const char* fmt, ...);
 uint16_t f32_to_f16_rne(float f);
 float f16_to_f32(uint16_t h, bool ftz);
 
-// Matrix storage formats on the device.
-enum Fmt : int { FMT_Q4 = 0, FMT_F32 = 1 };
+// Matrix storage formats on the device.  FMT_Q4M is not a storage format:
+// it names the kernels' compute mode for Q4_0 matrices whose dot products
+// run on the int8 matrix cores (Plan::mfma).
+enum Fmt : int { FMT_Q4 = 0, FMT_F32 = 1, FMT_Q4M = 2 };
 
 // Rows per tile of the device layout.  A tile stores, for every column
 // block kb, the 16-byte payloads of its 128 rows contiguously:
@@ -57,7 +59,7 @@ struct DMat {
     int tiles = 0;  // ceil(rows / 128)
 };
 
-inline int block_cols(int fmt) { return fmt == FMT_Q4 ? 32 : 4; }
+inline int block_cols(int fmt) { return fmt == FMT_F32 ? 4 : 32; }
 inline int pad_rows(int r) { return (r + TILE_ROWS - 1) / TILE_ROWS * TILE_ROWS; }
 
 // Device-side per-sequence step state (one per KV handle).
@@ -83,6 +85,7 @@ struct Plan {
     int S = 1;
     int kbw = 1;
     int rl = 2;  // rows per lane: 2 = 128-row workgroups, 1 = 64-row workgroups
+    int mfma = 0;  // Q4_0: dot products on the int8 matrix cores (1) or the VALU (0)
     int row_tiles(int tiles) const { return rl == 2 ? tiles : 2 * tiles; }
 };
 
@@ -296,6 +299,7 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
                      int p_begin, int p_end, int n_splits, float* part, float* out, hipStream_t s);
 int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t s);
 int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
+int launch_stream_read(const void* p, size_t bytes, float* sink, hipStream_t s);
 int launch_synth_normal(float* out, size_t n, uint64_t key, float sigma, hipStream_t s);
 constexpr int GH_ATTN_OP_MAX_NC = 256;  // chunks per kv head of the op-level attention
 int launch_sample_logits(const float* logits, int n, float inv_temp, uint64_t seed, uint64_t counter, float* scratch,

@@ -56,6 +56,9 @@ constexpr int NT = 256;  // threads per workgroup (4 wave64)
 constexpr int MAXS = 8;  // max column splits reduced by a prologue in one round trip
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------
@@ -138,6 +141,13 @@ __device__ __forceinline__ float group_sum(float v) {
         v += dpp<DPP_QUAD_XOR2>(v);
         return v + dpp<DPP_ROW_HALF_MIRROR>(v);
     }
+}
+
+// max over aligned groups of 8 lanes (result in every lane of the group)
+__device__ __forceinline__ float group_max8(float v) {
+    v = fmaxf(v, dpp<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp<DPP_QUAD_XOR2>(v));
+    return fmaxf(v, dpp<DPP_ROW_HALF_MIRROR>(v));
 }
 
 // Sum over the 256 threads, one barrier; `slot` (4 floats of LDS) must not
@@ -230,6 +240,10 @@ struct BufView {
         return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP));
     }
     template <int CP = 0>
+    __device__ __forceinline__ u32x2 u2(uint32_t off) const {
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP));
+    }
+    template <int CP = 0>
     __device__ __forceinline__ float f1(uint32_t off) const {
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP));
     }
@@ -311,6 +325,10 @@ template <int FMT>
 struct Blk;
 template <>
 struct Blk<FMT_Q4> {
+    static constexpr int BK = 32;
+};
+template <>
+struct Blk<FMT_Q4M> {
     static constexpr int BK = 32;
 };
 template <>
@@ -428,32 +446,40 @@ __device__ __forceinline__ void mv_compute(const WRegs<FMT, KBW>& r, int base, i
     }
 }
 
-// LDS layout of k_matvec (floats):
-//   red [512] | misc [64] | xs [per_split*BK] | sxs [per_split, padded to 4] | tmp [...]
+// LDS layout of k_matvec (floats), with P = per_split rounded up to 4 blocks:
+//   red [512] | misc [64] | xs [P*BK] | sxs [P] | zero [4] | tmp [...]
+// xs/sxs hold the input slice: floats and per-block sums (F32, VALU Q4_0)
+// or int8 limbs and per-block multipliers (Q4_0 on the matrix cores);
+// zero is a 16-byte zero operand.
 struct MvLds {
     float* red;
     float* misc;  // 16 slots of 4 floats for block reductions
     float* xs;
     float* sxs;
+    float* zero;
     float* tmp;
 };
 
+inline size_t mv_lds_floats(int fmt, int per_split, int tmp_floats) {
+    const size_t p4 = ((size_t)per_split + 3) & ~(size_t)3;
+    return 512 + 64 + p4 * block_cols(fmt) + p4 + 4 + (size_t)tmp_floats;
+}
 inline size_t mv_lds_bytes(int fmt, int per_split, int tmp_floats) {
-    const int bk = block_cols(fmt);
-    size_t f = 512 + 64 + (size_t)per_split * bk + (((size_t)per_split + 3) & ~(size_t)3) + tmp_floats;
-    return f * sizeof(float);
+    return mv_lds_floats(fmt, per_split, tmp_floats) * sizeof(float);
 }
 
 // LDS carve-up of one matvec work item (floats from `lds`).
 template <int FMT>
 __device__ __forceinline__ MvLds mv_lds(float* lds, int per_split) {
     constexpr int BK = Blk<FMT>::BK;
+    const int p4 = (per_split + 3) & ~3;
     MvLds L;
     L.red = lds;
     L.misc = lds + 512;
     L.xs = lds + 576;
-    L.sxs = L.xs + per_split * BK;
-    L.tmp = L.sxs + ((per_split + 3) & ~3);
+    L.sxs = L.xs + p4 * BK;
+    L.zero = L.sxs + p4;
+    L.tmp = L.zero + 4;
     return L;
 }
 
@@ -492,9 +518,170 @@ __device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, con
     }
 }
 
+// ------------------------------------------------------------------
+// Q4_0 matvec on the int8 matrix cores (v_mfma_i32_16x16x64_i8)
+// ------------------------------------------------------------------
+// A wave takes 16-row groups; one MFMA pair covers a group's rows x a quad
+// of 4 column blocks:
+//   A (16 rows x 64): lane m + 16g holds the 16 code bytes of row m, block
+//     4q+g; their low nibbles feed the first MFMA and the high ones the
+//     second, each as the int8 16*(q-8) (q ^ 8 is q-8 as a signed nibble);
+//   B (64 x 16): column n = 4*b + limb; lane n + 16g holds limb n%4 of
+//     elements 0..15 (first MFMA) or 16..31 (second) of block 4q+g when
+//     n/4 == g, and zeros otherwise;
+//   D[m][n] = 16 * sum_p (q_mp - 8) * limb_{n%4}(X_p) over block 4q + n/4,
+//     exact in int32; lane L holds rows 4(L/16)+i of column L%16.
+// Each lane scales its D by the rows' fp16 block scales and the block/limb
+// multiplier and accumulates in f32; a 16-lane sum adds a row's columns.
+template <int QB, int RL>
+struct QRegs {
+    u32x4 c[RL][QB];  // codes: row (lane & 15) of the row group, block 4q + lane/16
+    u32x2 s[RL][QB];  // fp16 scales: rows 4*(lane/16) .. +3, block 4q + (lane & 15)/4
+};
+
+// Loads of one register batch: quads q0 .. q0+QB-1 (first block kq) of the
+// wave's RL row groups; blocks at or past kb1 read zeros.
+template <int QB, int RL>
+__device__ __forceinline__ void mq_load(QRegs<QB, RL>& r, const DMat& w, const MatViews& v, int tile, int rbase,
+                                        int kq, int kb1) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const uint32_t tb = (uint32_t)tile * (uint32_t)w.nblk * TILE_ROWS;
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+        const int r16 = rbase + 16 * (wave * RL + j);
+#pragma unroll
+        for (int i = 0; i < QB; ++i) {
+            const int ka = kq + 4 * i + (lane >> 4), ks = kq + 4 * i + ((lane & 15) >> 2);
+            const uint32_t ea = tb + (uint32_t)ka * TILE_ROWS + (uint32_t)(r16 + (lane & 15));
+            const uint32_t es = tb + (uint32_t)ks * TILE_ROWS + (uint32_t)(r16 + 4 * (lane >> 4));
+            r.c[j][i] = v.codes.template u4<CP_NT>(ka < kb1 ? ea * 16u : OOB);
+            r.s[j][i] = v.scales.template u2<CP_NT>(ks < kb1 ? es * 2u : OOB);
+        }
+    }
+}
+
+// The MFMA pairs of quad i of a register batch; bl = first block of the quad
+// within the slice.
+template <int QB, int RL>
+__device__ __forceinline__ void mq_quad(const QRegs<QB, RL>& r, int i, int bl, const MvLds& L, float (&acc)[RL][4]) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const bool act = (n >> 2) == g;
+    const float lp = (float)(1u << (7 * (n & 3)));
+    // 16-byte limb chunks: block * 8 + half * 4 + limb
+    const i32x4* lb = (const i32x4*)L.xs + ((bl + g) * 8 + (n & 3));
+    const i32x4* zero = (const i32x4*)L.zero;
+    const i32x4 b0 = *(act ? lb : zero), b1 = *(act ? lb + 4 : zero);
+    const float mq = L.sxs[bl + (n >> 2)] * lp;
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+        const u32x4 c = r.c[j][i];
+        i32x4 alo, ahi;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {  // 16 * (q - 8) as int8: q ^ 8 is q - 8 as a signed nibble
+            ahi[k] = (int)((c[k] ^ 0x80808080u) & 0xF0F0F0F0u);
+            alo[k] = (int)(((c[k] << 4) ^ 0x80808080u) & 0xF0F0F0F0u);
+        }
+        i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, b0, (i32x4){0, 0, 0, 0}, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, b1, d, 0, 0, 0);
+        const u32x2 sc = r.s[j][i];
+        acc[j][0] = fmaf((float)d[0], h2f((uint16_t)sc.x) * mq, acc[j][0]);
+        acc[j][1] = fmaf((float)d[1], h2f((uint16_t)(sc.x >> 16)) * mq, acc[j][1]);
+        acc[j][2] = fmaf((float)d[2], h2f((uint16_t)sc.y) * mq, acc[j][2]);
+        acc[j][3] = fmaf((float)d[3], h2f((uint16_t)(sc.y >> 16)) * mq, acc[j][3]);
+    }
+}
+
+// The MFMA pairs of quads q0 .. min(q0+QB, nq)-1 (quad q: blocks 4q.. of the slice).
+template <int QB, int RL>
+__device__ __forceinline__ void mq_compute(const QRegs<QB, RL>& r, int q0, int nq, const MvLds& L,
+                                           float (&acc)[RL][4]) {
+    if (q0 + QB <= nq) {  // full batch: straight-line (nq is wave-uniform)
+#pragma unroll
+        for (int i = 0; i < QB; ++i) mq_quad<QB, RL>(r, i, 4 * (q0 + i), L, acc);
+    } else {
+#pragma unroll
+        for (int i = 0; i < QB; ++i)
+            if (q0 + i < nq) mq_quad<QB, RL>(r, i, 4 * (q0 + i), L, acc);
+    }
+}
+
+// One Q4_0 work item on the matrix cores (same contract as mv_item_v): wave
+// w takes row groups w*RL .. w*RL+RL-1 over all of the split's blocks, in
+// register batches of QB quads.
+template <int QB, int RL, int V, class Pro, class Epi>
+__device__ __forceinline__ void mq_item_v(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
+                                          const MvLds& L) {
+    const int tile = RL == 2 ? rt : rt >> 1, rbase = RL == 2 ? 0 : (rt & 1) * 64;
+    const int nb = w.nblk;
+    const int per_split = (nb + S - 1) / S;
+    const int kb0 = min(nb, s * per_split), kb1 = min(nb, kb0 + per_split);
+    const int nk = kb1 - kb0, nq = (nk + 3) >> 2;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+
+    GH_MARK(0);
+    typename Pro::Regs pr;
+    if constexpr (HasLoadVariants<Pro>::value) pro.template load_v<V>(pr, kb0 * 32, nk * 32);
+    else pro.load(pr, kb0 * 32, nk * 32);
+    typename Epi::Regs er;
+    epi.load(er);
+    __builtin_amdgcn_sched_barrier(0);
+    const MatViews mv(w);
+    QRegs<QB, RL> r;
+    mq_load<QB, RL>(r, w, mv, tile, rbase, kb0, kb1);
+    __builtin_amdgcn_sched_barrier(0);
+    pro.template finish<FMT_Q4M>(L, pr, kb0 * 32, nk * 32);
+    if (threadIdx.x < 4) L.zero[threadIdx.x] = 0.0f;
+    GH_MARK(1);
+    __syncthreads();
+    GH_MARK(2);
+    float acc[RL][4];
+#pragma unroll
+    for (int j = 0; j < RL; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+    mq_compute<QB, RL>(r, 0, nq, L, acc);
+    for (int q0 = QB; q0 < nq; q0 += QB) {
+        mq_load<QB, RL>(r, w, mv, tile, rbase, kb0 + 4 * q0, kb1);
+        mq_compute<QB, RL>(r, q0, nq, L, acc);
+    }
+    GH_MARK(3);
+    // sum the 16 columns of each row; lane 16g then holds rows 4g .. 4g+3
+#pragma unroll
+    for (int j = 0; j < RL; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[j][k] = row16_sum(acc[j][k]);
+    if ((lane & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < RL; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) L.red[16 * (wave * RL + j) + 4 * (lane >> 4) + k] = acc[j][k];
+    }
+    __syncthreads();
+    GH_MARK(4);
+    if (wave == 0) {
+        const float y0 = L.red[lane], y1 = RL == 2 ? L.red[64 + lane] : 0.0f;
+        epi.template run<RL>(L, er, rt, tile * TILE_ROWS + rbase + lane, s, y0, y1);
+    }
+    GH_MARK(5);
+    GH_MARK_END();
+}
+
+template <int FMT, int KBW, int RL, int V, class Pro, class Epi>
+__device__ __forceinline__ void mv_item_valu(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
+                                             const MvLds& L);
+
 template <int FMT, int KBW, int RL, int V, class Pro, class Epi>
 __device__ __forceinline__ void mv_item_v(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
                                           const MvLds& L) {
+    if constexpr (FMT == FMT_Q4M) {
+        mq_item_v<KBW, RL, V>(w, rt, s, S, pro, epi, L);
+    } else {
+        mv_item_valu<FMT, KBW, RL, V>(w, rt, s, S, pro, epi, L);
+    }
+}
+
+// One work item with the dot products on the VALU (F32, Q4_0).
+template <int FMT, int KBW, int RL, int V, class Pro, class Epi>
+__device__ __forceinline__ void mv_item_valu(const DMat& w, int rt, int s, int S, const Pro& pro, const Epi& epi,
+                                             const MvLds& L) {
     constexpr int BK = Blk<FMT>::BK;
     const int tile = RL == 2 ? rt : rt >> 1, rbase = RL == 2 ? 0 : (rt & 1) * 64;
     const int nb = w.nblk;
@@ -566,14 +753,55 @@ __device__ __forceinline__ float4 fma4(float w, float4 o, float4 acc) {
 }
 __device__ __forceinline__ float4 f4z() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
+// 7-bit field of X starting at bit 7*l, as an int8 byte (l = 3: the signed top limb)
+template <int l>
+__device__ __forceinline__ uint32_t limb_byte(int X) {
+    return __builtin_amdgcn_ubfe((uint32_t)X, 7 * l, l == 3 ? 8 : 7);
+}
+
 // Store float4 group gi (< ng) of the input slice.  For Q4_0 the 8 groups of
-// a 32-element block sit in 8 consecutive lanes, which sum the block (sxs,
-// for the -8 * sum(x) term) and scale elements 16..31 by 1/16 (exact) for
-// the high-nibble products of dot_q4_word.  Called by every thread of the
-// workgroup with gi = base + threadIdx.x (base uniform, a multiple of NT).
+// a 32-element block sit in 8 consecutive lanes.  Called by every thread of
+// the workgroup with gi = base + threadIdx.x (base uniform, a multiple of NT).
+//
+// FMT_Q4M (Q4_0 on the matrix cores): the block's lanes find its largest |x| < 2^e and
+// write X = rint(x * 2^(27-e)) (|X| <= 2^27; the rounding error is at most
+// 2^(e-28), i.e. 2^-27 of the block's largest element) as four int8 limbs
+//   X = L0 + 2^7 L1 + 2^14 L2 + 2^21 L3   (L0..L2 in [0, 127], L3 in [-64, 64])
+// at limbs[block][half][limb][16 bytes] (byte p: element 16*half + p), and
+// the block multiplier 2^(e-31) = 2^-(27-e) * 2^-4 (the 4 undoes the x16 of
+// the signed nibbles; NaN when the block holds an Inf or NaN, so it
+// propagates).  Groups from ng up to the next 4-block boundary are zeros.
+//
+// FMT_Q4 (Q4_0 on the VALU): the lanes sum the block (sxs, for the -8 * sum(x) term)
+// and scale elements 16..31 by 1/16 (exact) for the high-nibble products of
+// dot_q4_word.
 template <int FMT>
 __device__ __forceinline__ void emit_x4(const MvLds& L, int gi, int ng, float4 v) {
-    if constexpr (FMT == FMT_Q4) {
+    if constexpr (FMT == FMT_Q4M) {
+        const int ngp = (ng + 31) & ~31;
+        if (__builtin_amdgcn_readfirstlane(gi - (int)(threadIdx.x & 63)) >= ngp) return;  // no group of this wave
+        if (gi >= ng) v = f4z();
+        // an Inf or NaN element makes the block maximum Inf (fmaxf drops NaNs)
+        const float fin = (v.x - v.x) + (v.y - v.y) + (v.z - v.z) + (v.w - v.w);
+        const float a4 = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        const float amax = group_max8(fin == 0.0f ? a4 : INFINITY);
+        const int e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e (0 for 0)
+        const int sh = 27 - e;
+        const int X0 = (int)rintf(ldexpf(v.x, sh)), X1 = (int)rintf(ldexpf(v.y, sh));
+        const int X2 = (int)rintf(ldexpf(v.z, sh)), X3 = (int)rintf(ldexpf(v.w, sh));
+        auto pack = [&](auto l) {
+            constexpr int L_ = decltype(l)::value;
+            return limb_byte<L_>(X0) | limb_byte<L_>(X1) << 8 | limb_byte<L_>(X2) << 16 | limb_byte<L_>(X3) << 24;
+        };
+        if (gi < ngp) {
+            uint32_t* d = (uint32_t*)L.xs + (gi >> 3) * 32 + ((gi & 7) >> 2) * 16 + (gi & 3);
+            d[0] = pack(std::integral_constant<int, 0>{});
+            d[4] = pack(std::integral_constant<int, 1>{});
+            d[8] = pack(std::integral_constant<int, 2>{});
+            d[12] = pack(std::integral_constant<int, 3>{});
+            if ((gi & 7) == 0) L.sxs[gi >> 3] = amax <= 3.4028235e38f ? ldexpf(1.0f, e - 31) : __builtin_nanf("");
+        }
+    } else if constexpr (FMT == FMT_Q4) {
         const float bs = group_sum<8>((v.x + v.y) + (v.z + v.w));
         if ((gi & 7) >= 4) v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
         if (gi < ng) {
@@ -1313,11 +1541,12 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
     };
     auto by_rl = [&](auto kbw) -> int {
         constexpr int KBW = decltype(kbw)::value;
-        if (w.fmt != FMT_Q4) return p.rl == 2 ? go(k_matvec<FMT_F32, 8, 2, Pro, Epi>) : go(k_matvec<FMT_F32, 8, 1, Pro, Epi>);
+        if (p.mfma) return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
         return p.rl == 2 ? go(k_matvec<FMT_Q4, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4, KBW, 1, Pro, Epi>);
     };
     if (p.rl != 1 && p.rl != 2) return set_error(GH_ERR_INVALID, "unsupported rows per lane %d", p.rl);
-    if (w.fmt != FMT_Q4) return by_rl(std::integral_constant<int, 8>{});
+    if (w.fmt != FMT_Q4)
+        return p.rl == 2 ? go(k_matvec<FMT_F32, 8, 2, Pro, Epi>) : go(k_matvec<FMT_F32, 8, 1, Pro, Epi>);
     switch (p.kbw) {
         case 1: return by_rl(std::integral_constant<int, 1>{});
         case 2: return by_rl(std::integral_constant<int, 2>{});
@@ -2568,7 +2797,7 @@ inline size_t persistent_lds_bytes(const gh_model* m) {
     const gh_config& c = m->cfg;
     const LayerDev& L0 = m->layers[0];
     size_t f = 0;
-    auto item = [&](int per_split, int tmp) { f = std::max(f, (size_t)(576 + per_split * 32 + ((per_split + 3) & ~3) + tmp)); };
+    auto item = [&](int per_split, int tmp) { f = std::max(f, mv_lds_floats(FMT_Q4, per_split, tmp)); };
     item(L0.qkv.nblk, c.hidden);
     item(L0.o.nblk, (c.n_heads + 2) * ATTN_MAX_NC);
     item(L0.gu.nblk, c.hidden);
@@ -3741,6 +3970,38 @@ int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s)
     // key points at a buffer of 1 + 1024 entries: [0] result, [1..] per-block keys
     hipLaunchKernelGGL(k_argmax_blocks, dim3(blocks), dim3(NT), 0, s, v, n, key + 1);
     hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(NT), 0, s, key + 1, blocks, key);
+    GH_HIP(hipGetLastError());
+    return GH_OK;
+}
+
+// ------------------------------------------------------------------
+// measured stream-read peak: every byte of a buffer read once with
+// non-temporal 16-byte loads; workgroup b reads the contiguous chunk
+// [b * chunk, (b + 1) * chunk) (the access shape of a matvec tile, and
+// faster on HBM than a grid-stride walk), eight loads in flight per thread
+// ------------------------------------------------------------------
+constexpr int SR_GRID = 4096, SR_UNROLL = 8;
+
+__global__ __launch_bounds__(NT) void k_stream_read(const void* p, uint32_t n4, uint32_t chunk4, float* sink) {
+    const BufView B(p, (size_t)n4 * 16);  // the last chunk's tail reads zeros
+    const uint32_t b = blockIdx.x * chunk4;
+    float4 acc = f4z();
+    for (uint32_t i = b + threadIdx.x; i < b + chunk4; i += SR_UNROLL * NT) {
+        float4 v[SR_UNROLL];
+#pragma unroll
+        for (int u = 0; u < SR_UNROLL; ++u) v[u] = B.f4<CP_NT>(16u * (i + u * NT));
+#pragma unroll
+        for (int u = 0; u < SR_UNROLL; ++u) acc = acc + v[u];
+    }
+    const float t = (acc.x + acc.y) + (acc.z + acc.w);
+    if (t == 1.5f) sink[blockIdx.x] = t;  // keeps the loads; the zero fill makes it never true
+}
+
+int launch_stream_read(const void* p, size_t bytes, float* sink, hipStream_t s) {
+    if (bytes % 16 || bytes > (1u << 31) - 16u) return set_error(GH_ERR_INVALID, "stream read: %zu bytes", bytes);
+    const uint32_t n4 = (uint32_t)(bytes / 16), step = SR_UNROLL * NT;
+    const uint32_t chunk4 = ((n4 + SR_GRID - 1) / SR_GRID + step - 1) / step * step;
+    hipLaunchKernelGGL(k_stream_read, dim3(SR_GRID), dim3(NT), 0, s, p, n4, chunk4, sink);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }

@@ -163,6 +163,16 @@ void make_plans(gh_model* m) {
     over(m->pd, "GH_PLAN_D_S", L.gu);
     over(m->pe, "GH_PLAN_E_S", L.down);
     // rows per lane (2: 128-row workgroups, 1: 64-row workgroups)
+    // Q4_0 dot products on the matrix cores: they shorten the dot phase of
+    // every work item, but their input limbs cost each workgroup's prologue
+    // more than the VALU path's input slice.  Measured on MI355X (1B): the
+    // LM head gains (4096 workgroups, dot-bound: 29.7 -> 28.2 us), the
+    // per-layer kernels lose 0.06-0.26 us each (their time is the prologue).
+    m->plm.mfma = env_int("GH_PLAN_LM_MFMA", 1);
+    m->pa.mfma = env_int("GH_PLAN_A_MFMA", 0);
+    m->pc.mfma = env_int("GH_PLAN_C_MFMA", 0);
+    m->pd.mfma = env_int("GH_PLAN_D_MFMA", 0);
+    m->pe.mfma = env_int("GH_PLAN_E_MFMA", 0);
     m->pa.rl = env_int("GH_PLAN_A_RL", m->pa.rl);
     m->pc.rl = env_int("GH_PLAN_C_RL", m->pc.rl);
     m->pd.rl = env_int("GH_PLAN_D_RL", m->pd.rl);
@@ -526,6 +536,10 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     // MI355X sweep of the C2 shapes: 6912x1152 5.5 us, 1152x6912 6.1 us)
     t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, env_int("GH_Q4_TARGET", 512), env_int("GH_Q4_MAXS", 16));
     t->plan.rl = env_int("GH_Q4_RL", 1) == 2 ? 2 : 1;
+    // matrix-core dot products when the matvec is dot-bound (at least 8
+    // workgroups per CU: 262144 x 1152 31.6 us vs 34.5 us on the VALU; the
+    // 6912-row shapes are faster on the VALU)
+    t->plan.mfma = env_int("GH_Q4_MFMA", t->plan.row_tiles(d.tiles) * t->plan.S >= 2048 ? 1 : 0);
     if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
     ctx->q4s.push_back(t.get());
     *out = t.release();
@@ -1302,6 +1316,39 @@ extern "C" int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t 
     *avg_us_out = per_step ? 1e3 * ms / ((double)n_reps * per_step) : 0.0;
     if (bytes_per_launch_out) *bytes_per_launch_out = bytes;
     if (launches_per_step_out) *launches_per_step_out = per_step;
+    return GH_OK;
+}
+
+extern "C" int gh_time_stream_read(gh_ctx* ctx, size_t bytes, int32_t n_reps, double* avg_us_out) {
+    if (!ctx || bytes < 16 || bytes % 16 || bytes > (1u << 31) - 16u || n_reps <= 0 || !avg_us_out)
+        return set_error(GH_ERR_INVALID, "gh_time_stream_read: bytes must be a multiple of 16 in [16, 2 GiB)");
+    GH_CHECK(ctx_bind(ctx));
+    Lock lk(ctx->mu);
+    hipStream_t s = ctx->stream;
+    void* buf = nullptr;
+    float* sink = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    float ms = 0.0f;
+    int rc = GH_OK;
+    if (hipMalloc(&buf, bytes) != hipSuccess || hipMalloc((void**)&sink, 4096 * sizeof(float)) != hipSuccess)
+        rc = set_error(GH_ERR_OOM, "gh_time_stream_read: hipMalloc of %zu bytes failed", bytes);
+    // zeros: the kernel's guarded store never fires
+    if (rc == GH_OK && hipMemsetAsync(buf, 0, bytes, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipMemsetAsync failed");
+    if (rc == GH_OK) rc = gh::launch_stream_read(buf, bytes, sink, s);  // warm-up
+    if (rc == GH_OK && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess))
+        rc = set_error(GH_ERR_HIP, "hipEventCreate failed");
+    if (rc == GH_OK && hipEventRecord(a, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
+    for (int i = 0; i < n_reps && rc == GH_OK; ++i) rc = gh::launch_stream_read(buf, bytes, sink, s);
+    if (rc == GH_OK && hipEventRecord(b, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventRecord failed");
+    if (rc == GH_OK && hipEventSynchronize(b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventSynchronize failed");
+    if (rc == GH_OK && hipEventElapsedTime(&ms, a, b) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipEventElapsedTime failed");
+    (void)hipStreamSynchronize(s);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (sink) (void)hipFree(sink);
+    if (buf) (void)hipFree(buf);
+    GH_CHECK(rc);
+    *avg_us_out = 1e3 * ms / n_reps;
     return GH_OK;
 }
 

@@ -554,3 +554,12 @@ def time_kernel(model: GemmaModel, cache: KVCache, name: str, n_reps: int = 50) 
     us, nb, per = C.c_double(), C.c_double(), C.c_int32()
     check(lib().gh_time_kernel(model.h, cache.h, name.encode(), n_reps, C.byref(us), C.byref(nb), C.byref(per)))
     return KernelTiming(name, us.value, nb.value, per.value)
+
+
+def stream_read_gbps(ctx: Context, nbytes: int = 1 << 30, n_reps: int = 20) -> tuple[float, float]:
+    """Measured stream-read peak of ctx's device: nbytes read once per
+    launch, n_reps launches back to back (gh_time_stream_read).  Returns
+    (GB/s, average microseconds per launch)."""
+    us = C.c_double()
+    check(lib().gh_time_stream_read(ctx.h, nbytes, n_reps, C.byref(us)))
+    return nbytes / (us.value * 1e-6) / 1e9, us.value

@@ -272,6 +272,15 @@ int gh_prefill_profile(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n,
  * Also replaces the gpu_print_profile_stats hook (BenchmarkKVCache.hs:38-42). */
 int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t n_reps, double* avg_us_out,
                    double* bytes_per_launch_out, int32_t* launches_per_step_out);
+/* Measured stream-read peak of the device (no reference counterpart: a
+ * measurement helper for the roofline): allocates `bytes` (a multiple of
+ * 16, below 2 GiB) on the context's device, reads every byte once per launch with
+ * non-temporal 16-byte loads, 4096 workgroups each streaming one
+ * contiguous chunk (the access shape of a matvec tile), n_reps launches back
+ * to back after one warm-up, and returns the average duration per launch.
+ * bytes / duration is the practical HBM read bandwidth the hot path's
+ * weight streaming is measured against beside the nominal 8 TB/s. */
+int gh_time_stream_read(gh_ctx* ctx, size_t bytes, int32_t n_reps, double* avg_us_out);
 
 /* ================================================================
  * Seeded synthetic weights (SplitMix64 + Box-Muller), identical on every

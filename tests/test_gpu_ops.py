@@ -57,12 +57,17 @@ def test_q4_0_dequant_all_scale_patterns(ctx):
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
+@pytest.mark.parametrize("mfma", [0, 1])
 @pytest.mark.parametrize("rl", [2, 1])
 @pytest.mark.parametrize("rows,cols", [(6912, 1152), (1152, 6912), (262144, 1152), (1536, 1152),
-                                       (1152, 1024), (4, 64), (130, 96)])
-def test_q4_0_matvec_shapes(ctx, rows, cols, rl, monkeypatch):
-    """Both workgroup shapes: 128 rows (2 per lane) and 64 rows (1 per lane)."""
+                                       (1152, 1024), (4, 64), (130, 96), (200, 480)])
+def test_q4_0_matvec_shapes(ctx, rows, cols, rl, mfma, monkeypatch):
+    """Both workgroup shapes, 128 rows (2 per lane) and 64 rows (1 per lane),
+    and both dot-product paths: VALU (mfma 0) and the int8 matrix cores
+    (mfma 1, whose input limbs round x to 2^-27 of its block maximum, far
+    inside the bound).  480 columns: 15 blocks, a partial last quad."""
     monkeypatch.setenv("GH_Q4_RL", str(rl))
+    monkeypatch.setenv("GH_Q4_MFMA", str(mfma))
     raw = _random_q4(rows, cols, rows + cols, subnormal_frac=0.005)
     x = np.random.default_rng(rows).normal(size=cols).astype(np.float32)
     t = gh.Q4Tensor(ctx, raw, rows, cols)
@@ -72,6 +77,19 @@ def test_q4_0_matvec_shapes(ctx, rows, cols, rl, monkeypatch):
     bound = 2 * cols * np.finfo(np.float32).eps * ay
     assert np.all(np.abs(y - y64) <= bound + 1e-30)
     assert rel_err(y, orc.q4_0_matvec(raw, x, rows, cols)) < 1e-5
+
+
+@pytest.mark.parametrize("mfma", [0, 1])
+def test_q4_0_matvec_nan_input_propagates(ctx, mfma, monkeypatch):
+    """A NaN in x reaches every output row on both dot-product paths (the
+    finish kernel's NaN check relies on it)."""
+    monkeypatch.setenv("GH_Q4_MFMA", str(mfma))
+    rows, cols = 256, 512
+    raw = _random_q4(rows, cols, 4)
+    x = np.random.default_rng(4).normal(size=cols).astype(np.float32)
+    x[37] = np.nan
+    y = gh.Q4Tensor(ctx, raw, rows, cols).matvec(x)
+    assert np.all(np.isnan(y))
 
 
 def test_runLinearQ4_reference_api(ctx):
