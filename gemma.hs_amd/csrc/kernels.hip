@@ -1959,121 +1959,6 @@ __global__ __launch_bounds__(NT) void k_attn(AttnArgs a) {
     attn_item<HD, G, STEP>(a, g, j, QkvPartials{a.part_qkv, a.Sa, a.ld_qkv}, AttnOutPlain{a.part});
 }
 
-// Long-range attention of one query token (op-level, head_dim 256): each
-// wave streams its own rounds of 8 positions with its own online softmax,
-// with K/V loaded two rounds ahead and no workgroup barrier inside the loop.
-// The four wave states are merged once at the end into the chunk state
-// {m[G], l[G], o[G][HD]} that k_attn_combine reads.
-//   scores: 8 lanes per position; lane kq holds 32 of the position's 256 K
-//           values (one 16 B piece of each 128 B line, as in attn_item), one
-//           3-step DPP sum per score;
-//   P.V:    lane = 4 dims; the 8 positions' weights come by readlane.
-template <int G>
-__global__ __launch_bounds__(NT) void k_attn_wave(AttnArgs a) {
-    constexpr int HD = 256, K4 = HD / 32, RP = 8;  // RP positions per round
-    __shared__ __align__(16) float qs[G * HD];
-    __shared__ float ms[4][G], ls[4][G];
-    __shared__ __align__(16) float os[4][G * HD];
-    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
-    if (j >= a.n_used) return;  // uniform per workgroup
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
-    const size_t pstride = (size_t)a.nkv * HD;
-    for (int i = tid; i < G * HD; i += NT) qs[i] = a.q[(size_t)g * G * HD + i];
-    const int kq = lane & 7, kp = lane >> 3;
-    const float* kbase = a.kc + (size_t)g * HD + 4 * kq;
-    const float* vbase = a.vc + (size_t)g * HD + 4 * lane;
-    const int nr = (c1 - c0 + RP - 1) / RP;  // rounds of the chunk; wave w takes w, w + 4, ...
-    // Chunks start at multiples of the chunk length, so without a rotation
-    // every workgroup would read the same offset of its chunk at the same
-    // time (the same HBM channels); round r of chunk j reads round
-    // (r + rot) % nr instead, a permutation, so the result is unchanged.
-    const int rot = (j * 5) % nr;
-    auto round_pos = [&](int r) { return c0 + RP * ((r + rot) % nr); };
-    float4 kr[2][K4], vr[2][RP];
-    // round r's K/V into slot u; positions clamped into the chunk so every
-    // call issues the same loads
-    auto load = [&](int u, int r) {
-        const int p0 = round_pos(min(r, nr - 1));
-        const float* ks = kbase + (size_t)min(p0 + kp, c1 - 1) * pstride;
-#pragma unroll
-        for (int i = 0; i < K4; ++i) kr[u][i] = *(const float4*)(ks + 32 * i);
-#pragma unroll
-        for (int k = 0; k < RP; ++k) vr[u][k] = *(const float4*)(vbase + (size_t)min(p0 + k, c1 - 1) * pstride);
-    };
-    float m[G], l[G];
-    float4 acc[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-        acc[h] = f4z();
-    }
-    load(0, wave);
-    load(1, wave + 4);
-    __syncthreads();  // qs complete
-    for (int r = wave; r < nr; r += 8) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int rr = r + 4 * u;
-            if (rr >= nr) break;  // uniform per wave
-            const int p0 = round_pos(rr);
-            const bool valid = p0 + kp < c1;
-            float pw[G];
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float sv = 0.0f;
-#pragma unroll
-                for (int i = 0; i < K4; ++i) sv += dot4(*(const float4*)&qs[h * HD + 32 * i + 4 * kq], kr[u][i]);
-                sv = group_sum<8>(sv) * a.scale;
-                sv = valid ? sv : -INFINITY;
-                const float mn = fmaxf(m[h], wave_max(sv));  // round has a valid position: mn finite
-                const float corr = __expf(m[h] - mn);         // m = -inf -> 0
-                pw[h] = valid ? __expf(sv - mn) : 0.0f;
-                l[h] = l[h] * corr + wave_sum(kq == 0 ? pw[h] : 0.0f);
-                m[h] = mn;
-                acc[h] = make_float4(acc[h].x * corr, acc[h].y * corr, acc[h].z * corr, acc[h].w * corr);
-            }
-#pragma unroll
-            for (int k = 0; k < RP; ++k) {
-                if (p0 + k < c1) {  // uniform per wave
-#pragma unroll
-                    for (int h = 0; h < G; ++h) acc[h] = fma4(readlane(pw[h], 8 * k), vr[u][k], acc[h]);
-                }
-            }
-            load(u, rr + 8);
-        }
-    }
-    // merge the four wave states
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            ms[wave][h] = m[h];
-            ls[wave][h] = l[h];
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) *(float4*)&os[wave][h * HD + 4 * lane] = acc[h];
-    __syncthreads();
-    const size_t ob = ((size_t)g * a.nc + j) * (G * (HD + 2));
-    for (int idx = tid; idx < G * HD; idx += NT) {
-        const int h = idx / HD;
-        const float M = fmaxf(fmaxf(ms[0][h], ms[1][h]), fmaxf(ms[2][h], ms[3][h]));
-        float o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) o += __expf(ms[w][h] - M) * os[w][idx];
-        a.part[ob + 2 * G + idx] = o;
-    }
-    if (tid < G) {
-        const float M = fmaxf(fmaxf(ms[0][tid], ms[1][tid]), fmaxf(ms[2][tid], ms[3][tid]));
-        float L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) L += __expf(ms[w][tid] - M) * ls[w][tid];
-        a.part[ob + tid] = M;
-        a.part[ob + G + tid] = L;
-    }
-}
-
 // One query token of the decode step over cache positions [pb, pe): split-K
 // over chunks as attn_item (workgroup (g, j): kv head g, chunk j; the same
 // {m[G], l[G], o[G][HD]} chunk state), with a short dependency chain:
@@ -2097,6 +1982,9 @@ __global__ __launch_bounds__(NT) void k_attn_wave(AttnArgs a) {
 // instruction costs its CU's address unit the same time, in range or not).
 // The kernel picks the body before issuing any load, so each body's
 // s_waitcnt counts stay exact.
+// OPQ (the op-level entry point): the G query heads of kv head g come
+// ready in a.q (normed and roped), K/V are complete in the cache; the
+// prologue loads q only, and there is no current row to append or score.
 template <int HD, int G>
 struct AttnStepLds {
     float qs[G * HD];
@@ -2106,7 +1994,7 @@ struct AttnStepLds {
     float os[4][G * HD];
 };
 
-template <int HD, int G, int PF, bool SKIP>
+template <int HD, int G, int PF, bool SKIP, bool OPQ = false>
 __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, AttnStepLds<HD, G>& S) {
     constexpr int LPH = HD / 4;                  // lanes per head vector (one float4 each)
     constexpr int NG4 = (G + 2) * LPH;           // float4 groups of q | k | v
@@ -2123,17 +2011,25 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     const int pos = a.pos;
     const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
-    const bool own = pos >= c0 && pos < c1;  // this chunk scores the current position
-    const bool need_kv = own || j == 0;      // j == 0 appends k, v to the cache
+    const bool own = !OPQ && pos >= c0 && pos < c1;  // this chunk scores the current position
+    const bool need_kv = own || (!OPQ && j == 0);    // j == 0 appends k, v to the cache
     const size_t pstride = (size_t)a.nkv * HD;
 
     // 1. prologue loads: partials, QK-norm weights, RoPE row (straight-line)
-    const BufView P(a.part_qkv, (size_t)a.Sa * a.ld_qkv * 4);
+    constexpr int QG4 = G * LPH, MQ4 = (QG4 + NT - 1) / NT;  // OPQ: float4 groups of q per thread
+    float4 qv[MQ4];
+    if constexpr (OPQ) {
+        const BufView Q(a.q + (size_t)g * G * HD, (size_t)G * HD * 4);
+#pragma unroll
+        for (int m = 0; m < MQ4; ++m) qv[m] = Q.f4(16u * (uint32_t)(tid + m * NT));
+    }
+    const BufView P(a.part_qkv, OPQ ? 0 : (size_t)a.Sa * a.ld_qkv * 4);
     const BufView QN(a.q_norm, a.use_qk_norm ? HD * 4 : 0), KN(a.k_norm, a.use_qk_norm ? HD * 4 : 0);
-    const BufView CS(a.rope + (size_t)pos * HD, HD * 4);
+    const BufView CS(OPQ ? nullptr : a.rope + (size_t)pos * HD, OPQ ? 0 : HD * 4);
     float4 pv[MG4][MAXS], wn[MG4], cs0[MG4], cs1[MG4];
 #pragma unroll
     for (int m = 0; m < MG4; ++m) {
+        if constexpr (OPQ) continue;
         if (SKIP && m == MG4 - 1) {
 #pragma unroll
             for (int s = 0; s < MAXS; ++s) pv[m][s] = f4z();
@@ -2178,8 +2074,14 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     GH_MARK(1);
 
     // 2. sums, QK-norm, RoPE in registers; q, k, v to LDS
+    if constexpr (OPQ) {
+#pragma unroll
+        for (int m = 0; m < MQ4; ++m)
+            if (tid + m * NT < QG4) *(float4*)&qs[4 * (tid + m * NT)] = qv[m];
+    }
 #pragma unroll
     for (int m = 0; m < MG4; ++m) {
+        if constexpr (OPQ) continue;
         const int gi = tid + m * NT, vec = gi / LPH, d = 4 * (gi % LPH);
         float4 v = pv[m][0];
 #pragma unroll
@@ -2214,7 +2116,7 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     }
     __syncthreads();
     GH_MARK(2);
-    if (j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
+    if (!OPQ && j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
         for (int i = tid; i < HD; i += NT) {
             a.kc[((size_t)pos * a.nkv + g) * HD + i] = ks[i];
             a.vc[((size_t)pos * a.nkv + g) * HD + i] = vs[i];
@@ -2334,6 +2236,20 @@ __global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
     }
 }
 
+// Op-level attention of one query token over [pb, pe) of a complete cache
+// (gh_attention_decode, head_dim 256): the step kernel's streaming body with
+// q read ready-made (OPQ); workgroup (g, j) writes chunk j's state for
+// k_attn_combine.
+template <int HD, int G>
+__global__ __launch_bounds__(NT) void k_attn_op(AttnArgs a) {
+    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
+    if (j >= a.n_used) return;  // uniform per workgroup
+    const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
+    __shared__ __align__(16) AttnStepLds<HD, G> lds;
+    if (c1 - c0 <= 32) attn_step_body<HD, G, 1, false, true>(a, g, j, lds);
+    else attn_step_body<HD, G, 2, false, true>(a, g, j, lds);
+}
+
 #if GH_IN_TU(1)
 static int launch_attn_step(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
     if (a.nc > ATTN_MAX_NC || a.nc < 1) return set_error(GH_ERR_INVALID, "attention: %d splits (1..%d)", a.nc, ATTN_MAX_NC);
@@ -2362,45 +2278,61 @@ static int launch_attn_t(Sink& k, double bytes, int hd, int G, const AttnArgs& a
     return set_error(GH_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
 
-// Merge of the split-K partials for the op-level entry point: workgroup
-// (q head h, 64-dim slice) loads the chunk states (m_j, l_j) in parallel,
-// then thread (c, d) sums dim d over chunks c, c + 4, ... (independent,
-// coalesced loads) and the four chunk groups are added in LDS.
+// Merge of the split-K partials for the op-level entry point (the
+// reference's softmax over all positions, combined from the chunk states
+// {m_j, l_j, o_j}): workgroup (q head h, 64-dim slice); thread t holds chunk
+// t's (m, l) and, as lane (c, q) = (t / 16, t % 16), dims 4q..4q+3 of chunks
+// c, c + 16, ...  Every load is issued before the first use, as straight-line
+// buffer loads (chunks past n_used read zeros), so the merge costs one round
+// trip; the 16 chunk groups are added in LDS.  VEC: float4 loads of o (the
+// state stride G*(HD+2) is a multiple of 4 when G is even), else 4 scalars.
 #if GH_IN_TU(4)
-constexpr int COMB_DIMS = 64;
+constexpr int COMB_DIMS = 64, COMB_CG = NT / (COMB_DIMS / 4), COMB_PER = GH_ATTN_OP_MAX_NC / COMB_CG;
+template <bool VEC>
 __global__ __launch_bounds__(NT) void k_attn_combine(const float* part, int nc, int n_used, int G, int HD, float* out) {
     __shared__ float wj[GH_ATTN_OP_MAX_NC];
     __shared__ float slot[8];
-    __shared__ float red[4][COMB_DIMS];
+    __shared__ __align__(16) float red[COMB_CG][COMB_DIMS];
+    static_assert(GH_ATTN_OP_MAX_NC <= NT, "one chunk state per thread");
     const int nds = (HD + COMB_DIMS - 1) / COMB_DIMS;
-    const int h = blockIdx.x / nds, d = (blockIdx.x % nds) * COMB_DIMS + (threadIdx.x & (COMB_DIMS - 1));
-    const int g = h / G, hl = h % G, tid = threadIdx.x, cg = tid / COMB_DIMS;
-    const int stride = G * (HD + 2);
-    const float* base = part + (size_t)g * nc * stride;
-    float m = -INFINITY, l = 0.0f;
-    if (tid < n_used) {
-        m = base[(size_t)tid * stride + hl];
-        l = base[(size_t)tid * stride + G + hl];
+    const int h = blockIdx.x / nds, d0 = (blockIdx.x % nds) * COMB_DIMS;
+    const int g = h / G, hl = h % G, tid = threadIdx.x;
+    const int dq = 4 * (tid % (COMB_DIMS / 4)), cg = tid / (COMB_DIMS / 4);
+    const uint32_t stride = (uint32_t)(G * (HD + 2));
+    const BufView P(part + (size_t)g * nc * stride, (size_t)n_used * stride * 4);
+    const float m = P.f1(tid < n_used ? 4u * (tid * stride + hl) : OOB);
+    const float l = P.f1(tid < n_used ? 4u * (tid * stride + G + hl) : OOB);
+    const bool dok = d0 + dq < HD;  // HD is a multiple of 4
+    float4 ov[COMB_PER];
+#pragma unroll
+    for (int k = 0; k < COMB_PER; ++k) {
+        const int j = cg + COMB_CG * k;
+        const uint32_t off = dok && j < n_used ? 4u * (j * stride + 2 * G + hl * HD + d0 + dq) : OOB;
+        if (VEC) {
+            ov[k] = P.f4(off);
+        } else {
+            const uint32_t o1 = off == OOB ? OOB : off + 4u, o2 = off == OOB ? OOB : off + 8u, o3 = off == OOB ? OOB : off + 12u;
+            ov[k] = make_float4(P.f1(off), P.f1(o1), P.f1(o2), P.f1(o3));
+        }
     }
-    // block max of m over the chunks (n_used <= NT)
-    float mx = wave_max(m);
+    // block max of m over the chunks
+    const float mx = wave_max(tid < n_used ? m : -INFINITY);
     if ((tid & 63) == 0) slot[tid >> 6] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(slot[0], slot[1]), fmaxf(slot[2], slot[3]));
     const float w = tid < n_used ? expf(m - M) : 0.0f;
-    if (tid < n_used) wj[tid] = w;
+    wj[tid] = w;
     const float den = block_sum(l * w, slot + 4);  // barrier: wj complete
-    float num = 0.0f;
-    if (d < HD) {
-        const float* o = base + 2 * G + hl * HD + d;
-#pragma unroll 8
-        for (int j = cg; j < n_used; j += 4) num += o[(size_t)j * stride] * wj[j];
-    }
-    red[cg][tid & (COMB_DIMS - 1)] = num;
+    float4 num = f4z();
+#pragma unroll
+    for (int k = 0; k < COMB_PER; ++k) num = fma4(wj[cg + COMB_CG * k], ov[k], num);
+    *(float4*)&red[cg][dq] = num;
     __syncthreads();
-    if (cg == 0 && d < HD) {
-        const int dl = tid & (COMB_DIMS - 1);
-        out[(size_t)h * HD + d] = ((red[0][dl] + red[1][dl]) + (red[2][dl] + red[3][dl])) / den;
+    if (tid < COMB_DIMS && d0 + tid < HD) {
+        float t = 0.0f;
+#pragma unroll
+        for (int c = 0; c < COMB_CG; ++c) t += red[c][tid];
+        out[(size_t)h * HD + d0 + tid] = t / den;
     }
 }
 #endif
@@ -3860,23 +3792,24 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     Sink k;
     k.s = s;
     const int G = nq / nkv;
-    // chunks of at least GH_ATTN_WAVE_MIN (default 64) positions: the
-    // wave-streaming kernel (head_dim 256)
-    static const int wave_min = [] {
-        const char* e = std::getenv("GH_ATTN_WAVE_MIN");
-        return e ? std::atoi(e) : 64;
-    }();
-    if (hd == 256 && a.ch >= wave_min && wave_min > 0 && (G == 1 || G == 2 || G == 4 || G == 8)) {
+    // head_dim 256, chunks of 64 positions or more: the step kernel's
+    // streaming body (16 % faster than a separate wave-streaming kernel at
+    // 8192 and 32768 positions on MI355X); shorter chunks: the 32-position
+    // sub-chunk kernel (0.3 us faster on the last 512)
+    const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8;
+    const bool views_ok = (size_t)p_end * nkv * hd * 4 <= 0x7fffffffu;  // the body's buffer views
+    if (hd == 256 && g_ok && views_ok && a.ch >= 64) {
         const dim3 grid(nkv * a.nc);
-        if (G == 1) hipLaunchKernelGGL(k_attn_wave<1>, grid, dim3(NT), 0, s, a);
-        else if (G == 2) hipLaunchKernelGGL(k_attn_wave<2>, grid, dim3(NT), 0, s, a);
-        else if (G == 4) hipLaunchKernelGGL(k_attn_wave<4>, grid, dim3(NT), 0, s, a);
-        else hipLaunchKernelGGL(k_attn_wave<8>, grid, dim3(NT), 0, s, a);
+        if (G == 1) hipLaunchKernelGGL((k_attn_op<256, 1>), grid, dim3(NT), 0, s, a);
+        else if (G == 2) hipLaunchKernelGGL((k_attn_op<256, 2>), grid, dim3(NT), 0, s, a);
+        else if (G == 4) hipLaunchKernelGGL((k_attn_op<256, 4>), grid, dim3(NT), 0, s, a);
+        else hipLaunchKernelGGL((k_attn_op<256, 8>), grid, dim3(NT), 0, s, a);
     } else {
         GH_CHECK(launch_attn_t<false>(k, 0.0, hd, G, a, nkv));
     }
-    hipLaunchKernelGGL(k_attn_combine, dim3(nq * ((hd + COMB_DIMS - 1) / COMB_DIMS)), dim3(NT), 0, s, part, n_splits,
-                       a.n_used, G, hd, out);
+    const dim3 cgrid(nq * ((hd + COMB_DIMS - 1) / COMB_DIMS));
+    if (G % 2 == 0) hipLaunchKernelGGL(k_attn_combine<true>, cgrid, dim3(NT), 0, s, part, n_splits, a.n_used, G, hd, out);
+    else hipLaunchKernelGGL(k_attn_combine<false>, cgrid, dim3(NT), 0, s, part, n_splits, a.n_used, G, hd, out);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }
