@@ -80,6 +80,23 @@ def test_q4_0_matvec_shapes(ctx, rows, cols, rl, mfma, monkeypatch):
 
 
 @pytest.mark.parametrize("mfma", [0, 1])
+@pytest.mark.parametrize("rl", [2, 1])
+@pytest.mark.parametrize("rows,cols", [(256, 4096), (192, 2592)])
+def test_q4_0_matvec_single_split_many_batches(ctx, rows, cols, rl, mfma, monkeypatch):
+    """One column split (GH_Q4_MAXS=1): every work item walks all 128 / 81
+    column blocks in several register batches, the last one partial."""
+    monkeypatch.setenv("GH_Q4_RL", str(rl))
+    monkeypatch.setenv("GH_Q4_MFMA", str(mfma))
+    monkeypatch.setenv("GH_Q4_MAXS", "1")
+    raw = _random_q4(rows, cols, rows * 7 + cols, subnormal_frac=0.005)
+    x = np.random.default_rng(cols).normal(size=cols).astype(np.float32)
+    y = gh.Q4Tensor(ctx, raw, rows, cols).matvec(x)
+    y64, ay = orc.q4_0_matvec_f64(raw, x, rows, cols)
+    bound = 2 * cols * np.finfo(np.float32).eps * ay
+    assert np.all(np.abs(y - y64) <= bound + 1e-30)
+
+
+@pytest.mark.parametrize("mfma", [0, 1])
 def test_q4_0_matvec_nan_input_propagates(ctx, mfma, monkeypatch):
     """A NaN in x reaches every output row on both dot-product paths (the
     finish kernel's NaN check relies on it)."""
