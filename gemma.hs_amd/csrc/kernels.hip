@@ -1541,7 +1541,12 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
     };
     auto by_rl = [&](auto kbw) -> int {
         constexpr int KBW = decltype(kbw)::value;
-        if (p.mfma) return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
+        // the matrix-core dot products are built for plain input vectors
+        // (the LM head, op-level matvecs); other prologues use the VALU
+        if constexpr (std::is_same_v<Pro, ProPlain>) {
+            if (p.mfma)
+                return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
+        }
         return p.rl == 2 ? go(k_matvec<FMT_Q4, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4, KBW, 1, Pro, Epi>);
     };
     if (p.rl != 1 && p.rl != 2) return set_error(GH_ERR_INVALID, "unsupported rows per lane %d", p.rl);
@@ -1554,6 +1559,7 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
         case 4: return by_rl(std::integral_constant<int, 4>{});
         case 6: return by_rl(std::integral_constant<int, 6>{});
         case 9: return by_rl(std::integral_constant<int, 9>{});
+        case 10: return by_rl(std::integral_constant<int, 10>{});
         default: return set_error(GH_ERR_INVALID, "unsupported register batch %d", p.kbw);
     }
 }

@@ -145,6 +145,11 @@ void make_plans(gh_model* m) {
     m->pa = choose_plan(m->fmt, L.qkv.tiles, L.qkv.nblk, 256);
     m->pc = choose_plan(m->fmt, L.o.tiles, L.o.nblk, 256);
     m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, std::max(1, (384 + L.gu.tiles / 2) / L.gu.tiles) * L.gu.tiles);
+    // gate/up: more splits until a wave's share of a split fits one register
+    // batch of at most 9 blocks of its two rows per lane; a second batch's
+    // loads wait for the first's dot products, and a 10-block batch of two
+    // rows spills (4B: 2 -> 3 splits, gate/up 14.3 -> 11.9 us, 651 -> 690 tok/s)
+    while (m->fmt == FMT_Q4 && m->pd.S < 8 && ((L.gu.nblk + m->pd.S - 1) / m->pd.S + 3) / 4 > 9) ++m->pd.S;
     m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 8 * L.down.tiles);
     m->plm = choose_plan(m->fmt, m->embd.tiles, m->embd.nblk, 1);
     m->pc.rl = m->pe.rl = m->plm.rl = 1;
@@ -163,16 +168,12 @@ void make_plans(gh_model* m) {
     over(m->pd, "GH_PLAN_D_S", L.gu);
     over(m->pe, "GH_PLAN_E_S", L.down);
     // rows per lane (2: 128-row workgroups, 1: 64-row workgroups)
-    // Q4_0 dot products on the matrix cores: they shorten the dot phase of
-    // every work item, but their input limbs cost each workgroup's prologue
-    // more than the VALU path's input slice.  Measured on MI355X (1B): the
-    // LM head gains (4096 workgroups, dot-bound: 29.7 -> 28.2 us), the
-    // per-layer kernels lose 0.06-0.26 us each (their time is the prologue).
+    // Q4_0 dot products on the matrix cores: the LM head only.  They shorten
+    // the dot phase of every work item, but their input limbs lengthen each
+    // workgroup's prologue, and the per-layer kernels are prologue-bound:
+    // measured on MI355X with every phase on the matrix cores, 1B decode
+    // 1420 vs 1452 tok/s and 4B 580 vs 650 tok/s.
     m->plm.mfma = env_int("GH_PLAN_LM_MFMA", 1);
-    m->pa.mfma = env_int("GH_PLAN_A_MFMA", 0);
-    m->pc.mfma = env_int("GH_PLAN_C_MFMA", 0);
-    m->pd.mfma = env_int("GH_PLAN_D_MFMA", 0);
-    m->pe.mfma = env_int("GH_PLAN_E_MFMA", 0);
     m->pa.rl = env_int("GH_PLAN_A_RL", m->pa.rl);
     m->pc.rl = env_int("GH_PLAN_C_RL", m->pc.rl);
     m->pd.rl = env_int("GH_PLAN_D_RL", m->pd.rl);

@@ -101,17 +101,18 @@ def test_step_and_generate_agree_and_cache_grows(ctx):
     np.testing.assert_array_equal(gh.generate(m, kv1, prompt, 10), ids)
 
 
-@pytest.mark.parametrize("mode,rl,mfma", [(gh.MODE_GEMMA3, 2, 0), (gh.MODE_REF, 2, 0), (gh.MODE_GEMMA3, 1, 0),
-                                          (gh.MODE_GEMMA3, 2, 1), (gh.MODE_GEMMA3, 1, 1)])
-def test_small_q4_gqa_model_local_global_live_oracle(ctx, mode, rl, mfma, monkeypatch):
+@pytest.mark.parametrize("mode,rl,lm_mfma", [(gh.MODE_GEMMA3, 2, 1), (gh.MODE_REF, 2, 1), (gh.MODE_GEMMA3, 1, 1),
+                                             (gh.MODE_GEMMA3, 1, 0)])
+def test_small_q4_gqa_model_local_global_live_oracle(ctx, mode, rl, lm_mfma, monkeypatch):
     """A 4B-shaped miniature: Q4_0, 8 q heads / 4 kv heads (group 2),
     head_dim 256, local window 5 with global every 2nd layer, per-type theta;
     the live oracle checks every layer at every step (window binds).  rl=1
-    runs every matvec phase with 64-row workgroups; mfma selects the int8
-    matrix-core dot products (1) or the VALU ones (0) for every phase."""
+    runs every matvec phase with 64-row workgroups; lm_mfma puts the LM
+    head's dot products on the int8 matrix cores (1, the default) or the
+    VALU (0)."""
     for v in ("A", "C", "D", "E", "LM"):
         monkeypatch.setenv(f"GH_PLAN_{v}_RL", str(rl))
-        monkeypatch.setenv(f"GH_PLAN_{v}_MFMA", str(mfma))
+    monkeypatch.setenv("GH_PLAN_LM_MFMA", str(lm_mfma))
     cfg = gh.preset("gemma3-4b")
     cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 4, 1024
     cfg.sliding_window, cfg.global_every, cfg.max_seq, cfg.mode = 5, 2, 64, mode
