@@ -29,9 +29,13 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 KERNEL_TUS = 4  # kernels.hip: step, persistent step, prefill, op level
 ARCH = "gfx950"
 # Packed FP32 (v_pk_*_f32) is disabled for every HIP translation unit.
+# MFMA results go to VGPRs (gfx950 allows it): the compiler's default AGPR
+# destinations cost two v_accvgpr_read per MFMA in the prefill GEMM and the
+# matrix-core matvec, whose results feed VALU scale-and-add.
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-result", "-Wno-unused-value",
 ]
 HOST_CXX = shutil.which("g++") or "c++"

@@ -3238,6 +3238,13 @@ __device__ __forceinline__ uint4 q4_f16_frag(uint32_t w) {
 
 constexpr int PF_DEPTH = 4;  // column blocks in flight per workgroup
 
+// LDS slot of B-operand lane s (0..63) of a fragment: s ^ 4 * (s / 16).  The
+// 16 lanes of a write phase (4 rows x the 4 k-groups of one code dword's
+// row) and of a read phase (16 lanes of one k-group) then fall on 16
+// different 16-byte bank groups (without it, a row's four k-groups sit
+// 256 bytes apart: the same banks).
+__device__ __forceinline__ int pf_swz(int s) { return s ^ ((s >> 4) << 2); }
+
 // Q4_0 weights on v_mfma_f32_16x16x32_f16.  Workgroup = 64 token rows x
 // 16*NS weight rows (NS = 8: one 128-row tile, NS = 4: half a tile) x one
 // split; wave w owns token rows 16w..16w+15 and all NS row subtiles.
@@ -3272,7 +3279,7 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
 #pragma unroll
     for (int q = 0; q < NI; ++q) {
         const int item = tid + NT * q, row = item >> 2;
-        frag[q] = &bs[0][row >> 4][(row & 15) + 16 * (item & 3)];
+        frag[q] = &bs[0][row >> 4][pf_swz((row & 15) + 16 * (item & 3))];
     }
     uint32_t rb[PF_DEPTH][NI];
     uint16_t rs[PF_DEPTH];
@@ -3310,7 +3317,7 @@ __global__ __launch_bounds__(NT) void k_pf_gemm_q4(PfGemm g) {
             load(j, i + PF_DEPTH);
 #pragma unroll
             for (int n = 0; n < NS; ++n) {
-                const f16x8_t b = __builtin_bit_cast(f16x8_t, bs[buf][n][lane]);
+                const f16x8_t b = __builtin_bit_cast(f16x8_t, bs[buf][n][pf_swz(lane)]);
                 const float d = ss[buf][16 * n + (lane & 15)];
                 f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, c, 0, 0, 0);
