@@ -33,10 +33,10 @@ WEIGHT_SEED = 1234
 PROMPT_SEED = 1
 N_PROMPT = 128
 # HBM bytes per LM-head launch from two rocprofv3 --pmc passes
-# (profiles/lm_head_gemma3-1b_decode.md): FETCH_SIZE 83,517.9 KiB x 1.99977 and
+# (profiles/lm_head_gemma3-1b_decode.md): FETCH_SIZE 83,584.2 KiB x 1.99978 and
 # WRITE_SIZE 1,152.0 KiB x 1.0, each factor = the bytes a 256 MiB device copy
 # moves / what the counter reads for that copy.
-LM_HEAD_TRAFFIC_BYTES = 172_204_406
+LM_HEAD_TRAFFIC_BYTES = 172_340_835
 # Back-to-back replays per kernel kind in the event-timed pass (a few ms
 # each).  The LM head gets 40 (1.1 ms of streaming): inside the decode loop it
 # runs once per ~700 us of latency-bound kernels, and a longer back-to-back
