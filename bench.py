@@ -232,7 +232,7 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only; multi-GPU runs (--gpus > 1) are not "
-              "part of it (the decode path would shard as described in DESIGN.md)", file=sys.stderr)
+              "part of it (independent sequences would run one per GPU with no exchange)", file=sys.stderr)
         return 2
 
     import numpy as np
