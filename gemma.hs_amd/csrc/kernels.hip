@@ -3119,6 +3119,14 @@ template <int MG>
 __global__ __launch_bounds__(NT) void k_pf_rows(PfRows r) {
     __shared__ float slot[12];
     const int t = r.t0 + blockIdx.x, tid = threadIdx.x, NG = r.H >> 2;
+    // The row's global loads (split partials, residual, both norm weights)
+    // are issued here, before the first use, as straight-line buffer loads
+    // (absent splits, groups past H and a null w_post read zeros): one round
+    // trip instead of one per reduction.
+    const BufView WN(r.w_norm, (size_t)r.H * 4);
+    float4 wn[MG];
+#pragma unroll
+    for (int k = 0; k < MG; ++k) wn[k] = WN.f4(tid + k * NT < NG ? 16u * (uint32_t)(tid + k * NT) : OOB);
     float4 xv[MG];
     if (r.tok) {
         const int tk = min(max(r.tok[t], 0), r.embd.rows - 1);
@@ -3132,28 +3140,34 @@ __global__ __launch_bounds__(NT) void k_pf_rows(PfRows r) {
             }
         }
     } else {
+        const BufView P(r.part + (size_t)t * r.ld, ((size_t)(r.S - 1) * r.Pp * r.ld + r.H) * 4);
+        const BufView B(r.base + (size_t)t * r.H, (size_t)r.H * 4);
+        const BufView WP(r.w_post, r.w_post ? (size_t)r.H * 4 : 0);
+        float4 pv[MG][MAXS], bv[MG], wp[MG];
+#pragma unroll
+        for (int k = 0; k < MG; ++k) {
+            const int g = tid + k * NT;
+            const bool ok = g < NG;
+#pragma unroll
+            for (int s = 0; s < MAXS; ++s)
+                pv[k][s] = P.f4(ok && s < r.S ? 4u * (uint32_t)(s * r.Pp * r.ld) + 16u * (uint32_t)g : OOB);
+            bv[k] = B.f4(ok ? 16u * (uint32_t)g : OOB);
+            wp[k] = WP.f4(ok ? 16u * (uint32_t)g : OOB);
+        }
         float4 dv[MG];
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < MG; ++k) {
-            const int g = tid + k * NT;
-            dv[k] = f4z();
-            if (g < NG) {
-                dv[k] = sum_splits4(r.part + (size_t)t * r.ld, r.S, r.Pp * r.ld, g);
-                ss += dot4(dv[k], dv[k]);
-            }
+            dv[k] = pv[k][0];
+#pragma unroll
+            for (int s = 1; s < MAXS; ++s) dv[k] = dv[k] + pv[k][s];  // absent splits read zeros
+            ss += dot4(dv[k], dv[k]);
         }
         float rms = 1.0f;
         if (r.w_post) rms = sqrtf(block_sum(ss, slot) / (float)r.H + r.eps);
 #pragma unroll
-        for (int k = 0; k < MG; ++k) {
-            const int g = tid + k * NT;
-            xv[k] = f4z();
-            if (g < NG) {
-                const float4 b = ((const float4*)(r.base + (size_t)t * r.H))[g];
-                xv[k] = b + (r.w_post ? norm4(dv[k], rms, ((const float4*)r.w_post)[g], r.zc) : dv[k]);
-            }
-        }
+        for (int k = 0; k < MG; ++k)
+            xv[k] = tid + k * NT < NG ? bv[k] + (r.w_post ? norm4(dv[k], rms, wp[k], r.zc) : dv[k]) : f4z();
     }
     float ss = 0.0f;
 #pragma unroll
@@ -3171,7 +3185,7 @@ __global__ __launch_bounds__(NT) void k_pf_rows(PfRows r) {
 #pragma unroll
     for (int k = 0; k < MG; ++k) {
         const int g = tid + k * NT;
-        y[k] = g < NG ? norm4(xv[k], rms, ((const float4*)r.w_norm)[g], r.zc) : f4z();
+        y[k] = g < NG ? norm4(xv[k], rms, wn[k], r.zc) : f4z();
         mx = fmaxf(mx, amax4(y[k]));
     }
     if (r.xn_out) {
