@@ -3516,25 +3516,50 @@ __global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const 
 
 // h = gelu_tanh(sum_s g_s) * sum_s u_s (MLP.hs:384-447) -> GEMM operand A.
 // The row is staged in dynamic LDS (F floats) for its scale.
-__global__ __launch_bounds__(NT) void k_pf_geglu(const float* part, int S, int ld, int Pp, int F, int up_off, PfA a) {
+template <int S>
+__global__ __launch_bounds__(NT) void k_pf_geglu(const float* part, int ld, int Pp, int F, int up_off, PfA a) {
     extern __shared__ __align__(16) float rowbuf[];
     __shared__ float slot[4];
     const int t = blockIdx.x;
-    float mx = 0.0f;
-    for (int i = 4 * threadIdx.x; i < F; i += 4 * NT) {
-        float4 gs = f4z(), us = f4z();
+    // the S split partials of gate and up for elements i..i+3, as
+    // straight-line buffer loads (past F: zeros); the next group's loads go
+    // out before this group's GELU, so a row costs one round trip, not one
+    // per group
+    const BufView P(part + (size_t)t * ld, ((size_t)(S - 1) * Pp * ld + up_off + F) * 4);
+    const uint32_t ss = 4u * (uint32_t)(Pp * ld);
+    float4 g[2][S], u[2][S];
+    auto load = [&](int b, int i) {
+        const bool ok = i < F;
+#pragma unroll
         for (int s = 0; s < S; ++s) {
-            const float* row = part + ((size_t)s * Pp + t) * ld;
-            gs = gs + *(const float4*)(row + i);
-            us = us + *(const float4*)(row + up_off + i);
+            g[b][s] = P.f4(ok ? s * ss + 4u * (uint32_t)i : OOB);
+            u[b][s] = P.f4(ok ? s * ss + 4u * (uint32_t)(up_off + i) : OOB);
+        }
+    };
+    float mx = 0.0f;
+    auto compute = [&](int b, int i) {
+        float4 gs = g[b][0], us = u[b][0];
+#pragma unroll
+        for (int s = 1; s < S; ++s) {
+            gs = gs + g[b][s];
+            us = us + u[b][s];
         }
         const float4 h = make_float4(gelu_tanh(gs.x) * us.x, gelu_tanh(gs.y) * us.y, gelu_tanh(gs.z) * us.z,
                                      gelu_tanh(gs.w) * us.w);
         *(float4*)&rowbuf[i] = h;
         mx = fmaxf(mx, amax4(h));
+    };
+    int i = 4 * threadIdx.x;
+    load(0, i);
+    for (; i < F; i += 8 * NT) {
+        load(1, i + 4 * NT);
+        compute(0, i);
+        if (i + 4 * NT >= F) break;
+        load(0, i + 8 * NT);
+        compute(1, i + 4 * NT);
     }
     const float sc = a.row_scale(t, block_max(mx, slot));  // barrier: rowbuf complete
-    for (int i = 4 * threadIdx.x; i < F; i += 4 * NT) a.put4(t, i, *(const float4*)&rowbuf[i], sc);
+    for (int k = 4 * threadIdx.x; k < F; k += 4 * NT) a.put4(t, k, *(const float4*)&rowbuf[k], sc);
 }
 
 // Split count of a prefill GEMM over Pp token rows: enough for two
@@ -3695,8 +3720,24 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
             GH_CHECK(rows("pf_rows", r, n));
         }
         GH_CHECK(gemm("pf_gate_up", L.gu, &S));
-        GH_CHECK(sink_launch(sink, "pf_geglu", 0.0, k_pf_geglu, dim3(n), dim3(NT), sizeof(float) * F, (const float*)B.part, S,
-                             L.gu.tiles * TILE_ROWS, Pp, F, m->f_pad, A(F)));
+        {
+            auto geglu = [&](auto sc) {
+                return sink_launch(sink, "pf_geglu", 0.0, k_pf_geglu<decltype(sc)::value>, dim3(n), dim3(NT),
+                                   sizeof(float) * F, (const float*)B.part, L.gu.tiles * TILE_ROWS, Pp, F, m->f_pad,
+                                   A(F));
+            };
+            switch (S) {
+                case 1: GH_CHECK(geglu(std::integral_constant<int, 1>{})); break;
+                case 2: GH_CHECK(geglu(std::integral_constant<int, 2>{})); break;
+                case 3: GH_CHECK(geglu(std::integral_constant<int, 3>{})); break;
+                case 4: GH_CHECK(geglu(std::integral_constant<int, 4>{})); break;
+                case 5: GH_CHECK(geglu(std::integral_constant<int, 5>{})); break;
+                case 6: GH_CHECK(geglu(std::integral_constant<int, 6>{})); break;
+                case 7: GH_CHECK(geglu(std::integral_constant<int, 7>{})); break;
+                case 8: GH_CHECK(geglu(std::integral_constant<int, 8>{})); break;
+                default: return set_error(GH_ERR_INVALID, "prefill: %d gate/up splits (1..8)", S);
+            }
+        }
         GH_CHECK(gemm("pf_down", L.down, &S));
     }
     if (!head) {
