@@ -50,28 +50,81 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg, seconds: float, threads: int) -> dict:
-    """The oracle (C port of the reference's arithmetic) on the host cores:
-    greedy decode steps from position 0 until `seconds` have elapsed."""
+def host_cpu() -> dict:
+    """The host's CPU model (lscpu's 'Model name', from /proc/cpuinfo), its
+    logical CPU count and the threads this process may use: the pool sets
+    OMP_NUM_THREADS to the box's CPU share, which os.cpu_count() does not see."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    n = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS") or n)
+    try:
+        share = min(share, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    return {"cpu_model": model, "logical_cpus": n, "threads": max(1, min(n, share))}
+
+
+def cpu_baseline(cfg, seconds: float) -> dict:
+    """The CPU baseline on the host cores, on a bounded sample of the same
+    workload (greedy decode of the seeded gemma3-1b Q4_0 model from position
+    1, about `seconds` of CPU work per leg):
+      - the headline leg: the PyTorch-CPU restatement (oracle/torch_ref.py),
+        Q4_0 dequantised to f32 once (untimed), every thread of the box's
+        share (torch.set_num_threads);
+      - beside it, the C oracle (oracle/gemma_oracle.c, OpenMP) on the same
+        threads, reading the Q4_0 bytes directly.
+    The reference's own path (the WGSL shaders on Dawn's SwiftShader CPU
+    adapter) does not exist in this image."""
     import gemma_hip as gh
     import pyoracle as orc
+    host = host_cpu()
+    threads = host["threads"]
+    tensors = list(gh.synth_tensors(cfg, WEIGHT_SEED, True))
+    prompt = gh.synth_tokens(PROMPT_SEED, "prompt", N_PROMPT, cfg.vocab)
+
+    def run(step, label):
+        step(int(prompt[0]), 0)  # warm caches / page in
+        t0 = time.perf_counter()
+        n, tok = 0, int(prompt[1])
+        while time.perf_counter() - t0 < seconds:
+            tok = step(tok, n + 1)
+            n += 1
+        dt = time.perf_counter() - t0
+        log(f"  cpu baseline ({label}, {threads} threads): {n} steps in {dt:.1f} s -> {n / dt:.2f} tok/s")
+        return n, dt
+
     orc.set_threads(threads)
     om = orc.OracleModel(cfg)
-    for name, dtype, arr in gh.synth_tensors(cfg, WEIGHT_SEED, True):
+    for name, dtype, arr in tensors:
         om.set_tensor(name, arr, dtype)
-    prompt = gh.synth_tokens(PROMPT_SEED, "prompt", N_PROMPT, cfg.vocab)
-    om.step(int(prompt[0]), 0)  # warm caches / page in
-    t0 = time.perf_counter()
-    n, tok = 0, int(prompt[1])
-    while time.perf_counter() - t0 < seconds:
-        _, _, tok = om.step(tok, n + 1)
-        n += 1
-    dt = time.perf_counter() - t0
+    on, odt = run(lambda t, p: om.step(t, p)[2], "C oracle")
     om.close()
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps of the same seeded gemma3-1b Q4_0 model at positions "
-                      f"1..{n} ({dt:.1f} s, oracle/gemma_oracle.c, {threads} OpenMP threads); the per-step "
-                      f"cost is the 562 MB weight pass, position-independent at these lengths"}
+    oracle_leg = {"value": round(on / odt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                  "sample": f"{on} greedy steps at positions 1..{on} ({odt:.1f} s), oracle/gemma_oracle.c"}
+    try:
+        import torch
+        import torch_ref
+    except ImportError as e:  # torch absent on the box: the C-oracle leg is the baseline
+        return {**oracle_leg, "host": host, "torch_leg": f"not run: {e}"}
+    torch.set_num_threads(threads)
+    t0 = time.perf_counter()
+    tm = torch_ref.TorchModel(cfg, tensors, max_seq=N_PROMPT + 4096)
+    prep = time.perf_counter() - t0
+    tn, tdt = run(lambda t, p: tm.step(t, p)[1], "PyTorch-CPU")
+    del tm
+    return {"value": round(tn / tdt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{tn} greedy decode steps of the seeded gemma3-1b Q4_0 model at positions 1..{tn} "
+                      f"({tdt:.1f} s; oracle/torch_ref.py, PyTorch {torch.__version__} on {threads} threads, "
+                      f"weights dequantised to f32 once in {prep:.1f} s, untimed); the per-step cost is the "
+                      f"weight pass, position-independent at these lengths",
+            "host": host, "torch_version": torch.__version__, "c_oracle": oracle_leg}
 
 
 def extras_c2_matvec(gh, ctx) -> dict:
@@ -291,8 +344,7 @@ def main(argv=None) -> int:
                          "c5_gemma3_4b_prefilled_4096": extras_c5_gemma3_4b(gh, ctx),
                          "f2_prefill_gemma3_1b": extras_f2_prefill(gh, ctx, model)}
     if not a.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        out["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds, threads)
+        out["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

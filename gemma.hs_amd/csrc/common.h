@@ -128,9 +128,11 @@ struct gh_ctx {
     hipEvent_t t0 = nullptr, t1 = nullptr;  // gh_timer_start / gh_timer_stop
     void* scratch = nullptr;                // op-level temporaries
     size_t scratch_bytes = 0;
-    // handles created on this context; gh_ctx_destroy destroys what is left
+    // open handles created on this context; a context whose destroy was
+    // called (released) is freed when the last of them is destroyed
     std::vector<gh_model*> models;
     std::vector<gh_q4*> q4s;
+    bool released = false;
 };
 
 struct gh_q4 {
@@ -226,7 +228,8 @@ struct gh_model {
     // presence tracking
     bool has_embd = false, has_out_norm = false;
     std::vector<uint32_t> present;  // per layer bitmask of tensor kinds
-    std::vector<gh_kv*> kvs;
+    std::vector<gh_kv*> kvs;  // open caches; a released model is freed when the last goes
+    bool released = false;    // gh_model_destroy was called
     // persistent step (GH_PERSISTENT=1): exchange words, launch counter, grid
     int persistent = 0;
     uint64_t* w_qkv = nullptr;
@@ -261,6 +264,7 @@ struct gh_kv {
     std::vector<std::unique_ptr<gh::NodeArgsBase>> graph_args;
     std::vector<gh::PosPatch> patches;
     void* d_players = nullptr;  // persistent step: per-layer pointer table
+    ~gh_kv();                   // frees the device buffers and the graph
 };
 
 namespace gh {
@@ -300,7 +304,6 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
 int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t s);
 int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
 int launch_stream_read(const void* p, size_t bytes, float* sink, hipStream_t s);
-int launch_synth_normal(float* out, size_t n, uint64_t key, float sigma, hipStream_t s);
 constexpr int GH_ATTN_OP_MAX_NC = 256;  // chunks per kv head of the op-level attention
 int launch_sample_logits(const float* logits, int n, float inv_temp, uint64_t seed, uint64_t counter, float* scratch,
                          int32_t* token_dev, hipStream_t s);

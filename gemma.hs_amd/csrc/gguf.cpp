@@ -11,8 +11,10 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cmath>
 #include <cstring>
 #include <map>
+#include <new>
 #include <string>
 
 #include "common.h"
@@ -36,12 +38,17 @@ struct TInfo {
     uint64_t offset = 0;
 };
 
+// Every size and offset below comes from the file, so each bound check is
+// written so that it cannot wrap: remaining bytes are n - off (off <= n
+// always holds), and products of file values go through mul_ok.
+bool mul_ok(uint64_t a, uint64_t b, uint64_t* out) { return !__builtin_mul_overflow(a, b, out); }
+
 struct Reader {
     const uint8_t* p;
     size_t n, off = 0;
     bool ok = true;
-    bool need(size_t k) {
-        if (!ok || off + k > n) ok = false;
+    bool need(uint64_t k) {
+        if (!ok || k > (uint64_t)(n - off)) ok = false;
         return ok;
     }
     template <class T>
@@ -102,9 +109,10 @@ bool read_value(Reader& r, uint32_t t, Meta& m) {
         } else if (et == 9) {
             return false;  // nested arrays are not used by GGUF models
         } else {
-            size_t es = scalar_size(et);
-            if (!es || !r.need(es * cnt)) return false;
-            r.off += es * cnt;
+            const uint64_t es = scalar_size(et);
+            uint64_t bytes = 0;
+            if (!es || !mul_ok(es, cnt, &bytes) || !r.need(bytes)) return false;
+            r.off += bytes;
         }
     } else {
         m.num = scalar_value(r, t);
@@ -122,13 +130,44 @@ struct Mapped {
     }
 };
 
+struct TData {
+    int dtype;
+    uint64_t off;    // from the start of the file
+    uint64_t bytes;  // off + bytes <= file size
+};
+
 struct Parsed {
     Mapped mp;
     std::map<std::string, Meta> meta;
     std::map<std::string, TInfo> tens;
+    std::map<std::string, TData> data;  // validated extent and dtype of every tensor
     uint64_t data0 = 0;
     gh_config cfg{};
 };
+
+// dtype and byte size of a tensor, with overflow-checked products; Q4_0
+// rows (the innermost dimension) must hold whole 32-weight blocks.
+int tensor_bytes(const std::string& name, const TInfo& ti, int* dtype, uint64_t* bytes) {
+    uint64_t ne = 1;
+    for (uint64_t d : ti.dims)
+        if (d == 0 || d > (1ull << 40) || !mul_ok(ne, d, &ne) || ne > (1ull << 48))
+            return set_error(GH_ERR_FORMAT, "tensor '%s' has an implausible shape", name.c_str());
+    if (ti.type == GGML_F32) {
+        *dtype = GH_DTYPE_F32;
+        *bytes = ne * 4;
+    } else if (ti.type == GGML_F16) {
+        *dtype = GH_DTYPE_F16;
+        *bytes = ne * 2;
+    } else if (ti.type == GGML_Q4_0) {
+        if (ti.dims.empty() || ti.dims[0] % 32)
+            return set_error(GH_ERR_FORMAT, "Q4_0 tensor '%s': row length not a multiple of 32", name.c_str());
+        *dtype = GH_DTYPE_Q4_0;
+        *bytes = ne / 32 * 18;
+    } else {
+        return set_error(GH_ERR_FORMAT, "tensor '%s' has unsupported ggml type %u", name.c_str(), ti.type);
+    }
+    return GH_OK;
+}
 
 // Parse header, metadata and tensor infos; build the config (configFromGGUF).
 int parse_gguf(const char* path, int32_t max_seq, Parsed& P) {
@@ -167,8 +206,23 @@ int parse_gguf(const char* path, int32_t max_seq, Parsed& P) {
     }
     uint64_t align = 32;
     auto ia = P.meta.find("general.alignment");
-    if (ia != P.meta.end() && ia->second.num > 0) align = (uint64_t)ia->second.num;
+    if (ia != P.meta.end()) {
+        const double a = ia->second.num;
+        if (!(a >= 1 && a <= (1 << 20)) || ((uint64_t)a & ((uint64_t)a - 1)))
+            return set_error(GH_ERR_FORMAT, "general.alignment %g is not a power of two up to 2^20", a);
+        align = (uint64_t)a;
+    }
     P.data0 = (r.off + align - 1) / align * align;
+    if (P.data0 > mp.n) return set_error(GH_ERR_FORMAT, "GGUF data section starts past the end of the file");
+    for (auto& kvp : P.tens) {
+        TData td{};
+        GH_CHECK(tensor_bytes(kvp.first, kvp.second, &td.dtype, &td.bytes));
+        const uint64_t room = mp.n - P.data0;
+        if (kvp.second.offset > room || td.bytes > room - kvp.second.offset)
+            return set_error(GH_ERR_FORMAT, "tensor '%s' extends past the end of the file", kvp.first.c_str());
+        td.off = P.data0 + kvp.second.offset;
+        P.data[kvp.first] = td;
+    }
 
     auto num = [&](const char* key, bool required, double def, double& v) -> int {
         auto it = P.meta.find(key);
@@ -180,17 +234,28 @@ int parse_gguf(const char* path, int32_t max_seq, Parsed& P) {
         v = it->second.num;
         return GH_OK;
     };
+    // integer fields: whole numbers in [0, 2^30] (gh_model_create checks the rest)
+    auto count = [&](const char* key, bool required, double def, int& out) -> int {
+        double v = 0;
+        GH_CHECK(num(key, required, def, v));
+        if (!(v >= 0 && v <= (double)(1 << 30)) || v != (double)(int64_t)v)
+            return set_error(GH_ERR_FORMAT, "metadata %s = %g is not a count", key, v);
+        out = (int)v;
+        return GH_OK;
+    };
     gh_config& c = P.cfg;
     double v;
-    GH_CHECK(num("gemma3.block_count", true, 0, v)); c.n_layers = (int)v;
-    GH_CHECK(num("gemma3.embedding_length", true, 0, v)); c.hidden = (int)v;
-    GH_CHECK(num("gemma3.feed_forward_length", true, 0, v)); c.ffn = (int)v;
-    GH_CHECK(num("gemma3.attention.head_count", true, 0, v)); c.n_heads = (int)v;
-    GH_CHECK(num("gemma3.attention.head_count_kv", true, 0, v)); c.n_kv_heads = (int)v;
-    GH_CHECK(num("gemma3.attention.key_length", true, 0, v)); c.head_dim = (int)v;
+    GH_CHECK(count("gemma3.block_count", true, 0, c.n_layers));
+    GH_CHECK(count("gemma3.embedding_length", true, 0, c.hidden));
+    GH_CHECK(count("gemma3.feed_forward_length", true, 0, c.ffn));
+    GH_CHECK(count("gemma3.attention.head_count", true, 0, c.n_heads));
+    GH_CHECK(count("gemma3.attention.head_count_kv", true, 0, c.n_kv_heads));
+    GH_CHECK(count("gemma3.attention.key_length", true, 0, c.head_dim));
     GH_CHECK(num("gemma3.rope.freq_base", true, 0, v)); c.rope_theta_global = (float)v;
-    GH_CHECK(num("gemma3.attention.sliding_window", false, 512, v)); c.sliding_window = (int)v;
+    GH_CHECK(count("gemma3.attention.sliding_window", false, 512, c.sliding_window));
     GH_CHECK(num("gemma3.attention.layer_norm_rms_epsilon", false, 1e-6, v)); c.rms_eps = (float)v;
+    if (!(c.rope_theta_global > 0.0f) || !(c.rms_eps > 0.0f) || !std::isfinite(c.rope_theta_global))
+        return set_error(GH_ERR_FORMAT, "rope.freq_base and layer_norm_rms_epsilon must be positive");
     c.rope_theta_local = 10000.0f;
     c.global_every = 6;
     c.mode = GH_MODE_GEMMA3;
@@ -199,6 +264,7 @@ int parse_gguf(const char* path, int32_t max_seq, Parsed& P) {
     auto te = P.tens.find("token_embd.weight");
     if (te == P.tens.end() || te->second.dims.size() != 2)
         return set_error(GH_ERR_NOT_FOUND, "missing tensor token_embd.weight");
+    if (te->second.dims[1] > (1u << 30)) return set_error(GH_ERR_FORMAT, "token_embd.weight has too many rows");
     c.vocab = (int)te->second.dims[1];
     if ((int64_t)te->second.dims[0] != c.hidden)
         return set_error(GH_ERR_FORMAT, "token_embd.weight width %llu != embedding_length %d",
@@ -208,12 +274,25 @@ int parse_gguf(const char* path, int32_t max_seq, Parsed& P) {
     return GH_OK;
 }
 
+// parse_gguf behind a catch: an allocation failure (a huge metadata string
+// or count that passes the bounds checks on a huge file) must not unwind
+// through the C ABI
+int parse_safe(const char* path, int32_t max_seq, Parsed& P) {
+    try {
+        return parse_gguf(path, max_seq, P);
+    } catch (const std::bad_alloc&) {
+        return set_error(GH_ERR_OOM, "out of host memory while parsing '%s'", path);
+    } catch (...) {
+        return set_error(GH_ERR_FORMAT, "malformed GGUF file '%s'", path);
+    }
+}
+
 }  // namespace
 
 extern "C" int gh_gguf_inspect(const char* path, gh_config* out) {
     if (!path || !out) return set_error(GH_ERR_INVALID, "null argument");
     Parsed P;
-    GH_CHECK(parse_gguf(path, 0, P));
+    GH_CHECK(parse_safe(path, 0, P));
     *out = P.cfg;
     return GH_OK;
 }
@@ -221,30 +300,13 @@ extern "C" int gh_gguf_inspect(const char* path, gh_config* out) {
 extern "C" int gh_model_load_gguf(gh_ctx* ctx, const char* path, int32_t max_seq, gh_model** out) {
     if (!ctx || !path || !out) return set_error(GH_ERR_INVALID, "null argument");
     Parsed P;
-    GH_CHECK(parse_gguf(path, max_seq, P));
+    GH_CHECK(parse_safe(path, max_seq, P));
     gh_model* m = nullptr;
     GH_CHECK(gh_model_create(ctx, &P.cfg, &m));
-    for (auto& kvp : P.tens) {
+    for (auto& kvp : P.data) {
         const std::string& name = kvp.first;
-        const TInfo& ti = kvp.second;
-        uint64_t ne = 1;
-        for (uint64_t d : ti.dims) ne *= d;
-        uint64_t bytes;
-        int dtype;
-        if (ti.type == GGML_F32) { bytes = ne * 4; dtype = GH_DTYPE_F32; }
-        else if (ti.type == GGML_F16) { bytes = ne * 2; dtype = GH_DTYPE_F16; }
-        else if (ti.type == GGML_Q4_0) {
-            if (ne % 32) { gh_model_destroy(m); return set_error(GH_ERR_FORMAT, "Q4_0 tensor '%s' not a multiple of 32", name.c_str()); }
-            bytes = ne / 32 * 18; dtype = GH_DTYPE_Q4_0;
-        } else {
-            gh_model_destroy(m);
-            return set_error(GH_ERR_FORMAT, "tensor '%s' has unsupported ggml type %u", name.c_str(), ti.type);
-        }
-        if (P.data0 + ti.offset + bytes > P.mp.n) {
-            gh_model_destroy(m);
-            return set_error(GH_ERR_FORMAT, "tensor '%s' extends past the end of the file", name.c_str());
-        }
-        int rc = gh_model_set_tensor(m, name.c_str(), dtype, (const uint8_t*)P.mp.p + P.data0 + ti.offset, bytes);
+        const TData& td = kvp.second;  // extent checked against the file by parse_gguf
+        int rc = gh_model_set_tensor(m, name.c_str(), td.dtype, (const uint8_t*)P.mp.p + td.off, td.bytes);
         if (rc == GH_ERR_NOT_FOUND) continue;  // tensors the decode step does not use (e.g. rope_freqs)
         if (rc != GH_OK) {
             gh_model_destroy(m);

@@ -3915,23 +3915,6 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
-__global__ void k_synth_normal(float* out, size_t n, uint64_t key, float sigma) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        const uint64_t h = splitmix64(key ^ splitmix64(i));
-        const float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
-        const float u2 = (float)((h >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
-        out[i] = sigma * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307f * u2);
-    }
-}
-
-int launch_synth_normal(float* out, size_t n, uint64_t key, float sigma, hipStream_t s) {
-    if (n == 0) return GH_OK;
-    const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
-    hipLaunchKernelGGL(k_synth_normal, dim3((unsigned)blocks), dim3(256), 0, s, out, n, key, sigma);
-    GH_HIP(hipGetLastError());
-    return GH_OK;
-}
-
 // Op-level sampling: per-64-row-block softmax statistics, then the draw.
 __global__ __launch_bounds__(64) void k_sample_blocks(const float* logits, int n, float inv_t, float* bm, float* bs) {
     const int r = blockIdx.x * 64 + threadIdx.x;

@@ -6,6 +6,7 @@
 #include <cstring>
 #include <memory>
 #include <string>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -15,8 +16,57 @@ namespace {
 
 using Lock = std::lock_guard<std::recursive_mutex>;
 
+// ---------------------------------------------------------------------
+// Handle lifetimes.  Every handle the ABI returns is registered until its
+// destroy call.  A destroy (or any other call) on a handle that is not
+// registered -- destroyed already, or never returned -- is GH_ERR_STATE and
+// touches no memory.  A context or model whose destroy is called while
+// handles created from it are still open is only released: it stays alive
+// (stream, device memory) until the last of them is destroyed, so handles
+// may be destroyed in any order, as finalisers run them.  The registry
+// mutex is taken alone or before a context mutex, never after one.
+// ---------------------------------------------------------------------
+enum HandleKind { HK_CTX = 1, HK_MODEL, HK_KV, HK_Q4 };
+std::mutex& handles_mu() {
+    static auto* m = new std::mutex();  // never destroyed, as the map below
+    return *m;
+}
+std::unordered_map<const void*, int>& handles() {
+    static auto* h = new std::unordered_map<const void*, int>();  // never destroyed: finalisers may run at exit
+    return *h;
+}
+void handle_add(const void* h, int kind) {
+    std::lock_guard<std::mutex> g(handles_mu());
+    handles()[h] = kind;
+}
+bool handle_live(const void* h, int kind) {
+    std::lock_guard<std::mutex> g(handles_mu());
+    auto it = handles().find(h);
+    return it != handles().end() && it->second == kind;
+}
+const char* kind_name(int kind) {
+    return kind == HK_CTX ? "context" : kind == HK_MODEL ? "model" : kind == HK_KV ? "KV cache" : "Q4_0 tensor";
+}
+int dead_handle(const char* fn, int kind) {
+    return set_error(GH_ERR_STATE, "%s: not an open %s handle (destroyed already or never created)", fn, kind_name(kind));
+}
+#define GH_LIVE(h, kind)                                                  \
+    do {                                                                  \
+        if (!(h)) return set_error(GH_ERR_INVALID, "%s: null handle", __func__); \
+        if (!handle_live((h), (kind))) return dead_handle(__func__, (kind)); \
+    } while (0)
+
+// Entry points taking a context handle: it must be open.
 int ctx_bind(gh_ctx* ctx) {
     if (!ctx) return set_error(GH_ERR_INVALID, "null context");
+    if (!handle_live(ctx, HK_CTX)) return dead_handle("context", HK_CTX);
+    GH_HIP(hipSetDevice(ctx->device));
+    return GH_OK;
+}
+
+// Entry points taking a model / cache / tensor handle (checked open by the
+// caller): its context is alive, released or not.
+int dev_bind(gh_ctx* ctx) {
     GH_HIP(hipSetDevice(ctx->device));
     return GH_OK;
 }
@@ -384,22 +434,65 @@ extern "C" int gh_ctx_create(int device, gh_ctx** out) {
     c->device = device;
     GH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     *out = c.release();
+    handle_add(*out, HK_CTX);
     return GH_OK;
 }
 
+// Lifetime helpers (registry mutex held by the caller).
+namespace {
+
+// Frees a released context that has no open model or Q4_0 tensor left.
+void ctx_collect(gh_ctx* ctx) {
+    {
+        Lock lk(ctx->mu);
+        if (!ctx->released || !ctx->models.empty() || !ctx->q4s.empty()) return;
+        hipSetDevice(ctx->device);
+        hipStreamSynchronize(ctx->stream);
+        for (void* p : ctx->bufs) hipFree(p);
+        if (ctx->scratch) hipFree(ctx->scratch);
+        if (ctx->t0) hipEventDestroy(ctx->t0);
+        if (ctx->t1) hipEventDestroy(ctx->t1);
+        hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+}
+
+// Frees a released model that has no open KV cache left, then its context
+// if that was released too.
+void model_collect(gh_model* m) {
+    gh_ctx* ctx = m->ctx;
+    {
+        Lock lk(ctx->mu);
+        if (!m->released || !m->kvs.empty()) return;
+        hipSetDevice(ctx->device);
+        hipStreamSynchronize(ctx->stream);
+        free_prefill(m);
+        for (auto& b : m->owned) hipFree(b.p);
+        auto& v = ctx->models;
+        v.erase(std::remove(v.begin(), v.end(), m), v.end());
+        delete m;
+    }
+    ctx_collect(ctx);
+}
+
+bool handle_take(const void* h, int kind) {
+    auto it = handles().find(h);
+    if (it == handles().end() || it->second != kind) return false;
+    handles().erase(it);
+    return true;
+}
+
+}  // namespace
+
 extern "C" int gh_ctx_destroy(gh_ctx* ctx) {
     if (!ctx) return GH_OK;
-    hipSetDevice(ctx->device);
-    hipStreamSynchronize(ctx->stream);
-    // handles still open on the context go first: they use its stream
-    for (gh_model* m : std::vector<gh_model*>(ctx->models)) gh_model_destroy(m);
-    for (gh_q4* t : std::vector<gh_q4*>(ctx->q4s)) gh_q4_0_free(t);
-    for (void* p : ctx->bufs) hipFree(p);
-    if (ctx->scratch) hipFree(ctx->scratch);
-    if (ctx->t0) hipEventDestroy(ctx->t0);
-    if (ctx->t1) hipEventDestroy(ctx->t1);
-    hipStreamDestroy(ctx->stream);
-    delete ctx;
+    std::lock_guard<std::mutex> g(handles_mu());
+    if (!handle_take(ctx, HK_CTX)) return dead_handle("gh_ctx_destroy", HK_CTX);
+    {
+        Lock lk(ctx->mu);
+        ctx->released = true;
+    }
+    ctx_collect(ctx);
     return GH_OK;
 }
 
@@ -544,6 +637,7 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
     ctx->q4s.push_back(t.get());
     *out = t.release();
+    handle_add(*out, HK_Q4);
     return GH_OK;
 }
 
@@ -555,14 +649,18 @@ gh_q4::~gh_q4() {
 
 extern "C" int gh_q4_0_free(gh_q4* t) {
     if (!t) return GH_OK;
-    hipSetDevice(t->ctx->device);
-    hipStreamSynchronize(t->ctx->stream);
+    std::lock_guard<std::mutex> g(handles_mu());
+    if (!handle_take(t, HK_Q4)) return dead_handle("gh_q4_0_free", HK_Q4);
+    gh_ctx* ctx = t->ctx;
     {
-        Lock lk(t->ctx->mu);
-        auto& v = t->ctx->q4s;
+        Lock lk(ctx->mu);
+        hipSetDevice(ctx->device);
+        hipStreamSynchronize(ctx->stream);
+        auto& v = ctx->q4s;
         v.erase(std::remove(v.begin(), v.end(), t), v.end());
+        delete t;
     }
-    delete t;
+    ctx_collect(ctx);
     return GH_OK;
 }
 
@@ -594,8 +692,9 @@ static int ctx_scratch(gh_ctx* ctx, size_t bytes, void** out) {
 }
 
 extern "C" int gh_q4_0_dequant(gh_q4* t, float* out) {
+    GH_LIVE(t, HK_Q4);
     if (!t || !out) return set_error(GH_ERR_INVALID, "null argument");
-    GH_CHECK(ctx_bind(t->ctx));
+    GH_CHECK(dev_bind(t->ctx));
     Lock lk(t->ctx->mu);
     GH_CHECK(launch_q4_dequant(t->m, out, t->ctx->stream));
     GH_CHECK(op_sync(t->ctx));
@@ -603,9 +702,10 @@ extern "C" int gh_q4_0_dequant(gh_q4* t, float* out) {
 }
 
 extern "C" int gh_q4_0_matvec(gh_q4* t, const float* x, float* y, int softcap, float cap) {
+    GH_LIVE(t, HK_Q4);
     if (!t || !x || !y) return set_error(GH_ERR_INVALID, "null argument");
     if (softcap && !(cap > 0.0f)) return set_error(GH_ERR_INVALID, "soft-cap value must be > 0");
-    GH_CHECK(ctx_bind(t->ctx));
+    GH_CHECK(dev_bind(t->ctx));
     Lock lk(t->ctx->mu);
     GH_CHECK(launch_matvec_plain(t->m, t->plan, x, t->part, y, softcap, cap, t->ctx->stream));
     GH_CHECK(op_sync(t->ctx));
@@ -802,22 +902,19 @@ extern "C" int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out
     }
     ctx->models.push_back(m.get());
     *out = m.release();
+    handle_add(*out, HK_MODEL);
     return GH_OK;
 }
 
 extern "C" int gh_model_destroy(gh_model* m) {
     if (!m) return GH_OK;
-    hipSetDevice(m->ctx->device);
-    hipStreamSynchronize(m->ctx->stream);
-    for (gh_kv* kv : std::vector<gh_kv*>(m->kvs)) gh_kv_destroy(kv);
-    free_prefill(m);
+    std::lock_guard<std::mutex> g(handles_mu());
+    if (!handle_take(m, HK_MODEL)) return dead_handle("gh_model_destroy", HK_MODEL);
     {
         Lock lk(m->ctx->mu);
-        auto& v = m->ctx->models;
-        v.erase(std::remove(v.begin(), v.end(), m), v.end());
+        m->released = true;
     }
-    for (auto& b : m->owned) hipFree(b.p);
-    delete m;
+    model_collect(m);
     return GH_OK;
 }
 
@@ -840,8 +937,9 @@ static int ensure_fmt(gh_model* m, int dtype) {
 }
 
 extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, const void* data, size_t nbytes) {
+    GH_LIVE(m, HK_MODEL);
     if (!m || !name || !data) return set_error(GH_ERR_INVALID, "null argument");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     const gh_config& c = m->cfg;
     const bool ftz = !(c.flags & GH_FLAG_IEEE_SCALES);
@@ -916,6 +1014,7 @@ extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, con
 }
 
 extern "C" int gh_model_check(gh_model* m) {
+    GH_LIVE(m, HK_MODEL);
     if (!m) return set_error(GH_ERR_INVALID, "null model");
     if (!m->has_embd) return set_error(GH_ERR_NOT_FOUND, "missing tensor token_embd.weight");
     if (!m->has_out_norm) return set_error(GH_ERR_NOT_FOUND, "missing tensor output_norm.weight");
@@ -933,6 +1032,7 @@ extern "C" int gh_model_check(gh_model* m) {
 }
 
 extern "C" int gh_model_config(gh_model* m, gh_config* out) {
+    GH_LIVE(m, HK_MODEL);
     if (!m || !out) return set_error(GH_ERR_INVALID, "null argument");
     *out = m->cfg;
     return GH_OK;
@@ -942,22 +1042,24 @@ extern "C" int gh_model_config(gh_model* m, gh_config* out) {
 // KV cache handle
 // =====================================================================
 extern "C" int gh_kv_create(gh_model* m, int32_t max_seq, gh_kv** out) {
+    GH_LIVE(m, HK_MODEL);
     if (!m || !out) return set_error(GH_ERR_INVALID, "null argument");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     if (max_seq <= 0) max_seq = m->cfg.max_seq;
     const gh_config& c = m->cfg;
+    // the kernels address one layer's K (or V) through a buffer view of at
+    // most 2^31 - 1 bytes
+    if ((uint64_t)max_seq * c.n_kv_heads * c.head_dim * 4 > 0x7fffffffull)
+        return set_error(GH_ERR_RANGE, "max_seq %d: one layer's K cache would exceed 2 GiB", max_seq);
     std::unique_ptr<gh_kv> kv(new gh_kv);
     kv->m = m;
     kv->max_seq = max_seq;
     const size_t n = (size_t)c.n_layers * max_seq * c.n_kv_heads * c.head_dim;
     hipError_t e1 = hipMalloc((void**)&kv->k, n * 4);
     hipError_t e2 = hipMalloc((void**)&kv->v, n * 4);
-    if (e1 != hipSuccess || e2 != hipSuccess) {
-        if (kv->k) hipFree(kv->k);
-        if (kv->v) hipFree(kv->v);
+    if (e1 != hipSuccess || e2 != hipSuccess)
         return set_error(GH_ERR_OOM, "KV cache of %zu bytes does not fit", 2 * n * 4);
-    }
     GH_HIP(hipMalloc((void**)&kv->st, sizeof(StepState)));
     {
         // (cos, sin) of pos * inv_freq for both layer types, positions [0, max_seq)
@@ -973,44 +1075,64 @@ extern "C" int gh_kv_create(gh_model* m, int32_t max_seq, gh_kv** out) {
     GH_HIP(hipHostMalloc((void**)&kv->h_st, sizeof(StepState), hipHostMallocDefault));
     std::memset(kv->h_st, 0, sizeof(StepState));
     GH_HIP(hipMemcpy(kv->st, kv->h_st, sizeof(StepState), hipMemcpyHostToDevice));
-    m->kvs.push_back(kv.get());
-    *out = kv.release();
+    m->kvs.push_back(kv.release());
+    *out = m->kvs.back();
+    handle_add(*out, HK_KV);
     return GH_OK;
+}
+
+gh_kv::~gh_kv() {
+    if (graph_exec) hipGraphExecDestroy(graph_exec);
+    if (graph) hipGraphDestroy(graph);
+    for (void* p : {(void*)k, (void*)v, (void*)st, (void*)rope, (void*)d_prompt, (void*)d_ids, d_players})
+        if (p) hipFree(p);
+    if (h_st) hipHostFree(h_st);
 }
 
 extern "C" int gh_kv_destroy(gh_kv* kv) {
     if (!kv) return GH_OK;
+    std::lock_guard<std::mutex> g(handles_mu());
+    if (!handle_take(kv, HK_KV)) return dead_handle("gh_kv_destroy", HK_KV);
     gh_model* m = kv->m;
-    hipSetDevice(m->ctx->device);
-    hipStreamSynchronize(m->ctx->stream);
-    if (kv->graph_exec) hipGraphExecDestroy(kv->graph_exec);
-    if (kv->graph) hipGraphDestroy(kv->graph);
-    hipFree(kv->k);
-    hipFree(kv->v);
-    hipFree(kv->st);
-    hipFree(kv->rope);
-    hipFree(kv->d_prompt);
-    hipFree(kv->d_ids);
-    if (kv->d_players) hipFree(kv->d_players);
-    hipHostFree(kv->h_st);
-    m->kvs.erase(std::remove(m->kvs.begin(), m->kvs.end(), kv), m->kvs.end());
-    delete kv;
+    {
+        Lock lk(m->ctx->mu);
+        hipSetDevice(m->ctx->device);
+        hipStreamSynchronize(m->ctx->stream);
+        m->kvs.erase(std::remove(m->kvs.begin(), m->kvs.end(), kv), m->kvs.end());
+        delete kv;
+    }
+    model_collect(m);
     return GH_OK;
 }
 
+extern "C" void gh_ctx_release(gh_ctx* ctx) { (void)gh_ctx_destroy(ctx); }
+extern "C" void gh_model_release(gh_model* m) { (void)gh_model_destroy(m); }
+extern "C" void gh_kv_release(gh_kv* kv) { (void)gh_kv_destroy(kv); }
+extern "C" void gh_q4_0_release(gh_q4* t) { (void)gh_q4_0_free(t); }
+
 extern "C" int gh_kv_reset(gh_kv* kv) {
+    GH_LIVE(kv, HK_KV);
     if (!kv) return set_error(GH_ERR_INVALID, "null kv");
     kv->len = 0;
     return GH_OK;
 }
 
 extern "C" int gh_kv_length(gh_kv* kv, int32_t* len) {
+    GH_LIVE(kv, HK_KV);
     if (!kv || !len) return set_error(GH_ERR_INVALID, "null argument");
     *len = kv->len;
     return GH_OK;
 }
 
+extern "C" int gh_kv_truncate(gh_kv* kv, int32_t n) {
+    GH_LIVE(kv, HK_KV);
+    if (n < 0 || n > kv->len) return set_error(GH_ERR_RANGE, "gh_kv_truncate: %d outside [0, %d]", n, kv->len);
+    kv->len = n;
+    return GH_OK;
+}
+
 extern "C" int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed) {
+    GH_LIVE(kv, HK_KV);
     if (!kv) return set_error(GH_ERR_INVALID, "null kv");
     if (!(temperature >= 0.0f) || std::isinf(temperature))
         return set_error(GH_ERR_INVALID, "temperature must be finite and >= 0");
@@ -1020,20 +1142,25 @@ extern "C" int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed) {
 }
 
 extern "C" int gh_kv_synth(gh_kv* kv, uint64_t seed, int32_t n_pos, float sigma) {
+    GH_LIVE(kv, HK_KV);
     if (!kv) return set_error(GH_ERR_INVALID, "null kv");
     if (n_pos < 0 || n_pos > kv->max_seq) return set_error(GH_ERR_RANGE, "n_pos %d outside [0, %d]", n_pos, kv->max_seq);
     gh_model* m = kv->m;
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     const gh_config& c = m->cfg;
-    const size_t per_layer = (size_t)kv->max_seq * c.n_kv_heads * c.head_dim;
-    const size_t n = (size_t)n_pos * c.n_kv_heads * c.head_dim;
-    for (int l = 0; l < c.n_layers; ++l) {
-        const uint64_t key = seed * 0x9E3779B97F4A7C15ull + (uint64_t)l * 2;
-        GH_CHECK(launch_synth_normal(kv->k + l * per_layer, n, key, sigma, m->ctx->stream));
-        GH_CHECK(launch_synth_normal(kv->v + l * per_layer, n, key + 1, sigma, m->ctx->stream));
-    }
+    const int width = c.n_kv_heads * c.head_dim;
+    const size_t per_layer = (size_t)kv->max_seq * width;
+    const size_t n = (size_t)n_pos * width;
+    // generated on the host (gh_synth_kv: the bytes a CPU checker can
+    // regenerate), one layer at a time
+    std::vector<float> hk(n), hv(n);
     GH_HIP(hipStreamSynchronize(m->ctx->stream));
+    for (int l = 0; l < c.n_layers; ++l) {
+        GH_CHECK(gh_synth_kv(seed, l, n_pos, width, sigma, hk.data(), hv.data()));
+        GH_HIP(hipMemcpy(kv->k + l * per_layer, hk.data(), n * sizeof(float), hipMemcpyHostToDevice));
+        GH_HIP(hipMemcpy(kv->v + l * per_layer, hv.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    }
     kv->len = n_pos;
     return GH_OK;
 }
@@ -1042,8 +1169,10 @@ extern "C" int gh_kv_synth(gh_kv* kv, uint64_t seed, int32_t n_pos, float sigma)
 // step / generate / bench / profile
 // =====================================================================
 extern "C" int gh_step(gh_model* m, gh_kv* kv, int32_t token, float* logits, float* layer_out, int32_t* argmax_out) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     const gh_config& c = m->cfg;
@@ -1109,9 +1238,11 @@ static int run_device_fed(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t
 
 extern "C" int gh_generate(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
                            int32_t* ids_out) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
     if (n_gen <= 0 || !ids_out) return set_error(GH_ERR_INVALID, "n_gen must be > 0 with an output buffer");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     return run_device_fed(m, kv, prompt, n_prompt, n_prompt + n_gen - 1, 0, n_gen, nullptr, ids_out);
@@ -1119,9 +1250,11 @@ extern "C" int gh_generate(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_
 
 extern "C" int gh_bench_decode(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_warmup,
                                int32_t n_steps, float* ms_out, int32_t* ids_out) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m || !ms_out) return set_error(GH_ERR_INVALID, "bad arguments");
     if (n_warmup < 0 || n_steps <= 0) return set_error(GH_ERR_INVALID, "bad step counts");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     return run_device_fed(m, kv, prompt, n_prompt, n_prompt + n_warmup, n_steps, n_warmup + n_steps + 1, ms_out,
@@ -1191,8 +1324,10 @@ static int prefill_run(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n,
 
 extern "C" int gh_prefill(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, float* logits, float* layer_out,
                           int32_t* next_out) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     return prefill_run(m, kv, tokens, n, logits, layer_out, next_out);
@@ -1200,9 +1335,11 @@ extern "C" int gh_prefill(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t
 
 extern "C" int gh_generate_prefill(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_prompt, int32_t n_gen,
                                    int32_t* ids_out) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m) return set_error(GH_ERR_INVALID, "model / kv mismatch");
     if (n_gen <= 0 || !ids_out) return set_error(GH_ERR_INVALID, "n_gen must be > 0 with an output buffer");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     if (prompt && n_prompt > 0 && (long long)kv->len + n_prompt + n_gen - 1 > kv->max_seq)
@@ -1217,9 +1354,11 @@ extern "C" int gh_generate_prefill(gh_model* m, gh_kv* kv, const int32_t* prompt
 
 extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kernel_stat* stats, int32_t max_stats,
                                 int32_t* n_stats) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m || !stats || !n_stats || n_steps <= 0)
         return set_error(GH_ERR_INVALID, "bad arguments");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     if (kv->len + n_steps > kv->max_seq) return set_error(GH_ERR_RANGE, "KV cache full");
@@ -1243,8 +1382,10 @@ extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kern
 
 extern "C" int gh_prefill_profile(gh_model* m, gh_kv* kv, const int32_t* tokens, int32_t n, gh_kernel_stat* stats,
                                   int32_t max_stats, int32_t* n_stats) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m || !stats || !n_stats) return set_error(GH_ERR_INVALID, "bad arguments");
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     Profiler prof;
@@ -1256,13 +1397,15 @@ extern "C" int gh_prefill_profile(gh_model* m, gh_kv* kv, const int32_t* tokens,
 
 extern "C" int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t n_reps, double* avg_us_out,
                               double* bytes_per_launch_out, int32_t* launches_per_step_out) {
+    GH_LIVE(m, HK_MODEL);
+    GH_LIVE(kv, HK_KV);
     if (!m || !kv || kv->m != m || !name || n_reps <= 0 || !avg_us_out)
         return set_error(GH_ERR_INVALID, "bad arguments");
     static const char* kinds[] = {"qkv", "attention", "o_proj", "gate_up", "down", "final_norm", "lm_head"};
     bool known = false;
     for (const char* k : kinds) known = known || std::strcmp(k, name) == 0;
     if (!known) return set_error(GH_ERR_INVALID, "gh_time_kernel: unknown or non-idempotent kernel '%s'", name);
-    GH_CHECK(ctx_bind(m->ctx));
+    GH_CHECK(dev_bind(m->ctx));
     Lock lk(m->ctx->mu);
     GH_CHECK(model_ready(m));
     if (kv->len >= kv->max_seq) return set_error(GH_ERR_RANGE, "KV cache full");
@@ -1356,6 +1499,7 @@ extern "C" int gh_time_stream_read(gh_ctx* ctx, size_t bytes, int32_t n_reps, do
 // synthetic model
 // =====================================================================
 extern "C" int gh_synth_model(gh_model* m, uint64_t seed, int q4, float w_sigma, float scale_sigma, float norm_sigma) {
+    GH_LIVE(m, HK_MODEL);
     if (!m) return set_error(GH_ERR_INVALID, "null model");
     const gh_config& c = m->cfg;
     const int H = c.hidden, hd = c.head_dim, F = c.ffn;

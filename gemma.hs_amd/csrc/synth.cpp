@@ -78,7 +78,7 @@ uint16_t f32_to_f16_rne(float f) {
 static void parallel_rows(int64_t rows, const std::function<void(int64_t, int64_t)>& fn) {
     unsigned nt = std::thread::hardware_concurrency();
     if (nt > 16) nt = 16;
-    if (nt < 1 || rows < 4096) {
+    if (nt < 1 || rows < 512) {
         fn(0, rows);
         return;
     }
@@ -122,6 +122,24 @@ extern "C" int gh_synth_q4_0(uint64_t seed, const char* name, float scale_sigma,
                 std::memcpy(blk + 2, &c0, 8);
                 std::memcpy(blk + 10, &c1, 8);
             }
+        }
+    });
+    return GH_OK;
+}
+
+extern "C" int gh_synth_kv(uint64_t seed, int32_t layer, int32_t n_pos, int32_t width, float sigma, float* k_out,
+                           float* v_out) {
+    if (layer < 0 || n_pos < 0 || width <= 0 || (n_pos && (!k_out || !v_out)))
+        return set_error(GH_ERR_INVALID, "gh_synth_kv: bad arguments");
+    // one stream per (layer, K or V, position): rows of `width` values
+    parallel_rows(n_pos, [&](int64_t p0, int64_t p1) {
+        for (int64_t p = p0; p < p1; ++p) {
+            const uint64_t row = ((uint64_t)(uint32_t)layer << 32) | (uint64_t)p;
+            SplitMix gk(stream_seed(seed, "kv.k", row)), gv(stream_seed(seed, "kv.v", row));
+            float* kr = k_out + p * (int64_t)width;
+            float* vr = v_out + p * (int64_t)width;
+            for (int32_t i = 0; i < width; ++i) kr[i] = (float)(gk.normal() * (double)sigma);
+            for (int32_t i = 0; i < width; ++i) vr[i] = (float)(gv.normal() * (double)sigma);
         }
     });
     return GH_OK;

@@ -17,7 +17,6 @@ fallback: without libgemma_hip.so (or without a GPU) the calls raise.
 from __future__ import annotations
 
 import ctypes as C
-import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -32,7 +31,7 @@ __all__ = [
     "GemmaConfig", "GemmaHipError", "Context", "DeviceBuffer", "Q4Tensor", "GemmaModel", "KVCache",
     "preset", "runLinearQ4", "runGemmaInferenceCached", "runGemmaInferenceCachedWithLayer0",
     "generate", "prefill", "bench_decode", "profile_steps", "profile_prefill", "sample_logits", "time_kernel", "KernelTiming", "STEP_KERNELS", "synth_f32", "synth_q4_0", "synth_tokens",
-    "tensor_list", "synth_tensors", "device_count", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q4_0",
+    "tensor_list", "synth_tensors", "synth_kv", "center_q4_0", "device_count", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q4_0",
     "MODE_GEMMA3", "MODE_REF", "FLAG_QK_NORM", "FLAG_POST_ATTN_NORM", "FLAG_POST_FFN_NORM",
     "FLAG_ZERO_CENTERED", "FLAG_IEEE_SCALES",
 ]
@@ -63,8 +62,6 @@ class Context:
         h = C.c_void_p()
         check(lib().gh_ctx_create(device, C.byref(h)))
         self.h = h
-        # models and Q4_0 tensors created on this context: closed before it
-        self._children = weakref.WeakSet()
 
     def sync(self) -> None:
         check(lib().gh_ctx_sync(self.h))
@@ -92,11 +89,10 @@ class Context:
         return ms.value
 
     def close(self) -> None:
-        """Destroy the context; models (with their caches) and Q4_0 tensors
-        still open on it are closed first and their handles become None."""
+        """Destroy the context handle.  Models, caches and Q4_0 tensors made
+        on it stay usable; the library frees the context when the last of
+        them is closed (handles close in any order)."""
         if self.h:
-            for child in list(self._children):
-                child.close()
             lib().gh_ctx_destroy(self.h)
             self.h = None
 
@@ -160,7 +156,6 @@ class Q4Tensor:
         check(lib().gh_q4_0_upload(ctx.h, _ptr(raw), rows, cols, FLAG_IEEE_SCALES if ieee_scales else 0,
                                    C.byref(h)))
         self.ctx, self.h, self.rows, self.cols = ctx, h, rows, cols
-        ctx._children.add(self)
 
     def dequant(self) -> np.ndarray:
         out = DeviceBuffer(self.ctx, 4 * self.rows * self.cols)
@@ -304,6 +299,28 @@ def synth_tokens(seed: int, name: str, n: int, vocab: int) -> np.ndarray:
     return out
 
 
+def synth_kv(seed: int, layer: int, n_pos: int, width: int, sigma: float = 1.0):
+    """(K, V) [n_pos, width] of one layer as KVCache.synth fills it (gh_synth_kv)."""
+    k = np.empty((n_pos, width), np.float32)
+    v = np.empty((n_pos, width), np.float32)
+    check(lib().gh_synth_kv(seed, layer, n_pos, width, sigma, _ptr(k), _ptr(v)))
+    return k, v
+
+
+def center_q4_0(raw: np.ndarray) -> np.ndarray:
+    """Zero-mean variant of raw Q4_0 blocks: code 0 becomes 8, so the codes
+    have mean 8 and q - 8 mean 0.  Uniform codes give every row a common
+    -0.5 * d offset per block, which makes a random deep model's argmax
+    almost independent of its input; the centred codes do not."""
+    b = np.ascontiguousarray(raw, np.uint8).reshape(-1, 18).copy()
+    q = b[:, 2:]
+    lo, hi = q & 15, q >> 4
+    lo[lo == 0] = 8
+    hi[hi == 0] = 8
+    b[:, 2:] = lo | (hi << 4)
+    return b.reshape(-1)
+
+
 def tensor_list(cfg: GemmaConfig):
     """(name, kind, shape) of every tensor a config needs; kind 'mat' or 'vec'.
     GGUF names; the same order gh_synth_model uses."""
@@ -330,13 +347,15 @@ def tensor_list(cfg: GemmaConfig):
 
 
 def synth_tensors(cfg: GemmaConfig, seed: int, q4: bool, w_sigma: float = 0.02,
-                  scale_sigma: float = 0.01, norm_sigma: float = 0.02):
-    """Yield (name, dtype, array) with exactly the bytes gh_synth_model uploads."""
+                  scale_sigma: float = 0.01, norm_sigma: float = 0.02, centered: bool = False):
+    """Yield (name, dtype, array) with exactly the bytes gh_synth_model uploads
+    (centered: Q4_0 codes through center_q4_0)."""
     for name, kind, shape in tensor_list(cfg):
         if kind == "vec":
             yield name, DTYPE_F32, synth_f32(seed, name, norm_sigma, shape[0])
         elif q4:
-            yield name, DTYPE_Q4_0, synth_q4_0(seed, name, scale_sigma, shape[0], shape[1])
+            raw = synth_q4_0(seed, name, scale_sigma, shape[0], shape[1])
+            yield name, DTYPE_Q4_0, center_q4_0(raw) if centered else raw
         else:
             yield name, DTYPE_F32, synth_f32(seed, name, w_sigma, shape[0] * shape[1])
 
@@ -352,7 +371,6 @@ class GemmaModel:
             check(lib().gh_model_create(ctx.h, C.byref(cfg), C.byref(h)))
             handle = h
         self.h = handle
-        ctx._children.add(self)
         self.cfg = self.config()
 
     @classmethod
@@ -372,7 +390,11 @@ class GemmaModel:
         check(lib().gh_model_set_tensor(self.h, name.encode(), dtype, _ptr(a), a.nbytes))
 
     def synth(self, seed: int, q4: bool, w_sigma: float = 0.02, scale_sigma: float = 0.01,
-              norm_sigma: float = 0.02) -> None:
+              norm_sigma: float = 0.02, centered: bool = False) -> None:
+        if centered:
+            for name, dtype, arr in synth_tensors(self.cfg, seed, q4, w_sigma, scale_sigma, norm_sigma, True):
+                self.set_tensor(name, arr, dtype)
+            return
         check(lib().gh_synth_model(self.h, seed, int(q4), w_sigma, scale_sigma, norm_sigma))
 
     def check(self) -> None:
@@ -419,10 +441,14 @@ class KVCache:
     def reset(self) -> None:
         check(lib().gh_kv_reset(self.h))
 
+    def truncate(self, n: int) -> None:
+        """Rewind to the first n positions (gh_kv_truncate)."""
+        check(lib().gh_kv_truncate(self.h, int(n)))
+
     def close(self) -> None:
-        if self.h and self.model.h:
+        if self.h:
             lib().gh_kv_destroy(self.h)
-        self.h = None
+            self.h = None
 
     def __del__(self):
         try:

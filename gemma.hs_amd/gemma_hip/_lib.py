@@ -65,6 +65,10 @@ SIGNATURES = {
     "gh_device_count": (C.c_int, [_I32]),
     "gh_ctx_create": (C.c_int, [C.c_int, C.POINTER(_P)]),
     "gh_ctx_destroy": (C.c_int, [_P]),
+    "gh_ctx_release": (None, [_P]),
+    "gh_model_release": (None, [_P]),
+    "gh_kv_release": (None, [_P]),
+    "gh_q4_0_release": (None, [_P]),
     "gh_ctx_sync": (C.c_int, [_P]),
     "gh_buf_alloc": (C.c_int, [_P, C.c_size_t, C.POINTER(_P)]),
     "gh_buf_free": (C.c_int, [_P, _P]),
@@ -94,6 +98,7 @@ SIGNATURES = {
     "gh_kv_destroy": (C.c_int, [_P]),
     "gh_kv_reset": (C.c_int, [_P]),
     "gh_kv_length": (C.c_int, [_P, _I32]),
+    "gh_kv_truncate": (C.c_int, [_P, C.c_int32]),
     "gh_step": (C.c_int, [_P, _P, C.c_int32, _P, _P, _I32]),
     "gh_generate": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     "gh_prefill": (C.c_int, [_P, _P, _P, C.c_int32, _P, _P, _I32]),
@@ -113,6 +118,7 @@ SIGNATURES = {
     "gh_synth_f32": (C.c_int, [C.c_uint64, C.c_char_p, C.c_float, _P, C.c_size_t]),
     "gh_synth_q4_0": (C.c_int, [C.c_uint64, C.c_char_p, C.c_float, C.c_int64, C.c_int64, _P]),
     "gh_synth_tokens": (C.c_int, [C.c_uint64, C.c_char_p, C.c_int32, C.c_int32, _P]),
+    "gh_synth_kv": (C.c_int, [C.c_uint64, C.c_int32, C.c_int32, C.c_int32, C.c_float, _P, _P]),
     "gh_synth_model": (C.c_int, [_P, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_float]),
 }
 

@@ -1,32 +1,52 @@
-"""Single-kernel driver for hardware-counter runs.
+"""Hardware-counter driver and summariser for the step kernels.
 
-  python -m gemma_hip.kernel_profile [--kernel lm_head] [--reps 20] [--copy-mib 256]
-  python -m gemma_hip.kernel_profile --prefill 128 [--reps 5] [--copy-mib 256]
+Driver (run under rocprofv3 on the GPU box, eagerly: GH_NO_GRAPH=1):
 
-It builds the seeded gemma3-1b Q4_0 model and decodes a short prompt. Then it
-replays one step-kernel kind `reps` times at the cache's position
-(gh_time_kernel, the same launches bench.py times). With --prefill N it
-instead runs `reps` prefills of a seeded N-token prompt (gh_prefill, as
-bench.py's prefill extras do). Last, it copies a device buffer of
-`copy-mib` MiB once with hipMemcpy device-to-device.
+  python -m gemma_hip.kernel_profile run [--kernel all|KIND] [--config gemma3-1b] [--reps 20]
+                                         [--copy-mib 256] [--manifest FILE]
+  python -m gemma_hip.kernel_profile run --prefill 128 [--reps 5] [--copy-mib 256]
+  python -m gemma_hip.kernel_profile run --attention 32768 [--reps 20] [--copy-mib 256]
 
-That copy is the calibration kernel for byte counters: it reads and writes
-exactly copy-mib MiB, so FETCH_SIZE / WRITE_SIZE of the kernel under study
-scale by what the counters read for it.
+It builds the seeded model of the config and decodes a short prompt.  Then,
+for each step-kernel kind asked for, it launches a separator (two launches
+of the stream-read kernel over 4 KiB, a kernel that appears nowhere else)
+and replays that kind `reps` times at the cache's position (gh_time_kernel,
+the launches bench.py times).  Last comes one more separator and a
+device-to-device copy of `copy-mib` MiB: the calibration kernel for the
+byte counters, which reads and writes exactly that many bytes.  With
+--prefill N it instead runs `reps` prefills of a seeded N-token prompt;
+with --attention L, `reps` op-level attention decodes (4 q heads, 1 kv head,
+head_dim 256, global over L positions: the C4 case).  The manifest (JSON)
+lists the segments in order.
 
-The run is kept short and free of graph launches, so counter collection
-sees only plain kernel dispatches.
+Summariser (on any host, from rocprofv3's CSV output):
+
+  python -m gemma_hip.kernel_profile summarize --manifest FILE [--fetch DIR] [--write DIR] [--sq DIR]
+                                               [--trace DIR]
+
+It splits each run's dispatches at the separators, averages every counter
+over each segment's dispatches, scales FETCH_SIZE / WRITE_SIZE (KiB per
+dispatch) by the bytes / counter reading of the calibration copy, and
+prints a Markdown table per segment: HBM traffic against the algorithmic
+bytes, and the SQ counters (waves, wave cycles, busy cycles, wait cycles,
+VMEM / VALU / LDS instructions per wave).
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes as C
 import json
 import sys
+from collections import defaultdict
+from pathlib import Path
 
-from . import GemmaModel, KVCache, Context, STEP_KERNELS, bench_decode, prefill, preset, synth_tokens, time_kernel
+from . import (GemmaModel, KVCache, Context, STEP_KERNELS, attention_decode, bench_decode, prefill, preset,
+               stream_read_gbps, synth_tokens, time_kernel)
 
 HIP_MEMCPY_D2D = 3
+SEPARATOR = "k_stream_read"
+CALIBRATION = "__amd_rocclr_copyBuffer"
 
 
 def _hip():
@@ -56,39 +76,190 @@ def device_copy(n_bytes: int) -> None:
         hip.hipFree(dst)
 
 
-def main(argv=None) -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--kernel", default="lm_head", choices=STEP_KERNELS)
-    ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--copy-mib", type=int, default=256)
-    ap.add_argument("--prompt", type=int, default=8)
-    ap.add_argument("--prefill", type=int, default=0, help="time N-token prefills instead of a step kernel")
-    a = ap.parse_args(argv)
-    cfg = preset("gemma3-1b")
+def run(a) -> int:
+    cfg = preset(a.config)
     ctx = Context(0)
-    model = GemmaModel(ctx, cfg)
-    model.synth(1234, q4=True)
-    if a.prefill > 0:
-        toks = synth_tokens(1, "prefill", a.prefill, cfg.vocab)
-        kv = KVCache(model, a.prefill + 8)
-        ms = []
+    segments = []
+
+    def separator():
+        stream_read_gbps(ctx, 4096, 1)
+
+    if a.attention > 0:
+        import numpy as np
+        L, hd, nq, nkv = a.attention, 256, 4, 1
+        rng = np.random.default_rng(4)
+        q = rng.normal(size=nq * hd).astype(np.float32)
+        k = rng.normal(size=L * nkv * hd).astype(np.float32)
+        v = rng.normal(size=L * nkv * hd).astype(np.float32)
+        separator()
         for _ in range(a.reps):
-            kv.reset()
-            ctx.timer_start()
-            prefill(model, kv, toks, want_logits=False)
-            ms.append(ctx.timer_stop())
-        device_copy(a.copy_mib << 20)
-        print(json.dumps({"prefill_tokens": a.prefill, "reps": a.reps, "ms": [round(x, 4) for x in ms],
-                          "copy_bytes": a.copy_mib << 20}), flush=True)
-        return 0
-    kv = KVCache(model, a.prompt + 8)
-    bench_decode(model, kv, synth_tokens(1, "prompt", a.prompt, cfg.vocab), 0, 1)
-    t = time_kernel(model, kv, a.kernel, a.reps)
+            attention_decode(ctx, q, k, v, nq, nkv, hd, 0, L)
+        segments.append({"name": f"attention_c4_L{L}", "reps": a.reps,
+                         "bytes_per_launch": 2 * L * nkv * hd * 4 + 8 * nq * hd})
+    else:
+        model = GemmaModel(ctx, cfg)
+        model.synth(1234, q4=True)
+        if a.prefill > 0:
+            toks = synth_tokens(1, "prefill", a.prefill, cfg.vocab)
+            kv = KVCache(model, a.prefill + 8)
+            separator()
+            for _ in range(a.reps):
+                kv.reset()
+                prefill(model, kv, toks, want_logits=False)
+            segments.append({"name": f"prefill_{a.prefill}", "reps": a.reps})
+        else:
+            kv = KVCache(model, a.prompt + 8)
+            bench_decode(model, kv, synth_tokens(1, "prompt", a.prompt, cfg.vocab), 0, 1)
+            kinds = STEP_KERNELS if a.kernel == "all" else (a.kernel,)
+            for kind in kinds:
+                separator()
+                t = time_kernel(model, kv, kind, a.reps)
+                segments.append({"name": kind, "reps": a.reps, "launches_per_step": t.launches_per_step,
+                                 "bytes_per_launch": int(t.bytes_per_launch), "event_avg_us": round(t.avg_us, 3)})
+    separator()
     device_copy(a.copy_mib << 20)
-    print(json.dumps({"kernel": t.name, "reps": a.reps, "avg_us": round(t.avg_us, 3),
-                      "bytes_per_launch": int(t.bytes_per_launch), "gbps": round(t.gbps, 1),
-                      "copy_bytes": a.copy_mib << 20}), flush=True)
+    man = {"config": a.config, "position": a.prompt if a.prefill == 0 and a.attention == 0 else None,
+           "copy_bytes": a.copy_mib << 20, "segments": segments}
+    if a.manifest:
+        Path(a.manifest).write_text(json.dumps(man, indent=1))
+    print(json.dumps(man), flush=True)
     return 0
+
+
+def _dispatches(d: Path):
+    """{dispatch id: (kernel name, {counter: value}, duration ns)} of a rocprofv3 CSV directory."""
+    files = list(d.glob("**/*counter_collection.csv"))
+    out = {}
+    if files:
+        for row in csv.DictReader(open(files[0])):
+            i = int(row["Dispatch_Id"])
+            name, ctrs, dur = out.get(i, (row["Kernel_Name"], {}, 0))
+            ctrs[row["Counter_Name"]] = ctrs.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+            dur = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+            out[i] = (name, ctrs, dur)
+        return out
+    files = list(d.glob("**/*kernel_trace.csv"))
+    for row in csv.DictReader(open(files[0])):
+        i = int(row["Dispatch_Id"])
+        out[i] = (row["Kernel_Name"], {}, int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    return out
+
+
+def _segments(disp, n_seg):
+    """Split dispatches at separator launches: [(kernel dispatches of segment k)], calibration copies."""
+    order = sorted(disp)
+    groups, cur, seen_sep = [], None, False
+    for i in order:
+        name = disp[i][0]
+        if name.startswith(SEPARATOR) or SEPARATOR in name:
+            if not seen_sep or cur:
+                cur = []
+                groups.append(cur)
+            seen_sep = True
+            continue
+        if cur is not None:
+            cur.append(i)
+    segs = groups[:n_seg]
+    tail = groups[n_seg] if len(groups) > n_seg else []
+    cal = [i for i in tail if CALIBRATION in disp[i][0]]
+    return segs, cal
+
+
+def summarize(a) -> int:
+    man = json.loads(Path(a.manifest).read_text())
+    n = len(man["segments"])
+    rows = defaultdict(dict)
+    factors = {}
+    for label, d in (("fetch", a.fetch), ("write", a.write), ("sq", a.sq), ("trace", a.trace)):
+        if not d:
+            continue
+        disp = _dispatches(Path(d))
+        segs, cal = _segments(disp, n)
+        for k, seg in enumerate(segs):
+            if not seg:
+                continue
+            r = rows[man["segments"][k]["name"]]
+            ctr_sum = defaultdict(float)
+            for i in seg:
+                for c, v in disp[i][1].items():
+                    ctr_sum[c] += v
+            r.setdefault("dispatches", len(seg))
+            r.setdefault("kernels", sorted({disp[i][0].split("(")[0] for i in seg}))
+            for c, v in ctr_sum.items():
+                r[c] = v / len(seg)
+            if label == "trace":
+                r["trace_avg_us"] = sum(disp[i][2] for i in seg) / len(seg) / 1e3
+        for c in ("FETCH_SIZE", "WRITE_SIZE"):
+            vals = [disp[i][1][c] for i in cal if c in disp[i][1]]
+            if vals:
+                factors[c] = man["copy_bytes"] / max(vals)
+    print(f"Calibration: {man['copy_bytes']} B device copy; bytes per counter unit: "
+          + ", ".join(f"{c} {f:.5f}" for c, f in factors.items()))
+    print()
+    print("| segment | dispatches | algorithmic B / launch | FETCH B / launch | WRITE B / launch | traffic / algorithmic |")
+    print("|---|---|---|---|---|---|")
+    for s in man["segments"]:
+        r = rows.get(s["name"], {})
+        per = s.get("launches_per_step", 1)
+        algo = s.get("bytes_per_launch")
+        fb = r["FETCH_SIZE"] * factors["FETCH_SIZE"] if "FETCH_SIZE" in r and "FETCH_SIZE" in factors else None
+        wb = r["WRITE_SIZE"] * factors["WRITE_SIZE"] if "WRITE_SIZE" in r and "WRITE_SIZE" in factors else None
+        ratio = (fb + wb) / algo if fb is not None and wb is not None and algo else None
+        f = lambda x: f"{x:,.0f}" if x is not None else "-"
+        print(f"| {s['name']} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | "
+              f"{ratio:.3f} |" if ratio is not None else
+              f"| {s['name']} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | - |")
+        del per
+    sq = [c for c in ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_INSTS_VMEM_RD",
+                      "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_ACTIVE_INST_VALU") if any(c in r for r in rows.values())]
+    if sq:
+        print()
+        print("| segment | " + " | ".join(sq) + " | wait / wave cycles | VALU / wave | VMEM rd / wave |")
+        print("|---|" + "---|" * (len(sq) + 3))
+        for s in man["segments"]:
+            r = rows.get(s["name"], {})
+            waves = r.get("SQ_WAVES") or 1.0
+            cells = [f"{r.get(c, 0):,.0f}" for c in sq]
+            wait = r.get("SQ_WAIT_INST_ANY", 0) / max(r.get("SQ_WAVE_CYCLES", 0), 1)
+            print(f"| {s['name']} | " + " | ".join(cells) +
+                  f" | {wait:.3f} | {r.get('SQ_INSTS_VALU', 0) / waves:.1f} | {r.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} |")
+    if any("trace_avg_us" in r for r in rows.values()):
+        print()
+        print("| segment | kernels | traced avg us / dispatch | algorithmic GB/s | of 8 TB/s |")
+        print("|---|---|---|---|---|")
+        for s in man["segments"]:
+            r = rows.get(s["name"], {})
+            if "trace_avg_us" not in r:
+                continue
+            us = r["trace_avg_us"]
+            algo = s.get("bytes_per_launch")
+            gbps = algo / (us * 1e3) if algo else None
+            print(f"| {s['name']} | {', '.join(r['kernels'])} | {us:.3f} | "
+                  + (f"{gbps:.0f} | {gbps / 8000:.3f} |" if gbps else "- | - |"))
+    return 0
+
+
+def main(argv=None) -> int:
+    argv = list(sys.argv[1:] if argv is None else argv)
+    if not argv or argv[0] not in ("run", "summarize"):
+        argv = ["run", *argv]
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd")
+    r = sub.add_parser("run")
+    r.add_argument("--kernel", default="all", choices=("all",) + STEP_KERNELS)
+    r.add_argument("--config", default="gemma3-1b")
+    r.add_argument("--reps", type=int, default=20)
+    r.add_argument("--copy-mib", type=int, default=256)
+    r.add_argument("--prompt", type=int, default=8)
+    r.add_argument("--prefill", type=int, default=0, help="time N-token prefills instead of step kernels")
+    r.add_argument("--attention", type=int, default=0, help="op-level C4 attention over L positions")
+    r.add_argument("--manifest", default="")
+    s = sub.add_parser("summarize")
+    s.add_argument("--manifest", required=True)
+    for k in ("fetch", "write", "sq", "trace"):
+        s.add_argument(f"--{k}", default="")
+    a = ap.parse_args(argv)
+    return run(a) if a.cmd == "run" else summarize(a)
 
 
 if __name__ == "__main__":

@@ -11,6 +11,14 @@
  *    caches, gh_q4 tensors and gh_buf_alloc buffers).
  *  - One HIP stream per context; calls on one context are serialised by a
  *    mutex, so a Haskell RTS running with -N may call from any thread.
+ *  - Handles (gh_ctx, gh_model, gh_kv, gh_q4) may be destroyed in any
+ *    order, as garbage-collector finalisers run them: destroying a context
+ *    or model that still has open handles made from it only releases it,
+ *    and the library frees it with the last of them.  A call on a handle
+ *    already destroyed returns GH_ERR_STATE without touching its memory
+ *    (unless the address was since reused by a new handle).  The
+ *    gh_*_release functions are void-typed destroys for finalisers
+ *    (Foreign.ForeignPtr's FinalizerPtr).
  *  - Plain C types only: no HIP or torch types cross this boundary.
  *
  * Each declaration names the reference interface it replaces
@@ -67,6 +75,7 @@ int gh_ctx_create(int device, gh_ctx** out);
 /* Also destroys the models (with their KV caches) and Q4_0 tensors still
  * open on the context: their handles are invalid afterwards. */
 int gh_ctx_destroy(gh_ctx* ctx);
+void gh_ctx_release(gh_ctx* ctx); /* gh_ctx_destroy for finalisers */
 /* waitAll (src/Gemma/Model.hs:1432) */
 int gh_ctx_sync(gh_ctx* ctx);
 /* Event timer on the context stream (replaces the wall-clock timing of
@@ -103,6 +112,7 @@ typedef struct gh_q4 gh_q4;
  * the device tile layout; dequantised values are bit-identical. */
 int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_t cols, int flags, gh_q4** out);
 int gh_q4_0_free(gh_q4* t);
+void gh_q4_0_release(gh_q4* t); /* gh_q4_0_free for finalisers */
 /* out_dev: rows*cols f32, row-major (loadQ4_0Tensor's result). */
 int gh_q4_0_dequant(gh_q4* t, float* out_dev);
 /* y_dev[rows] = W x_dev[cols]; softcap != 0 applies cap*tanh(y/cap). */
@@ -164,6 +174,7 @@ int gh_config_preset(const char* name, gh_config* out);
 typedef struct gh_model gh_model;
 int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out);
 int gh_model_destroy(gh_model* m);
+void gh_model_release(gh_model* m); /* gh_model_destroy for finalisers */
 /* name: GGUF tensor name (token_embd.weight, output_norm.weight,
  * blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_q_norm,attn_k_norm,
  * attn_output,post_attention_norm,ffn_norm,ffn_gate,ffn_up,ffn_down,
@@ -188,12 +199,19 @@ int gh_gguf_inspect(const char* path, gh_config* out);
 typedef struct gh_kv gh_kv;
 int gh_kv_create(gh_model* m, int32_t max_seq, gh_kv** out);
 int gh_kv_destroy(gh_kv* kv);
+void gh_kv_release(gh_kv* kv); /* gh_kv_destroy for finalisers */
 int gh_kv_reset(gh_kv* kv);
 int gh_kv_length(gh_kv* kv, int32_t* len_out);
+/* Rewind to the first n positions (0 <= n <= length; GH_ERR_RANGE
+ * otherwise): the next step runs at position n.  The reference's KVCache
+ * is a persistent value whose layer-0 cacheLen is the next position
+ * (src/Gemma/Model.hs:1332-1334, src/Gemma/KVCache.hs:146-147), so stepping
+ * an older cache value continues from its own length. */
+int gh_kv_truncate(gh_kv* kv, int32_t n);
 /* Benchmark set-up with no reference counterpart: fill positions
  * [0, n_pos) of every layer's K and V with seeded N(0, sigma) values
- * (counter-based generator on the device) and set the cache length to
- * n_pos, standing in for a prefilled context. */
+ * (gh_synth_kv, generated on the host and uploaded) and set the cache
+ * length to n_pos, standing in for a prefilled context. */
 int gh_kv_synth(gh_kv* kv, uint64_t seed, int32_t n_pos, float sigma);
 /* Sampling of the next token for this cache's steps: temperature 0 is
  * greedy (the reference's sampleToken / sampleWithTemperature, which is an
@@ -292,6 +310,11 @@ int gh_synth_f32(uint64_t seed, const char* name, float sigma, float* out, size_
  * rounded to fp16 (round to nearest even). */
 int gh_synth_q4_0(uint64_t seed, const char* name, float scale_sigma, int64_t rows, int64_t cols,
                   uint8_t* out);
+/* K and V rows of one layer of gh_kv_synth: positions [0, n_pos), `width`
+ * (= n_kv_heads * head_dim) N(0, sigma) values per position each, one
+ * stream per (layer, K or V, position); k_out / v_out [n_pos * width]. */
+int gh_synth_kv(uint64_t seed, int32_t layer, int32_t n_pos, int32_t width, float sigma, float* k_out,
+                float* v_out);
 /* token ids uniform in [0, vocab) */
 int gh_synth_tokens(uint64_t seed, const char* name, int32_t n, int32_t vocab, int32_t* out);
 /* Populate every tensor of `m` from the seed (Q4_0 projections and

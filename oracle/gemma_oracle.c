@@ -25,8 +25,11 @@
  *       fp64, and the golden gelu_output within the +-2e-4 bound the
  *       reference itself allows (the fixture is erf-GELU) -- pinned.
  *   orc_argmax                          : numpy.argmax (first max) -- pinned.
- *   orc_softcap                         : parity unpinned (the reference's
- *       runMatmulQ4_0DSL body is absent; Gemma-2 form cap*tanh(y/cap)).
+ *   orc_softcap                         : the reference's runMatmulQ4_0DSL
+ *       body is absent, so the Gemma-2 form cap*tanh(y/cap) is pinned by the
+ *       properties that fix it: odd, |f| < cap and |f(y)| <= |y|, the Taylor
+ *       terms y - y^3/(3cap^2) at 0, saturation at +-cap, monotone, and
+ *       f(cap*atanh(1/2)) = cap/2; planted wrong forms fail them -- pinned.
  *   orc_philox4x32_10                   : the published Random123
  *       known-answer vectors for philox4x32-10 -- pinned.
  *   orc_sample                          : inversion sampling; pinned by the
@@ -296,7 +299,8 @@ int32_t orc_argmax(const float* v, int n) {
 }
 
 /* Gemma-2 style soft-cap cap*tanh(y/cap); the runLinearQ4 flag
- * (src/Gemma/Layers/LinearQ4.hs:41-48).  Parity unpinned. */
+ * (src/Gemma/Layers/LinearQ4.hs:37-48).  Pinned by its invariants (see the
+ * header comment). */
 void orc_softcap(float* y, int n, float cap) {
     for (int i = 0; i < n; ++i) y[i] = cap * tanhf(y[i] / cap);
 }
@@ -373,6 +377,15 @@ void orc_model_reset(orc_model* m) {
     size_t kv = (size_t)m->c.n_layers * m->c.max_seq * m->c.n_kv_heads * m->c.head_dim;
     memset(m->kc, 0, kv * sizeof(float));
     memset(m->vc, 0, kv * sizeof(float));
+}
+
+int orc_model_set_kv(orc_model* m, int layer, int n_pos, const float* k, const float* v) {
+    const orc_config* c = &m->c;
+    if (layer < 0 || layer >= c->n_layers || n_pos < 0 || n_pos > c->max_seq) return -1;
+    const size_t row = (size_t)c->n_kv_heads * c->head_dim, kv_layer = (size_t)c->max_seq * row;
+    memcpy(m->kc + layer * kv_layer, k, sizeof(float) * row * n_pos);
+    memcpy(m->vc + layer * kv_layer, v, sizeof(float) * row * n_pos);
+    return 0;
 }
 
 int orc_model_set_tensor(orc_model* m, const char* name, int dtype, const void* data, size_t nbytes) {

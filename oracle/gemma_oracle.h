@@ -82,6 +82,9 @@ void orc_model_destroy(orc_model* m);
 /* name: GGUF tensor name (token_embd.weight, blk.N.attn_q.weight, ...) */
 int orc_model_set_tensor(orc_model* m, const char* name, int dtype, const void* data, size_t nbytes);
 void orc_model_reset(orc_model* m);
+/* Positions [0, n_pos) of layer `layer`'s K and V cache ([n_pos][nkv*hd]
+ * each): a prefilled context (the checker's copy of gh_kv_synth). */
+int orc_model_set_kv(orc_model* m, int layer, int n_pos, const float* k, const float* v);
 /* One decode step at position pos (= current cache length).  logits [vocab]
  * and layer_out [n_layers*hidden] may be NULL.  Returns argmax or <0. */
 int orc_step(orc_model* m, int32_t token, int32_t pos, float* logits, float* layer_out);

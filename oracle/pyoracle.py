@@ -48,6 +48,7 @@ _SIG = {
     "orc_model_destroy": (None, [_P]),
     "orc_model_set_tensor": (C.c_int, [_P, C.c_char_p, C.c_int, _P, C.c_size_t]),
     "orc_model_reset": (None, [_P]),
+    "orc_model_set_kv": (C.c_int, [_P, C.c_int, C.c_int, _P, _P]),
     "orc_step": (C.c_int, [_P, C.c_int32, C.c_int32, _P, _P]),
     "orc_generate": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P]),
     "orc_set_threads": (None, [C.c_int]),
@@ -200,6 +201,13 @@ class OracleModel:
 
     def reset(self) -> None:
         lib().orc_model_reset(self.h)
+
+    def set_kv(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
+        """Positions [0, len(k)) of a layer's K/V cache ([n_pos, nkv*hd] each)."""
+        k, v = f32(k), f32(v)
+        rc = lib().orc_model_set_kv(self.h, layer, k.shape[0], _p(k), _p(v))
+        if rc != 0:
+            raise ValueError(f"oracle set_kv({layer}) -> {rc}")
 
     def step(self, token: int, pos: int, want_layers: bool = False):
         c = self.cfg

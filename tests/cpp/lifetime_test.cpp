@@ -1,0 +1,117 @@
+// Lifetime checks of libgemma_hip's C ABI on the CPU, linked against
+// hip_stub.cpp / kernel_stub.cpp and built with AddressSanitizer by
+// tests/test_lifetime.py.
+//
+//   lifetime_test          every destroy order of context, model, cache and
+//                          Q4_0 tensor is free of use-after-free and leaks;
+//                          a model and its cache keep working after their
+//                          context's destroy; a second destroy, or a call on
+//                          a destroyed or never-created handle, is
+//                          GH_ERR_STATE
+//   lifetime_test exit     only the order in which Python finalisers ran at
+//                          interpreter exit when a model outlived its
+//                          context (context first, then model, then cache)
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "gemma_hip.h"
+
+#define CHECK(c)                                                                                   \
+    do {                                                                                           \
+        if (!(c)) {                                                                                \
+            std::fprintf(stderr, "FAIL %s:%d: %s (last error: %s)\n", __FILE__, __LINE__, #c,     \
+                         gh_last_error());                                                         \
+            return 1;                                                                              \
+        }                                                                                          \
+    } while (0)
+
+namespace {
+
+struct Handles {
+    gh_ctx* ctx = nullptr;
+    gh_model* m = nullptr;
+    gh_kv* kv = nullptr;
+    gh_q4* t = nullptr;
+};
+
+int make(Handles& h) {
+    CHECK(gh_ctx_create(0, &h.ctx) == GH_OK);
+    gh_config c;
+    CHECK(gh_config_preset("tiny", &c) == GH_OK);
+    CHECK(gh_model_create(h.ctx, &c, &h.m) == GH_OK);
+    CHECK(gh_synth_model(h.m, 7, 1, 0.02f, 0.01f, 0.02f) == GH_OK);
+    CHECK(gh_kv_create(h.m, 16, &h.kv) == GH_OK);
+    std::vector<uint8_t> raw(64 * 18, 0);
+    CHECK(gh_q4_0_upload(h.ctx, raw.data(), 64, 32, 0, &h.t) == GH_OK);
+    int32_t next = -1;
+    CHECK(gh_step(h.m, h.kv, 3, nullptr, nullptr, &next) == GH_OK);
+    return 0;
+}
+
+int destroy(Handles& h, char what) {
+    switch (what) {
+        case 'c': return gh_ctx_destroy(h.ctx);
+        case 'm': return gh_model_destroy(h.m);
+        case 'k': return gh_kv_destroy(h.kv);
+        default: return gh_q4_0_free(h.t);
+    }
+}
+
+int any_order() {
+    const char* orders[] = {"cmkt", "ckmt", "mckt", "mkct", "kcmt", "kmct", "tcmk", "ctkm"};
+    for (const char* order : orders) {
+        Handles h;
+        if (make(h)) return 1;
+        for (const char* p = order; *p; ++p) {
+            CHECK(destroy(h, *p) == GH_OK);
+            const bool model_open = !std::strchr(order, 'm') || std::strchr(p + 1, 'm');
+            const bool kv_open = std::strchr(p + 1, 'k') != nullptr;
+            if (*p == 'c' && model_open && kv_open) {
+                // the context is released, not freed: its model still steps
+                int32_t next = -1;
+                CHECK(gh_step(h.m, h.kv, 5, nullptr, nullptr, &next) == GH_OK);
+            }
+            if (*p == 'm' && kv_open) {
+                int32_t next = -1;
+                CHECK(gh_step(h.m, h.kv, 5, nullptr, nullptr, &next) == GH_ERR_STATE);
+                int32_t len = -1;
+                CHECK(gh_kv_length(h.kv, &len) == GH_OK && len >= 1);
+            }
+        }
+        for (char w : {'c', 'm', 'k', 't'}) CHECK(destroy(h, w) == GH_ERR_STATE);
+    }
+    // handles that were never returned by the library
+    int local = 0;
+    CHECK(gh_model_destroy(reinterpret_cast<gh_model*>(&local)) == GH_ERR_STATE);
+    CHECK(gh_kv_length(reinterpret_cast<gh_kv*>(&local), &local) == GH_ERR_STATE);
+    CHECK(gh_ctx_sync(reinterpret_cast<gh_ctx*>(&local)) == GH_ERR_STATE);
+    // a handle of the wrong kind
+    Handles h;
+    if (make(h)) return 1;
+    CHECK(gh_kv_destroy(reinterpret_cast<gh_kv*>(h.m)) == GH_ERR_STATE);
+    gh_kv_release(h.kv);
+    gh_model_release(h.m);
+    gh_q4_0_release(h.t);
+    gh_ctx_release(h.ctx);
+    gh_ctx_release(h.ctx);  // void: a second release is ignored
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc > 1 && std::strcmp(argv[1], "exit") == 0) {
+        Handles h;
+        if (make(h)) return 1;
+        gh_q4_0_free(h.t);
+        gh_ctx_destroy(h.ctx);
+        gh_model_destroy(h.m);
+        gh_kv_destroy(h.kv);
+        std::printf("exit order ok\n");
+        return 0;
+    }
+    if (any_order()) return 1;
+    std::printf("lifetime ok\n");
+    return 0;
+}

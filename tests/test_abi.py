@@ -170,3 +170,168 @@ def test_cpp_host_api_header_compiles_and_test_library_exports_its_entry(tmp_pat
     import ctypes
     t = ctypes.CDLL(str(REPO / "tests" / "cpp" / "libhost_api_test.so"))
     assert hasattr(t, "gh_host_api_tests")
+
+
+# ---------------------------------------------------------------- GGUF fuzzing
+_FUZZ_DRIVER = r"""
+import ctypes as C, sys, numpy as np
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import gemma_hip as gh
+path, n = sys.argv[3], int(sys.argv[4])
+base = open(path, 'rb').read()
+rng = np.random.default_rng(int(sys.argv[5]))
+codes = {}
+def inspect(blob):
+    with open(path + '.m', 'wb') as f:
+        f.write(blob)
+    c = gh.GemmaConfig()
+    rc = gh.lib().gh_gguf_inspect((path + '.m').encode(), C.byref(c))
+    codes[rc] = codes.get(rc, 0) + 1
+    return rc
+# every truncation point of the header, metadata and tensor infos, then some in the data
+hdr = int(sys.argv[6])
+for cut in list(range(0, hdr + 40)) + list(range(hdr, len(base), max(1, (len(base) - hdr) // 64))):
+    rc = inspect(base[:cut])
+    assert rc != 0 or cut >= len(base), cut
+# random corruption of bytes in the first 2 KB (1 to 8 bytes per trial)
+for _ in range(n):
+    b = bytearray(base)
+    for _ in range(int(rng.integers(1, 9))):
+        i = int(rng.integers(0, min(len(b), 2048)))
+        b[i] = int(rng.integers(0, 256))
+    inspect(bytes(b))
+print(sorted(codes.items()))
+"""
+
+
+def _gguf_header_len(path) -> int:
+    """Offset of the data section of a GGUF file written by write_gguf."""
+    b = open(path, "rb").read()
+    import struct
+    n_t, n_kv = struct.unpack_from("<QQ", b, 8)
+    off = 24
+
+    def s(o):
+        (k,) = struct.unpack_from("<Q", b, o)
+        return o + 8 + k
+    for _ in range(n_kv):
+        off = s(off)
+        (t,) = struct.unpack_from("<I", b, off)
+        off += 4
+        if t == 8:
+            off = s(off)
+        elif t == 9:
+            et, cnt = struct.unpack_from("<IQ", b, off)
+            off += 12
+            for _ in range(cnt):
+                off = s(off)
+        else:
+            off += 4
+    for _ in range(n_t):
+        off = s(off)
+        (nd,) = struct.unpack_from("<I", b, off)
+        off += 4 + 8 * nd + 4 + 8
+    return off
+
+
+def test_gguf_parser_survives_truncation_and_corruption(tmp_path):
+    """Every truncation of the header/metadata/tensor-info region, and 400
+    seeded random corruptions of the first 2 KB, return an error code or a
+    config -- never a crash (run in a child process, so a crash fails the
+    test instead of the session)."""
+    import subprocess
+    import sys
+    cfg = gh.preset("tiny")
+    cfg.n_layers = 1
+    p = tmp_path / "tiny.gguf"
+    synth_gguf(p, cfg, 3, q4=True)
+    hdr = _gguf_header_len(p)
+    r = subprocess.run([sys.executable, "-c", _FUZZ_DRIVER, str(REPO / "gemma.hs_amd"), str(REPO / "oracle"),
+                        str(p), "400", "7", str(hdr)], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+
+
+def _raw_gguf(meta: bytes, n_kv: int, tinfo: bytes, n_t: int, data: bytes = b"") -> bytes:
+    import struct
+    b = struct.pack("<IIQQ", 0x46554747, 3, n_t, n_kv) + meta + tinfo
+    b += b"\0" * ((-len(b)) % 32)
+    return b + data
+
+
+def _kv_u32(key: str, v: int) -> bytes:
+    import struct
+    k = key.encode()
+    return struct.pack("<Q", len(k)) + k + struct.pack("<II", 4, v)
+
+
+def _tensor(name: str, dims, ggml_type: int, offset: int) -> bytes:
+    import struct
+    n = name.encode()
+    return (struct.pack("<Q", len(n)) + n + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+            + struct.pack("<IQ", ggml_type, offset))
+
+
+def _gemma_meta_bytes():
+    cfg = gh.preset("tiny")
+    keys = {"gemma3.block_count": 1, "gemma3.embedding_length": cfg.hidden, "gemma3.feed_forward_length": cfg.ffn,
+            "gemma3.attention.head_count": 4, "gemma3.attention.head_count_kv": 1,
+            "gemma3.attention.key_length": 32}
+    import struct
+    b = b"".join(_kv_u32(k, v) for k, v in keys.items())
+    k = b"gemma3.rope.freq_base"
+    b += struct.pack("<Q", len(k)) + k + struct.pack("<If", 6, 10000.0)
+    return b, len(keys) + 1
+
+
+@pytest.mark.parametrize("case", ["huge_string", "array_count_overflow", "huge_offset", "offset_plus_size_wraps",
+                                  "dims_product_overflows", "q4_row_not_block_multiple", "bad_alignment",
+                                  "huge_alignment", "count_not_integer", "negative_count", "tensor_past_end"])
+def test_gguf_malformed_sizes_are_format_errors(tmp_path, case):
+    """Sizes and offsets taken from the file that would wrap a 64-bit bound
+    check, or exceed the file, are GH_ERR_FORMAT (src/Gemma/GGUF.hs:186-239
+    reads with bounds-checked ByteString slices)."""
+    import struct
+    meta, n_kv = _gemma_meta_bytes()
+    H, V = 128, 1024
+    emb_bytes = V * H // 32 * 18
+    tinfo = _tensor("token_embd.weight", [H, V], 2, 0)
+    n_t = 1
+    data = b"\0" * emb_bytes
+    if case == "huge_string":
+        meta += struct.pack("<Q", 0xFFFFFFFFFFFFFFF0) + b"x"
+        n_kv += 1
+    elif case == "array_count_overflow":
+        k = b"x.arr"
+        meta += struct.pack("<Q", len(k)) + k + struct.pack("<IIQ", 9, 12, 0x2000000000000001)
+        n_kv += 1
+    elif case == "huge_offset":
+        tinfo = _tensor("token_embd.weight", [H, V], 2, 0xFFFFFFFFFFFFFF00)
+    elif case == "offset_plus_size_wraps":
+        tinfo += _tensor("blk.0.attn_norm.weight", [1 << 40, 1 << 8], 0, 0xFFFFFFFFFFFF0000)
+        n_t += 1
+    elif case == "dims_product_overflows":
+        tinfo += _tensor("blk.0.attn_q.weight", [1 << 33, 1 << 33, 1 << 33], 2, 0)
+        n_t += 1
+    elif case == "q4_row_not_block_multiple":
+        tinfo += _tensor("blk.0.attn_q.weight", [48, 64], 2, 0)  # 3072 weights, rows of 48
+        n_t += 1
+    elif case == "bad_alignment":
+        meta += _kv_u32("general.alignment", 3)
+        n_kv += 1
+    elif case == "huge_alignment":
+        k = b"general.alignment"
+        meta += struct.pack("<Q", len(k)) + k + struct.pack("<IQ", 10, 1 << 62)
+        n_kv += 1
+    elif case == "count_not_integer":
+        k = b"gemma3.block_count"
+        meta = meta.replace(_kv_u32("gemma3.block_count", 1), struct.pack("<Q", len(k)) + k + struct.pack("<If", 6, 1.5))
+    elif case == "negative_count":
+        k = b"gemma3.attention.head_count"
+        meta = meta.replace(_kv_u32("gemma3.attention.head_count", 4), struct.pack("<Q", len(k)) + k + struct.pack("<Ii", 5, -4))
+    elif case == "tensor_past_end":
+        data = data[:-1]
+    p = tmp_path / f"{case}.gguf"
+    p.write_bytes(_raw_gguf(meta, n_kv, tinfo, n_t, data))
+    with pytest.raises(gh.GemmaHipError) as e:
+        _inspect(p)
+    assert e.value.name == "GH_ERR_FORMAT", (case, str(e.value))

@@ -1,0 +1,62 @@
+"""Handle lifetimes of the C ABI, on the CPU.
+
+libgemma_hip's host code (model.cpp, gguf.cpp, repack.cpp, synth.cpp) is
+built with g++ and AddressSanitizer against a host-only stand-in for the
+HIP runtime (tests/cpp/hip_stub.cpp: streams, events and graphs are heap
+objects each call dereferences) and no-op kernel launchers
+(tests/cpp/kernel_stub.cpp), then driven by tests/cpp/lifetime_test.cpp:
+every destroy order of context, model, cache and Q4_0 tensor must be free
+of use-after-free and leaks (finalisers run in any order:
+src/Gemma/KVCache.hs:20-35 handles under a -threaded RTS, gemma.cabal:102),
+and a second destroy is GH_ERR_STATE.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+
+import pytest
+
+from conftest import REPO
+
+CSRC = REPO / "gemma.hs_amd" / "csrc"
+CPP = REPO / "tests" / "cpp"
+
+
+def build_lifetime_test(out_dir, sources=None):
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    srcs = sources or [CSRC / f for f in ("model.cpp", "gguf.cpp", "repack.cpp", "synth.cpp")]
+    exe = out_dir / "lifetime_test"
+    cmd = [gxx, "-std=c++17", "-g", "-O1", "-fsanitize=address", "-fno-omit-frame-pointer",
+           "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", f"-I{REPO / 'include'}",
+           *map(str, srcs), str(CPP / "hip_stub.cpp"), str(CPP / "kernel_stub.cpp"),
+           str(CPP / "lifetime_test.cpp"), "-o", str(exe), "-lpthread"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    return exe
+
+
+@pytest.fixture(scope="module")
+def lifetime_exe(tmp_path_factory):
+    return build_lifetime_test(tmp_path_factory.mktemp("lifetime"))
+
+
+def _run(exe, *args):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:exitcode=23")
+    env.pop("LD_PRELOAD", None)
+    return subprocess.run([str(exe), *args], capture_output=True, text=True, env=env, timeout=300)
+
+
+def test_handles_destroyed_in_any_order_are_clean_under_asan(lifetime_exe):
+    r = _run(lifetime_exe)
+    assert r.returncode == 0 and "lifetime ok" in r.stdout, r.stdout + r.stderr[-4000:]
+
+
+def test_interpreter_exit_finaliser_order_is_clean_under_asan(lifetime_exe):
+    """Context destroyed first, then the model, then its cache: the order
+    that, before handles were reference counted, read the freed context."""
+    r = _run(lifetime_exe, "exit")
+    assert r.returncode == 0 and "exit order ok" in r.stdout, r.stdout + r.stderr[-4000:]

@@ -251,9 +251,65 @@ def test_sampler_closed_forms_and_frequencies():
     assert np.max(np.abs(freq - p)) < 0.015
 
 
-def test_softcap_form():
-    y = np.array([0.0, 10.0, -100.0, 1000.0], np.float32)
-    np.testing.assert_allclose(orc.softcap(y, 30.0), 30.0 * np.tanh(y.astype(np.float64) / 30.0), rtol=1e-6)
+def _softcap_violations(f, cap: float) -> list[str]:
+    """Properties that fix a soft cap sigma * tanh(y / sigma) without
+    restating it (the body of runMatmulQ4_0DSL, which
+    src/Gemma/Layers/LinearQ4.hs:37-48 names, is absent from the reference):
+      odd               f(-y) = -f(y)
+      bounded           |f(y)| < cap and |f(y)| <= |y|
+      unit slope at 0   f(y) = y - y^3 / (3 cap^2) + O(y^5)  (slope and cubic term)
+      saturates         f(y) -> +-cap as y -> +-inf, monotone in between
+      known point       f(cap * atanh(1/2)) = cap / 2
+    Returns the names of the violated properties."""
+    bad = []
+    y = np.linspace(-8 * cap, 8 * cap, 4097).astype(np.float32)
+    fy = np.asarray(f(y.copy(), cap), np.float64)
+    fneg = np.asarray(f((-y).copy(), cap), np.float64)
+    if np.max(np.abs(fy + fneg)) > 1e-6 * cap:
+        bad.append("odd")
+    if np.any(np.abs(fy) > cap * (1 + 1e-6)) or np.any(np.abs(fy) > np.abs(y) * (1 + 1e-6) + 1e-30):
+        bad.append("bounded")
+    small = np.array([1e-3, 1e-2, 3e-2, 0.1], np.float64) * cap
+    fs = np.asarray(f(small.astype(np.float32), cap), np.float64)
+    ys = small.astype(np.float32).astype(np.float64)
+    taylor = ys - ys ** 3 / (3 * cap * cap)
+    # 5th-order remainder 2 y^5 / (15 cap^4) plus f32 rounding
+    if np.any(np.abs(fs - taylor) > 2 * ys ** 5 / (15 * cap ** 4) + 4e-7 * ys):
+        bad.append("taylor")
+    big = np.asarray(f(np.array([50 * cap, -50 * cap, 1e30], np.float32), cap), np.float64)
+    if abs(big[0] - cap) > 1e-6 * cap or abs(big[1] + cap) > 1e-6 * cap or abs(big[2] - cap) > 1e-6 * cap:
+        bad.append("saturates")
+    if np.any(np.diff(fy) < -1e-6 * cap):
+        bad.append("monotone")
+    p = np.asarray(f(np.array([cap * np.arctanh(0.5)], np.float32), cap), np.float64)[0]
+    if abs(p - cap / 2) > 2e-6 * cap:
+        bad.append("atanh_half")
+    return bad
+
+
+def test_softcap_pinned_by_invariants():
+    """orc_softcap (the runLinearQ4 soft-cap arm) satisfies every property,
+    at the reference's default sigma 30 (src/Gemma/Layers/LinearQ4.hs:38)
+    and other caps."""
+    for cap in (30.0, 1.0, 7.5):
+        assert _softcap_violations(orc.softcap, cap) == [], cap
+
+
+def test_softcap_invariants_catch_planted_forms():
+    """Plausible wrong soft caps each violate at least one property: a
+    missing 1/cap inside tanh, a missing cap outside, a halved output, a
+    rational cap, a hard clip and the identity."""
+    planted = {
+        "cap*tanh(y)": lambda y, c: c * np.tanh(y.astype(np.float64)),
+        "tanh(y/cap)": lambda y, c: np.tanh(y.astype(np.float64) / c),
+        "cap/2*tanh(y/cap)": lambda y, c: c / 2 * np.tanh(y.astype(np.float64) / c),
+        "y/(1+|y|/cap)": lambda y, c: y.astype(np.float64) / (1 + np.abs(y.astype(np.float64)) / c),
+        "clip": lambda y, c: np.clip(y.astype(np.float64), -c, c),
+        "identity": lambda y, c: y.astype(np.float64),
+        "cap*tanh(y/(2cap))": lambda y, c: c * np.tanh(y.astype(np.float64) / (2 * c)),
+    }
+    for name, f in planted.items():
+        assert _softcap_violations(f, 30.0), name
 
 
 # ---------------------------------------------------------------- whole model
@@ -366,3 +422,29 @@ def test_planted_mistakes_are_caught():
     b[2] = 0x1F  # element 0 = 15, element 16 = 1
     got = orc.q4_0_dequant(b)
     assert got[0] == 7.0 and got[16] == -7.0
+
+
+@pytest.mark.parametrize("q4,mode", [(False, 0), (True, 0), (True, 1)])
+def test_torch_cpu_restatement_agrees_with_the_c_oracle(q4, mode):
+    """oracle/torch_ref.py (bench.py's PyTorch-CPU baseline) against the C
+    oracle on the tiny model: logits within 1e-5 relative and the same
+    argmax at every step of a 24-token run (window 5 binds in both modes)."""
+    import torch_ref
+    import gemma_hip as gh
+    cfg = gh.preset("tiny")
+    cfg.sliding_window, cfg.global_every, cfg.max_seq, cfg.mode = 5, 2, 32, mode
+    cfg.rope_theta_global = 1e6
+    om = orc.OracleModel(cfg)
+    tens = list(gh.synth_tensors(cfg, 11, q4))
+    for name, dtype, arr in tens:
+        om.set_tensor(name, arr, dtype)
+    tm = torch_ref.TorchModel(cfg, tens)
+    toks = gh.synth_tokens(3, "t", 24, cfg.vocab)
+    for pos, t in enumerate(toks):
+        ol, _, ob = om.step(int(t), pos)
+        tl, tb = tm.step(int(t), pos)
+        tl = tl.numpy()
+        assert np.max(np.abs(tl - ol)) / np.max(np.abs(ol)) < 1e-5, pos
+        s = np.sort(ol)
+        if s[-1] - s[-2] > 1e-4 * np.max(np.abs(ol)):
+            assert tb == ob, pos
