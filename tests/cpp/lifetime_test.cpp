@@ -81,6 +81,16 @@ int any_order() {
         }
         for (char w : {'c', 'm', 'k', 't'}) CHECK(destroy(h, w) == GH_ERR_STATE);
     }
+    // gh_kv_truncate rewinds within [0, length]
+    {
+        Handles h;
+        if (make(h)) return 1;
+        int32_t len = -1;
+        CHECK(gh_kv_truncate(h.kv, 2) == GH_ERR_RANGE);
+        CHECK(gh_kv_truncate(h.kv, -1) == GH_ERR_RANGE);
+        CHECK(gh_kv_truncate(h.kv, 0) == GH_OK && gh_kv_length(h.kv, &len) == GH_OK && len == 0);
+        for (char w : {'k', 'm', 't', 'c'}) CHECK(destroy(h, w) == GH_OK);
+    }
     // handles that were never returned by the library
     int local = 0;
     CHECK(gh_model_destroy(reinterpret_cast<gh_model*>(&local)) == GH_ERR_STATE);

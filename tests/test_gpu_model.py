@@ -388,10 +388,6 @@ def test_temperature_sampling_in_the_step(ctx):
         kv.set_sampling(-1.0, 0)
 
 
-@pytest.mark.skip(reason="persistent step (GH_PERSISTENT=1): the model tests pass on MI355X but the test "
-                         "process aborted at exit (std::bad_variant_access raised inside the HIP runtime "
-                         "during teardown) in two runs; the cause is not found yet, so the mode stays off "
-                         "and this test stays skipped until it is")
 def test_persistent_step_matches_graph_step(ctx, monkeypatch):
     """The persistent step kernel (one workgroup per CU, phases exchanging
     epoch-tagged words) gives the graph step's ids and per-layer states."""
