@@ -305,6 +305,12 @@ int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t
 int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
 int launch_stream_read(const void* p, size_t bytes, float* sink, hipStream_t s);
 constexpr int GH_ATTN_OP_MAX_NC = 256;  // chunks per kv head of the op-level attention
+// Capacity (floats) of the static chunk-state array of
+// gh_attention_decode_noalloc: nkv * n_splits * (nq / nkv) * (head_dim + 2)
+// floats per call; 1 Mi floats = 4 MiB (C4: 264,192; 4B shapes: 528,384).
+constexpr size_t ATTN_NOALLOC_SCRATCH_FLOATS = size_t(1) << 20;
+// this device's address of that array (hipGetSymbolAddress, once per device)
+int attn_noalloc_scratch(float** out);
 int launch_sample_logits(const float* logits, int n, float inv_temp, uint64_t seed, uint64_t counter, float* scratch,
                          int32_t* token_dev, hipStream_t s);
 

@@ -3906,13 +3906,34 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     return GH_OK;
 }
 
-// Seeded N(0, sigma) values, counter-based: element i hashes (key, i) with
-// SplitMix64 and maps the 64 bits to two uniforms for Box-Muller.
-__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
-    z += 0x9E3779B97F4A7C15ull;
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
+// ------------------------------------------------------------------
+// Scratch of the allocation-free attention entry point
+// (gh_attention_decode_noalloc): the split-K chunk states live in this
+// file-scope device array instead of the context's scratch, so the call
+// makes no hipMalloc.  Each GPU holds its own copy, at its own address: the
+// host takes that address once per device with hipGetSymbolAddress (the
+// array's name is a host-side stand-in, not a device pointer) and passes it
+// to the kernels.  Every chunk state the merge reads is written by the same
+// call first, so nothing needs clearing; calls that overlap on one GPU
+// share the array and race.
+// ------------------------------------------------------------------
+static __device__ __align__(256) float scratch[ATTN_NOALLOC_SCRATCH_FLOATS];
+
+int attn_noalloc_scratch(float** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static float* ptr[kMaxDevices] = {};
+    int dev = -1;
+    GH_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(GH_ERR_INVALID, "device %d out of range", dev);
+    std::lock_guard<std::mutex> g(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        GH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        ptr[dev] = (float*)p;
+    }
+    *out = ptr[dev];
+    return GH_OK;
 }
 
 // Op-level sampling: per-64-row-block softmax statistics, then the draw.

@@ -794,6 +794,25 @@ extern "C" int gh_attention_decode(gh_ctx* ctx, const float* q, const float* kc,
     return op_sync(ctx);
 }
 
+extern "C" int gh_attention_decode_noalloc(gh_ctx* ctx, const float* q, const float* kc, const float* vc, int nq,
+                                           int nkv, int hd, int p_begin, int p_end, int n_splits, float* out) {
+    OP_ENTER(ctx);
+    if (!q || !kc || !vc || !out || nkv <= 0 || nq <= 0 || nq % nkv || p_begin < 0 || p_end <= p_begin)
+        return set_error(GH_ERR_INVALID, "gh_attention_decode_noalloc: bad arguments");
+    const int n_pos = p_end - p_begin;
+    if (n_splits <= 0) n_splits = std::max(1, std::min((n_pos + 31) / 32, GH_ATTN_OP_MAX_NC));
+    n_splits = std::min(std::min(n_splits, n_pos), GH_ATTN_OP_MAX_NC);
+    const size_t need = (size_t)nkv * n_splits * (nq / nkv) * ((size_t)hd + 2);
+    if (need > ATTN_NOALLOC_SCRATCH_FLOATS)
+        return set_error(GH_ERR_RANGE,
+                         "gh_attention_decode_noalloc: %zu floats of chunk states exceed the static %zu-float "
+                         "scratch (fewer splits or gh_attention_decode)", need, ATTN_NOALLOC_SCRATCH_FLOATS);
+    float* part = nullptr;
+    GH_CHECK(attn_noalloc_scratch(&part));
+    GH_CHECK(launch_attention(q, kc, vc, nq, nkv, hd, p_begin, p_end, n_splits, part, out, ctx->stream));
+    return op_sync(ctx);
+}
+
 extern "C" int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, float* h) {
     OP_ENTER(ctx);
     if (!g || !u || !h || n <= 0) return set_error(GH_ERR_INVALID, "gh_gelu_mul: bad arguments");

@@ -84,6 +84,8 @@ SIGNATURES = {
     "gh_rope": (C.c_int, [_P, _P, C.c_int, C.c_int, C.c_float, C.c_int]),
     "gh_attention_decode": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                       C.c_int, _P]),
+    "gh_attention_decode_noalloc": (C.c_int, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                              C.c_int, _P]),
     "gh_gelu_mul": (C.c_int, [_P, _P, _P, C.c_int, _P]),
     "gh_argmax": (C.c_int, [_P, _P, C.c_int, _I32]),
     "gh_config_preset": (C.c_int, [C.c_char_p, C.POINTER(GhConfig)]),

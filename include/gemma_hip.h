@@ -72,8 +72,8 @@ const char* gh_version(void);
 typedef struct gh_ctx gh_ctx;
 int gh_device_count(int* n_out);
 int gh_ctx_create(int device, gh_ctx** out);
-/* Also destroys the models (with their KV caches) and Q4_0 tensors still
- * open on the context: their handles are invalid afterwards. */
+/* Releases the context: models, caches and Q4_0 tensors made on it stay
+ * usable, and the context is freed with the last of them. */
 int gh_ctx_destroy(gh_ctx* ctx);
 void gh_ctx_release(gh_ctx* ctx); /* gh_ctx_destroy for finalisers */
 /* waitAll (src/Gemma/Model.hs:1432) */
@@ -141,6 +141,17 @@ int gh_rope(gh_ctx* ctx, float* x, int n_heads, int head_dim, float theta, int p
 int gh_attention_decode(gh_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
                         int nq, int nkv, int head_dim, int p_begin, int p_end, int n_splits,
                         float* out);
+/* gh_attention_decode that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * The split-K chunk states go to a static per-GPU array of 4 MiB instead of
+ * the context's scratch; a call that needs more, nkv * n_splits *
+ * (nq / nkv) * (head_dim + 2) floats > 2^20, returns GH_ERR_RANGE.  The
+ * array keeps the last call's contents; calls that overlap on one GPU (on
+ * different contexts or threads) share it and race. */
+int gh_attention_decode_noalloc(gh_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
+                                int nq, int nkv, int head_dim, int p_begin, int p_end, int n_splits,
+                                float* out);
 /* geluMultiplyFusedShader, src/Gemma/Layers/MLP.hs:384-447 */
 int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, float* h);
 /* sampleToken / sampleWithTemperature, app/Main.hs:488-507 (first max) */
