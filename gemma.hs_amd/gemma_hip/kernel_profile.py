@@ -3,7 +3,7 @@
 Driver (run under rocprofv3 on the GPU box, eagerly: GH_NO_GRAPH=1):
 
   python -m gemma_hip.kernel_profile run [--kernel all|KIND] [--config gemma3-1b] [--reps 20]
-                                         [--copy-mib 256] [--manifest FILE]
+                                         [--kv-synth N] [--copy-mib 256] [--manifest FILE]
   python -m gemma_hip.kernel_profile run --prefill 128 [--reps 5] [--copy-mib 256]
   python -m gemma_hip.kernel_profile run --attention 32768 [--reps 20] [--copy-mib 256]
 
@@ -41,11 +41,12 @@ import sys
 from collections import defaultdict
 from pathlib import Path
 
-from . import (GemmaModel, KVCache, Context, STEP_KERNELS, attention_decode, bench_decode, prefill, preset,
+from . import (GemmaModel, KVCache, Context, DeviceBuffer, STEP_KERNELS, bench_decode, prefill, preset,
                stream_read_gbps, synth_tokens, time_kernel)
+from ._lib import check, lib
 
 HIP_MEMCPY_D2D = 3
-SEPARATOR = "k_stream_read"
+SEPARATOR = "k_stream_read"  # preceded by a fill of its buffer (__amd_rocclr_fillBufferAligned), skipped too
 CALIBRATION = "__amd_rocclr_copyBuffer"
 
 
@@ -88,13 +89,18 @@ def run(a) -> int:
         import numpy as np
         L, hd, nq, nkv = a.attention, 256, 4, 1
         rng = np.random.default_rng(4)
-        q = rng.normal(size=nq * hd).astype(np.float32)
-        k = rng.normal(size=L * nkv * hd).astype(np.float32)
-        v = rng.normal(size=L * nkv * hd).astype(np.float32)
+        # inputs uploaded once; each rep is one gh_attention_decode on device
+        # pointers (the attention kernel and its merge, nothing else)
+        q = DeviceBuffer.from_numpy(ctx, rng.normal(size=nq * hd).astype(np.float32))
+        k = DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
+        v = DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
+        o = DeviceBuffer(ctx, 4 * nq * hd)
+        check(lib().gh_attention_decode(ctx.h, q.ptr, k.ptr, v.ptr, nq, nkv, hd, 0, L, 0, o.ptr))  # scratch
         separator()
         for _ in range(a.reps):
-            attention_decode(ctx, q, k, v, nq, nkv, hd, 0, L)
-        segments.append({"name": f"attention_c4_L{L}", "reps": a.reps,
+            check(lib().gh_attention_decode(ctx.h, q.ptr, k.ptr, v.ptr, nq, nkv, hd, 0, L, 0, o.ptr))
+        # one unit = the attention kernel + its merge (two dispatches)
+        segments.append({"name": f"attention_c4_L{L}", "reps": a.reps, "dispatches_per_unit": 2,
                          "bytes_per_launch": 2 * L * nkv * hd * 4 + 8 * nq * hd})
     else:
         model = GemmaModel(ctx, cfg)
@@ -108,7 +114,9 @@ def run(a) -> int:
                 prefill(model, kv, toks, want_logits=False)
             segments.append({"name": f"prefill_{a.prefill}", "reps": a.reps})
         else:
-            kv = KVCache(model, a.prompt + 8)
+            kv = KVCache(model, a.kv_synth + a.prompt + 8)
+            if a.kv_synth > 0:  # the C5 start: a prefilled cache of that many positions
+                kv.synth(5, a.kv_synth)
             bench_decode(model, kv, synth_tokens(1, "prompt", a.prompt, cfg.vocab), 0, 1)
             kinds = STEP_KERNELS if a.kernel == "all" else (a.kernel,)
             for kind in kinds:
@@ -118,7 +126,7 @@ def run(a) -> int:
                                  "bytes_per_launch": int(t.bytes_per_launch), "event_avg_us": round(t.avg_us, 3)})
     separator()
     device_copy(a.copy_mib << 20)
-    man = {"config": a.config, "position": a.prompt if a.prefill == 0 and a.attention == 0 else None,
+    man = {"config": a.config, "position": a.kv_synth + a.prompt if a.prefill == 0 and a.attention == 0 else None,
            "copy_bytes": a.copy_mib << 20, "segments": segments}
     if a.manifest:
         Path(a.manifest).write_text(json.dumps(man, indent=1))
@@ -151,6 +159,8 @@ def _segments(disp, n_seg):
     groups, cur, seen_sep = [], None, False
     for i in order:
         name = disp[i][0]
+        if "__amd_rocclr_fill" in name:  # the separator's buffer fill
+            continue
         if name.startswith(SEPARATOR) or SEPARATOR in name:
             if not seen_sep or cur:
                 cur = []
@@ -200,16 +210,15 @@ def summarize(a) -> int:
     print("|---|---|---|---|---|---|")
     for s in man["segments"]:
         r = rows.get(s["name"], {})
-        per = s.get("launches_per_step", 1)
+        per = s.get("dispatches_per_unit", 1)  # counters are per dispatch; bytes_per_launch per unit
         algo = s.get("bytes_per_launch")
-        fb = r["FETCH_SIZE"] * factors["FETCH_SIZE"] if "FETCH_SIZE" in r and "FETCH_SIZE" in factors else None
-        wb = r["WRITE_SIZE"] * factors["WRITE_SIZE"] if "WRITE_SIZE" in r and "WRITE_SIZE" in factors else None
+        fb = r["FETCH_SIZE"] * factors["FETCH_SIZE"] * per if "FETCH_SIZE" in r and "FETCH_SIZE" in factors else None
+        wb = r["WRITE_SIZE"] * factors["WRITE_SIZE"] * per if "WRITE_SIZE" in r and "WRITE_SIZE" in factors else None
         ratio = (fb + wb) / algo if fb is not None and wb is not None and algo else None
         f = lambda x: f"{x:,.0f}" if x is not None else "-"
         print(f"| {s['name']} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | "
               f"{ratio:.3f} |" if ratio is not None else
               f"| {s['name']} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | - |")
-        del per
     sq = [c for c in ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_INSTS_VMEM_RD",
                       "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_ACTIVE_INST_VALU") if any(c in r for r in rows.values())]
     if sq:
@@ -225,13 +234,13 @@ def summarize(a) -> int:
                   f" | {wait:.3f} | {r.get('SQ_INSTS_VALU', 0) / waves:.1f} | {r.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} |")
     if any("trace_avg_us" in r for r in rows.values()):
         print()
-        print("| segment | kernels | traced avg us / dispatch | algorithmic GB/s | of 8 TB/s |")
+        print("| segment | kernels | traced avg us / unit | algorithmic GB/s | of 8 TB/s |")
         print("|---|---|---|---|---|")
         for s in man["segments"]:
             r = rows.get(s["name"], {})
             if "trace_avg_us" not in r:
                 continue
-            us = r["trace_avg_us"]
+            us = r["trace_avg_us"] * s.get("dispatches_per_unit", 1)
             algo = s.get("bytes_per_launch")
             gbps = algo / (us * 1e3) if algo else None
             print(f"| {s['name']} | {', '.join(r['kernels'])} | {us:.3f} | "
@@ -251,6 +260,7 @@ def main(argv=None) -> int:
     r.add_argument("--reps", type=int, default=20)
     r.add_argument("--copy-mib", type=int, default=256)
     r.add_argument("--prompt", type=int, default=8)
+    r.add_argument("--kv-synth", type=int, default=0, help="fill the cache with this many positions first")
     r.add_argument("--prefill", type=int, default=0, help="time N-token prefills instead of step kernels")
     r.add_argument("--attention", type=int, default=0, help="op-level C4 attention over L positions")
     r.add_argument("--manifest", default="")

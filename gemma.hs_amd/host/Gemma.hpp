@@ -56,7 +56,8 @@ inline GemmaConfig configFromGGUF(const std::string& path) {
 }
 
 // The Dawn Context (createContext, src/Gemma/Model.hs:419): one device, one
-// stream.  Destroying it also destroys the models and tensors made on it.
+// stream.  Destroying it releases it: models and caches made on it keep it
+// alive until they are destroyed.
 class Context {
   public:
     explicit Context(int device = 0) {

@@ -329,6 +329,58 @@ def test_gguf_loaded_model_matches_synth_model(ctx, tmp_path, preset):
     np.testing.assert_array_equal(gh.generate(mg, kg, [int(prompt[-1])], 10), gh.generate(ms, ks, [int(prompt[-1])], 10))
 
 
+@pytest.mark.parametrize("preset", ["tiny", "mini4b"])
+def test_gguf_loaded_model_matches_oracle_from_an_independent_read(ctx, tmp_path, preset):
+    """loadGemmaModelFromGGUF (src/Gemma/Model.hs:908-1234; tensor format
+    src/Gemma/GGUF.hs:186-239) against the oracle: the GPU model comes from
+    gh_model_load_gguf, the oracle's from tests/gguf_reader.py's own reading
+    of the same file (metadata -> config, tensor infos -> bytes).  Every
+    layer's hidden state and the logits agree within 1e-4 relative at every
+    step, and so do the argmaxes where the margin allows."""
+    import sys
+    sys.path.insert(0, str(GOLDEN.parent))
+    from gguf_reader import GGUF
+    from gguf_writer import synth_gguf
+    if preset == "tiny":
+        cfg = gh.preset("tiny")
+    else:
+        cfg = gh.preset("gemma3-4b")
+        cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 3, 1024
+        cfg.sliding_window = 5
+    path = tmp_path / f"{preset}.gguf"
+    synth_gguf(path, cfg, 33, q4=True)
+    mg = gh.GemmaModel.load_gguf(ctx, str(path), max_seq=64)
+    f = GGUF(path)
+    oc = orc.OrcConfig()
+    md = f.meta
+    shape = {"vocab": f.infos["token_embd.weight"][0][1], "hidden": md["gemma3.embedding_length"],
+             "n_layers": md["gemma3.block_count"], "n_heads": md["gemma3.attention.head_count"],
+             "n_kv_heads": md["gemma3.attention.head_count_kv"], "head_dim": md["gemma3.attention.key_length"],
+             "ffn": md["gemma3.feed_forward_length"], "max_seq": 64,
+             "sliding_window": md["gemma3.attention.sliding_window"],
+             # the Gemma-3 conventions the loader applies (gguf.cpp): every 6th layer global, local theta 1e4
+             "global_every": 6, "rope_theta_local": 1e4, "rope_theta_global": md["gemma3.rope.freq_base"],
+             "rms_eps": md["gemma3.attention.layer_norm_rms_epsilon"], "mode": orc.MODE_GEMMA3,
+             "flags": orc.QK_NORM | orc.POST_ATTN_NORM | orc.POST_FFN_NORM | orc.ZERO_CENTERED}
+    for k, v in shape.items():
+        setattr(oc, k, v)
+    om = orc.OracleModel(oc)
+    for name in f.infos:
+        dtype, arr = f.tensor(name)
+        om.set_tensor(name, arr, dtype)
+    kv = gh.KVCache(mg, 64)
+    toks = gh.synth_tokens(12, "t", 12, int(shape["vocab"]))
+    for pos, t in enumerate(toks):
+        logits, _, layers, nxt = gh.runGemmaInferenceCachedWithLayer0(mg, int(t), kv)
+        olog, olay, obest = om.step(int(t), pos, want_layers=True)
+        for l in range(oc.n_layers):
+            assert rel_err(layers[l], olay[l]) < ACT_TOL, (pos, l)
+        assert rel_err(logits, olog) < ACT_TOL, pos
+        srt = np.sort(olog)
+        if srt[-1] - srt[-2] > 1e-3 * np.max(np.abs(olog)):
+            assert nxt == obest, pos
+
+
 def test_kv_synth_prefill_and_timer(ctx):
     """gh_kv_synth fills a cache deterministically and sets its length;
     decoding then continues from that position; the event timer measures
