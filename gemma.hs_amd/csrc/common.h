@@ -230,18 +230,20 @@ struct gh_model {
     std::vector<uint32_t> present;  // per layer bitmask of tensor kinds
     std::vector<gh_kv*> kvs;  // open caches; a released model is freed when the last goes
     bool released = false;    // gh_model_destroy was called
-    // persistent step (GH_PERSISTENT=1): exchange words, launch counter, grid
+    // persistent step (GH_PERSISTENT=1): exchange words, launch counter,
+    // grid, the interleaved gate/up matrices and the number of down partials
     int persistent = 0;
-    uint64_t* w_qkv = nullptr;
-    uint64_t* w_attn = nullptr;
-    uint64_t* w_o = nullptr;
-    uint64_t* w_gu = nullptr;
-    uint64_t* w_down = nullptr;
-    uint64_t* w_x = nullptr;
-    uint64_t* w_x1 = nullptr;
-    uint64_t* w_xn = nullptr;
+    uint64_t* w_qkv = nullptr;   // q | k | v rows
+    uint64_t* w_attn = nullptr;  // attention chunk states
+    uint64_t* w_o = nullptr;     // merged attention output
+    uint64_t* w_a = nullptr;     // O-projection rows
+    uint64_t* w_p = nullptr;     // down partials [p_np][H]
+    uint64_t* w_down = nullptr;  // down rows
     uint32_t p_tick = 0;
     int p_grid = 0;
+    int p_np = 0;
+    std::vector<gh::DMat> p_gi;  // per layer: gate/up in 64-row chunks of 32 gate + 32 up rows
+    bool p_gi_ok = false;        // p_gi matches the uploaded gate/up weights
     // batched prompt prefill
     gh::PfBufs pf;
 };
@@ -284,6 +286,8 @@ struct Profiler {
 // kernels.hip: one decode step at position `pos` (patched per replay in graphs)
 int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos);
 int persistent_supported(const gh_model* m);
+size_t persistent_land(const gh_model* m);  // floats of the persistent step's landing area
+int launch_interleave_gu(const DMat& gu, int f_pad, int F, const DMat& gi, hipStream_t s);
 int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos);
 // kernels.hip: batched prefill of n tokens (ids in m->pf.tok) at positions
 // pos0 .. pos0+n-1; with `head`, also the final norm, LM head and next-token

@@ -499,6 +499,11 @@ __device__ __forceinline__ MvLds mv_lds(float* lds, int per_split) {
 // same time whether or not its offset is in range.  The variant is chosen
 // before any load, so each variant's s_waitcnt counts stay exact.
 template <class P, class = void>
+struct HasSettle : std::false_type {};
+template <class P>
+struct HasSettle<P, std::void_t<decltype(&P::template settle<1>)>> : std::true_type {};
+
+template <class P, class = void>
 struct HasLoadVariants : std::false_type {};
 template <class P>
 struct HasLoadVariants<P, std::void_t<decltype(&P::template load_v<0>)>> : std::true_type {};
@@ -1173,194 +1178,6 @@ __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __noinline__ float poll_word_slow(const uint64_t* p, uint32_t epoch, int* err) {
-    for (int spin = 0; spin < XCHG_SPIN; ++spin) {
-        const uint64_t v = ld_word(p);
-        if ((uint32_t)(v >> 32) == epoch) return __uint_as_float((uint32_t)v);
-        if ((spin & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return 0.0f;
-    }
-    __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return 0.0f;
-}
-
-// A source of float4 groups published as words.
-struct WSrc {
-    const uint64_t* w;
-    uint32_t epoch;
-    int* err;
-    __device__ float g1(size_t i) const {
-        const uint64_t v = ld_word(w + i);
-        return (uint32_t)(v >> 32) == epoch ? __uint_as_float((uint32_t)v) : poll_word_slow(w + i, epoch, err);
-    }
-    // elements i .. i+3
-    __device__ float4 g4e(size_t i) const {
-        const uint64_t* p = w + i;
-        const uint64_t a = ld_word(p), b = ld_word(p + 1), c = ld_word(p + 2), d = ld_word(p + 3);
-        float4 r;
-        r.x = (uint32_t)(a >> 32) == epoch ? __uint_as_float((uint32_t)a) : poll_word_slow(p, epoch, err);
-        r.y = (uint32_t)(b >> 32) == epoch ? __uint_as_float((uint32_t)b) : poll_word_slow(p + 1, epoch, err);
-        r.z = (uint32_t)(c >> 32) == epoch ? __uint_as_float((uint32_t)c) : poll_word_slow(p + 2, epoch, err);
-        r.w = (uint32_t)(d >> 32) == epoch ? __uint_as_float((uint32_t)d) : poll_word_slow(p + 3, epoch, err);
-        return r;
-    }
-};
-
-__device__ __forceinline__ void st_word4(uint64_t* p, uint32_t epoch, float4 v) {
-    st_word(p, epoch, v.x);
-    st_word(p + 1, epoch, v.y);
-    st_word(p + 2, epoch, v.z);
-    st_word(p + 3, epoch, v.w);
-}
-
-// Residual stream update + RMSNorm from published words (persistent step):
-//   x = E[token] * sqrt(H)                       (layer 0, src/Gemma/Model.hs:1346-1361)
-//     or base + postnorm(sum_s part_s)           (TBG:305-343, TBG:413-444)
-//   xs = norm(x) with w_norm
-// The item with `publish` set stores x as words (for the next residual
-// update) and, when given, to layer_out_row.  out_norm_words (optional):
-// instead of building a matvec input, publish norm(x) as words (final norm).
-template <int MG>
-struct ProResidW {
-    int from_embedding;
-    DMat embd;
-    const StepState* st;
-    float escale;
-    WSrc base;
-    WSrc part;  // S splits of ld words each
-    int S, ld;
-    const float* w_post;  // nullable
-    const float* w_norm;
-    float eps;
-    int zc, H;
-    int publish;
-    uint64_t* x_out;  // words, epoch x_epoch
-    uint32_t x_epoch;
-    float* layer_out_row;  // nullable
-    struct Regs {};
-    __device__ void load(Regs&, int, int) const {}
-    // x in registers (xv) and LDS tmp; returns rms of x
-    __device__ float build_x(const MvLds& L, float4 (&xv)[MG]) const {
-        const int NG = H >> 2, tid = threadIdx.x;
-        if (from_embedding) {
-            const int tok = min(max(st->token, 0), embd.rows - 1);
-#pragma unroll
-            for (int k = 0; k < MG; ++k) {
-                const int g = tid + k * NT;
-                if (g < NG) {
-                    const float4 e = dq_elem4(embd, tok, 4 * g);
-                    xv[k] = make_float4(e.x * escale, e.y * escale, e.z * escale, e.w * escale);
-                }
-            }
-        } else {
-            float4 dv[MG], bv[MG];
-            float ss = 0.0f;
-#pragma unroll
-            for (int k = 0; k < MG; ++k) {
-                const int g = tid + k * NT;
-                dv[k] = bv[k] = f4z();
-                if (g < NG) {
-                    bv[k] = base.g4e(4 * (size_t)g);
-                    for (int s = 0; s < S; ++s) dv[k] = dv[k] + part.g4e((size_t)s * ld + 4 * (size_t)g);
-                    ss += dot4(dv[k], dv[k]);
-                }
-            }
-            float rms = 1.0f;
-            if (w_post) rms = sqrtf(block_sum(ss, L.misc) / (float)H + eps);
-#pragma unroll
-            for (int k = 0; k < MG; ++k) {
-                const int g = tid + k * NT;
-                if (g < NG)
-                    xv[k] = bv[k] + (w_post ? norm4(dv[k], rms, ((const float4*)w_post)[g], zc) : dv[k]);
-            }
-        }
-        float ss = 0.0f;
-#pragma unroll
-        for (int k = 0; k < MG; ++k) {
-            const int g = tid + k * NT;
-            if (g < NG) {
-                ((float4*)L.tmp)[g] = xv[k];
-                ss += dot4(xv[k], xv[k]);
-                if (publish) {
-                    if (x_out) st_word4(x_out + 4 * (size_t)g, x_epoch, xv[k]);
-                    if (layer_out_row) ((float4*)layer_out_row)[g] = xv[k];
-                }
-            }
-        }
-        return sqrtf(block_sum(ss, L.misc + 4) / (float)H + eps);  // barrier: tmp complete
-    }
-    template <int FMT>
-    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
-        float4 xv[MG];
-        const float rms = build_x(L, xv);
-        const int ng = n >> 2, tid = threadIdx.x;
-        const float4* t4 = (const float4*)(L.tmp + c0);
-        for (int b = 0; b < ng; b += NT) {
-            const int gi = b + tid;
-            emit_x4<FMT>(L, gi, ng, gi < ng ? norm4(t4[gi], rms, ((const float4*)(w_norm + c0))[gi], zc) : f4z());
-        }
-    }
-};
-
-// O-projection input from published attention chunk states (persistent step).
-struct ProAttnCombineW {
-    WSrc part;  // [nkv][nc][G][HD+2] words
-    int nc, G, HD, n_used;
-    struct Regs {};
-    __device__ void load(Regs&, int, int) const {}
-    template <int FMT>
-    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
-        const int stride = G * (HD + 2), tid = threadIdx.x;
-        const int h0 = c0 / HD, nh = (c0 + n - 1) / HD - h0 + 1;
-        float* wts = L.tmp;
-        for (int hh = tid >> 6; hh < nh; hh += 4) {
-            const int j = tid & 63, hg = h0 + hh;
-            float mj = -INFINITY, lj = 0.0f;
-            if (j < n_used) {
-                const size_t bj = ((size_t)(hg / G) * nc + j) * stride;
-                mj = part.g1(bj + hg % G);
-                lj = part.g1(bj + G + hg % G);
-            }
-            const float M = wave_max(mj);
-            const float e = j < n_used ? expf(mj - M) : 0.0f;
-            const float den = wave_sum(lj * e);
-            wts[hh * ATTN_MAX_NC + j] = e / den;
-        }
-        __syncthreads();
-        const int ng = n >> 2;
-        for (int b = 0; b < ng; b += NT) {
-            const int gi = b + tid;
-            float4 acc = f4z();
-            if (gi < ng) {
-                const int c = c0 + 4 * gi, h = c / HD, d = c % HD;
-                const size_t pbase = (size_t)(h / G) * nc * stride + 2 * G + (h % G) * HD + d;
-                const float* wv = wts + (h - h0) * ATTN_MAX_NC;
-                for (int j = 0; j < n_used; ++j) acc = fma4(wv[j], part.g4e(pbase + (size_t)j * stride), acc);
-            }
-            emit_x4<FMT>(L, gi, ng, acc);
-        }
-    }
-};
-
-// Down-projection input from published gate/up outputs (persistent step).
-struct ProGegluW {
-    WSrc gu;  // gate rows [0, up_off), up rows [up_off, ...)
-    int up_off;
-    struct Regs {};
-    __device__ void load(Regs&, int, int) const {}
-    template <int FMT>
-    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
-        const int ng = n >> 2;
-        for (int b = 0; b < ng; b += NT) {
-            const int gi = b + threadIdx.x;
-            float4 h = f4z();
-            if (gi < ng) {
-                const float4 g = gu.g4e(c0 + 4 * (size_t)gi), u = gu.g4e(up_off + c0 + 4 * (size_t)gi);
-                h = make_float4(gelu_tanh(g.x) * u.x, gelu_tanh(g.y) * u.y, gelu_tanh(g.z) * u.z, gelu_tanh(g.w) * u.w);
-            }
-            emit_x4<FMT>(L, gi, ng, h);
-        }
-    }
-};
 
 // Input slice already in LDS from the previous item of the same matrix.
 struct ProKeep {
@@ -1368,20 +1185,6 @@ struct ProKeep {
     __device__ void load(Regs&, int, int) const {}
     template <int FMT>
     __device__ void finish(const MvLds&, Regs&, int, int) const {}
-};
-
-// Matvec outputs as words (split s at s * ld).
-struct EpiW {
-    uint64_t* w;
-    int ld;
-    uint32_t epoch;
-    struct Regs {};
-    __device__ void load(Regs&) const {}
-    template <int RL>
-    __device__ void run(const MvLds&, const Regs&, int, int row0, int s, float y0, float y1) const {
-        st_word(w + (size_t)s * ld + row0, epoch, y0);
-        if (RL == 2) st_word(w + (size_t)s * ld + row0 + 64, epoch, y1);
-    }
 };
 
 // ------------------------------------------------------------------
@@ -1698,12 +1501,6 @@ struct QkvPartials {
         return r;
     }
 };
-struct QkvWords {
-    WSrc w;
-    struct Pre {};
-    __device__ void issue(Pre&, int, bool) const {}
-    __device__ float4 get(const Pre&, int row) const { return w.g4e((size_t)row); }
-};
 // Sinks of the chunk state: plain floats or published words.
 struct AttnOutPlain {
     float* part;
@@ -1769,12 +1566,14 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
     //    not wait for the cache rows.
     if (STEP) {
         typename In::Pre pv[MG4];
+        int rowv[MG4];
 #pragma unroll
         for (int m = 0; m < MG4; ++m) {
             const int gi = tid + m * NT, i = 4 * gi;
             const int row = i < G * HD ? a.q_off + g * G * HD + i
                           : i < (G + 1) * HD ? a.k_off + g * HD + (i - G * HD)
                                              : a.v_off + g * HD + (i - (G + 1) * HD);
+            rowv[m] = row;
             in.issue(pv[m], row, gi < NG4);
         }
         const BufView QN(a.q_norm, a.use_qk_norm ? HD * 4 : 0), KN(a.k_norm, a.use_qk_norm ? HD * 4 : 0);
@@ -1791,6 +1590,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
         load_k(c0);
         load_v(c0);
         __builtin_amdgcn_sched_barrier(0);
+        // a source whose words may still be in flight (persistent step)
+        // waits for all of them here, the K/V loads already issued
+        if constexpr (HasSettle<In>::value) in.template settle<MG4>(pv, rowv);
         GH_MARK(1);
         // 2. q, k, v of this token into LDS
 #pragma unroll
@@ -2497,16 +2299,36 @@ __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, cons
 
 #if GH_IN_TU(2)
 // ------------------------------------------------------------------
-// persistent step: one cooperative launch per token.  Every workgroup runs
-// the same phase sequence (per layer: QKV, attention, O, gate/up, down;
-// then the final norm and the LM head) and takes the work items of each
-// phase that map to it; phases exchange their outputs as published words
-// (st_word / WSrc), so the only waits are on the data each item needs.
-// Buffer reuse is safe: a phase's buffer is rewritten one layer later,
-// after a dependency chain that passes through every reader of it.
+// Persistent step (GH_PERSISTENT=1): the layers of one token as one kernel
+// of one workgroup per CU, then the LM head and the finish kernel.
+//
+// Phases of layer l and who does them (W = workgroups = CUs):
+//   A  QKV: 8-row groups of the fused matrix, round-robin over the
+//      workgroups.  Every workgroup first updates its own copy of the
+//      residual stream x (x = x1 + postnorm(d), d from phase E) and norms it.
+//   B  attention: chunk items (kv group, chunk) on workgroups 0.. (q/k/v of
+//      the group from phase A; QK-norm, RoPE, KV append, split-K chunk state).
+//   B2 merge: (q head, 64-dim slice) items on the last workgroups: the chunk
+//      states of the head -> its attention output slice.
+//   C  O projection: 8-row groups (input: the merged output).
+//   D  every workgroup: x1 = x + postnorm(o) and n2 = norm(x1); workgroup w
+//      takes 64-row chunks w, w + W, ... of the gate/up matrix interleaved as
+//      32 gate + 32 up rows (so a chunk yields 32 GeGLU values), and
+//      multiplies them into the matching 32-column block of the down matrix:
+//      one down partial P_w[H] per workgroup.
+//   E  down reduction: 8-row groups of H summed over the partials.
+// Phases exchange their outputs as self-validating 64-bit words (epoch <<
+// 32 | float bits; st_word / ld_word): a consumer polls exactly the words
+// it needs, all loads of a batch issued before any check (ps_poll), so an
+// exchange costs about one round trip after the producer's store.  Each
+// workgroup keeps x and x1 in LDS; what crosses workgroups per layer is
+// q/k/v, the chunk states, the merged output, the O rows, the partials and
+// the down rows.  A phase's buffer is rewritten one layer later, after a
+// dependency chain through all of its readers.  Every wait is bounded
+// (StepState::xchg_err; once set, every wait returns at once).
 // ------------------------------------------------------------------
 struct PLayer {
-    DMat qkv, o, gu, down;
+    DMat qkv, o, gi, down;  // gi: gate/up interleaved in 64-row chunks (32 gate, 32 up rows)
     const float* attn_norm;
     const float* q_norm;
     const float* k_norm;
@@ -2525,28 +2347,22 @@ struct PArgs {
     const float* out_norm;
     StepState* st;
     int pos;
-    uint32_t tick;  // epoch of layer l = tick * (L + 2) + l + 1; final norm: l = L
+    uint32_t tick;  // epoch of layer l = tick * (L + 1) + l + 1
     const float* rope_local;
     const float* rope_global;
-    uint64_t* w_qkv;
-    uint64_t* w_attn;
-    uint64_t* w_o;
-    uint64_t* w_gu;
-    uint64_t* w_down;
-    uint64_t* w_x;
-    uint64_t* w_x1;
-    uint64_t* w_xn;
-    int L, H, nkv, q_rows_pad, kv_rows_pad, f_pad, S_down, nc;
+    uint64_t* w_qkv;  // [q_rows_pad + 2 kv_rows_pad] raw q | k | v rows
+    uint64_t* w_st;   // [nkv][nc][G][HD + 2] chunk states
+    uint64_t* w_o;    // [nq * HD] merged attention output
+    uint64_t* w_a;    // [H] O-projection rows
+    uint64_t* w_p;    // [np][H] down partials
+    uint64_t* w_d;    // [H] down rows
+    float* xn_final;  // [H] normed final state (plain stores; read by the LM head kernel)
+    float* layer_out; // [L][H]
+    int L, H, nq, nkv, q_rows_pad, kv_rows_pad, n_chunks, nc, np, land;
     float eps, escale, scale;
     int zc, use_qk_norm, post_attn_norm, post_ffn_norm, mode, window;
     int pb[2], pe[2], ch[2], n_used[2];  // attention range at pos: [0] local, [1] global layer
-    float* logits;
-    unsigned long long* cand;
-    float* bm;
-    float* bs;
-    float* layer_out;
-    int V;
-    uint32_t* host_tick;  // host-side launch counter (not used on the device)
+    uint32_t* host_tick;                 // host-side launch counter (not used on the device)
     // position-dependent arguments of one replay: position, a fresh epoch
     // base, and the attention range of local and global layers
     void set_pos(int p) {
@@ -2567,65 +2383,346 @@ struct PArgs {
     }
 };
 
-// Final-norm input published once: xs = words of norm(x_L) (LM head).
-struct ProXnW {
-    WSrc xn;
-    struct Regs {};
-    __device__ void load(Regs&, int, int) const {}
+static int enqueue_head(gh_model* m, gh_kv* kv, Sink& sink, int pos);  // LM head + finish (below)
+
+constexpr int PS_PW = 8;    // words per thread per poll batch
+constexpr int PS_MAXP = 3;  // (block, row) pairs per thread of an 8-row group: K <= 3072
+constexpr int PS_MG = 3;    // float4 groups per thread of an H-vector: H <= 3072
+constexpr int PS_KR = 10;   // down-partial rows per thread: H <= 2560
+
+__device__ __forceinline__ bool ps_failed(int* err) {
+    return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
+// dst[i] <- the float of word addr(i), i < n, once that word carries epoch
+// e.  Each thread issues the loads of its batch of PS_PW words before it
+// checks any; stale words are polled again, all of them per round.  The
+// caller synchronises before reading dst.
+template <class Addr>
+__device__ void ps_poll(int n, Addr addr, uint32_t e, float* dst, int* err) {
+    for (int base = 0; base < n; base += PS_PW * NT) {
+        uint64_t v[PS_PW];
+#pragma unroll
+        for (int k = 0; k < PS_PW; ++k) {
+            const int i = base + (int)threadIdx.x + k * NT;
+            v[k] = i < n ? ld_word(addr(i)) : (uint64_t)e << 32;
+        }
+        uint32_t pend = 0;
+#pragma unroll
+        for (int k = 0; k < PS_PW; ++k) {
+            const int i = base + (int)threadIdx.x + k * NT;
+            if ((uint32_t)(v[k] >> 32) == e) {
+                if (i < n) dst[i] = __uint_as_float((uint32_t)v[k]);
+            } else {
+                pend |= 1u << k;
+            }
+        }
+        for (int spin = 1; pend; ++spin) {
+            if (spin >= XCHG_SPIN) {
+                __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if ((spin & 63) == 0 && ps_failed(err)) break;
+#pragma unroll
+            for (int k = 0; k < PS_PW; ++k)
+                if (pend >> k & 1u) v[k] = ld_word(addr(base + (int)threadIdx.x + k * NT));
+#pragma unroll
+            for (int k = 0; k < PS_PW; ++k) {
+                if ((pend >> k & 1u) && (uint32_t)(v[k] >> 32) == e) {
+                    dst[base + threadIdx.x + k * NT] = __uint_as_float((uint32_t)v[k]);
+                    pend &= ~(1u << k);
+                }
+            }
+        }
+    }
+}
+
+// Sum of squares of LDS v[0, n) over the workgroup (one barrier; slot: 4 floats).
+__device__ __forceinline__ float ps_sumsq(const float* v, int n, float* slot) {
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += NT) s += v[i] * v[i];
+    return block_sum(s, slot);
+}
+
+// xs/sxs <- src[0, K) (LDS), normed by inv and (1 + w) / w when w is given,
+// in the VALU Q4_0 input format (emit_x4).
+__device__ __forceinline__ void ps_emit(const MvLds& L, const float* src, int K, float inv, const float* w, int zc) {
+    const int ng = K >> 2;
+    for (int b = 0; b < ng; b += NT) {
+        const int gi = b + threadIdx.x;
+        float4 v = f4z();
+        if (gi < ng) {
+            v = ((const float4*)src)[gi];
+            if (w) v = norm4i(v, inv, ((const float4*)w)[gi], zc);
+        }
+        emit_x4<FMT_Q4>(L, gi, ng, v);
+    }
+}
+
+// Weights of 8-row group grp (rows 8 grp .. 8 grp + 7) of a tiled Q4_0
+// matrix: thread t holds the pairs p = t + 256 k, block p / 8 of row p % 8
+// (8 consecutive lanes read one 128-byte line); pairs past the matrix read
+// zeros.
+struct RowRegs {
+    u32x4 c[PS_MAXP];
+    uint16_t s[PS_MAXP];
+};
+
+__device__ __forceinline__ void rg_load(RowRegs& R, const DMat& W, const MatViews& V, int grp) {
+    const int row0 = grp * 8;
+    const uint32_t tb = (uint32_t)(row0 >> 7) * (uint32_t)W.nblk * TILE_ROWS + (uint32_t)(row0 & 127);
+#pragma unroll
+    for (int k = 0; k < PS_MAXP; ++k) {
+        const int p = threadIdx.x + k * NT, kb = p >> 3;
+        const uint32_t e = tb + (uint32_t)kb * TILE_ROWS + (uint32_t)(p & 7);
+        const bool ok = kb < W.nblk;
+        R.c[k] = V.codes.template u4<CP_NT>(ok ? e * 16u : OOB);
+        R.s[k] = V.scales.template h1<CP_NT>(ok ? e * 2u : OOB);
+    }
+}
+
+// The group's 8 dot products with the slice in xs/sxs; thread r < 8 returns
+// row r's (the others return 0).  Two barriers (red: 32 floats of LDS).
+__device__ __forceinline__ float rg_dot(const RowRegs& R, int nblk, const MvLds& L, float* red) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PS_MAXP; ++k) {
+        const int kb = (threadIdx.x + k * NT) >> 3;
+        if (kb < nblk) {
+            const float4* xv = (const float4*)(L.xs + kb * 32);
+            const uint32_t w[4] = {R.c[k].x, R.c[k].y, R.c[k].z, R.c[k].w};
+            float d = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) d = dot_q4_word(w[j], xv[j], xv[4 + j], d);
+            acc = fmaf(h2f(R.s[k]), d - 8.0f * L.sxs[kb], acc);
+        }
+    }
+    acc += __shfl_xor(acc, 8, 64);
+    acc += __shfl_xor(acc, 16, 64);
+    acc += __shfl_xor(acc, 32, 64);
+    const int lane = threadIdx.x & 63;
+    if (lane < 8) red[(threadIdx.x >> 6) * 8 + lane] = acc;
+    __syncthreads();
+    const float y = threadIdx.x < 8 ? (red[threadIdx.x] + red[8 + threadIdx.x]) + (red[16 + threadIdx.x] + red[24 + threadIdx.x])
+                                    : 0.0f;
+    __syncthreads();
+    return y;
+}
+
+// q | k | v rows of this token as published words: issue() starts the
+// loads of a float4 group's 4 words early (before the K/V loads), settle()
+// waits until every group of the thread carries the step's epoch (stale
+// words are polled again together, bounded), get() returns a group.
+struct QkvPoll {
+    const uint64_t* w;
+    uint32_t e;
+    int* err;
+    struct Pre {
+        uint64_t v[4];
+    };
+    __device__ void issue(Pre& p, int row, bool ok) const {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p.v[j] = ok ? ld_word(w + row + j) : (uint64_t)e << 32;
+    }
+    template <int M>
+    __device__ void settle(Pre (&p)[M], const int (&row)[M]) const {
+        uint32_t pend = 0;
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if ((uint32_t)(p[m].v[j] >> 32) != e) pend |= 1u << (4 * m + j);
+        for (int spin = 1; pend; ++spin) {
+            if (spin >= XCHG_SPIN) {
+                __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if ((spin & 63) == 0 && ps_failed(err)) break;
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (pend >> (4 * m + j) & 1u) p[m].v[j] = ld_word(w + row[m] + j);
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if ((pend >> (4 * m + j) & 1u) && (uint32_t)(p[m].v[j] >> 32) == e) pend &= ~(1u << (4 * m + j));
+        }
+    }
+    __device__ float4 get(const Pre& p, int) const {
+        return make_float4(__uint_as_float((uint32_t)p.v[0]), __uint_as_float((uint32_t)p.v[1]),
+                           __uint_as_float((uint32_t)p.v[2]), __uint_as_float((uint32_t)p.v[3]));
+    }
+};
+
+// LDS scratch of the persistent step (floats after the matvec region).
+struct PsLds {
+    float* xr;    // [H] residual stream entering the layer
+    float* x1;    // [H] residual after attention
+    float* land;  // [a.land] polled words
+    float* red;   // [64] reductions
+    float* gu;    // [64] gate/up rows of a chunk
+};
+
+// Phase D input, run by every workgroup: poll the O rows, x1 = x +
+// postnorm(o) (kept for the next layer), xs = norm(x1) with the pre-FFN
+// weight (ffn_norm, else post_attention_norm: src/Gemma/Model.hs:337-339).
+struct ProFfnPs {
+    const uint64_t* w_a;
+    const float* post_attn;  // nullable: no post-attention norm
+    const float* ffn_w;      // pre-FFN norm weight
+    PsLds S;
+    uint32_t e;
+    int* err;
+    int H, zc;
+    float eps;
+    struct Regs {
+        float4 wp[PS_MG], wf[PS_MG];
+    };
+    __device__ void load(Regs& r, int, int) const {
+        const int ng4 = H >> 2;
+        const BufView WP(post_attn, post_attn ? (size_t)H * 4 : 0), WF(ffn_w, (size_t)H * 4);
+#pragma unroll
+        for (int b = 0; b < PS_MG; ++b) {
+            const int gi = threadIdx.x + b * NT;
+            r.wp[b] = WP.f4(gi < ng4 ? 16u * gi : OOB);
+            r.wf[b] = WF.f4(gi < ng4 ? 16u * gi : OOB);
+        }
+    }
     template <int FMT>
-    __device__ void finish(const MvLds& L, Regs&, int c0, int n) const {
-        const int ng = n >> 2;
-        for (int b = 0; b < ng; b += NT) {
-            const int gi = b + threadIdx.x;
-            emit_x4<FMT>(L, gi, ng, gi < ng ? xn.g4e(c0 + 4 * (size_t)gi) : f4z());
+    __device__ void finish(const MvLds& L, Regs& r, int, int) const {
+        const int ng4 = H >> 2;
+        const uint64_t* wa = w_a;
+        ps_poll(H, [=](int i) { return wa + i; }, e, S.land, err);
+        __syncthreads();
+        float inv = 1.0f;
+        if (post_attn) inv = 1.0f / sqrtf(ps_sumsq(S.land, H, S.red) / (float)H + eps);
+        float4 xv[PS_MG];
+        float ss = 0.0f;
+#pragma unroll
+        for (int b = 0; b < PS_MG; ++b) {
+            const int gi = threadIdx.x + b * NT;
+            xv[b] = f4z();
+            if (gi < ng4) {
+                const float4 o = ((const float4*)S.land)[gi];
+                xv[b] = ((const float4*)S.xr)[gi] + (post_attn ? norm4i(o, inv, r.wp[b], zc) : o);
+                ((float4*)S.x1)[gi] = xv[b];
+                ss += dot4(xv[b], xv[b]);
+            }
+        }
+        const float inv2 = 1.0f / sqrtf(block_sum(ss, S.red + 4) / (float)H + eps);
+#pragma unroll
+        for (int b = 0; b < PS_MG; ++b) {
+            const int gi = threadIdx.x + b * NT;
+            emit_x4<FMT_Q4>(L, gi, ng4, gi < ng4 ? norm4i(xv[b], inv2, r.wf[b], zc) : f4z());
         }
     }
 };
 
-constexpr int P_KBW = 9;
+// Gate/up chunk output rows into LDS (64 rows: gate 0..31, up 32..63).
+struct EpiLdsRows {
+    float* y;
+    struct Regs {};
+    __device__ void load(Regs&) const {}
+    template <int RL>
+    __device__ void run(const MvLds&, const Regs&, int, int, int, float y0, float) const {
+        y[threadIdx.x & 63] = y0;
+    }
+};
 
-template <int HD, int G, int MG>
-__global__ __launch_bounds__(NT) void k_step_persistent(PArgs a) {
+template <int HD, int G, int KBW>
+__global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
     extern __shared__ float lds[];
-    const int nwg = gridDim.x, wg = blockIdx.x;
+    const int nwg = gridDim.x, wg = blockIdx.x, tid = threadIdx.x;
     int* err = &a.st->xchg_err;
-    int off = 0;  // items of consecutive phases start at consecutive workgroups
-    auto each = [&](int n_items, auto&& f) {
-        for (int i = ((wg - off) % nwg + nwg) % nwg; i < n_items; i += nwg) {
-            __syncthreads();  // LDS of the previous item is free
-            f(i);
+    const int H = a.H, QK = a.nq * HD;
+    const int nbx = (H > QK ? H : QK) / 32;
+    const MvLds L = mv_lds<FMT_Q4>(lds, nbx);
+    PsLds S;
+    S.xr = lds + 512 + 64 + ((nbx + 3) & ~3) * 33 + 4;  // after the matvec region (mv_lds_floats, Q4_0)
+    S.x1 = S.xr + H;
+    S.land = S.x1 + H;
+    S.red = S.land + a.land;
+    S.gu = S.red + 64;
+    const float eps = a.eps;
+    const int zc = a.zc;
+
+    // layer-0 input, in every workgroup: x = E[token] * sqrt(H) (Embedding.hs:30-64, Model.hs:1357-1361)
+    {
+        const int tok = min(max(a.st->token, 0), a.embd.rows - 1);
+        for (int i = 4 * tid; i < H; i += 4 * NT) {
+            const float4 ev = dq_elem4(a.embd, tok, i);
+            *(float4*)&S.xr[i] = make_float4(ev.x * a.escale, ev.y * a.escale, ev.z * a.escale, ev.w * a.escale);
         }
-        off = (off + n_items) % nwg;
-    };
-    const int H = a.H;
+    }
+    __syncthreads();
+
     for (int l = 0; l < a.L; ++l) {
         const PLayer& P = a.layers[l];
-        const uint32_t e = a.tick * (uint32_t)(a.L + 2) + (uint32_t)l + 1u, ep = e - 1u;
-        // QKV: residual update from the previous layer's down partials, pre-attention norm
-        each(P.qkv.tiles * 2, [&](int rt) {
-            ProResidW<MG> pro;
-            pro.from_embedding = l == 0;
-            pro.embd = a.embd;
-            pro.st = a.st;
-            pro.escale = a.escale;
-            pro.base = WSrc{a.w_x1, ep, err};
-            pro.part = WSrc{a.w_down, ep, err};
-            pro.S = a.S_down;
-            pro.ld = l > 0 ? a.layers[l - 1].down.tiles * TILE_ROWS : 0;
-            pro.w_post = l > 0 && a.post_ffn_norm ? a.layers[l - 1].post_ffw : nullptr;
-            pro.w_norm = P.attn_norm;
-            pro.eps = a.eps;
-            pro.zc = a.zc;
-            pro.H = H;
-            pro.publish = rt == 0;
-            pro.x_out = a.w_x;
-            pro.x_epoch = e;
-            pro.layer_out_row = l > 0 ? a.layer_out + (size_t)(l - 1) * H : nullptr;
-            mv_item<FMT_Q4, P_KBW, 1>(P.qkv, rt, 0, 1, pro, EpiW{a.w_qkv, 0, e}, mv_lds<FMT_Q4>(lds, P.qkv.nblk));
-        });
-        // attention: QK-norm, RoPE, KV append, split-K chunks
+        const uint32_t e = a.tick * (uint32_t)(a.L + 1) + (uint32_t)l + 1u;
+        // ---------------- A: residual update, pre-attention norm, QKV rows
         {
-            const int t = P.global ? 1 : 0;
+            const int ngrp = P.qkv.tiles * (TILE_ROWS / 8);
+            const MatViews V(P.qkv);
+            RowRegs R;
+            rg_load(R, P.qkv, V, wg);  // out of range: zeros, no traffic
+            // the norm weights of this thread's float4 groups, in flight with the weights
+            const int ng4 = H >> 2;
+            const bool pn = l > 0 && a.post_ffn_norm && a.layers[l - 1].post_ffw;
+            const BufView WP(pn ? a.layers[l - 1].post_ffw : nullptr, pn ? (size_t)H * 4 : 0), WN(P.attn_norm, (size_t)H * 4);
+            float4 wpv[PS_MG], wnv[PS_MG];
+#pragma unroll
+            for (int b = 0; b < PS_MG; ++b) {
+                const int gi = tid + b * NT;
+                wpv[b] = WP.f4(gi < ng4 ? 16u * gi : OOB);
+                wnv[b] = WN.f4(gi < ng4 ? 16u * gi : OOB);
+            }
+            float4 xv[PS_MG];
+            if (l > 0) {
+                const uint64_t* wd = a.w_d;
+                ps_poll(H, [=](int i) { return wd + i; }, e - 1u, S.land, err);
+                __syncthreads();
+                float inv = 1.0f;
+                if (pn) inv = 1.0f / sqrtf(ps_sumsq(S.land, H, S.red) / (float)H + eps);
+#pragma unroll
+                for (int b = 0; b < PS_MG; ++b) {
+                    const int gi = tid + b * NT;
+                    if (gi < ng4) {
+                        const float4 d = ((const float4*)S.land)[gi];
+                        xv[b] = ((const float4*)S.x1)[gi] + (pn ? norm4i(d, inv, wpv[b], zc) : d);
+                        ((float4*)S.xr)[gi] = xv[b];
+                        if (wg == 0) ((float4*)(a.layer_out + (size_t)(l - 1) * H))[gi] = xv[b];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int b = 0; b < PS_MG; ++b) {
+                    const int gi = tid + b * NT;
+                    xv[b] = gi < ng4 ? ((const float4*)S.xr)[gi] : f4z();
+                }
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (int b = 0; b < PS_MG; ++b)
+                if (tid + b * NT < ng4) ss += dot4(xv[b], xv[b]);
+            const float inv = 1.0f / sqrtf(block_sum(ss, S.red + 4) / (float)H + eps);
+#pragma unroll
+            for (int b = 0; b < PS_MG; ++b) {
+                const int gi = tid + b * NT;
+                emit_x4<FMT_Q4>(L, gi, ng4, gi < ng4 ? norm4i(xv[b], inv, wnv[b], zc) : f4z());
+            }
+            __syncthreads();
+            for (int grp = wg; grp < ngrp; grp += nwg) {
+                if (grp != wg) rg_load(R, P.qkv, V, grp);
+                const float y = rg_dot(R, P.qkv.nblk, L, S.red + 8);
+                if (tid < 8) st_word(a.w_qkv + grp * 8 + tid, e, y);
+            }
+        }
+        // ---------------- B: attention chunks
+        const int gsel = P.global ? 1 : 0;
+        const int nu = a.n_used[gsel];
+        {
             AttnArgs aa{};
             aa.q_off = 0;
             aa.k_off = a.q_rows_pad;
@@ -2633,8 +2730,8 @@ __global__ __launch_bounds__(NT) void k_step_persistent(PArgs a) {
             aa.q_norm = P.q_norm;
             aa.k_norm = P.k_norm;
             aa.use_qk_norm = a.use_qk_norm && P.q_norm && P.k_norm;
-            aa.zc = a.zc;
-            aa.eps = a.eps;
+            aa.zc = zc;
+            aa.eps = eps;
             aa.rope = (a.mode == GH_MODE_REF || P.global) ? a.rope_global : a.rope_local;
             aa.pos = a.pos;
             aa.global = P.global;
@@ -2645,108 +2742,207 @@ __global__ __launch_bounds__(NT) void k_step_persistent(PArgs a) {
             aa.nkv = a.nkv;
             aa.scale = a.scale;
             aa.nc = a.nc;
-            aa.pb = a.pb[t];
-            aa.pe = a.pe[t];
-            aa.ch = a.ch[t];
-            aa.n_used = a.n_used[t];
-            const int nu = aa.n_used;
-            each(a.nkv * nu, [&](int it) {
-                attn_item<HD, G, true>(aa, it / nu, it % nu, QkvWords{WSrc{a.w_qkv, e, err}},
-                                       AttnOutWords{a.w_attn, e});
-            });
-            // O projection: merge of the chunk states
-            each(P.o.tiles * 2, [&](int rt) {
-                ProAttnCombineW pro{WSrc{a.w_attn, e, err}, a.nc, G, HD, nu};
-                mv_item<FMT_Q4, P_KBW, 1>(P.o, rt, 0, 1, pro, EpiW{a.w_o, 0, e}, mv_lds<FMT_Q4>(lds, P.o.nblk));
-            });
+            aa.pb = a.pb[gsel];
+            aa.pe = a.pe[gsel];
+            aa.ch = a.ch[gsel];
+            aa.n_used = nu;
+            for (int it = wg; it < a.nkv * nu; it += nwg) {
+                const int g = it / nu, j = it % nu;
+                attn_item<HD, G, true>(aa, g, j, QkvPoll{a.w_qkv, e, err}, AttnOutWords{a.w_st, e});
+                __syncthreads();
+            }
         }
-        // gate/up: post-attention residual update, pre-FFN norm
-        each(P.gu.tiles * 2, [&](int rt) {
-            ProResidW<MG> pro;
-            pro.from_embedding = 0;
-            pro.embd = a.embd;
-            pro.st = a.st;
-            pro.escale = 1.0f;
-            pro.base = WSrc{a.w_x, e, err};
-            pro.part = WSrc{a.w_o, e, err};
-            pro.S = 1;
-            pro.ld = P.o.tiles * TILE_ROWS;
-            pro.w_post = a.post_attn_norm ? P.post_attn : nullptr;
-            pro.w_norm = P.ffn_norm ? P.ffn_norm : P.post_attn;
-            pro.eps = a.eps;
-            pro.zc = a.zc;
-            pro.H = H;
-            pro.publish = rt == 0;
-            pro.x_out = a.w_x1;
-            pro.x_epoch = e;
-            pro.layer_out_row = nullptr;
-            mv_item<FMT_Q4, P_KBW, 1>(P.gu, rt, 0, 1, pro, EpiW{a.w_gu, 0, e}, mv_lds<FMT_Q4>(lds, P.gu.nblk));
-        });
-        // down: GeGLU of its column split
-        const int sd = a.S_down;
-        each(P.down.tiles * 2 * sd, [&](int it) {
-            ProGegluW pro{WSrc{a.w_gu, e, err}, a.f_pad};
-            mv_item<FMT_Q4, P_KBW, 1>(P.down, it / sd, it % sd, sd, pro, EpiW{a.w_down, P.down.tiles * TILE_ROWS, e},
-                                      mv_lds<FMT_Q4>(lds, (P.down.nblk + sd - 1) / sd));
-        });
+        // ---------------- B2: merge of the chunk states
+        {
+            constexpr int SL = HD < 64 ? HD : 64;
+            const int nsl = HD / SL, nitem = a.nq * nsl;
+            const size_t stride = (size_t)G * (HD + 2);
+            for (int it = nwg - 1 - wg; it >= 0 && it < nitem; it += nwg) {
+                const int h = it / nsl, d0 = (it % nsl) * SL, g = h / G, hl = h % G;
+                const uint64_t* base = a.w_st + (size_t)g * a.nc * stride;
+                // land: m[nu] | l[nu] | o[nu][SL]
+                ps_poll(nu * (2 + SL), [=](int i) {
+                    if (i < nu) return base + (size_t)i * stride + hl;
+                    if (i < 2 * nu) return base + (size_t)(i - nu) * stride + G + hl;
+                    const int j = (i - 2 * nu) / SL, d = (i - 2 * nu) % SL;
+                    return base + (size_t)j * stride + 2 * G + (size_t)hl * HD + d0 + d;
+                }, e, S.land, err);
+                __syncthreads();
+                if (tid < SL) {
+                    float M = -INFINITY;
+                    for (int j = 0; j < nu; ++j) M = fmaxf(M, S.land[j]);
+                    float den = 0.0f, o = 0.0f;
+                    for (int j = 0; j < nu; ++j) {
+                        const float w = __expf(S.land[j] - M);
+                        den += S.land[nu + j] * w;
+                        o += w * S.land[2 * nu + j * SL + tid];
+                    }
+                    st_word(a.w_o + (size_t)h * HD + d0 + tid, e, o / den);
+                }
+                __syncthreads();
+            }
+        }
+        // ---------------- C: O projection rows
+        {
+            const int ngrp = H / 8;
+            if (wg < ngrp) {
+                const MatViews V(P.o);
+                RowRegs R;
+                rg_load(R, P.o, V, wg);
+                const uint64_t* wo = a.w_o;
+                ps_poll(QK, [=](int i) { return wo + i; }, e, S.land, err);
+                __syncthreads();
+                ps_emit(L, S.land, QK, 1.0f, nullptr, zc);
+                __syncthreads();
+                for (int grp = wg; grp < ngrp; grp += nwg) {
+                    if (grp != wg) rg_load(R, P.o, V, grp);
+                    const float y = rg_dot(R, P.o.nblk, L, S.red + 8);
+                    if (tid < 8) st_word(a.w_a + grp * 8 + tid, e, y);
+                }
+            }
+        }
+        // ---------------- D: post-attention residual, pre-FFN norm, gate/up chunks, down partial
+        {
+            ProFfnPs pro{a.w_a, a.post_attn_norm ? P.post_attn : nullptr, P.ffn_norm ? P.ffn_norm : P.post_attn,
+                         S, e, err, H, zc, eps};
+            float part[PS_KR];  // this thread's rows t + 256 k of the down partial
+#pragma unroll
+            for (int k = 0; k < PS_KR; ++k) part[k] = 0.0f;
+            const MatViews VD(P.down);
+            u32x4 dw[PS_KR];
+            uint16_t ds[PS_KR];
+            // down-column block c of this thread's rows: issued before the gate/up item
+            auto load_down = [&](int c) {
+#pragma unroll
+                for (int k = 0; k < PS_KR; ++k) {
+                    const int r = tid + k * NT;
+                    const uint32_t el = ((uint32_t)(r >> 7) * (uint32_t)P.down.nblk + (uint32_t)c) * TILE_ROWS + (uint32_t)(r & 127);
+                    dw[k] = VD.codes.template u4<CP_NT>(r < H ? el * 16u : OOB);
+                    ds[k] = VD.scales.template h1<CP_NT>(r < H ? el * 2u : OOB);
+                }
+            };
+            bool built = false;
+            for (int c = wg; c < a.n_chunks; c += nwg) {
+                load_down(c);
+                if (!built) {
+                    mv_item_valu<FMT_Q4, KBW, 1, 1>(P.gi, c, 0, 1, pro, EpiLdsRows{S.gu}, L);
+                    built = true;
+                } else {
+                    mv_item_valu<FMT_Q4, KBW, 1, 1>(P.gi, c, 0, 1, ProKeep{}, EpiLdsRows{S.gu}, L);
+                }
+                __syncthreads();
+                // GeGLU of the chunk's 32 rows (MLP.hs:384-447) as a Q4_0 input block: h[0..31] in
+                // the emit format (16..31 scaled by 1/16) and sum(h)
+                float* hb = S.gu + 64;
+                if (tid < 64) {  // wave 0, all lanes (the sum is a wave reduction)
+                    const float hv = tid < 32 ? gelu_tanh(S.gu[tid]) * S.gu[32 + tid] : 0.0f;
+                    const float hsum = wave_sum(hv);
+                    if (tid < 32) hb[tid] = tid < 16 ? hv : hv * 0.0625f;
+                    if (tid == 0) hb[32] = hsum;
+                }
+                __syncthreads();
+                const float4* hv4 = (const float4*)hb;
+                const float hs8 = 8.0f * hb[32];
+#pragma unroll
+                for (int k = 0; k < PS_KR; ++k) {
+                    if (tid + k * NT < H) {
+                        float d = 0.0f;
+                        d = dot_q4_word(dw[k].x, hv4[0], hv4[4], d);
+                        d = dot_q4_word(dw[k].y, hv4[1], hv4[5], d);
+                        d = dot_q4_word(dw[k].z, hv4[2], hv4[6], d);
+                        d = dot_q4_word(dw[k].w, hv4[3], hv4[7], d);
+                        part[k] = fmaf(h2f(ds[k]), d - hs8, part[k]);
+                    }
+                }
+                __syncthreads();
+            }
+            if (!built) {  // no chunk here: x1 and n2 are still this workgroup's to keep
+                ProFfnPs::Regs r0;
+                pro.load(r0, 0, H);
+                pro.template finish<FMT_Q4>(L, r0, 0, H);
+                __syncthreads();
+            } else if (wg < a.np) {
+                uint64_t* pw = a.w_p + (size_t)wg * H;
+#pragma unroll
+                for (int k = 0; k < PS_KR; ++k) {
+                    const int r = tid + k * NT;
+                    if (r < H) st_word(pw + r, e, part[k]);
+                }
+            }
+        }
+        // ---------------- E: down rows = sum of the partials
+        {
+            const int ngrp = H / 8;
+            for (int grp = wg; grp < ngrp; grp += nwg) {
+                // land[p * 8 + r] = partial p of row 8 grp + r
+                const uint64_t* wp = a.w_p + grp * 8;
+                ps_poll(a.np * 8, [=](int i) { return wp + (size_t)(i >> 3) * H + (i & 7); }, e, S.land, err);
+                __syncthreads();
+                float s = 0.0f;
+                for (int i = tid; i < a.np * 8; i += NT) s += S.land[i];  // row i & 7 == tid & 7
+                s += __shfl_xor(s, 8, 64);
+                s += __shfl_xor(s, 16, 64);
+                s += __shfl_xor(s, 32, 64);
+                if ((tid & 63) < 8) S.red[16 + (tid >> 6) * 8 + (tid & 7)] = s;
+                __syncthreads();
+                if (tid < 8)
+                    st_word(a.w_d + grp * 8 + tid, e,
+                            (S.red[16 + tid] + S.red[24 + tid]) + (S.red[32 + tid] + S.red[40 + tid]));
+                __syncthreads();
+            }
+        }
     }
-    // final residual + norm, published once
-    const uint32_t eL1 = a.tick * (uint32_t)(a.L + 2) + (uint32_t)a.L, eL = eL1 + 1u;
-    each(1, [&](int) {
-        const PLayer& P = a.layers[a.L - 1];
-        ProResidW<MG> pro;
-        pro.from_embedding = 0;
-        pro.embd = a.embd;
-        pro.st = a.st;
-        pro.escale = 1.0f;
-        pro.base = WSrc{a.w_x1, eL1, err};
-        pro.part = WSrc{a.w_down, eL1, err};
-        pro.S = a.S_down;
-        pro.ld = P.down.tiles * TILE_ROWS;
-        pro.w_post = a.post_ffn_norm ? P.post_ffw : nullptr;
-        pro.w_norm = a.out_norm;
-        pro.eps = a.eps;
-        pro.zc = a.zc;
-        pro.H = H;
-        pro.publish = 1;
-        pro.x_out = nullptr;
-        pro.x_epoch = eL;
-        pro.layer_out_row = a.layer_out + (size_t)(a.L - 1) * H;
-        MvLds L = mv_lds<FMT_F32>(lds, H / 4);
-        float4 xv[MG];
-        const float rms = pro.build_x(L, xv);
-        for (int g = threadIdx.x; g < H / 4; g += NT)
-            st_word4(a.w_xn + 4 * (size_t)g, eL, norm4(((const float4*)L.tmp)[g], rms, ((const float4*)a.out_norm)[g], a.zc));
-    });
-    // LM head (tied embedding): the normed vector is polled by a
-    // workgroup's first item and kept in LDS for its others
-    bool have_x = false;
-    each(a.embd.tiles * 2, [&](int rt) {
-        EpiLogits epi{a.logits, a.V, a.cand, a.st, a.bm, a.bs};
-        const MvLds L = mv_lds<FMT_Q4>(lds, a.embd.nblk);
-        if (!have_x) {
-            mv_item<FMT_Q4, P_KBW, 1>(a.embd, rt, 0, 1, ProXnW{WSrc{a.w_xn, eL, err}}, epi, L);
-            have_x = true;
-        } else {
-            mv_item<FMT_Q4, P_KBW, 1>(a.embd, rt, 0, 1, ProKeep{}, epi, L);
+    // final residual and norm (workgroup 0): layer_out[L-1], xn_final for the LM head
+    if (wg == 0) {
+        const PLayer& Q = a.layers[a.L - 1];
+        const uint32_t e = a.tick * (uint32_t)(a.L + 1) + (uint32_t)a.L;
+        const uint64_t* wd = a.w_d;
+        ps_poll(H, [=](int i) { return wd + i; }, e, S.land, err);
+        __syncthreads();
+        float inv = 1.0f;
+        const bool pn = a.post_ffn_norm && Q.post_ffw;
+        if (pn) inv = 1.0f / sqrtf(ps_sumsq(S.land, H, S.red) / (float)H + eps);
+        for (int i = tid; i < H; i += NT) S.xr[i] = S.x1[i] + (pn ? norm_apply_inv(S.land[i], inv, Q.post_ffw[i], zc) : S.land[i]);
+        __syncthreads();
+        const float inv2 = 1.0f / sqrtf(ps_sumsq(S.xr, H, S.red + 4) / (float)H + eps);
+        for (int i = tid; i < H; i += NT) {
+            a.layer_out[(size_t)(a.L - 1) * H + i] = S.xr[i];
+            a.xn_final[i] = norm_apply(S.xr[i], 1.0f / inv2, a.out_norm[i], zc);
         }
-    });
+    }
 }
 
-// Dynamic LDS of the persistent step (floats): the largest matvec item.
-inline size_t persistent_lds_bytes(const gh_model* m) {
-    const gh_config& c = m->cfg;
-    const LayerDev& L0 = m->layers[0];
-    size_t f = 0;
-    auto item = [&](int per_split, int tmp) { f = std::max(f, mv_lds_floats(FMT_Q4, per_split, tmp)); };
-    item(L0.qkv.nblk, c.hidden);
-    item(L0.o.nblk, (c.n_heads + 2) * ATTN_MAX_NC);
-    item(L0.gu.nblk, c.hidden);
-    item((L0.down.nblk + m->pe.S - 1) / m->pe.S, 0);
-    item(m->embd.nblk, 0);
-    // final norm: xs (H) + block-sum pad (H/4) + tmp (H)
-    f = std::max(f, (size_t)(576 + c.hidden + ((c.hidden / 4 + 3) & ~3) + c.hidden));
-    return f * sizeof(float);
+// Interleave a layer's [gate | up] matrix (f_pad rows each) into 64-row
+// chunks of 32 gate rows and the 32 up rows of the same FFN indices.
+__global__ void k_interleave_gu(DMat gu, int f_pad, int F, DMat gi) {
+    const size_t n = (size_t)gi.tiles * gi.nblk * TILE_ROWS;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (size_t)gridDim.x * blockDim.x) {
+        const int rr = (int)(idx % TILE_ROWS);
+        const size_t tk = idx / TILE_ROWS;
+        const int kb = (int)(tk % gi.nblk), t = (int)(tk / gi.nblk);
+        const int r = t * TILE_ROWS + rr, c = r / 64, i = r % 64;
+        const int f = 32 * c + (i & 31);
+        u32x4 code = {0u, 0u, 0u, 0u};
+        uint16_t sc = 0;
+        if (f < F) {
+            const int src = (i < 32 ? 0 : f_pad) + f;
+            const size_t sidx = ((size_t)(src >> 7) * gu.nblk + kb) * TILE_ROWS + (src & 127);
+            code = ((const u32x4*)gu.codes)[sidx];
+            sc = gu.scales[sidx];
+        }
+        ((u32x4*)gi.codes)[idx] = code;
+        ((uint16_t*)gi.scales)[idx] = sc;
+    }
+}
+
+int launch_interleave_gu(const DMat& gu, int f_pad, int F, const DMat& gi, hipStream_t s) {
+    if (gu.fmt != FMT_Q4 || gi.fmt != FMT_Q4 || gu.nblk != gi.nblk)
+        return set_error(GH_ERR_INVALID, "internal: gate/up interleave needs two Q4_0 matrices of one width");
+    const size_t n = (size_t)gi.tiles * gi.nblk * TILE_ROWS;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(k_interleave_gu, dim3(blocks), dim3(256), 0, s, gu, f_pad, F, gi);
+    GH_HIP(hipGetLastError());
+    return GH_OK;
 }
 
 // Per-cache table of layer pointers for the persistent step.
@@ -2760,7 +2956,7 @@ static int persistent_layers(gh_model* m, gh_kv* kv) {
         PLayer& p = h[i];
         p.qkv = L.qkv;
         p.o = L.o;
-        p.gu = L.gu;
+        p.gi = m->p_gi[i];
         p.down = L.down;
         p.attn_norm = L.attn_norm;
         p.q_norm = L.q_norm;
@@ -2783,23 +2979,38 @@ static int persistent_layers(gh_model* m, gh_kv* kv) {
     return GH_OK;
 }
 
+// Shapes the persistent step is built for: Q4_0 weights, head_dim 32 with
+// group 4 (tiny), head_dim 256 with group 2 or 4 (4B, 1B); every K of a
+// row-group matvec within 3072 and H within the down partial's registers.
 int persistent_supported(const gh_model* m) {
     const gh_config& c = m->cfg;
-    const int G = c.n_heads / c.n_kv_heads, MG = (c.hidden / 4 + NT - 1) / NT;
+    const int G = c.n_heads / c.n_kv_heads;
     if (m->fmt != FMT_Q4) return 0;
-    return (c.head_dim == 32 && G == 4 && MG == 1) || (c.head_dim == 256 && G == 4 && MG == 2) ||
-           (c.head_dim == 256 && G == 2 && (MG == 1 || MG == 3));
+    const bool shape = (c.head_dim == 32 && G == 4) || (c.head_dim == 256 && (G == 2 || G == 4));
+    return shape && c.hidden <= 2560 && c.n_heads * c.head_dim <= 3072 && c.hidden % 8 == 0;
 }
 
-// One decode step as the persistent kernel (one workgroup per CU) + the
-// finish kernel, into a sink (graph nodes or stream launches).  The grid
-// is the CU count at one workgroup per CU, so all workgroups are resident;
-// the bounded waits turn anything else into GH_ERR_STATE, not a hang.
+// Word buffers of the persistent step, in floats' worth of words.
+size_t persistent_land(const gh_model* m) {
+    const gh_config& c = m->cfg;
+    const int SL = c.head_dim < 64 ? c.head_dim : 64;
+    size_t f = (size_t)std::max(c.hidden, c.n_heads * c.head_dim);
+    f = std::max(f, (size_t)(m->q_rows_pad + 2 * m->kv_rows_pad));
+    f = std::max(f, (size_t)ATTN_MAX_NC * (2 + SL));
+    f = std::max(f, (size_t)m->p_np * 8);
+    return (f + 3) & ~(size_t)3;
+}
+
+// One decode step as the persistent kernel (one workgroup per CU) + the LM
+// head and the finish kernel, into a sink (graph nodes or stream launches).
+// The grid is the CU count at one workgroup per CU (the dynamic LDS keeps a
+// second one off each CU), so all workgroups are resident; the bounded
+// waits turn anything else into GH_ERR_STATE, not a hang.
 int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     const gh_config& c = m->cfg;
     if (!persistent_supported(m)) return set_error(GH_ERR_INVALID, "persistent step: unsupported shape");
     GH_CHECK(persistent_layers(m, kv));
-    const int hd = c.head_dim, G = c.n_heads / c.n_kv_heads, H = c.hidden, MG = (H / 4 + NT - 1) / NT;
+    const int hd = c.head_dim, G = c.n_heads / c.n_kv_heads, H = c.hidden;
     PArgs a{};
     a.layers = (const PLayer*)kv->d_players;
     a.embd = m->embd;
@@ -2808,21 +3019,23 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     a.rope_local = kv->rope;
     a.rope_global = kv->rope + (size_t)kv->max_seq * hd;
     a.w_qkv = m->w_qkv;
-    a.w_attn = m->w_attn;
+    a.w_st = m->w_attn;
     a.w_o = m->w_o;
-    a.w_gu = m->w_gu;
-    a.w_down = m->w_down;
-    a.w_x = m->w_x;
-    a.w_x1 = m->w_x1;
-    a.w_xn = m->w_xn;
+    a.w_a = m->w_a;
+    a.w_p = m->w_p;
+    a.w_d = m->w_down;
+    a.xn_final = m->xn_final;
+    a.layer_out = m->layer_out;
     a.L = c.n_layers;
     a.H = H;
+    a.nq = c.n_heads;
     a.nkv = c.n_kv_heads;
     a.q_rows_pad = m->q_rows_pad;
     a.kv_rows_pad = m->kv_rows_pad;
-    a.f_pad = m->f_pad;
-    a.S_down = m->pe.S;
+    a.n_chunks = c.ffn / 32;
     a.nc = m->attn_nc;
+    a.np = m->p_np;
+    a.land = (int)persistent_land(m);
     a.eps = c.rms_eps;
     a.escale = sqrtf((float)H);
     a.scale = 1.0f / sqrtf((float)hd);
@@ -2832,25 +3045,31 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     a.post_ffn_norm = (c.flags & GH_FLAG_POST_FFN_NORM) ? 1 : 0;
     a.mode = c.mode;
     a.window = c.sliding_window;
-    a.logits = m->logits;
-    a.cand = m->lm_cand;
-    a.bm = m->lm_m;
-    a.bs = m->lm_s;
-    a.layer_out = m->layer_out;
-    a.V = c.vocab;
     a.host_tick = &m->p_tick;
     a.set_pos(pos);
-    const size_t lds = persistent_lds_bytes(m);
+    const int nbx = std::max(H, c.n_heads * hd) / 32;
+    size_t lds = (mv_lds_floats(FMT_Q4, nbx, 0) + 2 * (size_t)H + a.land + 64 + 64 + 40) * sizeof(float);
+    lds = std::max<size_t>(lds, 96 << 10);  // one workgroup per CU
+    const int kbw = kbw_for(FMT_Q4, (m->layers[0].qkv.nblk + 3) / 4);
     const dim3 grid(m->p_grid), block(NT);
     auto go = [&](void (*fn)(PArgs)) { return sink_launch<0>(sink, "step", 0.0, fn, grid, block, lds, a); };
-    if (hd == 32 && G == 4 && MG == 1) GH_CHECK(go(k_step_persistent<32, 4, 1>));
-    else if (hd == 256 && G == 4 && MG == 2) GH_CHECK(go(k_step_persistent<256, 4, 2>));
-    else if (hd == 256 && G == 2 && MG == 1) GH_CHECK(go(k_step_persistent<256, 2, 1>));
-    else GH_CHECK(go(k_step_persistent<256, 2, 3>));
-    const int n_cand = 2 * m->embd.tiles;  // 64-row LM-head items
-    return sink_launch<1>(sink, "finish", 0.0, k_step_finish<0>, dim3(1), dim3(NT), 0, kv->st, pos,
-                          (const unsigned long long*)m->lm_cand, n_cand, (const float*)m->lm_m, (const float*)m->lm_s, 64,
-                          (const float*)m->logits, c.vocab, (const int32_t*)kv->d_prompt, kv->d_ids);
+    auto by_kbw = [&](auto hdc, auto gc) -> int {
+        constexpr int HD_ = decltype(hdc)::value, G_ = decltype(gc)::value;
+        switch (kbw) {
+            case 1: return go(k_step_ps<HD_, G_, 1>);
+            case 2: return go(k_step_ps<HD_, G_, 2>);
+            case 3: return go(k_step_ps<HD_, G_, 3>);
+            case 4: return go(k_step_ps<HD_, G_, 4>);
+            case 6: return go(k_step_ps<HD_, G_, 6>);
+            case 9: return go(k_step_ps<HD_, G_, 9>);
+            case 10: return go(k_step_ps<HD_, G_, 10>);
+            default: return set_error(GH_ERR_INVALID, "persistent step: register batch %d", kbw);
+        }
+    };
+    if (hd == 32) GH_CHECK(by_kbw(std::integral_constant<int, 32>{}, std::integral_constant<int, 4>{}));
+    else if (G == 4) GH_CHECK(by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 4>{}));
+    else GH_CHECK(by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 2>{}));
+    return enqueue_head(m, kv, sink, pos);
 }
 
 #endif  // GH_IN_TU(2)

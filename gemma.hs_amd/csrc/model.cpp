@@ -271,21 +271,19 @@ int ensure_scratch(gh_model* m) {
             m->persistent = 0;
         } else {
             m->p_grid = cus;
-            GH_CHECK(dev_alloc(m, &m->w_qkv, (size_t)L.qkv.tiles * TILE_ROWS));
-            GH_CHECK(dev_alloc(m, &m->w_attn, (size_t)c.n_kv_heads * m->attn_nc * G * (c.head_dim + 2)));
-            GH_CHECK(dev_alloc(m, &m->w_o, (size_t)L.o.tiles * TILE_ROWS));
-            GH_CHECK(dev_alloc(m, &m->w_gu, (size_t)L.gu.tiles * TILE_ROWS));
-            GH_CHECK(dev_alloc(m, &m->w_down, (size_t)m->pe.S * L.down.tiles * TILE_ROWS));
-            GH_CHECK(dev_alloc(m, &m->w_x, (size_t)c.hidden));
-            GH_CHECK(dev_alloc(m, &m->w_x1, (size_t)c.hidden));
-            GH_CHECK(dev_alloc(m, &m->w_xn, (size_t)c.hidden));
-            // epoch 0 everywhere: no published word matches before its phase
-            const size_t nw[] = {(size_t)L.qkv.tiles * TILE_ROWS, (size_t)c.n_kv_heads * m->attn_nc * G * (c.head_dim + 2),
-                                 (size_t)L.o.tiles * TILE_ROWS, (size_t)L.gu.tiles * TILE_ROWS,
-                                 (size_t)m->pe.S * L.down.tiles * TILE_ROWS, (size_t)c.hidden, (size_t)c.hidden,
+            m->p_np = std::min(c.ffn / 32, cus);
+            const size_t nw[] = {(size_t)L.qkv.tiles * TILE_ROWS,
+                                 (size_t)c.n_kv_heads * m->attn_nc * G * (c.head_dim + 2),
+                                 (size_t)c.n_heads * c.head_dim, (size_t)c.hidden, (size_t)m->p_np * c.hidden,
                                  (size_t)c.hidden};
-            uint64_t* ws[] = {m->w_qkv, m->w_attn, m->w_o, m->w_gu, m->w_down, m->w_x, m->w_x1, m->w_xn};
-            for (int i = 0; i < 8; ++i) GH_HIP(hipMemset(ws[i], 0, nw[i] * sizeof(uint64_t)));
+            uint64_t** ws[] = {&m->w_qkv, &m->w_attn, &m->w_o, &m->w_a, &m->w_p, &m->w_down};
+            for (int i = 0; i < 6; ++i) {
+                GH_CHECK(dev_alloc(m, ws[i], nw[i]));
+                // epoch 0 everywhere: no published word matches before its phase
+                GH_HIP(hipMemset(*ws[i], 0, nw[i] * sizeof(uint64_t)));
+            }
+            m->p_gi.resize(c.n_layers);
+            for (int l = 0; l < c.n_layers; ++l) GH_CHECK(alloc_mat(m, m->p_gi[l], FMT_Q4, 2 * c.ffn, c.hidden));
         }
     }
     return GH_OK;
@@ -338,7 +336,14 @@ int prefill_reserve(gh_model* m, int n) {
 int model_ready(gh_model* m) {
     if (!m) return set_error(GH_ERR_INVALID, "null model");
     GH_CHECK(gh_model_check(m));
-    return ensure_scratch(m);
+    GH_CHECK(ensure_scratch(m));
+    if (m->persistent && !m->p_gi_ok) {  // the persistent step's gate/up layout, from the uploaded weights
+        for (int l = 0; l < m->cfg.n_layers; ++l)
+            GH_CHECK(launch_interleave_gu(m->layers[l].gu, m->f_pad, m->cfg.ffn, m->p_gi[l], m->ctx->stream));
+        GH_HIP(hipStreamSynchronize(m->ctx->stream));
+        m->p_gi_ok = true;
+    }
+    return GH_OK;
 }
 
 // The step as a graph: a linear chain of kernel nodes built explicitly, so
@@ -1016,10 +1021,12 @@ extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, con
             GH_CHECK(upload_rows(m->ctx, L.o, 0, dtype, data, nbytes, H, c.n_heads * hd, ftz));
             break;
         case K_GATE:
+            m->p_gi_ok = false;
             GH_CHECK(ensure_fmt(m, dtype));
             GH_CHECK(upload_rows(m->ctx, L.gu, 0, dtype, data, nbytes, c.ffn, H, ftz));
             break;
         case K_UP:
+            m->p_gi_ok = false;
             GH_CHECK(ensure_fmt(m, dtype));
             GH_CHECK(upload_rows(m->ctx, L.gu, m->f_pad, dtype, data, nbytes, c.ffn, H, ftz));
             break;

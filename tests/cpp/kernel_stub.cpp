@@ -14,6 +14,8 @@ int Profiler::kind_of(const char* name) {
 int enqueue_step(gh_model*, gh_kv*, Sink&, int) { return GH_OK; }
 int persistent_supported(const gh_model*) { return 0; }
 int enqueue_persistent(gh_model*, gh_kv*, Sink&, int) { return GH_OK; }
+size_t persistent_land(const gh_model*) { return 0; }
+int launch_interleave_gu(const DMat&, int, int, const DMat&, hipStream_t) { return GH_OK; }
 int pf_splits(const DMat&, int, int* kb_per) {
     if (kb_per) *kb_per = 1;
     return 1;

@@ -440,13 +440,37 @@ def test_temperature_sampling_in_the_step(ctx):
         kv.set_sampling(-1.0, 0)
 
 
-def test_persistent_step_matches_graph_step(ctx, monkeypatch):
-    """The persistent step kernel (one workgroup per CU, phases exchanging
-    epoch-tagged words) gives the graph step's ids and per-layer states."""
-    cfg = gh.preset("gemma3-1b")
+@pytest.mark.parametrize("shape", ["tiny", "gemma3-1b", "mini4b"])
+def test_persistent_step_matches_graph_step(ctx, monkeypatch, shape):
+    """The persistent step (GH_PERSISTENT=1: one workgroup per CU, phases
+    exchanging epoch-tagged words) against the graph step on the same
+    weights: every layer's hidden state and the logits within 1e-4 relative
+    at every step, the same argmax where the margin allows, and the same
+    generated ids.  mini4b: 4B head shapes (8 q / 4 kv heads), window 5,
+    global every 2nd layer."""
+    if shape == "tiny":
+        cfg = gh.preset("tiny")
+    elif shape == "gemma3-1b":
+        cfg = gh.preset("gemma3-1b")
+    else:
+        cfg = gh.preset("gemma3-4b")
+        cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 4, 1024
+        cfg.sliding_window, cfg.global_every = 5, 2
+    cfg.max_seq = 64
     ref = _gpu_model(ctx, cfg, 1234, True)
-    prompt = gh.synth_tokens(1, "prompt", 16, cfg.vocab)
-    want = gh.generate(ref, gh.KVCache(ref, 256), prompt, 24)
+    gh.runGemmaInferenceCached(ref, 0, gh.KVCache(ref, 4), want_logits=False)  # fixes ref's mode: graph step
     monkeypatch.setenv("GH_PERSISTENT", "1")
     m = _gpu_model(ctx, cfg, 1234, True)
-    np.testing.assert_array_equal(gh.generate(m, gh.KVCache(m, 256), prompt, 24), want)
+    prompt = gh.synth_tokens(1, "prompt", 12, cfg.vocab)
+    kr, kp = gh.KVCache(ref, 64), gh.KVCache(m, 64)
+    for pos, t in enumerate(prompt):
+        lr, _, yr, nr = gh.runGemmaInferenceCachedWithLayer0(ref, int(t), kr)
+        lp, _, yp, npers = gh.runGemmaInferenceCachedWithLayer0(m, int(t), kp)
+        for l in range(cfg.n_layers):
+            assert rel_err(yp[l], yr[l]) < ACT_TOL, (pos, l)
+        assert rel_err(lp, lr) < ACT_TOL, pos
+        srt = np.sort(lr)
+        if srt[-1] - srt[-2] > 1e-3 * np.max(np.abs(lr)):
+            assert npers == nr, pos
+    want = gh.generate(ref, gh.KVCache(ref, 64), prompt, 20)
+    np.testing.assert_array_equal(gh.generate(m, gh.KVCache(m, 64), prompt, 20), want)
