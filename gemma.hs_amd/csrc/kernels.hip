@@ -2359,6 +2359,7 @@ struct PArgs {
     float* xn_final;  // [H] normed final state (plain stores; read by the LM head kernel)
     float* layer_out; // [L][H]
     int L, H, nq, nkv, q_rows_pad, kv_rows_pad, n_chunks, nc, np, land;
+    int pf_gu, pf_down, pf_off;  // phase D weights staged in LDS (at float pf_off of the dynamic LDS)
     float eps, escale, scale;
     int zc, use_qk_norm, post_attn_norm, post_ffn_norm, mode, window;
     int pb[2], pe[2], ch[2], n_used[2];  // attention range at pos: [0] local, [1] global layer
@@ -2631,6 +2632,85 @@ struct EpiLdsRows {
     }
 };
 
+// Phase D weights staged in LDS ahead of the phase (floats from the region
+// base): the gate/up chunk's codes [nb][64 rows][16 B] (gc) and scales
+// [nb][64][2 B] (gs); with the down block, its codes [rows][16 B] (dc) and
+// scales [rows][2 B] (ds).  Each part is whole 1 KiB wave loads.
+struct PfLayout {
+    int gc, gs, dc, ds, total;
+};
+__host__ __device__ inline PfLayout pf_layout(int nb, int down_tiles, bool down) {
+    PfLayout p;
+    p.gc = 0;
+    p.gs = nb * 256;
+    p.dc = p.gs + (nb + 7) / 8 * 256;
+    p.ds = p.dc + (down ? 2 * down_tiles * 256 : 0);
+    p.total = p.ds + (down ? (down_tiles + 3) / 4 * 256 : 0);
+    return p;
+}
+
+// 16 bytes per lane from a buffer view straight into LDS: lane i's bytes
+// land at dst + 16 i (dst wave-uniform); offsets outside the view write zeros.
+__device__ __forceinline__ void lds_dma16(const BufView& v, uint32_t off, float* dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(v.r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, CP_NT);
+}
+
+// Issue the staging of chunk c (gate/up rows 64c .. 64c + 63 of the
+// interleaved matrix: tile c / 2, half c % 2) and, with `down`, of column
+// block c of the down matrix.  The loads are only issued here; the next
+// wait on this workgroup's vector memory (the O-row poll) covers them.
+__device__ void ps_prefetch(const PLayer& P, int c, float* pf, bool down) {
+    const PfLayout Y = pf_layout(P.gi.nblk, P.down.tiles, down);
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const MatViews G(P.gi);
+    const uint32_t nb = (uint32_t)P.gi.nblk, t = (uint32_t)(c >> 1), rh = (uint32_t)(c & 1) * 64u;
+    for (int kb = wave; kb < (int)nb; kb += 4)
+        lds_dma16(G.codes, ((t * nb + (uint32_t)kb) * TILE_ROWS + rh + (uint32_t)lane) * 16u, pf + Y.gc + kb * 256);
+    for (int i = wave; i < ((int)nb + 7) / 8; i += 4) {
+        const uint32_t kb = (uint32_t)(8 * i + (lane >> 3));
+        lds_dma16(G.scales, kb < nb ? ((t * nb + kb) * TILE_ROWS + rh) * 2u + (uint32_t)(lane & 7) * 16u : OOB,
+                  pf + Y.gs + i * 256);
+    }
+    if (down) {
+        const MatViews D(P.down);
+        const uint32_t nd = (uint32_t)P.down.nblk, td = (uint32_t)P.down.tiles, cc = (uint32_t)c;
+        for (int j = wave; j < 2 * (int)td; j += 4)
+            lds_dma16(D.codes, (((uint32_t)(j >> 1) * nd + cc) * TILE_ROWS + (uint32_t)(j & 1) * 64u + (uint32_t)lane) * 16u,
+                      pf + Y.dc + j * 256);
+        for (int i = wave; i < ((int)td + 3) / 4; i += 4) {
+            const uint32_t tt = (uint32_t)(4 * i + (lane >> 4));
+            lds_dma16(D.scales, tt < td ? (tt * nd + cc) * TILE_ROWS * 2u + (uint32_t)(lane & 15) * 16u : OOB,
+                      pf + Y.ds + i * 256);
+        }
+    }
+}
+
+// The staged chunk's 64 gate/up rows against the slice in xs/sxs (the
+// whole row): wave w sums blocks [w nb / 4, (w + 1) nb / 4) of row lane in
+// block order, then wave 0 adds the four waves' sums, the summation of the
+// register path (mv_item_valu with KBW-block batches), into y[0 .. 63].
+__device__ void ps_gu_lds(const float* pf, int nb, const MvLds& L, float* y) {
+    const PfLayout Y = pf_layout(nb, 0, false);
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int k0 = nb * wave >> 2, k1 = nb * (wave + 1) >> 2;
+    const u32x4* cw = (const u32x4*)(pf + Y.gc) + lane;
+    const uint16_t* sw = (const uint16_t*)(pf + Y.gs) + lane;
+    float acc = 0.0f;
+    for (int kb = k0; kb < k1; ++kb) {
+        const u32x4 w = cw[kb * 64];
+        const float4* xv = (const float4*)(L.xs + kb * 32);
+        float d = 0.0f;
+        d = dot_q4_word(w.x, xv[0], xv[4], d);
+        d = dot_q4_word(w.y, xv[1], xv[5], d);
+        d = dot_q4_word(w.z, xv[2], xv[6], d);
+        d = dot_q4_word(w.w, xv[3], xv[7], d);
+        acc = fmaf(h2f(sw[kb * 64]), d - 8.0f * L.sxs[kb], acc);
+    }
+    L.red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave == 0) y[lane] = (L.red[lane] + L.red[64 + lane]) + (L.red[128 + lane] + L.red[192 + lane]);
+}
+
 template <int HD, int G, int KBW>
 __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
     extern __shared__ float lds[];
@@ -2645,6 +2725,8 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
     S.land = S.x1 + H;
     S.red = S.land + a.land;
     S.gu = S.red + 64;
+    float* const pf = lds + a.pf_off;
+    const bool staged = a.pf_gu && wg < a.n_chunks;  // chunk wg's phase D weights go through LDS
     const float eps = a.eps;
     const int zc = a.zc;
 
@@ -2782,6 +2864,9 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 __syncthreads();
             }
         }
+        // this workgroup's attention and merge waits are behind it: stage its
+        // phase D weights now, so they stream during phase C
+        if (staged) ps_prefetch(P, wg, pf, a.pf_down != 0);
         // ---------------- C: O projection rows
         {
             const int ngrp = H / 8;
@@ -2823,14 +2908,33 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
             };
             bool built = false;
             for (int c = wg; c < a.n_chunks; c += nwg) {
-                load_down(c);
-                if (!built) {
+                const bool from_lds = staged && c == wg, down_lds = from_lds && a.pf_down;
+                if (!down_lds) load_down(c);
+                if (from_lds) {
+                    ProFfnPs::Regs r0;
+                    pro.load(r0, 0, H);
+                    pro.template finish<FMT_Q4>(L, r0, 0, H);
+                    __syncthreads();
+                    ps_gu_lds(pf, P.gi.nblk, L, S.gu);
+                    built = true;
+                } else if (!built) {
                     mv_item_valu<FMT_Q4, KBW, 1, 1>(P.gi, c, 0, 1, pro, EpiLdsRows{S.gu}, L);
                     built = true;
                 } else {
                     mv_item_valu<FMT_Q4, KBW, 1, 1>(P.gi, c, 0, 1, ProKeep{}, EpiLdsRows{S.gu}, L);
                 }
                 __syncthreads();
+                if (down_lds) {  // the staged down block of this thread's rows
+                    const PfLayout Y = pf_layout(P.gi.nblk, P.down.tiles, true);
+#pragma unroll
+                    for (int k = 0; k < PS_KR; ++k) {
+                        const int r = tid + k * NT;
+                        if (r < H) {
+                            dw[k] = ((const u32x4*)(pf + Y.dc))[r];
+                            ds[k] = ((const uint16_t*)(pf + Y.ds))[r];
+                        }
+                    }
+                }
                 // GeGLU of the chunk's 32 rows (MLP.hs:384-447) as a Q4_0 input block: h[0..31] in
                 // the emit format (16..31 scaled by 1/16) and sum(h)
                 float* hb = S.gu + 64;
@@ -3047,28 +3151,45 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     a.window = c.sliding_window;
     a.host_tick = &m->p_tick;
     a.set_pos(pos);
-    const int nbx = std::max(H, c.n_heads * hd) / 32;
-    size_t lds = (mv_lds_floats(FMT_Q4, nbx, 0) + 2 * (size_t)H + a.land + 64 + 64 + 40) * sizeof(float);
-    lds = std::max<size_t>(lds, 96 << 10);  // one workgroup per CU
     const int kbw = kbw_for(FMT_Q4, (m->layers[0].qkv.nblk + 3) / 4);
-    const dim3 grid(m->p_grid), block(NT);
-    auto go = [&](void (*fn)(PArgs)) { return sink_launch<0>(sink, "step", 0.0, fn, grid, block, lds, a); };
-    auto by_kbw = [&](auto hdc, auto gc) -> int {
+    void (*fn)(PArgs) = nullptr;
+    auto by_kbw = [&](auto hdc, auto gc) {
         constexpr int HD_ = decltype(hdc)::value, G_ = decltype(gc)::value;
         switch (kbw) {
-            case 1: return go(k_step_ps<HD_, G_, 1>);
-            case 2: return go(k_step_ps<HD_, G_, 2>);
-            case 3: return go(k_step_ps<HD_, G_, 3>);
-            case 4: return go(k_step_ps<HD_, G_, 4>);
-            case 6: return go(k_step_ps<HD_, G_, 6>);
-            case 9: return go(k_step_ps<HD_, G_, 9>);
-            case 10: return go(k_step_ps<HD_, G_, 10>);
-            default: return set_error(GH_ERR_INVALID, "persistent step: register batch %d", kbw);
+            case 1: fn = k_step_ps<HD_, G_, 1>; break;
+            case 2: fn = k_step_ps<HD_, G_, 2>; break;
+            case 3: fn = k_step_ps<HD_, G_, 3>; break;
+            case 4: fn = k_step_ps<HD_, G_, 4>; break;
+            case 6: fn = k_step_ps<HD_, G_, 6>; break;
+            case 9: fn = k_step_ps<HD_, G_, 9>; break;
+            case 10: fn = k_step_ps<HD_, G_, 10>; break;
+            default: break;
         }
     };
-    if (hd == 32) GH_CHECK(by_kbw(std::integral_constant<int, 32>{}, std::integral_constant<int, 4>{}));
-    else if (G == 4) GH_CHECK(by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 4>{}));
-    else GH_CHECK(by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 2>{}));
+    if (hd == 32) by_kbw(std::integral_constant<int, 32>{}, std::integral_constant<int, 4>{});
+    else if (G == 4) by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 4>{});
+    else by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 2>{});
+    if (!fn) return set_error(GH_ERR_INVALID, "persistent step: register batch %d", kbw);
+    // dynamic LDS: the matvec slice, x, x1, the landing area, reductions and
+    // the chunk rows, then the staged phase D weights where the CU's LDS
+    // holds them beside the kernel's static arrays
+    const int nbx = std::max(H, c.n_heads * hd) / 32;
+    const size_t base = ((mv_lds_floats(FMT_Q4, nbx, 0) + 2 * (size_t)H + a.land + 64 + 128 + 3) & ~(size_t)3) * sizeof(float);
+    hipFuncAttributes fa{};
+    GH_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)));
+    int dev_lds = 0;
+    GH_HIP(hipDeviceGetAttribute(&dev_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, m->ctx->device));
+    const size_t budget = (size_t)dev_lds > fa.sharedSizeBytes ? (size_t)dev_lds - fa.sharedSizeBytes : 0;
+    const int nb_gu = m->p_gi[0].nblk, td = m->layers[0].down.tiles;
+    const size_t with_down = (size_t)pf_layout(nb_gu, td, true).total * sizeof(float);
+    const size_t gu_only = (size_t)pf_layout(nb_gu, td, false).total * sizeof(float);
+    a.pf_off = (int)(base / sizeof(float));
+    a.pf_gu = base + gu_only <= budget ? 1 : 0;
+    a.pf_down = base + with_down <= budget ? 1 : 0;
+    const size_t need = base + (a.pf_down ? with_down : a.pf_gu ? gu_only : 0);
+    const size_t lds = std::max<size_t>(need, 96 << 10);  // one workgroup per CU
+    if (lds > budget) return set_error(GH_ERR_INVALID, "persistent step: %zu B of LDS exceed the device's %zu", lds, budget);
+    GH_CHECK(sink_launch<0>(sink, "step", 0.0, fn, dim3(m->p_grid), dim3(NT), lds, a));
     return enqueue_head(m, kv, sink, pos);
 }
 
