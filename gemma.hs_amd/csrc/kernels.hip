@@ -1170,12 +1170,15 @@ struct ProGeglu {
 // ------------------------------------------------------------------
 constexpr int XCHG_SPIN = 1 << 18;
 
+// (global address space: vector-memory instructions only, so LDS waits
+// never wait for a word in flight)
+typedef __attribute__((address_space(1))) uint64_t gword;
 __device__ __forceinline__ void st_word(uint64_t* p, uint32_t epoch, float v) {
-    __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((gword*)p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((gword*)const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 
@@ -1542,22 +1545,24 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
     const int pg = lane / LPV, dq = lane % LPV, slot = wave * PGW + pg;
     const int kq = lane & 7;                       // score phase: lane within the position's 8
     const int kp = wave * 8 + (lane >> 3);         // score phase: position within the sub-chunk
-    const float* kbase = a.kc + (size_t)g * HD + 4 * kq;
-    const float* vbase = a.vc + (size_t)g * HD + 4 * dq;
+    // K/V rows [0, pe) as buffer views: vector-memory loads only, so the LDS
+    // waits between them (lgkmcnt) never wait for the cache rows in flight
+    const BufView KC(a.kc, (size_t)a.pe * pstride * 4), VC(a.vc, (size_t)a.pe * pstride * 4);
+    const uint32_t kcol = 4u * (uint32_t)(g * HD + 4 * kq), vcol = 4u * (uint32_t)(g * HD + 4 * dq);
 
     // Loads are unconditional, from rows clamped into [c0, c1): rows past the
     // chunk are masked in the softmax / P.V, and row pos is replaced from LDS.
     float4 kr[K4], vr[VPS];
     auto load_k = [&](int s0) {
-        const float* src = kbase + (size_t)min(s0 + kp, c1 - 1) * pstride;
+        const uint32_t ko = 4u * (uint32_t)min(s0 + kp, c1 - 1) * (uint32_t)pstride + kcol;
 #pragma unroll
-        for (int i = 0; i < K4; ++i) kr[i] = *(const float4*)(src + 32 * i);
+        for (int i = 0; i < K4; ++i) kr[i] = KC.f4(ko + 128u * i);
     };
     auto load_v = [&](int s0) {
 #pragma unroll
         for (int k = 0; k < VPS; ++k) {
             const int pl = min(slot + k * NSLOT, SUB - 1);
-            vr[k] = *(const float4*)(vbase + (size_t)min(s0 + pl, c1 - 1) * pstride);
+            vr[k] = VC.f4(4u * (uint32_t)min(s0 + pl, c1 - 1) * (uint32_t)pstride + vcol);
         }
     };
     // 1. the QKV partials of this token (step mode), the QK-norm weights and
@@ -1631,10 +1636,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int j, const
         }
         __syncthreads();
         GH_MARK(3);
-        if (j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
+        if (j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534); global stores (no LDS counter)
+            typedef __attribute__((address_space(1))) float gfloat;
             for (int i = tid; i < HD; i += NT) {
-                a.kc[((size_t)pos * a.nkv + g) * HD + i] = ks[i];
-                a.vc[((size_t)pos * a.nkv + g) * HD + i] = vs[i];
+                ((gfloat*)a.kc)[((size_t)pos * a.nkv + g) * HD + i] = ks[i];
+                ((gfloat*)a.vc)[((size_t)pos * a.nkv + g) * HD + i] = vs[i];
             }
         }
     } else {
@@ -2740,8 +2746,16 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
     }
     __syncthreads();
 
+    const float* prev_post_ffw = nullptr;  // post-FFN norm weight of layer l - 1
     for (int l = 0; l < a.L; ++l) {
-        const PLayer& P = a.layers[l];
+        const PLayer P = a.layers[l];  // one scalar-load burst, in flight with the layer's first wait
+        // The exchange buffers' addresses are re-derived in every layer (the
+        // empty asm hides that they do not change): per-thread addresses built
+        // from them would otherwise be hoisted out of the layer loop and held
+        // in registers for the whole kernel.
+        uint64_t *w_qkv = a.w_qkv, *w_st = a.w_st, *w_o = a.w_o, *w_a = a.w_a, *w_p = a.w_p, *w_d = a.w_d;
+        float* layer_out = a.layer_out;
+        asm volatile("" : "+s"(w_qkv), "+s"(w_st), "+s"(w_o), "+s"(w_a), "+s"(w_p), "+s"(w_d), "+s"(layer_out));
         const uint32_t e = a.tick * (uint32_t)(a.L + 1) + (uint32_t)l + 1u;
         // ---------------- A: residual update, pre-attention norm, QKV rows
         {
@@ -2751,8 +2765,8 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
             rg_load(R, P.qkv, V, wg);  // out of range: zeros, no traffic
             // the norm weights of this thread's float4 groups, in flight with the weights
             const int ng4 = H >> 2;
-            const bool pn = l > 0 && a.post_ffn_norm && a.layers[l - 1].post_ffw;
-            const BufView WP(pn ? a.layers[l - 1].post_ffw : nullptr, pn ? (size_t)H * 4 : 0), WN(P.attn_norm, (size_t)H * 4);
+            const bool pn = l > 0 && a.post_ffn_norm && prev_post_ffw;
+            const BufView WP(pn ? prev_post_ffw : nullptr, pn ? (size_t)H * 4 : 0), WN(P.attn_norm, (size_t)H * 4);
             float4 wpv[PS_MG], wnv[PS_MG];
 #pragma unroll
             for (int b = 0; b < PS_MG; ++b) {
@@ -2762,7 +2776,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
             }
             float4 xv[PS_MG];
             if (l > 0) {
-                const uint64_t* wd = a.w_d;
+                const uint64_t* wd = w_d;
                 ps_poll(H, [=](int i) { return wd + i; }, e - 1u, S.land, err);
                 __syncthreads();
                 float inv = 1.0f;
@@ -2774,7 +2788,9 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                         const float4 d = ((const float4*)S.land)[gi];
                         xv[b] = ((const float4*)S.x1)[gi] + (pn ? norm4i(d, inv, wpv[b], zc) : d);
                         ((float4*)S.xr)[gi] = xv[b];
-                        if (wg == 0) ((float4*)(a.layer_out + (size_t)(l - 1) * H))[gi] = xv[b];
+                        if (wg == 0)
+                            *(__attribute__((address_space(1))) f32x4*)(layer_out + (size_t)(l - 1) * H + 4 * gi) =
+                                __builtin_bit_cast(f32x4, xv[b]);
                     }
                 }
             } else {
@@ -2798,7 +2814,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
             for (int grp = wg; grp < ngrp; grp += nwg) {
                 if (grp != wg) rg_load(R, P.qkv, V, grp);
                 const float y = rg_dot(R, P.qkv.nblk, L, S.red + 8);
-                if (tid < 8) st_word(a.w_qkv + grp * 8 + tid, e, y);
+                if (tid < 8) st_word(w_qkv + grp * 8 + tid, e, y);
             }
         }
         // ---------------- B: attention chunks
@@ -2830,7 +2846,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
             aa.n_used = nu;
             for (int it = wg; it < a.nkv * nu; it += nwg) {
                 const int g = it / nu, j = it % nu;
-                attn_item<HD, G, true>(aa, g, j, QkvPoll{a.w_qkv, e, err}, AttnOutWords{a.w_st, e});
+                attn_item<HD, G, true>(aa, g, j, QkvPoll{w_qkv, e, err}, AttnOutWords{w_st, e});
                 __syncthreads();
             }
         }
@@ -2841,7 +2857,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
             const size_t stride = (size_t)G * (HD + 2);
             for (int it = nwg - 1 - wg; it >= 0 && it < nitem; it += nwg) {
                 const int h = it / nsl, d0 = (it % nsl) * SL, g = h / G, hl = h % G;
-                const uint64_t* base = a.w_st + (size_t)g * a.nc * stride;
+                const uint64_t* base = w_st + (size_t)g * a.nc * stride;
                 // land: m[nu] | l[nu] | o[nu][SL]
                 ps_poll(nu * (2 + SL), [=](int i) {
                     if (i < nu) return base + (size_t)i * stride + hl;
@@ -2859,7 +2875,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                         den += S.land[nu + j] * w;
                         o += w * S.land[2 * nu + j * SL + tid];
                     }
-                    st_word(a.w_o + (size_t)h * HD + d0 + tid, e, o / den);
+                    st_word(w_o + (size_t)h * HD + d0 + tid, e, o / den);
                 }
                 __syncthreads();
             }
@@ -2874,7 +2890,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 const MatViews V(P.o);
                 RowRegs R;
                 rg_load(R, P.o, V, wg);
-                const uint64_t* wo = a.w_o;
+                const uint64_t* wo = w_o;
                 ps_poll(QK, [=](int i) { return wo + i; }, e, S.land, err);
                 __syncthreads();
                 ps_emit(L, S.land, QK, 1.0f, nullptr, zc);
@@ -2882,13 +2898,13 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 for (int grp = wg; grp < ngrp; grp += nwg) {
                     if (grp != wg) rg_load(R, P.o, V, grp);
                     const float y = rg_dot(R, P.o.nblk, L, S.red + 8);
-                    if (tid < 8) st_word(a.w_a + grp * 8 + tid, e, y);
+                    if (tid < 8) st_word(w_a + grp * 8 + tid, e, y);
                 }
             }
         }
         // ---------------- D: post-attention residual, pre-FFN norm, gate/up chunks, down partial
         {
-            ProFfnPs pro{a.w_a, a.post_attn_norm ? P.post_attn : nullptr, P.ffn_norm ? P.ffn_norm : P.post_attn,
+            ProFfnPs pro{w_a, a.post_attn_norm ? P.post_attn : nullptr, P.ffn_norm ? P.ffn_norm : P.post_attn,
                          S, e, err, H, zc, eps};
             float part[PS_KR];  // this thread's rows t + 256 k of the down partial
 #pragma unroll
@@ -2966,7 +2982,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 pro.template finish<FMT_Q4>(L, r0, 0, H);
                 __syncthreads();
             } else if (wg < a.np) {
-                uint64_t* pw = a.w_p + (size_t)wg * H;
+                uint64_t* pw = w_p + (size_t)wg * H;
 #pragma unroll
                 for (int k = 0; k < PS_KR; ++k) {
                     const int r = tid + k * NT;
@@ -2979,7 +2995,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
             const int ngrp = H / 8;
             for (int grp = wg; grp < ngrp; grp += nwg) {
                 // land[p * 8 + r] = partial p of row 8 grp + r
-                const uint64_t* wp = a.w_p + grp * 8;
+                const uint64_t* wp = w_p + grp * 8;
                 ps_poll(a.np * 8, [=](int i) { return wp + (size_t)(i >> 3) * H + (i & 7); }, e, S.land, err);
                 __syncthreads();
                 float s = 0.0f;
@@ -2990,11 +3006,12 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 if ((tid & 63) < 8) S.red[16 + (tid >> 6) * 8 + (tid & 7)] = s;
                 __syncthreads();
                 if (tid < 8)
-                    st_word(a.w_d + grp * 8 + tid, e,
+                    st_word(w_d + grp * 8 + tid, e,
                             (S.red[16 + tid] + S.red[24 + tid]) + (S.red[32 + tid] + S.red[40 + tid]));
                 __syncthreads();
             }
         }
+        prev_post_ffw = P.post_ffw;
     }
     // final residual and norm (workgroup 0): layer_out[L-1], xn_final for the LM head
     if (wg == 0) {
@@ -3151,7 +3168,7 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     a.window = c.sliding_window;
     a.host_tick = &m->p_tick;
     a.set_pos(pos);
-    const int kbw = kbw_for(FMT_Q4, (m->layers[0].qkv.nblk + 3) / 4);
+    int kbw = kbw_for(FMT_Q4, (m->layers[0].qkv.nblk + 3) / 4);
     void (*fn)(PArgs) = nullptr;
     auto by_kbw = [&](auto hdc, auto gc) {
         constexpr int HD_ = decltype(hdc)::value, G_ = decltype(gc)::value;
@@ -3166,10 +3183,14 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             default: break;
         }
     };
-    if (hd == 32) by_kbw(std::integral_constant<int, 32>{}, std::integral_constant<int, 4>{});
-    else if (G == 4) by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 4>{});
-    else by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 2>{});
-    if (!fn) return set_error(GH_ERR_INVALID, "persistent step: register batch %d", kbw);
+    auto pick = [&] {
+        fn = nullptr;
+        if (hd == 32) by_kbw(std::integral_constant<int, 32>{}, std::integral_constant<int, 4>{});
+        else if (G == 4) by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 4>{});
+        else by_kbw(std::integral_constant<int, 256>{}, std::integral_constant<int, 2>{});
+        return fn != nullptr;
+    };
+    if (!pick()) return set_error(GH_ERR_INVALID, "persistent step: register batch %d", kbw);
     // dynamic LDS: the matvec slice, x, x1, the landing area, reductions and
     // the chunk rows, then the staged phase D weights where the CU's LDS
     // holds them beside the kernel's static arrays
@@ -3186,6 +3207,15 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     a.pf_off = (int)(base / sizeof(float));
     a.pf_gu = base + gu_only <= budget ? 1 : 0;
     a.pf_down = base + with_down <= budget ? 1 : 0;
+    // every chunk staged: the register path (the only user of the batch
+    // width) never runs, and the narrowest variant has the fewest registers
+    if (a.pf_gu && a.n_chunks <= m->p_grid && kbw != 1) {
+        kbw = 1;
+        if (!pick()) return set_error(GH_ERR_INVALID, "persistent step: register batch %d", kbw);
+        hipFuncAttributes f1{};
+        GH_HIP(hipFuncGetAttributes(&f1, reinterpret_cast<const void*>(fn)));
+        if (f1.sharedSizeBytes != fa.sharedSizeBytes) return set_error(GH_ERR_INVALID, "persistent step: static LDS differs by batch width");
+    }
     const size_t need = base + (a.pf_down ? with_down : a.pf_gu ? gu_only : 0);
     const size_t lds = std::max<size_t>(need, 96 << 10);  // one workgroup per CU
     if (lds > budget) return set_error(GH_ERR_INVALID, "persistent step: %zu B of LDS exceed the device's %zu", lds, budget);
