@@ -11,9 +11,9 @@ stream, device-synchronised on both sides).
 
 Prints ONE JSON line with tok/s; per-kernel-kind durations (HIP events
 around back-to-back replays of that kernel kind at the last decoded
-position, on the step stream); the roofline of the LM head, the largest
-Q4_0 matvec; and the CPU baseline (the C oracle on the host cores, bounded
-sample).
+position, on the step stream); the roofline of gate/up, the per-layer
+kernel with the largest share of the step (the LM head, the largest single
+matvec, beside it); and the CPU baseline (bounded samples on the host cores).
 """
 from __future__ import annotations
 
@@ -32,10 +32,11 @@ HBM_PEAK_GBPS = 8000.0
 WEIGHT_SEED = 1234
 PROMPT_SEED = 1
 N_PROMPT = 128
-# HBM bytes per LM-head launch from two rocprofv3 --pmc passes
-# (profiles/lm_head_gemma3-1b_decode.md): FETCH_SIZE 83,584.2 KiB x 1.99978 and
-# WRITE_SIZE 1,152.0 KiB x 1.0, each factor = the bytes a 256 MiB device copy
-# moves / what the counter reads for that copy.
+# HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, then
+# WRITE_SIZE, each scaled by bytes / counter of a 256 MiB device copy):
+# gate/up from profiles/step_kernels_gemma3-1b_decode.md (9,611,151 fetched +
+# 225,792 written), the LM head from profiles/lm_head_gemma3-1b_decode.md.
+GATE_UP_TRAFFIC_BYTES = 9_836_943
 LM_HEAD_TRAFFIC_BYTES = 172_340_835
 # Back-to-back replays per kernel kind in the event-timed pass (a few ms
 # each).  The LM head gets 40 (1.1 ms of streaming): inside the decode loop it
@@ -311,16 +312,22 @@ def main(argv=None) -> int:
     for t in timings.values():
         log(f"  {t.name:10s} x{t.launches_per_step:3d}/step avg {t.avg_us:8.2f} us  {t.gbps:8.1f} GB/s")
     step_bytes = sum(t.bytes_per_launch * t.launches_per_step for t in timings.values())
-    # roofline kernel: the LM head, the largest Q4_0 matvec (262144 x 1152)
-    lm = timings["lm_head"]
-    roofline = {"bound": "hbm", "achieved": round(lm.gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(lm.gbps / HBM_PEAK_GBPS, 4), "traffic": LM_HEAD_TRAFFIC_BYTES,
-                "traffic_source": "rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated)", "kernel": "lm_head",
-                "bytes_per_launch": int(lm.bytes_per_launch), "avg_us": round(lm.avg_us, 3)}
+    # roofline kernel: gate/up (26 launches per token, the largest share of
+    # the step); algorithmic bytes per launch = the fused [gate | up] Q4_0
+    # weights (2 x 6912 x 1152 / 32 x 18 B) + the input and the output rows
+    gu, lm = timings["gate_up"], timings["lm_head"]
+    roofline = {"bound": "hbm", "achieved": round(gu.gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(gu.gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
+                "traffic_source": "rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated)", "kernel": "gate_up",
+                "bytes_per_launch": int(gu.bytes_per_launch), "avg_us": round(gu.avg_us, 3),
+                "lm_head": {"achieved": round(lm.gbps, 1), "frac": round(lm.gbps / HBM_PEAK_GBPS, 4),
+                            "traffic": LM_HEAD_TRAFFIC_BYTES, "bytes_per_launch": int(lm.bytes_per_launch),
+                            "avg_us": round(lm.avg_us, 3)}}
     # the box's practical ceiling: 1 GiB read once per launch (non-temporal 16 B loads)
     sr_gbps, sr_us = gh.stream_read_gbps(ctx, 1 << 30, 20)
     log(f"  stream read 1 GiB: {sr_us:.1f} us -> {sr_gbps:.1f} GB/s")
     roofline["measured_stream_read"] = {"gbps": round(sr_gbps, 1), "bytes": 1 << 30, "avg_us": round(sr_us, 2),
+                                        "gate_up_frac": round(gu.gbps / sr_gbps, 4),
                                         "lm_head_frac": round(lm.gbps / sr_gbps, 4)}
 
     out = {
