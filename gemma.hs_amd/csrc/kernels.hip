@@ -2317,11 +2317,14 @@ __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, cons
 //   B2 merge: (q head, 64-dim slice) items on the last workgroups: the chunk
 //      states of the head -> its attention output slice.
 //   C  O projection: 8-row groups (input: the merged output).
-//   D  every workgroup: x1 = x + postnorm(o) and n2 = norm(x1); workgroup w
-//      takes 64-row chunks w, w + W, ... of the gate/up matrix interleaved as
-//      32 gate + 32 up rows (so a chunk yields 32 GeGLU values), and
-//      multiplies them into the matching 32-column block of the down matrix:
-//      one down partial P_w[H] per workgroup.
+//   D  every workgroup: x1 = x + postnorm(o) and n2 = norm(x1); the 64-row
+//      chunks of the gate/up matrix interleaved as 32 gate + 32 up rows (so a
+//      chunk yields 32 GeGLU values) go round-robin to the workgroups after
+//      the attention items' (first chunk c0, then c0 + W, ...), each
+//      multiplied into the matching 32-column block of the down matrix: one
+//      down partial P_c0[H] per workgroup.  The first chunk's weights are
+//      staged in LDS during phase C, and its gate/up rows run on the matrix
+//      cores.
 //   E  down reduction: 8-row groups of H summed over the partials.
 // Phases exchange their outputs as self-validating 64-bit words (epoch <<
 // 32 | float bits; st_word / ld_word): a consumer polls exactly the words
@@ -2449,6 +2452,40 @@ __device__ __forceinline__ float ps_sumsq(const float* v, int n, float* slot) {
     float s = 0.0f;
     for (int i = threadIdx.x; i < n; i += NT) s += v[i] * v[i];
     return block_sum(s, slot);
+}
+
+// Residual add and the RMS of its result from one block reduction (the
+// prologue ProResid's algebra): this thread's float4 groups t + 256 k of
+// x = b + postnorm(d) into xv (b, d in LDS; the post-norm weight groups wp
+// apply when pn), returning 1 / rms(x).  With e = d * w' and c = 1/rms(d):
+// sum x^2 = sum b^2 + 2 c sum b e + c^2 sum e^2.  slot: 16 floats of LDS.
+__device__ __forceinline__ float ps_resid_norm(const float* b, const float* d, const float4 (&wp)[PS_MG], bool pn,
+                                               int H, float eps, int zc, float* slot, float4 (&xv)[PS_MG]) {
+    const int ng4 = H >> 2;
+    float4 dv[PS_MG];
+    float dd = 0.0f, bb = 0.0f, be = 0.0f, ee = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PS_MG; ++k) {
+        const int gi = threadIdx.x + k * NT;
+        dv[k] = f4z();
+        xv[k] = f4z();
+        if (gi < ng4) {
+            dv[k] = ((const float4*)d)[gi];
+            xv[k] = ((const float4*)b)[gi];
+            const float4 w1 = zc ? make_float4(1.0f + wp[k].x, 1.0f + wp[k].y, 1.0f + wp[k].z, 1.0f + wp[k].w) : wp[k];
+            const float4 ev = pn ? make_float4(dv[k].x * w1.x, dv[k].y * w1.y, dv[k].z * w1.z, dv[k].w * w1.w) : dv[k];
+            dd += dot4(dv[k], dv[k]);
+            bb += dot4(xv[k], xv[k]);
+            be += dot4(xv[k], ev);
+            ee += dot4(ev, ev);
+        }
+    }
+    const float4 t = block_sum4(make_float4(dd, bb, be, ee), slot);
+    const float c = pn ? 1.0f / sqrtf(t.x / (float)H + eps) : 1.0f;
+#pragma unroll
+    for (int k = 0; k < PS_MG; ++k) xv[k] = xv[k] + (pn ? norm4i(dv[k], c, wp[k], zc) : dv[k]);
+    const float sxx = fmaxf(t.y + 2.0f * c * t.z + c * c * t.w, 0.0f);
+    return 1.0f / sqrtf(sxx / (float)H + eps);
 }
 
 // xs/sxs <- src[0, K) (LDS), normed by inv and (1 + w) / w when w is given,
@@ -2603,26 +2640,17 @@ struct ProFfnPs {
         const uint64_t* wa = w_a;
         ps_poll(H, [=](int i) { return wa + i; }, e, S.land, err);
         __syncthreads();
-        float inv = 1.0f;
-        if (post_attn) inv = 1.0f / sqrtf(ps_sumsq(S.land, H, S.red) / (float)H + eps);
         float4 xv[PS_MG];
-        float ss = 0.0f;
+        const float inv2 = ps_resid_norm(S.xr, S.land, r.wp, post_attn != nullptr, H, eps, zc, S.red + 48, xv);
 #pragma unroll
         for (int b = 0; b < PS_MG; ++b) {
             const int gi = threadIdx.x + b * NT;
-            xv[b] = f4z();
-            if (gi < ng4) {
-                const float4 o = ((const float4*)S.land)[gi];
-                xv[b] = ((const float4*)S.xr)[gi] + (post_attn ? norm4i(o, inv, r.wp[b], zc) : o);
-                ((float4*)S.x1)[gi] = xv[b];
-                ss += dot4(xv[b], xv[b]);
-            }
+            if (gi < ng4) ((float4*)S.x1)[gi] = xv[b];
         }
-        const float inv2 = 1.0f / sqrtf(block_sum(ss, S.red + 4) / (float)H + eps);
 #pragma unroll
         for (int b = 0; b < PS_MG; ++b) {
             const int gi = threadIdx.x + b * NT;
-            emit_x4<FMT_Q4>(L, gi, ng4, gi < ng4 ? norm4i(xv[b], inv2, r.wf[b], zc) : f4z());
+            emit_x4<FMT>(L, gi, ng4, gi < ng4 ? norm4i(xv[b], inv2, r.wf[b], zc) : f4z());
         }
     }
 };
@@ -2691,30 +2719,51 @@ __device__ void ps_prefetch(const PLayer& P, int c, float* pf, bool down) {
     }
 }
 
-// The staged chunk's 64 gate/up rows against the slice in xs/sxs (the
-// whole row): wave w sums blocks [w nb / 4, (w + 1) nb / 4) of row lane in
-// block order, then wave 0 adds the four waves' sums, the summation of the
-// register path (mv_item_valu with KBW-block batches), into y[0 .. 63].
-__device__ void ps_gu_lds(const float* pf, int nb, const MvLds& L, float* y) {
+// The staged chunk's 64 gate/up rows on the int8 matrix cores, against the
+// whole-row slice in xs/sxs in the FMT_Q4M limb format (L.zero cleared):
+// wave w takes rows 16w .. 16w + 15,
+// one MFMA pair per quad of column blocks as in mq_quad, with the codes and
+// scales read from the staged LDS copy (blocks past nb: zero codes and
+// scales against zero limbs).
+__device__ void ps_gu_lds_mfma(const float* pf, int nb, const MvLds& L, float* y) {
     const PfLayout Y = pf_layout(nb, 0, false);
-    const int wave = wave_id(), lane = threadIdx.x & 63;
-    const int k0 = nb * wave >> 2, k1 = nb * (wave + 1) >> 2;
-    const u32x4* cw = (const u32x4*)(pf + Y.gc) + lane;
-    const uint16_t* sw = (const uint16_t*)(pf + Y.gs) + lane;
-    float acc = 0.0f;
-    for (int kb = k0; kb < k1; ++kb) {
-        const u32x4 w = cw[kb * 64];
-        const float4* xv = (const float4*)(L.xs + kb * 32);
-        float d = 0.0f;
-        d = dot_q4_word(w.x, xv[0], xv[4], d);
-        d = dot_q4_word(w.y, xv[1], xv[5], d);
-        d = dot_q4_word(w.z, xv[2], xv[6], d);
-        d = dot_q4_word(w.w, xv[3], xv[7], d);
-        acc = fmaf(h2f(sw[kb * 64]), d - 8.0f * L.sxs[kb], acc);
+    const int wave = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4, r16 = 16 * wave;
+    const u32x4* cw = (const u32x4*)(pf + Y.gc);
+    const uint16_t* sw = (const uint16_t*)(pf + Y.gs);
+    const bool act = (n >> 2) == g;
+    const float lp = (float)(1u << (7 * (n & 3)));
+    const i32x4* zero = (const i32x4*)L.zero;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int nq = (nb + 3) >> 2;
+    for (int q = 0; q < nq; ++q) {
+        const int ka = 4 * q + g, ks = 4 * q + (n >> 2);
+        const u32x4 c = ka < nb ? cw[ka * 64 + r16 + n] : (u32x4){0u, 0u, 0u, 0u};
+        const u32x2 sc = ks < nb ? *(const u32x2*)(sw + ks * 64 + r16 + 4 * g) : (u32x2){0u, 0u};
+        const i32x4* lb = (const i32x4*)L.xs + ((4 * q + g) * 8 + (n & 3));
+        const i32x4 b0 = *(act ? lb : zero), b1 = *(act ? lb + 4 : zero);
+        const float mq = L.sxs[4 * q + (n >> 2)] * lp;
+        i32x4 alo, ahi;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {  // 16 * (q - 8) as int8: q ^ 8 is q - 8 as a signed nibble
+            ahi[k] = (int)((c[k] ^ 0x80808080u) & 0xF0F0F0F0u);
+            alo[k] = (int)(((c[k] << 4) ^ 0x80808080u) & 0xF0F0F0F0u);
+        }
+        i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, b0, (i32x4){0, 0, 0, 0}, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, b1, d, 0, 0, 0);
+        acc[0] = fmaf((float)d[0], h2f((uint16_t)sc.x) * mq, acc[0]);
+        acc[1] = fmaf((float)d[1], h2f((uint16_t)(sc.x >> 16)) * mq, acc[1]);
+        acc[2] = fmaf((float)d[2], h2f((uint16_t)sc.y) * mq, acc[2]);
+        acc[3] = fmaf((float)d[3], h2f((uint16_t)(sc.y >> 16)) * mq, acc[3]);
     }
-    L.red[wave * 64 + lane] = acc;
+    // sum the 16 columns of each row; lane 16g then holds rows 4g .. 4g + 3
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] = row16_sum(acc[k]);
+    if (n == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) L.red[r16 + 4 * g + k] = acc[k];
+    }
     __syncthreads();
-    if (wave == 0) y[lane] = (L.red[lane] + L.red[64 + lane]) + (L.red[128 + lane] + L.red[192 + lane]);
+    if (wave == 0) y[lane] = L.red[lane];
 }
 
 template <int HD, int G, int KBW>
@@ -2732,7 +2781,6 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
     S.red = S.land + a.land;
     S.gu = S.red + 64;
     float* const pf = lds + a.pf_off;
-    const bool staged = a.pf_gu && wg < a.n_chunks;  // chunk wg's phase D weights go through LDS
     const float eps = a.eps;
     const int zc = a.zc;
 
@@ -2775,18 +2823,16 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 wnv[b] = WN.f4(gi < ng4 ? 16u * gi : OOB);
             }
             float4 xv[PS_MG];
+            float inv;  // 1 / rms of the layer's input x
             if (l > 0) {
                 const uint64_t* wd = w_d;
                 ps_poll(H, [=](int i) { return wd + i; }, e - 1u, S.land, err);
                 __syncthreads();
-                float inv = 1.0f;
-                if (pn) inv = 1.0f / sqrtf(ps_sumsq(S.land, H, S.red) / (float)H + eps);
+                inv = ps_resid_norm(S.x1, S.land, wpv, pn, H, eps, zc, S.red + 48, xv);
 #pragma unroll
                 for (int b = 0; b < PS_MG; ++b) {
                     const int gi = tid + b * NT;
                     if (gi < ng4) {
-                        const float4 d = ((const float4*)S.land)[gi];
-                        xv[b] = ((const float4*)S.x1)[gi] + (pn ? norm4i(d, inv, wpv[b], zc) : d);
                         ((float4*)S.xr)[gi] = xv[b];
                         if (wg == 0)
                             *(__attribute__((address_space(1))) f32x4*)(layer_out + (size_t)(l - 1) * H + 4 * gi) =
@@ -2794,17 +2840,15 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                     }
                 }
             } else {
+                float ss = 0.0f;
 #pragma unroll
                 for (int b = 0; b < PS_MG; ++b) {
                     const int gi = tid + b * NT;
                     xv[b] = gi < ng4 ? ((const float4*)S.xr)[gi] : f4z();
+                    ss += dot4(xv[b], xv[b]);
                 }
+                inv = 1.0f / sqrtf(block_sum(ss, S.red + 4) / (float)H + eps);
             }
-            float ss = 0.0f;
-#pragma unroll
-            for (int b = 0; b < PS_MG; ++b)
-                if (tid + b * NT < ng4) ss += dot4(xv[b], xv[b]);
-            const float inv = 1.0f / sqrtf(block_sum(ss, S.red + 4) / (float)H + eps);
 #pragma unroll
             for (int b = 0; b < PS_MG; ++b) {
                 const int gi = tid + b * NT;
@@ -2820,6 +2864,12 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
         // ---------------- B: attention chunks
         const int gsel = P.global ? 1 : 0;
         const int nu = a.n_used[gsel];
+        // FFN chunks start past the attention items' workgroups (chunk c on
+        // workgroup (c + items) mod W), so that an attention workgroup's
+        // staging loads do not delay its O-row poll; c0 = this workgroup's first
+        const int n_att = a.nkv * nu;
+        const int c0 = ((wg - n_att) % nwg + nwg) % nwg;
+        const bool staged = a.pf_gu && c0 < a.n_chunks;  // chunk c0's phase D weights go through LDS
         {
             AttnArgs aa{};
             aa.q_off = 0;
@@ -2882,7 +2932,7 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
         }
         // this workgroup's attention and merge waits are behind it: stage its
         // phase D weights now, so they stream during phase C
-        if (staged) ps_prefetch(P, wg, pf, a.pf_down != 0);
+        if (staged) ps_prefetch(P, c0, pf, a.pf_down != 0);
         // ---------------- C: O projection rows
         {
             const int ngrp = H / 8;
@@ -2923,17 +2973,20 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 }
             };
             bool built = false;
-            for (int c = wg; c < a.n_chunks; c += nwg) {
-                const bool from_lds = staged && c == wg, down_lds = from_lds && a.pf_down;
+            for (int c = c0; c < a.n_chunks; c += nwg) {
+                const bool from_lds = staged && c == c0, down_lds = from_lds && a.pf_down;
                 if (!down_lds) load_down(c);
                 if (from_lds) {
                     ProFfnPs::Regs r0;
                     pro.load(r0, 0, H);
-                    pro.template finish<FMT_Q4>(L, r0, 0, H);
+                    pro.template finish<FMT_Q4M>(L, r0, 0, H);
+                    if (tid < 4) L.zero[tid] = 0.0f;
                     __syncthreads();
-                    ps_gu_lds(pf, P.gi.nblk, L, S.gu);
+                    ps_gu_lds_mfma(pf, P.gi.nblk, L, S.gu);
                     built = true;
-                } else if (!built) {
+                } else if (!built || staged) {
+                    // first chunk, or one after the staged chunk, whose slice is in the
+                    // limb format: the prologue (re)builds the VALU-format slice
                     mv_item_valu<FMT_Q4, KBW, 1, 1>(P.gi, c, 0, 1, pro, EpiLdsRows{S.gu}, L);
                     built = true;
                 } else {
@@ -2981,8 +3034,8 @@ __global__ __launch_bounds__(NT) void k_step_ps(PArgs a) {
                 pro.load(r0, 0, H);
                 pro.template finish<FMT_Q4>(L, r0, 0, H);
                 __syncthreads();
-            } else if (wg < a.np) {
-                uint64_t* pw = w_p + (size_t)wg * H;
+            } else {  // partial slot c0 (< np: every slot below np has its first chunk)
+                uint64_t* pw = w_p + (size_t)c0 * H;
 #pragma unroll
                 for (int k = 0; k < PS_KR; ++k) {
                     const int r = tid + k * NT;
