@@ -3872,30 +3872,162 @@ __global__ __launch_bounds__(NT) void k_pf_attn(AttnArgs a, const float* q, int 
                             AttnOutPlain{state + (size_t)t * a.nkv * PF_ATTN_NC * G * (HD + 2)});
 }
 
-// The same per (token, kv head, chunk) on the decode step's streaming body
-// with q ready-made (head_dim 256): every row of the prompt is in the cache
-// before the attention runs, so there is no current row to special-case.
-// 17 % faster than k_pf_attn at 512 prompt tokens (1.50 vs 1.80 ms).
-template <int HD, int G>
-__global__ __launch_bounds__(NT) void k_pf_attn_op(AttnArgs a, const float* q, int pos0, float* state) {
-    const int j = blockIdx.x % a.nc, tg = blockIdx.x / a.nc;
-    const int t = tg / a.nkv, g = tg % a.nkv;
-    AttnArgs b = a;
-    b.q = q + (size_t)t * a.nkv * G * HD;
-    b.set_pos(pos0 + t);
-    if (j >= b.n_used) return;  // uniform per workgroup
-    b.part = state + (size_t)t * a.nkv * PF_ATTN_NC * G * (HD + 2);
-    const int c0 = b.pb + j * b.ch, c1 = min(b.pe, c0 + b.ch);
-    __shared__ __align__(16) AttnStepLds<HD, G> lds;
-    if (c1 - c0 <= 32) attn_step_body<HD, G, 1, false, true>(b, g, j, lds);
-    else attn_step_body<HD, G, 2, false, true>(b, g, j, lds);
+// Causal attention of the prompt on the f32 matrix cores (head_dim 256,
+// v_mfma_f32_16x16x4f32): workgroup (query tile, kv head g, key chunk j).
+// A wave owns 16 query rows, (token, q head) pairs of 16 / G tokens, and the
+// workgroup's 4 waves share every staged 16-key block of K and V in LDS
+// (double-buffered, one barrier per block).  Per block and wave:
+//   S^T = K Q^T: 64 MFMAs; lane i supplies K[key i%16][d] and
+//     Q[row i%16][d] over the dims d = 16u + 4(i/16) + e (the sum runs over
+//     every dim once, in this order), and holds S^T[key 4(i/16)+r][row i%16];
+//   online softmax per row (its 4 lane copies reduced by xor 16, 32);
+//   O^T += V^T P^T: 64 MFMAs; the K dimension of MFMA j is key 4(i/16) + j,
+//     so lane i's own probabilities are its B operand, and output block
+//     (gamma, b') holds the dims 64 gamma + 4m + b' of row i%16.
+// Keys outside a row's window or past the chunk are masked.  The chunk's
+// state {m, l, o} goes to slot j of the token's states, in the layout the
+// merge (k_pf_attn_out) reads.
+constexpr int FA_KB = 16;       // keys per staged block
+constexpr int FA_LD = 256 + 4;  // LDS row stride (floats) of a staged K or V row
+inline size_t pf_fa_lds_bytes() { return sizeof(float) * 2 * 2 * FA_KB * FA_LD; }
+template <int G>
+__global__ __launch_bounds__(NT) void k_pf_fa(AttnArgs a, const float* q, int pos0, int n, int nch, int ch,
+                                              float* state) {
+    constexpr int HD = 256, TPW = 16 / G, TPB = 4 * TPW;
+    static_assert(G >= 1 && G <= 16 && 16 % G == 0, "16 query rows per wave");
+    extern __shared__ __align__(16) float fa_lds[];
+    const int j = blockIdx.x % nch, tg = blockIdx.x / nch, g = tg % a.nkv, tile = tg / a.nkv;
+    const int wave = wave_id(), lane = threadIdx.x & 63, qr = lane & 15, kq = lane >> 4;
+    const int t0 = tile * TPB, tl = min(t0 + TPB, n) - 1;  // the workgroup's tokens
+    const int tw0 = t0 + wave * TPW, twl = min(tw0 + TPW, n) - 1;  // the wave's (tw0 > twl: none)
+    const int t = tw0 + qr / G, hl = qr % G;  // this lane's query row
+    const bool tok_ok = t < n;
+    int pb = 0, pe = 0, wpb = 0, wpe = 0, dump = 0, vpb = 0, vpe = 0;
+    if (tok_ok) attn_window(pos0 + t, a.global, a.window, a.mode, pb, pe);
+    // windows are monotone in the position: the workgroup's union is
+    // [pb(t0), pe(tl)), cut to chunk j
+    attn_window(pos0 + t0, a.global, a.window, a.mode, wpb, dump);
+    attn_window(pos0 + tl, a.global, a.window, a.mode, dump, wpe);
+    const int k_lo = max(wpb, j * ch), k_hi = min(wpe, (j + 1) * ch);
+    if (tw0 <= twl) {
+        attn_window(pos0 + tw0, a.global, a.window, a.mode, vpb, dump);
+        attn_window(pos0 + twl, a.global, a.window, a.mode, dump, vpe);
+    }
+    const size_t rs = (size_t)a.nkv * HD;  // cache row stride (floats)
+    // this lane's q row, dims 16u + 4 kq .. + 3
+    float4 qv[16];
+    const float* qrow = q + (size_t)(tok_ok ? t : 0) * a.nkv * G * HD + (size_t)(g * G + hl) * HD;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) qv[u] = tok_ok ? *(const float4*)(qrow + 16 * u + 4 * kq) : f4z();
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[c][b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    // staging: thread -> key tid / 16, dims 16 (tid % 16) .. + 15; rows at or
+    // past wpe read zeros (the views end there) and are masked
+    const BufView KC(a.kc, (size_t)wpe * rs * 4), VC(a.vc, (size_t)wpe * rs * 4);
+    float4 sk[4], sv[4];
+    const int skey = threadIdx.x >> 4, sdim = 16 * (threadIdx.x & 15);
+    auto stage_load = [&](int k0) {
+        const uint32_t off = 4u * ((uint32_t)(k0 + skey) * (uint32_t)rs + (uint32_t)(g * HD + sdim));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sk[e] = KC.f4(off + 16u * e);
+            sv[e] = VC.f4(off + 16u * e);
+        }
+    };
+    auto slab = [&](int buf, int which) { return fa_lds + (size_t)((buf * 2 + which) * FA_KB) * FA_LD; };
+    const int kb_lo = k_lo / FA_KB * FA_KB;
+    if (k_lo < k_hi) stage_load(kb_lo);
+    int buf = 0;
+    for (int k0 = kb_lo; k0 < k_hi; k0 += FA_KB, buf ^= 1) {
+        float* Ks = slab(buf, 0);
+        float* Vs = slab(buf, 1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            *(float4*)(Ks + skey * FA_LD + sdim + 4 * e) = sk[e];
+            *(float4*)(Vs + skey * FA_LD + sdim + 4 * e) = sv[e];
+        }
+        __syncthreads();  // this block staged; the block two back no longer read
+        if (k0 + FA_KB < k_hi) stage_load(k0 + FA_KB);
+        if (tw0 > twl || k0 >= vpe || k0 + FA_KB <= vpb) continue;  // no row of this wave sees the block
+        f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float4 kv = *(const float4*)(Ks + qr * FA_LD + 16 * u + 4 * kq);
+            sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qv[u].x, sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qv[u].y, sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qv[u].z, sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qv[u].w, sc, 0, 0, 0);
+        }
+        // row qr, keys k0 + 4 kq + r
+        float p[4], bm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = k0 + 4 * kq + r;
+            const bool ok = tok_ok && key >= pb && key < pe && key >= k_lo && key < k_hi;
+            p[r] = ok ? sc[r] * a.scale : -INFINITY;
+            bm = fmaxf(bm, p[r]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const float mn = fmaxf(m, bm);
+        float corr = 1.0f;
+        if (mn == -INFINITY) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[r] = 0.0f;
+        } else {
+            corr = m == -INFINITY ? 0.0f : __expf(m - mn);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[r] = p[r] == -INFINITY ? 0.0f : __expf(p[r] - mn);
+        }
+        float ps = (p[0] + p[1]) + (p[2] + p[3]);
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc[c][b] *= corr;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float4 vv = *(const float4*)(Vs + (4 * kq + jj) * FA_LD + 64 * c + 4 * qr);
+                acc[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, p[jj], acc[c][0], 0, 0, 0);
+                acc[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, p[jj], acc[c][1], 0, 0, 0);
+                acc[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, p[jj], acc[c][2], 0, 0, 0);
+                acc[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, p[jj], acc[c][3], 0, 0, 0);
+            }
+        }
+    }
+    if (!tok_ok) return;
+    const size_t cs = (size_t)G * (HD + 2);
+    float* st = state + (size_t)t * a.nkv * PF_ATTN_NC * cs + ((size_t)g * nch + j) * cs;
+    if (kq == 0) {
+        st[hl] = m;
+        st[G + hl] = l;
+    }
+    // lane holds dims 64 c + 16 kq + 4 r + b of its row
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *(float4*)(st + 2 * G + hl * HD + 64 * c + 16 * kq + 4 * r) =
+                make_float4(acc[c][0][r], acc[c][1][r], acc[c][2][r], acc[c][3][r]);
 }
 
 // Merge of token t's chunk states per head, o = sum_j w_j o_j / sum_j w_j l_j
+// (all_chunks: the a.nc prompt-wide chunks of k_pf_fa, empty ones with
+// m = -inf, l = 0; else the token's own n_used chunks)
 // with w_j = exp(m_j - max_j m_j), into GEMM operand A.  The row (all heads)
 // is staged in dynamic LDS for its scale.
 template <int HD, int G>
-__global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const float* state, PfA out) {
+__global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const float* state, PfA out,
+                                                    int all_chunks) {
     extern __shared__ __align__(16) float rowbuf[];
     __shared__ float wj[8 * G][PF_ATTN_NC];
     __shared__ float den[8 * G];
@@ -3903,7 +4035,7 @@ __global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const 
     const int t = blockIdx.x, nq = a.nkv * G, n = nq * HD, tid = threadIdx.x;
     AttnArgs b = a;
     b.set_pos(pos0 + t);
-    const int nu = b.n_used;
+    const int nu = all_chunks ? a.nc : b.n_used;  // k_pf_fa writes every chunk of the prompt
     const size_t cstride = (size_t)G * (HD + 2);  // one chunk state
     const float* st = state + (size_t)t * a.nkv * PF_ATTN_NC * cstride;
     // chunk weights per head (nq <= 8 G heads, one thread per head)
@@ -4109,16 +4241,30 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
             a.nc = std::max(1, std::min(PF_ATTN_NC, (pos0 + n + 127) / 128));
 
             const PfA ao = A(c.n_heads * hd);
+            // head_dim 256: the matrix-core kernel over prompt-wide key chunks
+            // (multiples of 16 positions, at most PF_ATTN_NC of them), merged by
+            // k_pf_attn_out: ~64 positions per chunk, shorter until the grid has
+            // about 256 workgroups
+            AttnArgs af = a;
+            const int ptot = pos0 + n, fa_tiles = (n + 64 / G - 1) / (64 / G) * nkv;
+            const int want = std::max((ptot + 63) / 64, (256 + fa_tiles - 1) / fa_tiles);
+            int fa_ch = std::max(1, std::min(PF_ATTN_NC, want));
+            fa_ch = ((ptot + fa_ch - 1) / fa_ch + FA_KB - 1) / FA_KB * FA_KB;
+            af.nc = (ptot + fa_ch - 1) / fa_ch;  // <= PF_ATTN_NC
 #define GH_PF_ATTN(HD_, G_)                                                                                      \
     if (hd == HD_ && G == G_) {                                                                                  \
-        if constexpr (HD_ == 256)                                                                                \
-            GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_attn_op<HD_, G_>, dim3(n * nkv * a.nc), dim3(NT), 0, \
-                                 a, (const float*)B.q, pos0, B.st));                                            \
-        else                                                                                                     \
+        if constexpr (HD_ == 256) {                                                                              \
+            GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_fa<G_>,                                             \
+                                 dim3((n + 64 / G_ - 1) / (64 / G_) * nkv * af.nc), dim3(NT), pf_fa_lds_bytes(), \
+                                 af, (const float*)B.q, pos0, n, af.nc, fa_ch, B.st));                          \
+            GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT),            \
+                                 sizeof(float) * c.n_heads * hd, af, pos0, (const float*)B.st, ao, 1));         \
+        } else {                                                                                                 \
             GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_attn<HD_, G_>, dim3(n * nkv * a.nc), dim3(NT), 0,    \
                                  a, (const float*)B.q, pos0, B.st));                                            \
-        GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT),                \
-                             sizeof(float) * c.n_heads * hd, a, pos0, (const float*)B.st, ao));                 \
+            GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT),            \
+                                 sizeof(float) * c.n_heads * hd, a, pos0, (const float*)B.st, ao, 0));          \
+        }                                                                                                        \
     } else
             GH_PF_ATTN(256, 1) GH_PF_ATTN(256, 2) GH_PF_ATTN(256, 4) GH_PF_ATTN(256, 8)
             GH_PF_ATTN(128, 1) GH_PF_ATTN(128, 2) GH_PF_ATTN(128, 4) GH_PF_ATTN(128, 8)
