@@ -149,6 +149,30 @@ def test_prefill_passes_chunks_and_ragged_sizes(ctx):
     np.testing.assert_array_equal(gb, gc)
 
 
+@pytest.mark.parametrize("nq,nkv", [(4, 4), (8, 1)])
+def test_prefill_matrix_core_attention_groups_ragged_windows(ctx, nq, nkv):
+    """head_dim 256 with GQA groups 1 and 8 (the 2 and 4 of the other tests
+    aside): 150 tokens prefilled as pieces of 70, 1 and 79 (so later pieces
+    start past position 0 and their key chunks cover earlier pieces), a
+    40-token window on the local layer; the last token's logits and next
+    token against the decode step fed token by token, then both caches
+    continue identically."""
+    cfg = _mini4b(gh.MODE_GEMMA3, window=40, layers=2)
+    cfg.n_heads, cfg.n_kv_heads, cfg.max_seq = nq, nkv, 160
+    m = _gpu_model(ctx, cfg, 23, True)
+    toks = gh.synth_tokens(12, "fa", 150, cfg.vocab)
+    kv_a = gh.KVCache(m, 160)
+    at = 0
+    for k in (70, 1, 79):
+        la, _, na = gh.prefill(m, kv_a, toks[at:at + k])
+        at += k
+    kv_b = gh.KVCache(m, 160)
+    for t in toks:
+        lb, _, nb = gh.runGemmaInferenceCached(m, int(t), kv_b)
+    assert rel_err(la, lb) < ACT_TOL and na == nb
+    np.testing.assert_array_equal(gh.generate(m, kv_a, [na], 5), gh.generate(m, kv_b, [nb], 5))
+
+
 def test_prefill_single_token_equals_step(ctx):
     """A prefill of one token is the decode step of that token."""
     cfg = _mini4b(gh.MODE_GEMMA3, layers=2)
