@@ -3886,7 +3886,7 @@ __global__ __launch_bounds__(NT) void k_pf_attn(AttnArgs a, const float* q, int 
 //     (gamma, b') holds the dims 64 gamma + 4m + b' of row i%16.
 // Keys outside a row's window or past the chunk are masked.  The chunk's
 // state {m, l, o} goes to slot j of the token's states, in the layout the
-// merge (k_pf_attn_out) reads.
+// merge (k_pf_attn_out) reads, for the rows whose window meets the chunk.
 constexpr int FA_KB = 16;       // keys per staged block
 constexpr int FA_LD = 256 + 4;  // LDS row stride (floats) of a staged K or V row
 inline size_t pf_fa_lds_bytes() { return sizeof(float) * 2 * 2 * FA_KB * FA_LD; }
@@ -4004,30 +4004,42 @@ __global__ __launch_bounds__(NT) void k_pf_fa(AttnArgs a, const float* q, int po
             }
         }
     }
-    if (!tok_ok) return;
+    // The state of a row whose window meets the chunk (the merge reads
+    // exactly those): m and l from the row's first lane copy; o through LDS
+    // (the K/V buffers, free once every wave is past the loop), so that each
+    // row leaves as one contiguous 1 KB store of the wave.
     const size_t cs = (size_t)G * (HD + 2);
-    float* st = state + (size_t)t * a.nkv * PF_ATTN_NC * cs + ((size_t)g * nch + j) * cs;
-    if (kq == 0) {
+    const bool keep = tok_ok && max(pb, j * ch) < min(pe, (j + 1) * ch);
+    if (keep && kq == 0) {
+        float* st = state + (size_t)t * a.nkv * PF_ATTN_NC * cs + ((size_t)g * nch + j) * cs;
         st[hl] = m;
         st[G + hl] = l;
     }
-    // lane holds dims 64 c + 16 kq + 4 r + b of its row
+    __syncthreads();
+    float* ob = fa_lds + (size_t)wave * 16 * HD;  // this wave's 16 rows (64 KB for 4 waves)
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            *(float4*)(st + 2 * G + hl * HD + 64 * c + 16 * kq + 4 * r) =
+        for (int r = 0; r < 4; ++r)  // lane holds dims 64 c + 16 kq + 4 r + b of its row
+            *(float4*)(ob + qr * HD + 64 * c + 16 * kq + 4 * r) =
                 make_float4(acc[c][0][r], acc[c][1][r], acc[c][2][r], acc[c][3][r]);
+    const unsigned long long kept = __ballot(keep);  // bit qr (lanes 0..15) = row qr kept
+    for (int row = 0; row < 16; ++row) {
+        if (!(kept >> row & 1ull)) continue;  // wave-uniform
+        const int tr = tw0 + row / G, hr = row % G;
+        float* st = state + (size_t)tr * a.nkv * PF_ATTN_NC * cs + ((size_t)g * nch + j) * cs;
+        *(float4*)(st + 2 * G + hr * HD + 4 * lane) = *(const float4*)(ob + row * HD + 4 * lane);
+    }
 }
 
 // Merge of token t's chunk states per head, o = sum_j w_j o_j / sum_j w_j l_j
-// (all_chunks: the a.nc prompt-wide chunks of k_pf_fa, empty ones with
-// m = -inf, l = 0; else the token's own n_used chunks)
+// (fa_ch > 0: the prompt-wide k_pf_fa chunks of fa_ch positions that meet
+// the token's window; else the token's own n_used chunks)
 // with w_j = exp(m_j - max_j m_j), into GEMM operand A.  The row (all heads)
 // is staged in dynamic LDS for its scale.
 template <int HD, int G>
 __global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const float* state, PfA out,
-                                                    int all_chunks) {
+                                                    int fa_ch) {
     extern __shared__ __align__(16) float rowbuf[];
     __shared__ float wj[8 * G][PF_ATTN_NC];
     __shared__ float den[8 * G];
@@ -4035,7 +4047,15 @@ __global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const 
     const int t = blockIdx.x, nq = a.nkv * G, n = nq * HD, tid = threadIdx.x;
     AttnArgs b = a;
     b.set_pos(pos0 + t);
-    const int nu = all_chunks ? a.nc : b.n_used;  // k_pf_fa writes every chunk of the prompt
+    // the token's chunks: its own n_used, or (fa_ch > 0) the k_pf_fa chunks of
+    // fa_ch positions that meet its window
+    int c_lo = 0, c_hi = b.n_used;
+    if (fa_ch > 0) {
+        int pb, pe;
+        attn_window(pos0 + t, a.global, a.window, a.mode, pb, pe);
+        c_lo = pb / fa_ch;
+        c_hi = (pe - 1) / fa_ch + 1;
+    }
     const size_t cstride = (size_t)G * (HD + 2);  // one chunk state
     const float* st = state + (size_t)t * a.nkv * PF_ATTN_NC * cstride;
     // chunk weights per head (nq <= 8 G heads, one thread per head)
@@ -4043,9 +4063,9 @@ __global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const 
         const int g = tid / G, hl = tid % G;
         const float* sg = st + (size_t)g * a.nc * cstride;  // attn_item's layout: (g * nc + chunk)
         float M = -INFINITY;
-        for (int c = 0; c < nu; ++c) M = fmaxf(M, sg[c * cstride + hl]);
+        for (int c = c_lo; c < c_hi; ++c) M = fmaxf(M, sg[c * cstride + hl]);
         float dsum = 0.0f;
-        for (int c = 0; c < nu; ++c) {
+        for (int c = c_lo; c < c_hi; ++c) {
             const float w = expf(sg[c * cstride + hl] - M);
             wj[tid][c] = w;
             dsum += w * sg[c * cstride + G + hl];
@@ -4058,7 +4078,7 @@ __global__ __launch_bounds__(NT) void k_pf_attn_out(AttnArgs a, int pos0, const 
         const int h = i / HD, d = i % HD, g = h / G, hl = h % G;
         const float* o = st + (size_t)g * a.nc * cstride + 2 * G + hl * HD + d;
         float4 v = f4z();
-        for (int c = 0; c < nu; ++c) {
+        for (int c = c_lo; c < c_hi; ++c) {
             const float w = wj[h][c];
             const float* oc = o + c * cstride;
             v = make_float4(v.x + w * oc[0], v.y + w * oc[1], v.z + w * oc[2], v.w + w * oc[3]);
@@ -4258,7 +4278,7 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
                                  dim3((n + 64 / G_ - 1) / (64 / G_) * nkv * af.nc), dim3(NT), pf_fa_lds_bytes(), \
                                  af, (const float*)B.q, pos0, n, af.nc, fa_ch, B.st));                          \
             GH_CHECK(sink_launch(sink, "pf_attn_out", 0.0, k_pf_attn_out<HD_, G_>, dim3(n), dim3(NT),            \
-                                 sizeof(float) * c.n_heads * hd, af, pos0, (const float*)B.st, ao, 1));         \
+                                 sizeof(float) * c.n_heads * hd, af, pos0, (const float*)B.st, ao, fa_ch));         \
         } else {                                                                                                 \
             GH_CHECK(sink_launch(sink, "pf_attn", 0.0, k_pf_attn<HD_, G_>, dim3(n * nkv * a.nc), dim3(NT), 0,    \
                                  a, (const float*)B.q, pos0, B.st));                                            \
