@@ -1,9 +1,10 @@
 """PyTorch-CPU restatement of gemma.hs's decode step -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/ and bench.py's cpu_baseline leg may import this module: it is
-the CPU baseline that BASELINE.md names (the reference's own path, Dawn's
-SwiftShader adapter, does not exist in this image) and a second checker
-beside the C oracle.  Nothing in the product imports it.
+the benchmark's CPU baseline, a PyTorch restatement on all host cores (the
+reference's own path, Dawn's SwiftShader adapter, does not exist in this
+image), and a second checker beside the C oracle.  Nothing in the product
+imports it.
 
 The arithmetic contract is the one oracle/gemma_oracle.c restates (each
 step cites the same reference lines): f32 everywhere; Q4_0 weights
