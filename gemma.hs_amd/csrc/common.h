@@ -308,6 +308,7 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
 int launch_gelu_mul(const float* g, const float* u, int n, float* h, hipStream_t s);
 int launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
 int launch_stream_read(const void* p, size_t bytes, float* sink, hipStream_t s);
+int launch_xchg_probe(uint64_t* words, int n_wg, int rounds, int* err, unsigned long long* stamps, hipStream_t s);
 constexpr int GH_ATTN_OP_MAX_NC = 256;  // chunks per kv head of the op-level attention
 // Capacity (floats) of the static chunk-state array of
 // gh_attention_decode_noalloc: nkv * n_splits * (nq / nkv) * (head_dim + 2)

@@ -4627,6 +4627,46 @@ int launch_stream_read(const void* p, size_t bytes, float* sink, hipStream_t s) 
     return GH_OK;
 }
 
+// Exchange probe (gh_time_exchange): `rounds` all-to-all exchanges among the
+// grid's workgroups through the persistent step's self-validating words.  In
+// round r each workgroup publishes its word (epoch epoch0 + r) in buffer
+// r % 2, then its first n_wg threads poll every workgroup's word of that
+// buffer until it carries the round's epoch.  A workgroup starts round r + 1
+// only after seeing every round-r word, so no one is two rounds ahead of a
+// reader of the same buffer.  Workgroup 0 stamps s_memrealtime (100 MHz)
+// before the first round and after the last.  Every wait is bounded: a
+// timeout sets *err, after which all waits give up at once.
+__global__ __launch_bounds__(NT) void k_xchg_probe(uint64_t* words, int n_wg, int rounds, uint32_t epoch0, int* err,
+                                                   unsigned long long* stamps) {
+    const int wg = blockIdx.x, tid = threadIdx.x;
+    if (wg == 0 && tid == 0) stamps[0] = __builtin_amdgcn_s_memrealtime();
+    for (int r = 0; r < rounds; ++r) {
+        const uint32_t e = epoch0 + (uint32_t)r;
+        uint64_t* buf = words + (size_t)(r & 1) * n_wg;
+        if (tid == 0) st_word(buf + wg, e, (float)r);
+        if (tid < n_wg) {
+            uint64_t v = ld_word(buf + tid);
+            for (int spin = 1; (uint32_t)(v >> 32) != e; ++spin) {
+                if (spin >= XCHG_SPIN || ((spin & 63) == 0 &&
+                                          __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+                    __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                v = ld_word(buf + tid);
+            }
+        }
+        __syncthreads();
+    }
+    if (wg == 0 && tid == 0) stamps[1] = __builtin_amdgcn_s_memrealtime();
+}
+
+int launch_xchg_probe(uint64_t* words, int n_wg, int rounds, int* err, unsigned long long* stamps, hipStream_t s) {
+    if (n_wg < 1 || n_wg > NT || rounds < 1) return set_error(GH_ERR_INVALID, "internal: exchange probe of %d workgroups", n_wg);
+    hipLaunchKernelGGL(k_xchg_probe, dim3(n_wg), dim3(NT), 0, s, words, n_wg, rounds, 1u, err, stamps);
+    GH_HIP(hipGetLastError());
+    return GH_OK;
+}
+
 #endif  // GH_IN_TU(4)
 
 }  // namespace gh

@@ -1521,6 +1521,42 @@ extern "C" int gh_time_stream_read(gh_ctx* ctx, size_t bytes, int32_t n_reps, do
     return GH_OK;
 }
 
+extern "C" int gh_time_exchange(gh_ctx* ctx, int32_t n_wg, int32_t rounds, double* us_out) {
+    if (!ctx || !us_out || rounds < 1 || rounds > 1000000)
+        return set_error(GH_ERR_INVALID, "gh_time_exchange: rounds must be in [1, 1000000]");
+    GH_CHECK(ctx_bind(ctx));
+    int cus = 0;
+    GH_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
+    if (n_wg < 1 || n_wg > 256 || n_wg > cus)
+        return set_error(GH_ERR_RANGE, "gh_time_exchange: %d workgroups (1 .. min(256, %d CUs))", n_wg, cus);
+    Lock lk(ctx->mu);
+    hipStream_t s = ctx->stream;
+    void* dev = nullptr;
+    const size_t words = 2 * sizeof(uint64_t) * (size_t)n_wg;
+    const size_t bytes = words + 64 + 2 * sizeof(unsigned long long);
+    int rc = GH_OK;
+    if (hipMalloc(&dev, bytes) != hipSuccess) rc = set_error(GH_ERR_OOM, "gh_time_exchange: hipMalloc failed");
+    // zeros: epoch 0 is never a round's
+    if (rc == GH_OK && hipMemsetAsync(dev, 0, bytes, s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipMemsetAsync failed");
+    uint64_t* w = (uint64_t*)dev;
+    int* err = (int*)((char*)dev + words);
+    unsigned long long* stamps = (unsigned long long*)((char*)dev + words + 64);
+    if (rc == GH_OK) rc = gh::launch_xchg_probe(w, n_wg, rounds, err, stamps, s);
+    int herr = 0;
+    unsigned long long hs[2] = {0, 0};
+    if (rc == GH_OK && hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess)
+        rc = set_error(GH_ERR_HIP, "hipMemcpyAsync failed");
+    if (rc == GH_OK && hipMemcpyAsync(hs, stamps, sizeof(hs), hipMemcpyDeviceToHost, s) != hipSuccess)
+        rc = set_error(GH_ERR_HIP, "hipMemcpyAsync failed");
+    if (rc == GH_OK && hipStreamSynchronize(s) != hipSuccess) rc = set_error(GH_ERR_HIP, "hipStreamSynchronize failed");
+    (void)hipStreamSynchronize(s);
+    if (dev) (void)hipFree(dev);
+    GH_CHECK(rc);
+    if (herr) return set_error(GH_ERR_STATE, "gh_time_exchange: a wait timed out (workgroups not co-resident?)");
+    *us_out = (double)(hs[1] - hs[0]) * 0.01 / rounds;  // s_memrealtime ticks at 100 MHz
+    return GH_OK;
+}
+
 // =====================================================================
 // synthetic model
 // =====================================================================

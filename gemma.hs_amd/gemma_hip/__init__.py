@@ -582,6 +582,15 @@ def time_kernel(model: GemmaModel, cache: KVCache, name: str, n_reps: int = 50) 
     return KernelTiming(name, us.value, nb.value, per.value)
 
 
+def time_exchange(ctx: Context, n_wg: int, rounds: int = 2000) -> float:
+    """Microseconds per all-to-all exchange of one self-validating word per
+    workgroup among n_wg co-resident workgroups (gh_time_exchange), the
+    synchronisation the persistent step uses between its phases."""
+    us = C.c_double()
+    check(lib().gh_time_exchange(ctx.h, n_wg, rounds, C.byref(us)))
+    return us.value
+
+
 def stream_read_gbps(ctx: Context, nbytes: int = 1 << 30, n_reps: int = 20) -> tuple[float, float]:
     """Measured stream-read peak of ctx's device: nbytes read once per
     launch, n_reps launches back to back (gh_time_stream_read).  Returns

@@ -117,6 +117,7 @@ SIGNATURES = {
     "gh_sample_logits": (C.c_int, [_P, _P, C.c_int, C.c_float, C.c_uint64, C.c_uint64, _I32]),
     "gh_time_kernel": (C.c_int, [_P, _P, C.c_char_p, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double), _I32]),
     "gh_time_stream_read": (C.c_int, [_P, C.c_size_t, C.c_int32, C.POINTER(C.c_double)]),
+    "gh_time_exchange": (C.c_int, [_P, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
     "gh_synth_f32": (C.c_int, [C.c_uint64, C.c_char_p, C.c_float, _P, C.c_size_t]),
     "gh_synth_q4_0": (C.c_int, [C.c_uint64, C.c_char_p, C.c_float, C.c_int64, C.c_int64, _P]),
     "gh_synth_tokens": (C.c_int, [C.c_uint64, C.c_char_p, C.c_int32, C.c_int32, _P]),

@@ -6,6 +6,7 @@ Driver (run under rocprofv3 on the GPU box, eagerly: GH_NO_GRAPH=1):
                                          [--kv-synth N] [--copy-mib 256] [--manifest FILE]
   python -m gemma_hip.kernel_profile run --prefill 128 [--reps 5] [--copy-mib 256]
   python -m gemma_hip.kernel_profile run --attention 32768 [--reps 20] [--copy-mib 256]
+  python -m gemma_hip.kernel_profile exchange [--wgs 8 64 128 256] [--rounds 2000]
 
 It builds the seeded model of the config and decodes a short prompt.  Then,
 for each step-kernel kind asked for, it launches a separator (two launches
@@ -17,7 +18,9 @@ byte counters, which reads and writes exactly that many bytes.  With
 --prefill N it instead runs `reps` prefills of a seeded N-token prompt;
 with --attention L, `reps` op-level attention decodes (4 q heads, 1 kv head,
 head_dim 256, global over L positions: the C4 case).  The manifest (JSON)
-lists the segments in order.
+lists the segments in order.  `exchange` needs no profiler: it prints the
+cost of one all-to-all word exchange among n co-resident workgroups
+(gh_time_exchange, the persistent step's synchronisation).
 
 Summariser (on any host, from rocprofv3's CSV output):
 
@@ -248,9 +251,23 @@ def summarize(a) -> int:
     return 0
 
 
+def exchange(a) -> int:
+    """Cost of one all-to-all word exchange among n co-resident workgroups
+    (gh_time_exchange), for each n of --wgs: a markdown table."""
+    from . import time_exchange
+    ctx = Context(0)
+    time_exchange(ctx, 8, 100)  # warm-up (code object load)
+    print("| workgroups | rounds | us per exchange (median of 5 runs) |")
+    print("|---|---|---|")
+    for n in a.wgs:
+        us = sorted(time_exchange(ctx, n, a.rounds) for _ in range(5))
+        print(f"| {n} | {a.rounds} | {us[2]:.3f} |")
+    return 0
+
+
 def main(argv=None) -> int:
     argv = list(sys.argv[1:] if argv is None else argv)
-    if not argv or argv[0] not in ("run", "summarize"):
+    if not argv or argv[0] not in ("run", "summarize", "exchange"):
         argv = ["run", *argv]
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd")
@@ -264,11 +281,16 @@ def main(argv=None) -> int:
     r.add_argument("--prefill", type=int, default=0, help="time N-token prefills instead of step kernels")
     r.add_argument("--attention", type=int, default=0, help="op-level C4 attention over L positions")
     r.add_argument("--manifest", default="")
+    x = sub.add_parser("exchange")
+    x.add_argument("--wgs", type=int, nargs="+", default=[8, 64, 128, 256])
+    x.add_argument("--rounds", type=int, default=2000)
     s = sub.add_parser("summarize")
     s.add_argument("--manifest", required=True)
     for k in ("fetch", "write", "sq", "trace"):
         s.add_argument(f"--{k}", default="")
     a = ap.parse_args(argv)
+    if a.cmd == "exchange":
+        return exchange(a)
     return run(a) if a.cmd == "run" else summarize(a)
 
 

@@ -310,6 +310,13 @@ int gh_time_kernel(gh_model* m, gh_kv* kv, const char* name, int32_t n_reps, dou
  * bytes / duration is the practical HBM read bandwidth the hot path's
  * weight streaming is measured against beside the nominal 8 TB/s. */
 int gh_time_stream_read(gh_ctx* ctx, size_t bytes, int32_t n_reps, double* avg_us_out);
+/* All-to-all exchange cost (no reference counterpart; the measurement
+ * behind the persistent step): `rounds` exchanges of one self-validating
+ * 64-bit word per workgroup among n_wg co-resident workgroups (one kernel,
+ * agent-scope relaxed stores and polled loads).  *us_out = microseconds per
+ * exchange (workgroup 0's clock over all rounds).  GH_ERR_RANGE for n_wg
+ * outside 1 .. min(256, CUs); GH_ERR_STATE if a bounded wait timed out. */
+int gh_time_exchange(gh_ctx* ctx, int32_t n_wg, int32_t rounds, double* us_out);
 
 /* ================================================================
  * Seeded synthetic weights (SplitMix64 + Box-Muller), identical on every

@@ -33,6 +33,7 @@ int launch_attention(const float*, const float*, const float*, int, int, int, in
 int launch_gelu_mul(const float*, const float*, int, float*, hipStream_t) { return GH_OK; }
 int launch_argmax(const float*, int, unsigned long long*, hipStream_t) { return GH_OK; }
 int launch_stream_read(const void*, size_t, float*, hipStream_t) { return GH_OK; }
+int launch_xchg_probe(uint64_t*, int, int, int*, unsigned long long*, hipStream_t) { return GH_OK; }
 int attn_noalloc_scratch(float** out) {
     static float buf[16];
     *out = buf;

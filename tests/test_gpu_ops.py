@@ -233,3 +233,15 @@ def test_sample_logits_matches_oracle(ctx):
             want, margin = orc.sample(logits, T, orc.philox_uniform(99, c))
             assert got == want or margin < 1e-4, (n, T, c, got, want, margin)
         assert gh.sample_logits(ctx, logits, 0.0, 99, 0) == int(np.argmax(logits))
+
+
+def test_exchange_probe(ctx):
+    """gh_time_exchange: a positive, finite time per all-to-all exchange for
+    small and chip-wide groups; group sizes past the CUs or 256 are refused."""
+    for n in (8, 64):
+        us = gh.time_exchange(ctx, n, 500)
+        assert 0.0 < us < 1e3, (n, us)
+    for bad in (0, 257):
+        with pytest.raises(gh.GemmaHipError):
+            gh.time_exchange(ctx, bad, 10)
+
