@@ -75,6 +75,7 @@ struct StepState {
     float inv_temp;     // 1/temperature; 0 = greedy
     uint32_t seed_lo, seed_hi;  // Philox key of the sampler
     int32_t xchg_err;   // persistent step: an exchange wait timed out
+    int32_t top_k;      // sampler: draw among the top_k largest logits (0 = all)
     unsigned long long keys[2];  // argmax keys, slot pos & 1
 };
 
@@ -260,6 +261,7 @@ struct gh_kv {
     int32_t* d_ids = nullptr;     // [max_seq]
     float inv_temp = 0.0f;        // sampler: 1/temperature (0 = greedy)
     uint64_t seed = 0;            // sampler: Philox key
+    int top_k = 0;                // sampler: candidates (0 = every logit)
     gh::StepState* h_st = nullptr;  // pinned staging
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -316,8 +318,9 @@ constexpr int GH_ATTN_OP_MAX_NC = 256;  // chunks per kv head of the op-level at
 constexpr size_t ATTN_NOALLOC_SCRATCH_FLOATS = size_t(1) << 20;
 // this device's address of that array (hipGetSymbolAddress, once per device)
 int attn_noalloc_scratch(float** out);
-int launch_sample_logits(const float* logits, int n, float inv_temp, uint64_t seed, uint64_t counter, float* scratch,
-                         int32_t* token_dev, hipStream_t s);
+// top_k 0: every logit; 1..GH_TOP_K_MAX (gemma_hip.h): the top_k largest
+int launch_sample_logits(const float* logits, int n, float inv_temp, int top_k, uint64_t seed, uint64_t counter,
+                         float* scratch, int32_t* token_dev, hipStream_t s);
 
 // repack.cpp
 void repack_q4_0(const uint8_t* raw, int64_t rows, int64_t cols, bool ftz, uint8_t* codes,

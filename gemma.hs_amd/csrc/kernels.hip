@@ -2183,72 +2183,392 @@ __host__ __device__ inline float philox_uniform(uint64_t seed, uint64_t counter)
     return (float)(o.x >> 8) * (1.0f / 16777216.0f);
 }
 
-// Categorical draw from softmax(l / T) over n logits given per-block
-// statistics (block b = rows [b*R, b*R+R): max bm[b], sum bs[b] of
+// ---- samplers ----
+// Inversion draws: with weights w_i over an ordered set and u in [0, 1), the
+// pick is the first element whose running sum of weights exceeds u * total
+// (if rounding leaves none, the last element with a positive weight).
+
+// inclusive running sum over the 64 lanes, lane order
+__device__ __forceinline__ float wave_scan_incl(float v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(v, o, 64);
+        if (lane >= o) v += y;
+    }
+    return v;
+}
+
+// One wave walks rows r0 .. r1-1 (64 at a time) for the first row whose
+// running sum of exp((l - M) / T) exceeds `target`; all lanes return it.
+__device__ __forceinline__ int wave_row_walk(const float* logits, int r0, int r1, float M, float inv_t, float target) {
+    const int lane = threadIdx.x & 63;
+    const BufView L(logits, (size_t)r1 * 4);
+    float base = 0.0f;
+    int last = r0;
+    for (int s = r0; s < r1; s += 64) {
+        const int r = s + lane;
+        const float y = L.f1(r < r1 ? 4u * r : OOB);
+        const float wt = r < r1 ? expf((y - M) * inv_t) : 0.0f;
+        const float c = base + wave_scan_incl(wt);
+        const unsigned long long hit = __ballot(wt > 0.0f && c > target);
+        if (hit) return s + __builtin_ctzll(hit);
+        const unsigned long long any = __ballot(wt > 0.0f);
+        if (any) last = s + 63 - __builtin_clzll(any);
+        base = readlane(c, 63);
+    }
+    return last;
+}
+
+// Categorical draw from softmax(l / T) over n logits in index order, given
+// per-block statistics (block b = rows [b*R, b*R+R): max bm[b], sum bs[b] of
 // exp((l - bm[b]) / T)):  M = max bm, W_b = bs[b] exp((bm[b] - M) / T),
-// target = u * sum W; the block whose running sum of W passes the target,
-// then the row whose running sum of exp((l - M) / T) inside it passes the
-// remainder.  Called by all NT threads; returns the row in every thread.
-__device__ int sample_select(const float* bm, const float* bs, int nb, int R, const float* logits, int n, float inv_t,
+// target = u * sum W.  Thread t holds the W of its `per` consecutive blocks
+// and their sum; a block-wide running sum over the threads finds the thread,
+// the thread's own running sum the block, and wave 0's running sum over the
+// block's rows the row.  Called by all NT threads; returns the row in every
+// thread.
+__device__ __forceinline__ int sample_select(const float* bm, const float* bs, int nb, int R, const float* logits, int n, float inv_t,
                              float u) {
-    __shared__ float part[NT];
+    constexpr int BPT = 16;  // blocks per thread kept in registers
     __shared__ float slot[8];
-    __shared__ int chosen;
-    const int tid = threadIdx.x;
-    float m = -INFINITY;
-    for (int b = tid; b < nb; b += NT) m = fmaxf(m, bm[b]);
-    const float M = block_max(m, slot);
+    __shared__ float wsum[4];
+    __shared__ int hit_t[4], last_t[4];
+    __shared__ int sel_b;
+    __shared__ float sel_rem;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const BufView BM(bm, (size_t)nb * 4), BS(bs, (size_t)nb * 4);
     const int per = (nb + NT - 1) / NT, b0 = min(nb, tid * per), b1 = min(nb, b0 + per);
-    float w = 0.0f;
-    for (int b = b0; b < b1; ++b) w += bs[b] * expf((bm[b] - M) * inv_t);
-    part[tid] = w;
+    // the thread's blocks as one batch of loads (per <= BPT), M, their weights
+    float xb[BPT], sb[BPT], wb[BPT];
+    float m = -INFINITY, part = 0.0f;
+    if (per <= BPT) {
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+            const int b = b0 + j;
+            xb[j] = BM.f1(b < b1 ? 4u * b : OOB);
+            sb[j] = BS.f1(b < b1 ? 4u * b : OOB);
+        }
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) m = b0 + j < b1 ? fmaxf(m, xb[j]) : m;
+    } else {
+        for (int b = b0; b < b1; ++b) m = fmaxf(m, bm[b]);
+    }
+    const float M = block_max(m, slot);
+    if (per <= BPT) {
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+            wb[j] = b0 + j < b1 ? sb[j] * expf((xb[j] - M) * inv_t) : 0.0f;
+            part += wb[j];
+        }
+    } else {
+        for (int b = b0; b < b1; ++b) part += bs[b] * expf((bm[b] - M) * inv_t);
+    }
+    // threads in order: the first whose running sum passes the target
+    const float c = wave_scan_incl(part);
+    if (lane == 63) wsum[w] = c;
     __syncthreads();
-    if (tid == 0) {
-        float z = 0.0f;
-        for (int t = 0; t < NT; ++t) z += part[t];
-        float target = u * z, acc = 0.0f;
-        int t = 0, last_t = -1;
-        for (; t < NT; ++t) {
-            if (part[t] > 0.0f) last_t = t;
-            if (acc + part[t] > target && part[t] > 0.0f) break;
-            acc += part[t];
-        }
-        if (t == NT) {  // rounding: the target landed past the total
-            t = last_t;
-            acc = z - part[t];
-        }
-        target -= acc;
-        const int c0 = min(nb, t * per), c1 = min(nb, c0 + per);
-        int bsel = -1, last_b = -1;
-        float acc_b = 0.0f;
-        for (int b = c0; b < c1; ++b) {
-            const float wb = bs[b] * expf((bm[b] - M) * inv_t);
-            if (wb > 0.0f) last_b = b;
-            if (acc_b + wb > target && wb > 0.0f) {
-                bsel = b;
-                break;
+    float base = 0.0f, Z = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        base += i < w ? wsum[i] : 0.0f;
+        Z += wsum[i];
+    }
+    const float target = u * Z, incl = base + c;
+    const unsigned long long hit = __ballot(part > 0.0f && incl > target);
+    const unsigned long long any = __ballot(part > 0.0f);
+    if (lane == 0) {
+        hit_t[w] = hit ? 64 * w + __builtin_ctzll(hit) : -1;
+        last_t[w] = any ? 64 * w + 63 - __builtin_clzll(any) : -1;
+    }
+    __syncthreads();
+    int t_sel = -1, t_last = -1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (t_sel < 0) t_sel = hit_t[i];
+        t_last = max(t_last, last_t[i]);
+    }
+    if (t_sel < 0) t_sel = max(t_last, 0);  // rounding: the target landed past the total (NaN: none, row 0)
+    if (tid == t_sel) {
+        float rem = target - (incl - part), acc = 0.0f;
+        int bsel = -1, blast = b0;
+        if (per <= BPT) {
+#pragma unroll
+            for (int j = 0; j < BPT; ++j) {
+                if (bsel < 0 && b0 + j < b1) {
+                    if (wb[j] > 0.0f) blast = b0 + j;
+                    if (acc + wb[j] > rem && wb[j] > 0.0f) bsel = b0 + j;
+                    else acc += wb[j];
+                }
             }
-            acc_b += wb;
-        }
-        if (bsel < 0) {
-            bsel = last_b;
-            acc_b = 0.0f;
-            for (int b = c0; b < bsel; ++b) acc_b += bs[b] * expf((bm[b] - M) * inv_t);
-        }
-        target -= acc_b;
-        const int r0 = bsel * R, r1 = min(n, r0 + R);
-        int row = -1, last_r = r0;
-        float acc_r = 0.0f;
-        for (int r = r0; r < r1; ++r) {
-            const float wr = expf((logits[r] - M) * inv_t);
-            if (wr > 0.0f) last_r = r;
-            if (acc_r + wr > target && wr > 0.0f) {
-                row = r;
-                break;
+        } else {
+            for (int b = b0; b < b1 && bsel < 0; ++b) {
+                const float wj = bs[b] * expf((bm[b] - M) * inv_t);
+                if (wj > 0.0f) blast = b;
+                if (acc + wj > rem && wj > 0.0f) bsel = b;
+                else acc += wj;
             }
-            acc_r += wr;
         }
-        chosen = row >= 0 ? row : last_r;
+        sel_b = bsel >= 0 ? bsel : blast;
+        // rounding past the thread's total: the last positive row of its last positive block
+        sel_rem = bsel >= 0 ? rem - acc : INFINITY;
+    }
+    __syncthreads();
+    __shared__ int chosen;
+    if (w == 0) {
+        const int r0 = sel_b * R;
+        const int row = wave_row_walk(logits, r0, min(n, r0 + R), M, inv_t, sel_rem);
+        if (lane == 0) chosen = row;
+    }
+    __syncthreads();
+    return chosen;
+}
+
+// ---- top-k sampling ----
+// Keys are argmax_key(value, index): a larger key is a larger value, then a
+// lower index, and 0 is below every real key.  A wave keeps the 64 best keys
+// it has seen as a list sorted in descending order across its lanes
+// (GH_TOP_K_MAX = 64, one key per lane).
+
+__device__ __forceinline__ unsigned long long umin64(unsigned long long a, unsigned long long b) {
+    return a < b ? a : b;
+}
+
+__device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int src) {
+    const unsigned lo = __shfl((unsigned)v, src, 64), hi = __shfl((unsigned)(v >> 32), src, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)v, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(v >> 32), CTRL, 0xF, 0xF, false);
+    return ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo;
+}
+
+// the key of lane ^ S: DPP inside 16-lane rows (S = 4 as a half-row mirror,
+// lane ^ 7, then a quad reversal, lane ^ 3), a permute across rows
+template <int S>
+__device__ __forceinline__ unsigned long long lane_xor_u64(unsigned long long v) {
+    if constexpr (S == 1) {
+        return dpp_u64<DPP_QUAD_XOR1>(v);
+    } else if constexpr (S == 2) {
+        return dpp_u64<DPP_QUAD_XOR2>(v);
+    } else if constexpr (S == 4) {
+        return dpp_u64<0x1B>(dpp_u64<DPP_ROW_HALF_MIRROR>(v));  // quad_perm [3,2,1,0]
+    } else if constexpr (S == 8) {
+        return dpp_u64<DPP_ROW_ROR8>(v);
+    } else {
+        return shfl_xor_u64(v, S);
+    }
+}
+
+// compare-exchange steps STRIDE, STRIDE/2, .., 1 of a bitonic network whose
+// blocks of SIZE lanes sort descending (ascending if ASC) when SIZE = 64 and
+// alternate below
+template <int SIZE, int STRIDE, bool ASC>
+__device__ __forceinline__ unsigned long long bitonic_steps(unsigned long long key, int lane) {
+    const unsigned long long o = lane_xor_u64<STRIDE>(key);
+    const bool desc = ((lane & SIZE) == 0) != ASC;
+    key = (((lane & STRIDE) == 0) == desc) ? umax64(key, o) : umin64(key, o);
+    if constexpr (STRIDE > 1) return bitonic_steps<SIZE, STRIDE / 2, ASC>(key, lane);
+    return key;
+}
+
+template <bool ASC, int SIZE = 2>
+__device__ __forceinline__ unsigned long long wave_sort(unsigned long long key, int lane) {
+    key = bitonic_steps<SIZE, SIZE / 2, ASC>(key, lane);
+    if constexpr (SIZE < 64) return wave_sort<ASC, SIZE * 2>(key, lane);
+    return key;
+}
+
+// the 64 best of a descending list and an ascending one: their lane-wise max
+// is a bitonic sequence holding them, which one half-cleaner cascade sorts
+__device__ __forceinline__ unsigned long long wave_merge(unsigned long long desc, unsigned long long asc, int lane) {
+    return bitonic_steps<64, 32, false>(umax64(desc, asc), lane);
+}
+
+// Streaming top-k of one wave: keys that beat the list's k-th key gather in
+// a 128-key LDS buffer; each 64 of them are sorted and merged into the list.
+struct WaveTopK {
+    unsigned long long list = 0ull;  // descending, lane j = rank j
+    unsigned long long thr = 0ull;   // a key must exceed this to matter
+    unsigned long long floor = 0ull; // thr never drops below this bound
+    int count = 0;                   // keys in the buffer
+    unsigned long long* buf;
+
+    __device__ __forceinline__ void flush(int k, int lane) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const unsigned long long g = lane < count ? buf[lane] : 0ull;
+        const unsigned long long rest = lane + 64 < count ? buf[lane + 64] : 0ull;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane + 64 < count) buf[lane] = rest;
+        count = max(0, count - 64);
+        list = wave_merge(list, wave_sort<true>(g, lane), lane);
+        thr = umax64(floor, shfl_u64(list, k - 1));
+    }
+    __device__ __forceinline__ void push(unsigned long long key, int k, int lane) {
+        const bool pass = key > thr;
+        const unsigned long long m = __ballot(pass);
+        if (!m) return;
+        if (pass) buf[count + __builtin_popcountll(m & ((1ull << lane) - 1ull))] = key;
+        count += __builtin_popcountll(m);
+        if (count >= 64) flush(k, lane);
+    }
+};
+
+// the four waves' lists merged (one barrier; `lds` holds 256 keys and must
+// not be reused before every thread has returned); every wave gets the result
+__device__ __forceinline__ unsigned long long block_merge(unsigned long long list, unsigned long long* lds) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    lds[64 * w + 63 - lane] = list;  // reversed: ascending
+    __syncthreads();
+    list = lds[63 - lane];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) list = wave_merge(list, lds[64 * i + lane], lane);
+    return list;
+}
+
+__device__ __forceinline__ float key_value(unsigned long long key) {
+    const unsigned ord = (unsigned)(key >> 32);
+    return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord);
+}
+
+// Keys at or above `floor` among each thread's `VPT` keys, appended to
+// cand[] in thread order (one LDS atomic per wave); returns after a barrier
+// with every thread seeing the count.  `cnt` must be zero on entry to the
+// barrier before the first call and is left holding the count.
+template <int VPT>
+__device__ __forceinline__ int block_compact(const unsigned long long (&key)[VPT], unsigned long long floor,
+                                             unsigned long long* cand, int* cnt) {
+    const int lane = threadIdx.x & 63;
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) mine += key[j] != 0ull && key[j] >= floor;
+    int incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    int base = 0;
+    if (lane == 63 && incl) base = atomicAdd(cnt, incl);
+    int at = __shfl(base, 63, 64) + incl - mine;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+        if (key[j] != 0ull && key[j] >= floor) cand[at++] = key[j];
+    __syncthreads();
+    return *cnt;
+}
+
+// Draw from softmax(l / T) restricted to the k largest logits (k <= 64;
+// value descending, then lower index) by inversion in that rank order:
+// weights exp((l_j - l_0) / T).  bm[b] is the max over rows [b*R, b*R+R) (R
+// a multiple of 64).
+//   1. The k tiles with the largest (max, -tile): the k-th largest of the
+//      threads' own best tile keys bounds them from below (k threads hold a
+//      tile at or above it), so only tiles at or above it are kept, then
+//      streamed through each wave's top-k and merged.
+//   2. Those tiles hold the k largest logits: each holds a logit >= the k-th
+//      largest tile max m, so the k-th largest logit is >= m, while a logit
+//      outside them is <= m, and if equal to m it lies in a later tile than
+//      every chosen tile of max m, so at a higher row than logits it ties
+//      with.  Their rows at or above m are kept and streamed the same way.
+// Values arrive as one batch of loads per 4096.  Called by all NT threads;
+// returns the row in every thread.
+__device__ __forceinline__ int sample_top_k(const float* bm, int nb, int R, const float* logits, int n, int k,
+                                            float inv_t, float u) {
+    constexpr int CH = 4096;  // values per pass
+    constexpr int VPT = CH / NT;
+    __shared__ unsigned long long cand[CH];
+    __shared__ unsigned long long bufs[4][128];
+    __shared__ unsigned long long lists[3][NT];
+    __shared__ int tiles[GH_TOP_K_MAX];
+    __shared__ int cnt;
+    __shared__ int chosen;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    k = max(1, min(k, min(GH_TOP_K_MAX, n)));
+    WaveTopK s;
+    s.buf = bufs[w];
+    // 1. the k tiles
+    const BufView B(bm, (size_t)nb * 4);
+    for (int c0 = 0; c0 < nb; c0 += CH) {
+        if (c0) __syncthreads();  // the previous pass is consumed
+        if (tid == 0) cnt = 0;
+        const int cn = min(CH, nb - c0);
+        float v[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int e = tid + NT * j;
+            v[j] = B.f1(e < cn ? 4u * (c0 + e) : OOB);
+        }
+        unsigned long long key[VPT], tmax = 0ull;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int e = tid + NT * j;
+            key[j] = e < cn ? argmax_key(v[j], c0 + e) : 0ull;
+            tmax = umax64(tmax, key[j]);
+        }
+        const unsigned long long tm = block_merge(wave_sort<false>(tmax, lane), lists[0]);
+        const int nc = block_compact(key, shfl_u64(tm, k - 1), cand, &cnt);
+        for (int g = w; g * 64 < nc; g += 4) {
+            const int e = g * 64 + lane;
+            s.push(e < nc ? cand[e] : 0ull, k, lane);
+        }
+    }
+    if (s.count) s.flush(k, lane);
+    const unsigned long long tl = block_merge(s.list, lists[1]);
+    if (w == 0) tiles[lane] = (int)(0xFFFFFFFFu - (unsigned)tl);
+    // 2. the k best rows of those tiles, counting only rows at or above the
+    // k-th tile max
+    const unsigned kth_ord = (unsigned)(shfl_u64(tl, k - 1) >> 32);
+    const unsigned long long floor = kth_ord ? (unsigned long long)kth_ord << 32 : 1ull;
+    s.list = 0ull;
+    s.floor = s.thr = floor - 1ull;
+    s.count = 0;
+    const BufView L(logits, (size_t)n * 4);
+    const int total = k * R;
+    for (int c0 = 0; c0 < total; c0 += CH) {
+        __syncthreads();  // tiles written; the previous pass is consumed
+        if (tid == 0) cnt = 0;
+        __syncthreads();
+        const int cn = min(CH, total - c0);
+        float v[VPT];
+        int row[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int e = tid + NT * j, slot = min((c0 + e) / R, GH_TOP_K_MAX - 1);
+            row[j] = tiles[slot] * R + (c0 + e - slot * R);
+            v[j] = L.f1(e < cn && (unsigned)row[j] < (unsigned)n ? 4u * row[j] : OOB);
+        }
+        // (slots past the tiles that exist hold tile -1: negative rows)
+        unsigned long long key[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j)
+            key[j] = tid + NT * j < cn && (unsigned)row[j] < (unsigned)n ? argmax_key(v[j], row[j]) : 0ull;
+        const int nc = block_compact(key, floor, cand, &cnt);
+        for (int g = w; g * 64 < nc; g += 4) {
+            const int e = g * 64 + lane;
+            s.push(e < nc ? cand[e] : 0ull, k, lane);
+        }
+    }
+    if (s.count) s.flush(k, lane);
+    const unsigned long long best = block_merge(s.list, lists[2]);
+    // 3. inversion over ranks 0..k-1 (wave 0)
+    if (w == 0) {
+        const float v = key_value(best), v0 = readlane(v, 0);
+        const float wt = lane < k && best != 0ull ? expf((v - v0) * inv_t) : 0.0f;
+        const float c = wave_scan_incl(wt);
+        const float target = u * readlane(c, 63);
+        const unsigned long long hit = __ballot(wt > 0.0f && c > target);
+        const unsigned long long any = __ballot(wt > 0.0f);
+        const int pick = hit ? __builtin_ctzll(hit) : (any ? 63 - __builtin_clzll(any) : 0);
+        const unsigned row = 0xFFFFFFFFu - (unsigned)__builtin_amdgcn_readlane((int)(unsigned)best, pick);
+        if (lane == 0) chosen = row < (unsigned)n ? (int)row : 0;
     }
     __syncthreads();
     return chosen;
@@ -2270,7 +2590,10 @@ __global__ __launch_bounds__(NT) void k_step_finish(StepState* st, int pos, cons
     int tok;
     if (inv_t > 0.0f) {  // temperature sampling with a Philox draw keyed by the seed, counter = position
         const uint64_t seed = ((uint64_t)st->seed_hi << 32) | st->seed_lo;
-        tok = sample_select(bm, bs, n_cand, rows_per_cand, logits, V, inv_t, philox_uniform(seed, (uint64_t)pos));
+        const float u = philox_uniform(seed, (uint64_t)pos);
+        const int top_k = st->top_k;
+        tok = top_k > 0 ? sample_top_k(bm, n_cand, rows_per_cand, logits, V, top_k, inv_t, u)
+                        : sample_select(bm, bs, n_cand, rows_per_cand, logits, V, inv_t, u);
     } else {  // greedy: first maximum (sampleGreedy, examples/BenchmarkKVCache.hs:223-224)
         // the per-item keys as one batch of straight-line buffer loads (keys
         // past n_cand read zero, which no real key loses to)
@@ -4547,13 +4870,24 @@ __global__ __launch_bounds__(NT) void k_sample_select(const float* bm, const flo
     if (threadIdx.x == 0) *token = t;
 }
 
-int launch_sample_logits(const float* logits, int n, float inv_t, uint64_t seed, uint64_t counter, float* scratch,
-                         int32_t* token, hipStream_t s) {
+__global__ __launch_bounds__(NT) void k_sample_top_k(const float* bm, int nb, const float* logits, int n, int top_k,
+                                                     float inv_t, uint64_t seed, uint64_t counter, int32_t* token) {
+    const int t = sample_top_k(bm, nb, 64, logits, n, top_k, inv_t, philox_uniform(seed, counter));
+    if (threadIdx.x == 0) *token = t;
+}
+
+int launch_sample_logits(const float* logits, int n, float inv_t, int top_k, uint64_t seed, uint64_t counter,
+                         float* scratch, int32_t* token, hipStream_t s) {
     if (!(inv_t > 0.0f)) return set_error(GH_ERR_INVALID, "sampling needs a temperature > 0");
+    if (top_k < 0 || top_k > GH_TOP_K_MAX) return set_error(GH_ERR_RANGE, "top_k %d outside [0, %d]", top_k, GH_TOP_K_MAX);
     const int nb = (n + 63) / 64;
     hipLaunchKernelGGL(k_sample_blocks, dim3(nb), dim3(64), 0, s, logits, n, inv_t, scratch, scratch + nb);
-    hipLaunchKernelGGL(k_sample_select, dim3(1), dim3(NT), 0, s, (const float*)scratch, (const float*)(scratch + nb), nb,
-                       logits, n, inv_t, seed, counter, token);
+    if (top_k > 0)
+        hipLaunchKernelGGL(k_sample_top_k, dim3(1), dim3(NT), 0, s, (const float*)scratch, nb, logits, n, top_k, inv_t,
+                           seed, counter, token);
+    else
+        hipLaunchKernelGGL(k_sample_select, dim3(1), dim3(NT), 0, s, (const float*)scratch,
+                           (const float*)(scratch + nb), nb, logits, n, inv_t, seed, counter, token);
     GH_HIP(hipGetLastError());
     return GH_OK;
 }

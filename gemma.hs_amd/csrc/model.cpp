@@ -406,6 +406,7 @@ int put_state(gh_kv* kv, int pos, int token, int start, int n_prompt, int gen_ca
     h->seed_lo = (uint32_t)kv->seed;
     h->seed_hi = (uint32_t)(kv->seed >> 32);
     h->xchg_err = 0;
+    h->top_k = kv->top_k;
     GH_HIP(hipMemcpyAsync(kv->st, h, offsetof(StepState, keys), hipMemcpyHostToDevice, kv->m->ctx->stream));
     return GH_OK;
 }
@@ -828,18 +829,24 @@ extern "C" int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, f
 
 extern "C" int gh_sample_logits(gh_ctx* ctx, const float* logits, int n, float temperature, uint64_t seed,
                                 uint64_t counter, int32_t* token_out) {
+    return gh_sample_logits_top_k(ctx, logits, n, temperature, 0, seed, counter, token_out);
+}
+
+extern "C" int gh_sample_logits_top_k(gh_ctx* ctx, const float* logits, int n, float temperature, int32_t top_k,
+                                      uint64_t seed, uint64_t counter, int32_t* token_out) {
     OP_ENTER(ctx);
     if (!logits || !token_out || n <= 0) return set_error(GH_ERR_INVALID, "gh_sample_logits: bad arguments");
     if (!(temperature >= 0.0f) || std::isinf(temperature))
         return set_error(GH_ERR_INVALID, "temperature must be finite and >= 0");
+    if (top_k < 0 || top_k > GH_TOP_K_MAX)
+        return set_error(GH_ERR_RANGE, "top_k %d outside [0, %d]", top_k, GH_TOP_K_MAX);
     if (temperature == 0.0f) return gh_argmax(ctx, logits, n, token_out);
     const int nblk = (n + 63) / 64;
     void* scratch = nullptr;
     GH_CHECK(ctx_scratch(ctx, sizeof(float) * (2 * (size_t)nblk + 4), &scratch));
     float* sc = (float*)scratch;
     int32_t* tok_dev = (int32_t*)(sc + 2 * (size_t)nblk);
-    GH_CHECK(launch_sample_logits(logits, n, temperature > 0.0f ? 1.0f / temperature : 0.0f, seed, counter, sc, tok_dev,
-                                  ctx->stream));
+    GH_CHECK(launch_sample_logits(logits, n, 1.0f / temperature, top_k, seed, counter, sc, tok_dev, ctx->stream));
     int32_t tok = -1;
     GH_HIP(hipMemcpyAsync(&tok, tok_dev, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
     GH_CHECK(op_sync(ctx));
@@ -1164,6 +1171,15 @@ extern "C" int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed) {
         return set_error(GH_ERR_INVALID, "temperature must be finite and >= 0");
     kv->inv_temp = temperature > 0.0f ? 1.0f / temperature : 0.0f;
     kv->seed = seed;
+    return GH_OK;
+}
+
+extern "C" int gh_kv_set_top_k(gh_kv* kv, int32_t top_k) {
+    GH_LIVE(kv, HK_KV);
+    if (!kv) return set_error(GH_ERR_INVALID, "null kv");
+    if (top_k < 0 || top_k > GH_TOP_K_MAX)
+        return set_error(GH_ERR_RANGE, "top_k %d outside [0, %d]", top_k, GH_TOP_K_MAX);
+    kv->top_k = top_k;
     return GH_OK;
 }
 

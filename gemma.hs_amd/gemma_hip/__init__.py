@@ -248,14 +248,20 @@ def attention_decode(ctx: Context, q, k_cache, v_cache, nq: int, nkv: int, head_
             b.free()
 
 
-def sample_logits(ctx: Context, logits, temperature: float, seed: int, counter: int) -> int:
+def sample_logits(ctx: Context, logits, temperature: float, seed: int, counter: int, top_k: int = 0) -> int:
     """Draw from softmax(logits / T) with Philox4x32-10 (key seed, counter);
-    temperature 0 is the argmax (gh_sample_logits)."""
+    temperature 0 is the argmax (gh_sample_logits).  top_k > 0 restricts the
+    draw to the top_k largest logits, drawn in rank order
+    (gh_sample_logits_top_k)."""
     lb = _dev(ctx, logits)
     t = C.c_int32()
     try:
-        check(lib().gh_sample_logits(ctx.h, lb.ptr, len(logits), float(temperature), int(seed), int(counter),
-                                     C.byref(t)))
+        if top_k:
+            check(lib().gh_sample_logits_top_k(ctx.h, lb.ptr, len(logits), float(temperature), int(top_k), int(seed),
+                                               int(counter), C.byref(t)))
+        else:
+            check(lib().gh_sample_logits(ctx.h, lb.ptr, len(logits), float(temperature), int(seed), int(counter),
+                                         C.byref(t)))
         return t.value
     finally:
         lb.free()
@@ -437,6 +443,11 @@ class KVCache:
         (sampleToken, app/Main.hs:488-507); > 0 = draw from softmax(l / T)
         with Philox keyed by seed, counter = position (gh_kv_set_sampling)."""
         check(lib().gh_kv_set_sampling(self.h, float(temperature), int(seed)))
+
+    def set_top_k(self, top_k: int) -> None:
+        """Restrict sampled steps to the top_k largest logits, 1..64, drawn in
+        rank order; 0 = every logit (gh_kv_set_top_k)."""
+        check(lib().gh_kv_set_top_k(self.h, int(top_k)))
 
     def reset(self) -> None:
         check(lib().gh_kv_reset(self.h))

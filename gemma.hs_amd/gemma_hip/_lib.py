@@ -115,6 +115,8 @@ SIGNATURES = {
     "gh_kv_synth": (C.c_int, [_P, C.c_uint64, C.c_int32, C.c_float]),
     "gh_kv_set_sampling": (C.c_int, [_P, C.c_float, C.c_uint64]),
     "gh_sample_logits": (C.c_int, [_P, _P, C.c_int, C.c_float, C.c_uint64, C.c_uint64, _I32]),
+    "gh_sample_logits_top_k": (C.c_int, [_P, _P, C.c_int, C.c_float, C.c_int32, C.c_uint64, C.c_uint64, _I32]),
+    "gh_kv_set_top_k": (C.c_int, [_P, C.c_int32]),
     "gh_time_kernel": (C.c_int, [_P, _P, C.c_char_p, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double), _I32]),
     "gh_time_stream_read": (C.c_int, [_P, C.c_size_t, C.c_int32, C.POINTER(C.c_double)]),
     "gh_time_exchange": (C.c_int, [_P, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),

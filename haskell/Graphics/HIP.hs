@@ -34,7 +34,7 @@ module Graphics.HIP
   , c_ctxCreate, c_ctxDestroy, p_ctxRelease, c_ctxSync
   , c_configPreset, c_modelCreate, c_modelDestroy, p_modelRelease
   , c_modelSetTensor, c_modelCheck, c_modelConfig, c_modelLoadGGUF, c_ggufInspect
-  , c_kvCreate, c_kvDestroy, p_kvRelease, c_kvReset, c_kvLength, c_kvTruncate, c_kvSetSampling
+  , c_kvCreate, c_kvDestroy, p_kvRelease, c_kvReset, c_kvLength, c_kvTruncate, c_kvSetSampling, c_kvSetTopK
   , c_step, c_generate, c_prefill, c_generatePrefill
   , c_q4Upload, c_q4Free, p_q4Release, c_q4Matvec, c_q4Dequant, c_linearQ4
     -- * Constants
@@ -138,6 +138,7 @@ foreign import ccall safe "gh_kv_reset" c_kvReset :: Ptr KvS -> IO CInt
 foreign import ccall safe "gh_kv_length" c_kvLength :: Ptr KvS -> Ptr Int32 -> IO CInt
 foreign import ccall safe "gh_kv_truncate" c_kvTruncate :: Ptr KvS -> Int32 -> IO CInt
 foreign import ccall safe "gh_kv_set_sampling" c_kvSetSampling :: Ptr KvS -> CFloat -> Word64 -> IO CInt
+foreign import ccall safe "gh_kv_set_top_k" c_kvSetTopK :: Ptr KvS -> Int32 -> IO CInt
 
 foreign import ccall safe "gh_step"
   c_step :: Ptr ModelS -> Ptr KvS -> Int32 -> Ptr CFloat -> Ptr CFloat -> Ptr Int32 -> IO CInt

@@ -161,6 +161,14 @@ int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx_out);
  * device code as the step's sampler. */
 int gh_sample_logits(gh_ctx* ctx, const float* logits, int n, float temperature, uint64_t seed, uint64_t counter,
                      int32_t* token_out);
+/* Top-k variant, no reference counterpart (the reference's sampler is an
+ * argmax, app/Main.hs:505-507): the draw is restricted to the top_k largest
+ * logits (value descending, then lower index) and made by inversion in that
+ * rank order; top_k 0 is gh_sample_logits, 1..GH_TOP_K_MAX (64) restricts,
+ * anything else is GH_ERR_RANGE.  Same device code as the step's sampler. */
+#define GH_TOP_K_MAX 64
+int gh_sample_logits_top_k(gh_ctx* ctx, const float* logits, int n, float temperature, int32_t top_k,
+                           uint64_t seed, uint64_t counter, int32_t* token_out);
 
 
 /* ================================================================
@@ -230,6 +238,10 @@ int gh_kv_synth(gh_kv* kv, uint64_t seed, int32_t n_pos, float sigma);
  * from softmax(logits / T) with Philox4x32-10 keyed by `seed`, counter =
  * the step's position, so a generation is reproducible. */
 int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed);
+/* Top-k restriction of that draw for this cache's steps (no reference
+ * counterpart): 0 = every logit (the default), 1..GH_TOP_K_MAX = the top_k
+ * largest, as gh_sample_logits_top_k; it has no effect at temperature 0. */
+int gh_kv_set_top_k(gh_kv* kv, int32_t top_k);
 
 /* runGemmaInferenceCached (src/Gemma/Model.hs:1313-1437) and its layer-0
  * variant runGemmaInferenceCachedWithLayer0 (src/Gemma/Model.hs:1441):

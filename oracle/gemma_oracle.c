@@ -37,6 +37,12 @@
  *       dominant logit, and by frequencies against softmax on small n.
  *       There is no reference counterpart: the reference's temperature
  *       path is an argmax (app/Main.hs:505-507).
+ *   orc_sample_top_k                    : the same draw over the k largest
+ *       logits in rank order; pinned by k = 1 (the first maximum for every
+ *       u), equal logits (index floor(u k)), k = n on logits that decrease
+ *       with the index (orc_sample's pick for every u), the picked value's
+ *       invariance under a permutation of distinct logits, and frequencies
+ *       against a numpy top-k softmax.  No reference counterpart.
  *   orc_step / orc_generate             : composition of the above; checked
  *       against an independent float64 numpy restatement in the tests.
  */
@@ -608,4 +614,42 @@ int32_t orc_sample(const float* logits, int n, float temperature, float u, doubl
     if (fabs(acc - target) < margin) margin = fabs(acc - target);
     if (margin_out) *margin_out = margin / z;
     return pick >= 0 ? pick : last;
+}
+
+/* Inversion draw of u from softmax(logits / T) restricted to the k largest
+ * logits, ranked by value descending then index ascending, walked in rank
+ * order; margin as orc_sample's, over the restricted total. */
+int32_t orc_sample_top_k(const float* logits, int n, float temperature, int k, float u, double* margin_out) {
+    if (k > n) k = n;
+    if (k < 1) k = 1;
+    int32_t* idx = (int32_t*)malloc((size_t)k * sizeof(int32_t));
+    int have = 0;
+    for (int i = 0; i < n; ++i) { /* insertion into the ranked prefix; ties keep the earlier index first */
+        const float v = logits[i];
+        if (have == k && !(v > logits[idx[k - 1]])) continue;
+        int j = have < k ? have++ : k - 1;
+        while (j > 0 && v > logits[idx[j - 1]]) {
+            idx[j] = idx[j - 1];
+            --j;
+        }
+        idx[j] = i;
+    }
+    const double m = logits[idx[0]];
+    double z = 0.0;
+    for (int j = 0; j < k; ++j) z += exp(((double)logits[idx[j]] - m) / temperature);
+    const double target = (double)u * z;
+    double acc = 0.0, margin = INFINITY;
+    int pick = -1, last = 0;
+    for (int j = 0; j < k; ++j) {
+        const double w = exp(((double)logits[idx[j]] - m) / temperature);
+        if (w > 0.0) last = j;
+        if (fabs(acc - target) < margin) margin = fabs(acc - target);
+        if (pick < 0 && acc + w > target && w > 0.0) pick = j;
+        acc += w;
+    }
+    if (fabs(acc - target) < margin) margin = fabs(acc - target);
+    if (margin_out) *margin_out = margin / z;
+    const int32_t row = idx[pick >= 0 ? pick : last];
+    free(idx);
+    return row;
 }

@@ -74,6 +74,7 @@ float orc_philox_uniform(uint64_t seed, uint64_t counter);
  * exceeds u * total.  margin_out (may be NULL): distance of u * total to
  * the nearest running-sum boundary, relative to the total. */
 int32_t orc_sample(const float* logits, int n, float temperature, float u, double* margin_out);
+int32_t orc_sample_top_k(const float* logits, int n, float temperature, int k, float u, double* margin_out);
 
 /* ---- whole model ---- */
 typedef struct orc_model orc_model;

@@ -55,6 +55,7 @@ _SIG = {
     "orc_philox4x32_10": (None, [_P, _P, _P]),
     "orc_philox_uniform": (C.c_float, [C.c_uint64, C.c_uint64]),
     "orc_sample": (C.c_int32, [_P, C.c_int, C.c_float, C.c_float, C.POINTER(C.c_double)]),
+    "orc_sample_top_k": (C.c_int32, [_P, C.c_int, C.c_float, C.c_int, C.c_float, C.POINTER(C.c_double)]),
 }
 
 _lib = None
@@ -257,4 +258,13 @@ def sample(logits, temperature: float, u: float):
     x = f32(logits)
     m = C.c_double()
     i = lib().orc_sample(_p(x), len(x), temperature, u, C.byref(m))
+    return int(i), m.value
+
+
+def sample_top_k(logits, temperature: float, k: int, u: float):
+    """(index, margin): inversion draw of u from softmax(logits / T) over the
+    k largest logits (value descending, then lower index), in rank order."""
+    x = f32(logits)
+    m = C.c_double()
+    i = lib().orc_sample_top_k(_p(x), len(x), temperature, int(k), u, C.byref(m))
     return int(i), m.value

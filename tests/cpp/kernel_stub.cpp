@@ -39,6 +39,6 @@ int attn_noalloc_scratch(float** out) {
     *out = buf;
     return GH_OK;
 }
-int launch_sample_logits(const float*, int, float, uint64_t, uint64_t, float*, int32_t*, hipStream_t) { return GH_OK; }
+int launch_sample_logits(const float*, int, float, int, uint64_t, uint64_t, float*, int32_t*, hipStream_t) { return GH_OK; }
 
 }  // namespace gh

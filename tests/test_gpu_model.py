@@ -440,6 +440,61 @@ def test_temperature_sampling_in_the_step(ctx):
         kv.set_sampling(-1.0, 0)
 
 
+@pytest.mark.parametrize("shape", ["tiny", "wide-vocab"])
+def test_top_k_sampling_in_the_step(ctx, shape):
+    """gh_kv_set_top_k: k = 1 reproduces the greedy ids at any temperature;
+    k = 40 draws each step's token from softmax over the 40 largest logits in
+    rank order with Philox(seed, counter = position) -- checked against the
+    oracle's draw on the step's own logits, after a batched prefill too --
+    and the same seed reproduces the generation; k outside 0..64 is refused.
+    wide-vocab: the 1B shapes with 2 layers, so the LM head's 262144 rows run
+    on their full-size plan (its input token's own logit leads by about 20,
+    hence T = 20)."""
+    if shape == "tiny":
+        cfg, T = gh.preset("tiny"), 1.3
+    else:
+        cfg, T = gh.preset("gemma3-1b"), 20.0
+        cfg.n_layers = 2
+    cfg.max_seq = 64
+    m = gh.GemmaModel(ctx, cfg)
+    m.synth(7, True, centered=shape != "tiny")
+    prompt = gh.synth_tokens(3, "prompt", 6, cfg.vocab)
+    greedy = gh.generate(m, gh.KVCache(m, 64), prompt, 10)
+    kv = gh.KVCache(m, 64)
+    kv.set_sampling(T, 77)
+    kv.set_top_k(1)
+    np.testing.assert_array_equal(gh.generate(m, kv, prompt, 10), greedy)
+    seed, k = 1234, 40
+    runs = []
+    for _ in range(2):
+        kv = gh.KVCache(m, 64)
+        kv.set_sampling(T, seed)
+        kv.set_top_k(k)
+        runs.append(gh.generate(m, kv, prompt, 12))
+    np.testing.assert_array_equal(runs[0], runs[1])
+    kv = gh.KVCache(m, 64)
+    kv.set_sampling(T, seed)
+    kv.set_top_k(k)
+    toks, drawn = list(prompt), set()
+    for pos in range(len(prompt) + 8):
+        logits, _, nxt = gh.runGemmaInferenceCached(m, int(toks[pos]), kv)
+        want, margin = orc.sample_top_k(logits, T, k, orc.philox_uniform(seed, pos))
+        assert nxt == want or margin < 1e-4, (pos, nxt, want, margin)
+        drawn.add(nxt)
+        if pos >= len(prompt) - 1:
+            toks.append(nxt)
+    assert len(drawn) > 3  # the draws are not all the argmax
+    kv = gh.KVCache(m, 64)
+    kv.set_sampling(T, seed)
+    kv.set_top_k(k)
+    logits, _, nxt = gh.prefill(m, kv, prompt)
+    want, margin = orc.sample_top_k(logits, T, k, orc.philox_uniform(seed, len(prompt) - 1))
+    assert nxt == want or margin < 1e-4, (nxt, want, margin)
+    for bad in (-1, 65):
+        with pytest.raises(gh.GemmaHipError):
+            kv.set_top_k(bad)
+
+
 @pytest.mark.parametrize("shape", ["tiny", "gemma3-1b", "mini4b"])
 def test_persistent_step_matches_graph_step(ctx, monkeypatch, shape):
     """The persistent step (GH_PERSISTENT=1: one workgroup per CU, phases

@@ -235,6 +235,51 @@ def test_sample_logits_matches_oracle(ctx):
         assert gh.sample_logits(ctx, logits, 0.0, 99, 0) == int(np.argmax(logits))
 
 
+def test_sample_logits_top_k_matches_oracle(ctx):
+    """Top-k draw (tile selection, wave sorting networks, rank-order
+    inversion) against the oracle: equal logits give rank floor(u k) = that
+    index exactly; k = 1 is the first maximum with the tied maxima in
+    different tiles; random, heavily tied (values on a 0.5 grid, so the
+    k-th value is shared across tiles), clustered (the top 64 in one block)
+    and increasing logits, and more blocks than one staging pass holds
+    (n = 300000), give the oracle's index except
+    where u * total sits within 1e-4 of a boundary -- a tie broken the other
+    way moves the index but not the boundary, so the margin never excuses
+    it; k past n is n; out-of-range k is refused."""
+    for k in (1, 5, 64):
+        for c in range(8):
+            u = orc.philox_uniform(11, c)
+            got = gh.sample_logits(ctx, np.zeros(1000, np.float32), 0.9, 11, c, top_k=k)
+            assert got == int(np.floor(u * k)), (k, c, got)
+    rng = np.random.default_rng(4)
+    l = rng.normal(size=262144).astype(np.float32)
+    for i in (70000, 3, 250000):
+        l[i] = 9.0
+    for c in range(6):
+        assert gh.sample_logits(ctx, l, 1.7, 5, c, top_k=1) == 3
+    cases = [(262144, 1.0, 64, 3.0), (262144, 0.5, 17, 3.0), (5000, 2.0, 2, 3.0), (130, 1.0, 40, 3.0),
+             (40, 1.0, 64, 3.0), (300000, 1.0, 50, 3.0), (262144, 1.0, 64, "ties"), (262144, 0.7, 33, "ties"),
+             (262144, 4.0, 64, "cluster"), (262144, 30.0, 64, "ramp")]
+    for n, T, k, scale in cases:
+        if scale == "ties":  # a 0.5 grid: hundreds of exact ties at every top value
+            logits = (np.round(2 * rng.normal(size=n) * 1.5) / 2).astype(np.float32)
+        elif scale == "cluster":  # the 64 largest in one 64-row block, the next ones scattered
+            logits = rng.normal(size=n).astype(np.float32)
+            logits[131072:131136] = 8.0 + rng.normal(size=64).astype(np.float32)
+        elif scale == "ramp":  # increasing with the index: every tile beats the ones before it
+            logits = np.linspace(-20.0, 20.0, n, dtype=np.float32)
+        else:
+            logits = (scale * rng.normal(size=n)).astype(np.float32)
+        for c in range(12):
+            got = gh.sample_logits(ctx, logits, T, 21, c, top_k=k)
+            want, margin = orc.sample_top_k(logits, T, k, orc.philox_uniform(21, c))
+            assert got == want or margin < 1e-4, (n, T, k, scale, c, got, want, margin)
+    assert gh.sample_logits(ctx, l, 0.0, 5, 0, top_k=8) == 3
+    for bad in (-1, 65):
+        with pytest.raises(gh.GemmaHipError):
+            gh.sample_logits(ctx, l, 1.0, 5, 0, top_k=bad)
+
+
 def test_exchange_probe(ctx):
     """gh_time_exchange: a positive, finite time per all-to-all exchange for
     small and chip-wide groups; group sizes past the CUs or 256 are refused."""

@@ -251,6 +251,41 @@ def test_sampler_closed_forms_and_frequencies():
     assert np.max(np.abs(freq - p)) < 0.015
 
 
+def test_top_k_sampler_closed_forms_and_frequencies():
+    """Top-k draw: k = 1 is the first maximum for every u; equal logits rank
+    by index, so the pick is floor(u k); k = n over logits that decrease with
+    the index walks the same order as the full sampler (same pick for every
+    u); a permutation of the logits picks the same value; frequencies
+    match softmax over the k largest (numpy argsort, an independent
+    ranking)."""
+    rng = np.random.default_rng(5)
+    l = rng.normal(size=300).astype(np.float32)
+    l[[17, 90, 250]] = l.max() + 1.0  # tied maximum: the first one wins
+    us = [orc.philox_uniform(11, c) for c in range(200)]
+    assert all(orc.sample_top_k(l, 0.9, 1, u)[0] == 17 for u in us)
+    for k in (1, 5, 64):
+        for u in (0.0, 0.3, 0.77, 0.999):
+            assert orc.sample_top_k(np.zeros(100, np.float32), 1.3, k, u)[0] == int(np.floor(u * k))
+    dec = np.sort(rng.normal(size=40).astype(np.float32))[::-1].copy()
+    for u in us:
+        a, ma = orc.sample_top_k(dec, 0.7, 40, u)
+        b, mb = orc.sample(dec, 0.7, u)
+        assert a == b or min(ma, mb) < 1e-9
+    lp = l[rng.permutation(len(l))]
+    for k in (3, 40):
+        for u in us[:50]:  # the ranked values, hence the walk, do not depend on the order
+            assert l[orc.sample_top_k(l, 1.1, k, u)[0]] == lp[orc.sample_top_k(lp, 1.1, k, u)[0]]
+    logits = rng.normal(size=30).astype(np.float32) * 2
+    T, k = 0.8, 6
+    top = np.argsort(-logits, kind="stable")[:k]
+    p = np.exp((logits[top] - logits[top[0]]) / T)
+    p /= p.sum()
+    draws = [orc.sample_top_k(logits, T, k, orc.philox_uniform(4, c))[0] for c in range(20000)]
+    freq = np.array([np.mean(np.asarray(draws) == t) for t in top])
+    assert set(draws) <= set(top.tolist())
+    assert np.max(np.abs(freq - p)) < 0.015
+
+
 def _softcap_violations(f, cap: float) -> list[str]:
     """Properties that fix a soft cap sigma * tanh(y / sigma) without
     restating it (the body of runMatmulQ4_0DSL, which
