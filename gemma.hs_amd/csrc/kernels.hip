@@ -128,6 +128,12 @@ __device__ __forceinline__ float wave_max(float v) {
     return rows_combine(row16_max(v), -INFINITY, [](float x, float y) { return fmaxf(x, y); });
 }
 
+// wave-uniform max of a value that is already uniform within aligned groups
+// of 8 lanes (one DPP step instead of four inside each row)
+__device__ __forceinline__ float wave_max_g8(float v) {
+    return rows_combine(fmaxf(v, dpp<DPP_ROW_ROR8>(v)), -INFINITY, [](float x, float y) { return fmaxf(x, y); });
+}
+
 // sum over aligned groups of LP lanes (result in every lane of the group)
 template <int LP>
 __device__ __forceinline__ float group_sum(float v) {
@@ -1973,10 +1979,12 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
                 for (int i = 0; i < K4; ++i) sv += dot4(*(const float4*)&qs[h * HD + 32 * i + 4 * kq], kr[u][i]);
                 sv = group_sum<8>(sv) * a.scale;
                 sv = valid ? sv : -INFINITY;
-                const float mn = fmaxf(mrun[h], wave_max(sv));  // the round has a valid position: mn finite
-                const float corr = __expf(mrun[h] - mn);          // mrun = -inf -> 0
+                const float mn = fmaxf(mrun[h], wave_max_g8(sv));  // the round has a valid position: mn finite
+                const float corr = __expf(mrun[h] - mn);             // mrun = -inf -> 0
                 pw[h] = valid ? __expf(sv - mn) : 0.0f;
-                lrun[h] = lrun[h] * corr + wave_sum(kq == 0 ? pw[h] : 0.0f);
+                // per-lane running sums (lanes kq == 0 hold their position's
+                // terms), reduced once after the rounds
+                lrun[h] = lrun[h] * corr + (kq == 0 ? pw[h] : 0.0f);
                 mrun[h] = mn;
                 acc[h] = make_float4(acc[h].x * corr, acc[h].y * corr, acc[h].z * corr, acc[h].w * corr);
             }
@@ -1990,6 +1998,8 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
             if (PF == 2) load(u, rr + 8);
         }
     }
+#pragma unroll
+    for (int h = 0; h < G; ++h) lrun[h] = wave_sum(lrun[h]);
     GH_MARK(4);
     // 4. merge the four wave states; write the chunk's state
     if (lane == 0) {
