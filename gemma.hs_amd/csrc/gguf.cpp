@@ -6,6 +6,8 @@
 //    tokenizer array it skipped while parsing and so always gets 256000);
 //  - the Q4_0 projections and the tied LM head reach the device (the
 //    reference uploads zero placeholders and leaves the LM head undefined).
+// Q4_1 tensors are dequantised to f32 on load, as the reference's getTensor
+// does for the embedding and the norms (src/Gemma/GGUF.hs:649-656,762-795).
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -23,7 +25,9 @@ using namespace gh;
 
 namespace {
 
-enum : uint32_t { GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_0 = 2 };
+enum : uint32_t { GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_0 = 2, GGML_Q4_1 = 3 };
+// a tensor the loader dequantises to f32 before gh_model_set_tensor
+constexpr int DT_Q4_1_HOST = 100;
 
 struct Meta {
     uint32_t type = 0;
@@ -163,6 +167,11 @@ int tensor_bytes(const std::string& name, const TInfo& ti, int* dtype, uint64_t*
             return set_error(GH_ERR_FORMAT, "Q4_0 tensor '%s': row length not a multiple of 32", name.c_str());
         *dtype = GH_DTYPE_Q4_0;
         *bytes = ne / 32 * 18;
+    } else if (ti.type == GGML_Q4_1) {
+        if (ti.dims.empty() || ti.dims[0] % 32)
+            return set_error(GH_ERR_FORMAT, "Q4_1 tensor '%s': row length not a multiple of 32", name.c_str());
+        *dtype = DT_Q4_1_HOST;
+        *bytes = ne / 32 * 20;
     } else {
         return set_error(GH_ERR_FORMAT, "tensor '%s' has unsupported ggml type %u", name.c_str(), ti.type);
     }
@@ -287,6 +296,26 @@ int parse_safe(const char* path, int32_t max_seq, Parsed& P) {
     }
 }
 
+// Q4_1 blocks (fp16 d, fp16 m, 16 code bytes) to f32 as loadQ4_1Tensor
+// (src/Gemma/GGUF.hs:762-795) computes them: element i of a block is the low
+// nibble of code byte i/2 for even i and the high nibble for odd i (not the
+// split order of Q4_0), value q*d + m, with d and m through halfToFloat
+// (subnormals flushed to zero unless ieee).
+void q4_1_to_f32(const uint8_t* src, uint64_t n_blocks, bool ieee, float* out) {
+    for (uint64_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* blk = src + b * 20;
+        uint16_t hd, hm;
+        std::memcpy(&hd, blk, 2);
+        std::memcpy(&hm, blk + 2, 2);
+        const float d = f16_to_f32(hd, !ieee), m = f16_to_f32(hm, !ieee);
+        for (int i = 0; i < 32; ++i) {
+            const uint8_t byte = blk[4 + i / 2];
+            const int q = (i & 1) ? byte >> 4 : byte & 0x0F;
+            out[b * 32 + i] = (float)q * d + m;  // q*d is exact in f32
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" int gh_gguf_inspect(const char* path, gh_config* out) {
@@ -306,7 +335,21 @@ extern "C" int gh_model_load_gguf(gh_ctx* ctx, const char* path, int32_t max_seq
     for (auto& kvp : P.data) {
         const std::string& name = kvp.first;
         const TData& td = kvp.second;  // extent checked against the file by parse_gguf
-        int rc = gh_model_set_tensor(m, name.c_str(), td.dtype, (const uint8_t*)P.mp.p + td.off, td.bytes);
+        const uint8_t* src = (const uint8_t*)P.mp.p + td.off;
+        int rc;
+        if (td.dtype == DT_Q4_1_HOST) {
+            std::vector<float> f32;
+            try {
+                f32.resize(td.bytes / 20 * 32);
+            } catch (const std::bad_alloc&) {
+                gh_model_destroy(m);
+                return set_error(GH_ERR_OOM, "out of host memory dequantising '%s'", name.c_str());
+            }
+            q4_1_to_f32(src, td.bytes / 20, (P.cfg.flags & GH_FLAG_IEEE_SCALES) != 0, f32.data());
+            rc = gh_model_set_tensor(m, name.c_str(), GH_DTYPE_F32, f32.data(), f32.size() * 4);
+        } else {
+            rc = gh_model_set_tensor(m, name.c_str(), td.dtype, src, td.bytes);
+        }
         if (rc == GH_ERR_NOT_FOUND) continue;  // tensors the decode step does not use (e.g. rope_freqs)
         if (rc != GH_OK) {
             gh_model_destroy(m);

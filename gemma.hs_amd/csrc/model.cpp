@@ -132,7 +132,7 @@ int upload_rows(gh_ctx* ctx, const DMat& d, int row_off, int dtype, const void* 
         if (dtype == GH_DTYPE_F16) {
             if (nbytes != (size_t)rows * cols * 2) return set_error(GH_ERR_INVALID, "F16 tensor size mismatch");
             f32.resize((size_t)rows * cols);
-            for (size_t i = 0; i < f32.size(); ++i) f32[i] = f16_to_f32(((const uint16_t*)data)[i], false);
+            for (size_t i = 0; i < f32.size(); ++i) f32[i] = f16_to_f32(((const uint16_t*)data)[i], ftz);
             src = f32.data();
         } else if (dtype == GH_DTYPE_F32) {
             if (nbytes != (size_t)rows * cols * 4) return set_error(GH_ERR_INVALID, "F32 tensor size mismatch");
@@ -148,12 +148,12 @@ int upload_rows(gh_ctx* ctx, const DMat& d, int row_off, int dtype, const void* 
     return GH_OK;
 }
 
-int vec_to_f32(int dtype, const void* data, size_t nbytes, int n, std::vector<float>& out) {
+int vec_to_f32(int dtype, const void* data, size_t nbytes, int n, bool ftz, std::vector<float>& out) {
     out.resize(n);
     if (dtype == GH_DTYPE_F32 && nbytes == (size_t)n * 4) {
         std::memcpy(out.data(), data, nbytes);
     } else if (dtype == GH_DTYPE_F16 && nbytes == (size_t)n * 2) {
-        for (int i = 0; i < n; ++i) out[i] = f16_to_f32(((const uint16_t*)data)[i], false);
+        for (int i = 0; i < n; ++i) out[i] = f16_to_f32(((const uint16_t*)data)[i], ftz);
     } else {
         return set_error(GH_ERR_INVALID, "vector tensor: dtype %d with %zu bytes, expected %d elements", dtype, nbytes, n);
     }
@@ -201,7 +201,7 @@ void make_plans(gh_model* m) {
     // rows spills (4B: 2 -> 3 splits, gate/up 14.3 -> 11.9 us, 651 -> 690 tok/s)
     while (m->fmt == FMT_Q4 && m->pd.S < 8 && ((L.gu.nblk + m->pd.S - 1) / m->pd.S + 3) / 4 > 9) ++m->pd.S;
     m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 8 * L.down.tiles);
-    m->plm = choose_plan(m->fmt, m->embd.tiles, m->embd.nblk, 1);
+    m->plm = choose_plan(m->embd.fmt, m->embd.tiles, m->embd.nblk, 1);
     m->pc.rl = m->pe.rl = m->plm.rl = 1;
     m->pa.rl = L.qkv.tiles >= 32 ? 2 : 1;
     auto over = [&](Plan& p, const char* env, const DMat& d) {
@@ -949,6 +949,9 @@ extern "C" int gh_model_destroy(gh_model* m) {
     return GH_OK;
 }
 
+// The projections share one format (Q4_0 or f32), set by the first one
+// uploaded; the embedding (the tied LM head) has its own, so a Q4_0 model
+// can carry an embedding the GGUF loader dequantised (Q4_1).
 static int ensure_fmt(gh_model* m, int dtype) {
     const int want = dtype == GH_DTYPE_Q4_0 ? FMT_Q4 : FMT_F32;
     if (m->fmt < 0) {
@@ -960,10 +963,16 @@ static int ensure_fmt(gh_model* m, int dtype) {
             GH_CHECK(alloc_mat(m, L.gu, want, 2 * m->f_pad, c.hidden));
             GH_CHECK(alloc_mat(m, L.down, want, c.hidden, c.ffn));
         }
-        GH_CHECK(alloc_mat(m, m->embd, want, c.vocab, c.hidden));
     } else if (m->fmt != want) {
-        return set_error(GH_ERR_INVALID, "all projections and the embedding must share one format");
+        return set_error(GH_ERR_INVALID, "all projections must share one format");
     }
+    return GH_OK;
+}
+
+static int ensure_embd_fmt(gh_model* m, int dtype) {
+    const int want = dtype == GH_DTYPE_Q4_0 ? FMT_Q4 : FMT_F32;
+    if (!m->embd.codes) return alloc_mat(m, m->embd, want, m->cfg.vocab, m->cfg.hidden);
+    if (m->embd.fmt != want) return set_error(GH_ERR_INVALID, "token_embd.weight was uploaded in another format");
     return GH_OK;
 }
 
@@ -976,13 +985,13 @@ extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, con
     const bool ftz = !(c.flags & GH_FLAG_IEEE_SCALES);
     std::vector<float> v;
     if (!std::strcmp(name, "token_embd.weight")) {
-        GH_CHECK(ensure_fmt(m, dtype));
+        GH_CHECK(ensure_embd_fmt(m, dtype));
         GH_CHECK(upload_rows(m->ctx, m->embd, 0, dtype, data, nbytes, c.vocab, c.hidden, ftz));
         m->has_embd = true;
         return GH_OK;
     }
     if (!std::strcmp(name, "output_norm.weight")) {
-        GH_CHECK(vec_to_f32(dtype, data, nbytes, c.hidden, v));
+        GH_CHECK(vec_to_f32(dtype, data, nbytes, c.hidden, ftz, v));
         if (!m->out_norm) GH_CHECK(dev_alloc(m, &m->out_norm, c.hidden));
         GH_CHECK(upload(m->ctx, m->out_norm, v.data(), v.size() * 4));
         m->has_out_norm = true;
@@ -1000,7 +1009,7 @@ extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, con
     LayerDev& L = m->layers[l];
     const int H = c.hidden, hd = c.head_dim;
     auto vec = [&](float*& dst, int n) -> int {
-        GH_CHECK(vec_to_f32(dtype, data, nbytes, n, v));
+        GH_CHECK(vec_to_f32(dtype, data, nbytes, n, ftz, v));
         if (!dst) GH_CHECK(dev_alloc(m, &dst, n));
         return upload(m->ctx, dst, v.data(), (size_t)n * 4);
     };

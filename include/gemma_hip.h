@@ -59,7 +59,9 @@ extern "C" {
 #define GH_FLAG_POST_ATTN_NORM 2
 #define GH_FLAG_POST_FFN_NORM 4
 #define GH_FLAG_ZERO_CENTERED 8
-#define GH_FLAG_IEEE_SCALES 16 /* keep fp16 subnormal Q4_0 scales (default: flush to zero) */
+/* keep fp16 subnormals: Q4_0 scales and F16 tensor values (default: flush
+ * them to zero, as halfToFloat does, src/Gemma/GGUF.hs:797-820) */
+#define GH_FLAG_IEEE_SCALES 16
 
 const char* gh_last_error(void);
 /* Library version string. */
@@ -197,14 +199,18 @@ void gh_model_release(gh_model* m); /* gh_model_destroy for finalisers */
 /* name: GGUF tensor name (token_embd.weight, output_norm.weight,
  * blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_q_norm,attn_k_norm,
  * attn_output,post_attention_norm,ffn_norm,ffn_gate,ffn_up,ffn_down,
- * post_ffw_norm}.weight).  dtype GH_DTYPE_F32 / F16 / Q4_0 (raw bytes). */
+ * post_ffw_norm}.weight).  dtype GH_DTYPE_F32 / F16 / Q4_0 (raw bytes).
+ * The projections share one format (Q4_0, or f32 from F32/F16); the
+ * embedding may have its own. */
 int gh_model_set_tensor(gh_model* m, const char* name, int dtype, const void* data, size_t nbytes);
 /* 0 when every tensor the config needs is present. */
 int gh_model_check(gh_model* m);
 int gh_model_config(gh_model* m, gh_config* out);
 /* loadGemmaModelFromGGUF (src/Gemma/Model.hs:908-1234) + configFromGGUF
  * (src/Gemma/Model.hs:843-902): parse a GGUF v3 file, build the config from
- * its metadata (vocab from the token_embd shape) and upload every tensor. */
+ * its metadata (vocab from the token_embd shape) and upload every tensor.
+ * Tensor types: F32, F16, Q4_0, and Q4_1, which is dequantised to f32 on the
+ * host in the reference's element order (src/Gemma/GGUF.hs:762-795). */
 int gh_model_load_gguf(gh_ctx* ctx, const char* path, int32_t max_seq, gh_model** out);
 /* configFromGGUF alone (src/Gemma/Model.hs:843-902): parse the header,
  * metadata and tensor infos of a GGUF v3 file into a config; no device. */

@@ -13,7 +13,7 @@ import struct
 
 import numpy as np
 
-GGML_F32, GGML_F16, GGML_Q4_0 = 0, 1, 2
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_1 = 0, 1, 2, 3
 _SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
 
 
@@ -67,7 +67,33 @@ class GGUF:
         if t == GGML_F32:
             return 0, np.frombuffer(self.buf, np.float32, ne, start).copy()
         if t == GGML_F16:
-            return 0, np.frombuffer(self.buf, np.float16, ne, start).astype(np.float32)
+            return 0, half_ftz(np.frombuffer(self.buf, np.uint16, ne, start))
         if t == GGML_Q4_0:
             return 2, np.frombuffer(self.buf, np.uint8, ne // 32 * 18, start).copy()
+        if t == GGML_Q4_1:
+            return 0, q4_1_dequant(np.frombuffer(self.buf, np.uint8, ne // 32 * 20, start))
         raise ValueError(f"ggml type {t}")
+
+
+def half_ftz(h: np.ndarray) -> np.ndarray:
+    """fp16 bit patterns to f32 with subnormals flushed to a signed zero, as
+    halfToFloat (src/Gemma/GGUF.hs:797-820) decodes them."""
+    h = np.asarray(h, np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    sub = ((h & 0x7C00) == 0) & ((h & 0x03FF) != 0)
+    f[sub] = np.where(h[sub] & 0x8000, np.float32(-0.0), np.float32(0.0))
+    return f
+
+
+def q4_1_dequant(raw: np.ndarray) -> np.ndarray:
+    """Q4_1 blocks to f32 in loadQ4_1Tensor's order (src/Gemma/GGUF.hs:762-795):
+    element i of a block is code byte i // 2, low nibble for even i, high
+    for odd i; value q * d + m, with d and m through half_ftz."""
+    b = np.asarray(raw, np.uint8).reshape(-1, 20)
+    d = half_ftz(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    m = half_ftz(b[:, 2:4].copy().view(np.uint16)[:, 0])
+    codes = b[:, 4:]
+    q = np.empty((b.shape[0], 32), np.float32)
+    q[:, 0::2] = codes & 0x0F
+    q[:, 1::2] = codes >> 4
+    return (q * d[:, None] + m[:, None]).astype(np.float32).reshape(-1)

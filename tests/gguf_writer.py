@@ -11,7 +11,7 @@ import struct
 
 import numpy as np
 
-GGML = {"f32": 0, "f16": 1, "q4_0": 2}
+GGML = {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3}
 T_U32, T_I32, T_F32, T_STR, T_ARR = 4, 5, 6, 8, 9
 
 
@@ -83,15 +83,38 @@ def gemma3_meta(cfg) -> dict:
     }
 
 
-def synth_gguf(path, cfg, seed: int, q4: bool, **kw) -> None:
-    """The seeded synthetic model of gemma_hip.synth_tensors as a GGUF file."""
+def random_q4_1(rows: int, cols: int, seed: int, subnormal_frac: float = 0.02) -> np.ndarray:
+    """Raw Q4_1 bytes (20-byte blocks: fp16 d, fp16 m, 16 code bytes) with
+    random codes, d ~ |N(0, 0.01)| (some fp16 subnormal), m ~ N(0, 0.02)."""
+    rng = np.random.default_rng(seed)
+    nb = rows * cols // 32
+    b = rng.integers(0, 256, size=(nb, 20), dtype=np.uint8)
+    d = np.abs(rng.normal(0, 0.01, nb)).astype(np.float16)
+    sub = rng.random(nb) < subnormal_frac
+    d[sub] = rng.integers(1, 1024, size=int(sub.sum())).astype(np.uint16).view(np.float16)
+    b[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    b[:, 2:4] = rng.normal(0, 0.02, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)
+
+
+def synth_gguf(path, cfg, seed: int, q4: bool, embd_q4_1: bool = False, norms_f16: bool = False, **kw) -> None:
+    """The seeded synthetic model of gemma_hip.synth_tensors as a GGUF file;
+    embd_q4_1 replaces token_embd with random Q4_1 blocks, norms_f16 stores
+    the norm vectors as F16 (with a few subnormal values)."""
     import gemma_hip as gh
     shapes = {n: (k, s) for n, k, s in gh.tensor_list(cfg)}
     tensors = []
     for name, dtype, arr in gh.synth_tensors(cfg, seed, q4):
         kind, shape = shapes[name]
         if kind == "vec":
-            tensors.append((name, "f32", shape[0], None, arr))
+            if norms_f16:
+                h = np.asarray(arr, np.float32).astype(np.float16)
+                h[::97] = np.uint16(0x0203).view(np.float16)  # a subnormal: 0 after FTZ
+                tensors.append((name, "f16", shape[0], None, h))
+            else:
+                tensors.append((name, "f32", shape[0], None, arr))
+        elif name == "token_embd.weight" and embd_q4_1:
+            tensors.append((name, "q4_1", shape[0], shape[1], random_q4_1(shape[0], shape[1], seed + 1)))
         else:
             tensors.append((name, "q4_0" if dtype == gh.DTYPE_Q4_0 else "f32", shape[0], shape[1], arr))
     write_gguf(path, gemma3_meta(cfg), tensors, **kw)

@@ -141,6 +141,47 @@ def test_gguf_malformed_files_are_rejected(tmp_path, bad):
     assert e.value.name == "GH_ERR_NOT_FOUND"
 
 
+def test_q4_1_reader_known_answers():
+    """tests/gguf_reader.py's Q4_1 decode (the oracle side of the GGUF Q4_1
+    load) on closed forms: d = 1, m = 0.5 and code byte j holding nibbles
+    (2j mod 16, 2j+1 mod 16) give element i = (i mod 16) + 0.5 -- the
+    reference's interleaved order (src/Gemma/GGUF.hs:762-795), which the
+    split order of Q4_0 would read as 2j, 2j+16 -- and a subnormal d is
+    flushed, leaving m."""
+    from gguf_reader import q4_1_dequant, half_ftz
+    blk = np.zeros((2, 20), np.uint8)
+    blk[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    blk[:, 2:4] = np.array([0.5], np.float16).view(np.uint8)
+    j = np.arange(16)
+    blk[:, 4:] = (((2 * j + 1) % 16) << 4) | ((2 * j) % 16)
+    blk[1, 0:2] = np.array([0x0005], np.uint16).view(np.uint8)  # subnormal d
+    got = q4_1_dequant(blk.reshape(-1)).reshape(2, 32)
+    np.testing.assert_array_equal(got[0], (np.arange(32) % 16) + 0.5)
+    np.testing.assert_array_equal(got[1], np.full(32, 0.5, np.float32))
+    h = np.array([0x0001, 0x8200, 0x3C00, 0x0400, 0x7C00], np.uint16)
+    f = half_ftz(h)
+    assert f[0] == 0.0 and f[1] == 0.0 and np.signbit(f[1]) and f[2] == 1.0
+    assert f[3] == np.float32(2.0 ** -14) and np.isinf(f[4])
+
+
+def test_gguf_q4_1_tensors_parse_and_ragged_rows_are_rejected(tmp_path):
+    """A Q4_1 token_embd is accepted by the parser (it is dequantised on
+    load); a Q4_1 tensor whose rows are not whole 32-element blocks is
+    GH_ERR_FORMAT."""
+    from gguf_writer import random_q4_1
+    cfg = gh.preset("tiny")
+    p = tmp_path / "q41.gguf"
+    synth_gguf(p, cfg, 3, q4=True, embd_q4_1=True, norms_f16=True)
+    assert _inspect(p).vocab == cfg.vocab
+    meta = gemma3_meta(cfg)
+    bad = random_q4_1(4, 32, 1)
+    write_gguf(p, meta, [("token_embd.weight", "f32", cfg.vocab, cfg.hidden, np.zeros(cfg.vocab * cfg.hidden, np.float32)),
+                         ("blk.0.attn_q.weight", "q4_1", 4, 48, np.resize(bad, 4 * 48 // 32 * 20 + 20))])
+    with pytest.raises(gh.GemmaHipError) as e:
+        _inspect(p)
+    assert e.value.name == "GH_ERR_FORMAT"
+
+
 def test_tensor_list_matches_header_names():
     names = {n.split(".", 2)[-1] if n.startswith("blk.") else n for n, _, _ in gh.tensor_list(gh.preset("tiny"))}
     text = HEADER.read_text()

@@ -329,26 +329,30 @@ def test_gguf_loaded_model_matches_synth_model(ctx, tmp_path, preset):
     np.testing.assert_array_equal(gh.generate(mg, kg, [int(prompt[-1])], 10), gh.generate(ms, ks, [int(prompt[-1])], 10))
 
 
-@pytest.mark.parametrize("preset", ["tiny", "mini4b"])
+@pytest.mark.parametrize("preset", ["tiny", "mini4b", "tiny-q4_1", "mini4b-q4_1"])
 def test_gguf_loaded_model_matches_oracle_from_an_independent_read(ctx, tmp_path, preset):
     """loadGemmaModelFromGGUF (src/Gemma/Model.hs:908-1234; tensor format
     src/Gemma/GGUF.hs:186-239) against the oracle: the GPU model comes from
     gh_model_load_gguf, the oracle's from tests/gguf_reader.py's own reading
     of the same file (metadata -> config, tensor infos -> bytes).  Every
     layer's hidden state and the logits agree within 1e-4 relative at every
-    step, and so do the argmaxes where the margin allows."""
+    step, and so do the argmaxes where the margin allows.  -q4_1: token_embd
+    as Q4_1 (dequantised on load in the reference's element order, so the
+    embedding and the tied LM head run in f32 beside Q4_0 projections) and
+    the norms as F16 with subnormal entries (flushed, as halfToFloat does)."""
     import sys
     sys.path.insert(0, str(GOLDEN.parent))
     from gguf_reader import GGUF
     from gguf_writer import synth_gguf
-    if preset == "tiny":
+    if preset.startswith("tiny"):
         cfg = gh.preset("tiny")
     else:
         cfg = gh.preset("gemma3-4b")
         cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 3, 1024
         cfg.sliding_window = 5
     path = tmp_path / f"{preset}.gguf"
-    synth_gguf(path, cfg, 33, q4=True)
+    q41 = preset.endswith("q4_1")
+    synth_gguf(path, cfg, 33, q4=True, embd_q4_1=q41, norms_f16=q41)
     mg = gh.GemmaModel.load_gguf(ctx, str(path), max_seq=64)
     f = GGUF(path)
     oc = orc.OrcConfig()
@@ -379,6 +383,9 @@ def test_gguf_loaded_model_matches_oracle_from_an_independent_read(ctx, tmp_path
         srt = np.sort(olog)
         if srt[-1] - srt[-2] > 1e-3 * np.max(np.abs(olog)):
             assert nxt == obest, pos
+    if q41:  # the batched prefill over the same mixed-format model: last token's logits
+        plog, _, _ = gh.prefill(mg, gh.KVCache(mg, 64), toks)
+        assert rel_err(plog, olog) < ACT_TOL
 
 
 def test_kv_synth_prefill_and_timer(ctx):
