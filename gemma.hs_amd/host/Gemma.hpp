@@ -160,6 +160,16 @@ inline int cacheLength(const KVCache& cache) {
 // resetCache (src/Gemma/KVCache.hs:150-151): length 0 (all layers at once).
 inline void resetCache(KVCache& cache) { check(gh_kv_reset(cache.get())); }
 
+// Next-token rule of this cache's steps and generations; no reference
+// counterpart (sampleWithTemperature is an argmax, app/Main.hs:492-507).
+// temperature 0: the first maximum; > 0: a Philox draw (key seed, counter =
+// position) from softmax(logits / temperature), over the topK largest logits
+// in rank order when 1 <= topK <= 64 (0: all).
+inline void setSampling(KVCache& cache, float temperature, uint64_t seed, int topK = 0) {
+    check(gh_kv_set_sampling(cache.get(), temperature, seed));
+    check(gh_kv_set_top_k(cache.get(), topK));
+}
+
 // runGemmaInferenceCached (src/Gemma/Model.hs:1313-1437): one token through
 // the model at position cacheLength; returns the logits [vocab] and the
 // cache, one position longer.  Like the reference: exactly one token, else

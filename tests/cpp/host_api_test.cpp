@@ -95,6 +95,17 @@ orc_model* oracle_model(const gemma::GemmaConfig& c, uint64_t seed, bool q4) {
     return om;
 }
 
+// top_k outside 0..64 is GH_ERR_RANGE
+void threw_range(gemma::KVCache& kv) {
+    bool threw = false;
+    try {
+        gemma::setSampling(kv, 1.0f, 0, 65);
+    } catch (const gemma::GemmaError& e) {
+        threw = e.code == GH_ERR_RANGE;
+    }
+    require(threw, "top_k 65: GH_ERR_RANGE");
+}
+
 // runGemmaInferenceCached / ...WithLayer0 step by step against the oracle:
 // logits and every layer within 1e-4 relative, the argmax equal, the cache
 // one position longer per step (test/GemmaSpec.hs:599-644 in spirit).
@@ -140,6 +151,16 @@ void steps_match_oracle(std::ostringstream& log, const gemma::Context& ctx, cons
     require(gemma::cacheLength(kv1) == n_prompt + (int)want.size() - 1, "cache length after generate");
     gemma::resetCache(kv1);
     require(gemma::cacheLength(kv1) == 0, "resetCache");
+    // sampling extension: top-1 at any temperature is the greedy rule; a
+    // seeded draw reproduces itself
+    gemma::setSampling(kv1, 1.7f, 11, 1);
+    require(gemma::generate(model, kv1, prompt, (int)want.size()) == want, "top-1 sampling = greedy ids");
+    gemma::KVCache ka = gemma::initKVCache(model, 64), kb = gemma::initKVCache(model, 64);
+    gemma::setSampling(ka, 1.3f, 5, 16);
+    gemma::setSampling(kb, 1.3f, 5, 16);
+    require(gemma::generate(model, ka, prompt, (int)want.size()) == gemma::generate(model, kb, prompt, (int)want.size()),
+            "seeded top-k generation reproduces");
+    threw_range(kv1);
     orc_model_destroy(om);
     log << preset << (q4 ? " q4" : " f32") << ": " << (n_prompt + n_gen - 1) << " steps, generate and prefill ok\n";
 }
