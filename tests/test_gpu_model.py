@@ -536,3 +536,12 @@ def test_persistent_step_matches_graph_step(ctx, monkeypatch, shape):
             assert npers == nr, pos
     want = gh.generate(ref, gh.KVCache(ref, 64), prompt, 20)
     np.testing.assert_array_equal(gh.generate(m, gh.KVCache(m, 64), prompt, 20), want)
+    # the persistent step's sampler (the same LM head and finish kernels):
+    # top-k draws equal the oracle's on the step's own logits
+    kp = gh.KVCache(m, 64)
+    kp.set_sampling(2.0, 99)
+    kp.set_top_k(16)
+    for pos, t in enumerate(prompt[:6]):
+        lp, _, npers = gh.runGemmaInferenceCached(m, int(t), kp)
+        wk, margin = orc.sample_top_k(lp, 2.0, 16, orc.philox_uniform(99, pos))
+        assert npers == wk or margin < 1e-4, (pos, npers, wk, margin)
