@@ -1817,8 +1817,10 @@ struct AttnStepLds {
     float os[4][G * HD];
 };
 
-template <int HD, int G, int PF, bool SKIP, bool OPQ = false>
-__device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, AttnStepLds<HD, G>& S) {
+// GT: the kv group's q heads; this workgroup takes G of them, from head
+// hs * G of the group (GT / G workgroups per chunk read the same K/V).
+template <int HD, int G, int PF, bool SKIP, bool OPQ = false, int GT = G>
+__device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, AttnStepLds<HD, G>& S, int hs = 0) {
     constexpr int LPH = HD / 4;                  // lanes per head vector (one float4 each)
     constexpr int NG4 = (G + 2) * LPH;           // float4 groups of q | k | v
     constexpr int MG4 = (NG4 + NT - 1) / NT;     // groups per thread
@@ -1835,14 +1837,16 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
     const bool own = !OPQ && pos >= c0 && pos < c1;  // this chunk scores the current position
-    const bool need_kv = own || (!OPQ && j == 0);    // j == 0 appends k, v to the cache
+    const bool append = !OPQ && j == 0 && hs == 0;   // this workgroup appends k, v to the cache
+    const bool need_kv = own || append;
+    const int h0 = g * GT + hs * G;                  // first q head of this workgroup
     const size_t pstride = (size_t)a.nkv * HD;
 
     // 1. prologue loads: partials, QK-norm weights, RoPE row (straight-line)
     constexpr int QG4 = G * LPH, MQ4 = (QG4 + NT - 1) / NT;  // OPQ: float4 groups of q per thread
     float4 qv[MQ4];
     if constexpr (OPQ) {
-        const BufView Q(a.q + (size_t)g * G * HD, (size_t)G * HD * 4);
+        const BufView Q(a.q + (size_t)h0 * HD, (size_t)G * HD * 4);
 #pragma unroll
         for (int m = 0; m < MQ4; ++m) qv[m] = Q.f4(16u * (uint32_t)(tid + m * NT));
     }
@@ -1860,7 +1864,7 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
             continue;
         }
         const int gi = tid + m * NT, vec = gi / LPH, d = 4 * (gi % LPH);  // vector (G q heads, k, v), first dim
-        const int row = vec < G ? a.q_off + (g * G + vec) * HD + d : vec == G ? a.k_off + g * HD + d : a.v_off + g * HD + d;
+        const int row = vec < G ? a.q_off + (h0 + vec) * HD + d : vec == G ? a.k_off + g * HD + d : a.v_off + g * HD + d;
         const bool ok = gi < NG4 && (vec < G || need_kv);
 #pragma unroll
         for (int s = 0; s < MAXS; ++s) pv[m][s] = P.f4(ok ? 4u * (uint32_t)(s * a.ld_qkv + row) : OOB);
@@ -1939,7 +1943,7 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     }
     __syncthreads();
     GH_MARK(2);
-    if (!OPQ && j == 0) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
+    if (append) {  // appendKVCacheShader (AttentionGPU.hs:502-534)
         for (int i = tid; i < HD; i += NT) {
             a.kc[((size_t)pos * a.nkv + g) * HD + i] = ks[i];
             a.vc[((size_t)pos * a.nkv + g) * HD + i] = vs[i];
@@ -2015,7 +2019,7 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     }
     __syncthreads();
     GH_MARK(5);
-    const size_t ob = ((size_t)g * a.nc + j) * (G * (HD + 2));
+    const size_t ob = ((size_t)g * a.nc + j) * (GT * (HD + 2));
     // four consecutive outputs per thread (one head each: HD % 4 == 0)
     for (int q4 = tid; q4 < G * HD / 4; q4 += NT) {
         const int h = 4 * q4 / HD;
@@ -2024,7 +2028,7 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
         const float e0 = __expf(m0 - M), e1 = __expf(m1 - M), e2 = __expf(m2 - M), e3 = __expf(m3 - M);
         const float4 o0 = *(const float4*)&os[0][4 * q4], o1 = *(const float4*)&os[1][4 * q4];
         const float4 o2 = *(const float4*)&os[2][4 * q4], o3 = *(const float4*)&os[3][4 * q4];
-        float* dst = a.part + ob + 2 * G + 4 * q4;
+        float* dst = a.part + ob + 2 * GT + hs * G * HD + 4 * q4;
         dst[0] = ((e0 * o0.x + e1 * o1.x) + e2 * o2.x) + e3 * o3.x;
         dst[1] = ((e0 * o0.y + e1 * o1.y) + e2 * o2.y) + e3 * o3.y;
         dst[2] = ((e0 * o0.z + e1 * o1.z) + e2 * o2.z) + e3 * o3.z;
@@ -2035,31 +2039,34 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
         float L = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) L += __expf(ms[w][tid] - M) * ls[w][tid];
-        a.part[ob + tid] = M;
-        a.part[ob + G + tid] = L;
+        a.part[ob + hs * G + tid] = M;
+        a.part[ob + GT + hs * G + tid] = L;
     }
     GH_MARK(6);
     GH_MARK_END();
 }
 
-template <int HD, int G>
+// HSP workgroups per chunk, each taking G / HSP of the group's q heads.
+template <int HD, int G, int HSP = 1>
 __global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
-    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
+    constexpr int GW = G / HSP;
+    const int hs = blockIdx.x % HSP, gj = blockIdx.x / HSP;
+    const int g = gj / a.nc, j = gj % a.nc;
     if (j >= a.n_used) return;  // uniform per workgroup
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
-    __shared__ __align__(16) AttnStepLds<HD, G> lds;
+    __shared__ __align__(16) AttnStepLds<HD, GW> lds;
     // the first vector of this wave's groups in the last prologue round
-    constexpr int LPH = HD / 4, NG4 = (G + 2) * LPH, MG4 = (NG4 + NT - 1) / NT;
+    constexpr int LPH = HD / 4, NG4 = (GW + 2) * LPH, MG4 = (NG4 + NT - 1) / NT;
     const int vec_lo = ((MG4 - 1) * NT + wave_id() * 64) / LPH;
     const int pos = a.pos;
-    const bool need_kv = (pos >= c0 && pos < c1) || j == 0;
-    const bool skip = vec_lo >= G + 2 || (vec_lo >= G && !need_kv);
+    const bool need_kv = (pos >= c0 && pos < c1) || (j == 0 && hs == 0);
+    const bool skip = vec_lo >= GW + 2 || (vec_lo >= GW && !need_kv);
     if (c1 - c0 <= 32) {
-        if (skip) attn_step_body<HD, G, 1, true>(a, g, j, lds);
-        else attn_step_body<HD, G, 1, false>(a, g, j, lds);
+        if (skip) attn_step_body<HD, GW, 1, true, false, G>(a, g, j, lds, hs);
+        else attn_step_body<HD, GW, 1, false, false, G>(a, g, j, lds, hs);
     } else {
-        if (skip) attn_step_body<HD, G, 2, true>(a, g, j, lds);
-        else attn_step_body<HD, G, 2, false>(a, g, j, lds);
+        if (skip) attn_step_body<HD, GW, 2, true, false, G>(a, g, j, lds, hs);
+        else attn_step_body<HD, GW, 2, false, false, G>(a, g, j, lds, hs);
     }
 }
 
@@ -2080,9 +2087,19 @@ __global__ __launch_bounds__(NT) void k_attn_op(AttnArgs a) {
 #if GH_IN_TU(1)
 static int launch_attn_step(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
     if (a.nc > ATTN_MAX_NC || a.nc < 1) return set_error(GH_ERR_INVALID, "attention: %d splits (1..%d)", a.nc, ATTN_MAX_NC);
-    const dim3 grid(nkv * a.nc), block(NT);
-#define GH_ATTN_CASE(HD_, G_) \
-    if (hd == HD_ && G == G_) return sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_>, grid, block, 0, a);
+    // groups of 4+ q heads: two workgroups per chunk, each with half the
+    // heads (each reads half the q partials and does half the score work;
+    // the K/V rounds are read twice).  Measured on MI355X: 1B (4 heads per
+    // kv head) attention 5.15 -> 4.31 us, 1445 -> 1485 tok/s; with 2 heads
+    // per kv head (4B) one head per workgroup is slower (4.33 -> 4.88 us).
+    static const char* hs_env = std::getenv("GH_ATTN_HSPLIT");  // 0: one workgroup per chunk
+    const int hsp = G >= 4 && !(hs_env && *hs_env == '0') ? 2 : 1;
+    const dim3 grid(nkv * a.nc * hsp), block(NT);
+#define GH_ATTN_CASE(HD_, G_)                                                                                  \
+    if (hd == HD_ && G == G_)                                                                                  \
+        return hsp == 2 ? sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_, (G_ >= 4 ? 2 : 1)>, grid,  \
+                                         block, 0, a)                                                         \
+                        : sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_, 1>, grid, block, 0, a);
     GH_ATTN_CASE(256, 1) GH_ATTN_CASE(256, 2) GH_ATTN_CASE(256, 4) GH_ATTN_CASE(256, 8)
     GH_ATTN_CASE(128, 1) GH_ATTN_CASE(128, 2) GH_ATTN_CASE(128, 4) GH_ATTN_CASE(128, 8)
     GH_ATTN_CASE(32, 1) GH_ATTN_CASE(32, 2) GH_ATTN_CASE(32, 4) GH_ATTN_CASE(32, 8)
