@@ -2087,17 +2087,18 @@ __global__ __launch_bounds__(NT) void k_attn_op(AttnArgs a) {
 #if GH_IN_TU(1)
 static int launch_attn_step(Sink& k, double bytes, int hd, int G, const AttnArgs& a, int nkv) {
     if (a.nc > ATTN_MAX_NC || a.nc < 1) return set_error(GH_ERR_INVALID, "attention: %d splits (1..%d)", a.nc, ATTN_MAX_NC);
-    // groups of 4+ q heads: two workgroups per chunk, each with half the
-    // heads (each reads half the q partials and does half the score work;
-    // the K/V rounds are read twice).  Measured on MI355X: 1B (4 heads per
-    // kv head) attention 5.15 -> 4.31 us, 1445 -> 1485 tok/s; with 2 heads
-    // per kv head (4B) one head per workgroup is slower (4.33 -> 4.88 us).
+    // groups of 4+ q heads: one workgroup per (chunk, q head), each reading
+    // its head's q partials and the chunk's K/V rounds (read once per head).
+    // Measured on MI355X, 1B (4 heads per kv head): attention 5.15 us with
+    // one workgroup per chunk, 4.28 with two (two heads each), 3.91 with
+    // four; 1450 -> 1495 -> 1511 tok/s.  With 2 heads per kv head (4B) one
+    // head per workgroup is slower (4.33 -> 4.88 us), so those stay whole.
     static const char* hs_env = std::getenv("GH_ATTN_HSPLIT");  // 0: one workgroup per chunk
-    const int hsp = G >= 4 && !(hs_env && *hs_env == '0') ? 2 : 1;
+    const int hsp = G >= 4 && !(hs_env && *hs_env == '0') ? G : 1;
     const dim3 grid(nkv * a.nc * hsp), block(NT);
 #define GH_ATTN_CASE(HD_, G_)                                                                                  \
     if (hd == HD_ && G == G_)                                                                                  \
-        return hsp == 2 ? sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_, (G_ >= 4 ? 2 : 1)>, grid,  \
+        return hsp > 1 ? sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_, (G_ >= 4 ? G_ : 1)>, grid,   \
                                          block, 0, a)                                                         \
                         : sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_, 1>, grid, block, 0, a);
     GH_ATTN_CASE(256, 1) GH_ATTN_CASE(256, 2) GH_ATTN_CASE(256, 4) GH_ATTN_CASE(256, 8)
