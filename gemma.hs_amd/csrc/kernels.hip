@@ -2074,14 +2074,16 @@ __global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
 // (gh_attention_decode, head_dim 256): the step kernel's streaming body with
 // q read ready-made (OPQ); workgroup (g, j) writes chunk j's state for
 // k_attn_combine.
-template <int HD, int G>
+template <int HD, int G, int HSP = 1>
 __global__ __launch_bounds__(NT) void k_attn_op(AttnArgs a) {
-    const int g = blockIdx.x / a.nc, j = blockIdx.x % a.nc;
+    constexpr int GW = G / HSP;
+    const int hs = blockIdx.x % HSP, gj = blockIdx.x / HSP;
+    const int g = gj / a.nc, j = gj % a.nc;
     if (j >= a.n_used) return;  // uniform per workgroup
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
-    __shared__ __align__(16) AttnStepLds<HD, G> lds;
-    if (c1 - c0 <= 32) attn_step_body<HD, G, 1, false, true>(a, g, j, lds);
-    else attn_step_body<HD, G, 2, false, true>(a, g, j, lds);
+    __shared__ __align__(16) AttnStepLds<HD, GW> lds;
+    if (c1 - c0 <= 32) attn_step_body<HD, GW, 1, false, true, G>(a, g, j, lds, hs);
+    else attn_step_body<HD, GW, 2, false, true, G>(a, g, j, lds, hs);
 }
 
 #if GH_IN_TU(1)
@@ -4833,7 +4835,16 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     // sub-chunk kernel (0.3 us faster on the last 512)
     const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8;
     const bool views_ok = (size_t)p_end * nkv * hd * 4 <= 0x7fffffffu;  // the body's buffer views
-    if (hd == 256 && g_ok && views_ok && a.ch >= 64) {
+    // few chunks and 4+ q heads per kv head: one workgroup per (chunk, q
+    // head), as in the step, while that keeps the grid within one per CU
+    static const char* hs_env = std::getenv("GH_ATTN_HSPLIT");  // 0: one workgroup per chunk
+    const bool hsplit = hd == 256 && views_ok && (G == 4 || G == 8) && nkv * a.n_used * G <= 256 &&
+                        !(hs_env && *hs_env == '0');
+    if (hsplit) {
+        const dim3 grid(nkv * a.nc * G);
+        if (G == 4) hipLaunchKernelGGL((k_attn_op<256, 4, 4>), grid, dim3(NT), 0, s, a);
+        else hipLaunchKernelGGL((k_attn_op<256, 8, 8>), grid, dim3(NT), 0, s, a);
+    } else if (hd == 256 && g_ok && views_ok && a.ch >= 64) {
         const dim3 grid(nkv * a.nc);
         if (G == 1) hipLaunchKernelGGL((k_attn_op<256, 1>), grid, dim3(NT), 0, s, a);
         else if (G == 2) hipLaunchKernelGGL((k_attn_op<256, 2>), grid, dim3(NT), 0, s, a);
