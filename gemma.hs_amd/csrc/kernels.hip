@@ -4182,30 +4182,28 @@ struct PfQkv {
     float* vc;
 };
 
+// One wave per (token, kv head, vector): the G q heads, k and v are
+// independent until attention, so each vector's split sum, QK-norm and RoPE
+// run on a workgroup of their own (6x the workgroups of one per (token, kv
+// head) for G = 4: the per-token chains spread over the chip).
 template <int HD, int G>
-__global__ __launch_bounds__(NT) void k_pf_qkv(PfQkv p) {
-    __shared__ __align__(16) float buf[(G + 2) * HD];
-    const int t = blockIdx.x / p.nkv, g = blockIdx.x % p.nkv, tid = threadIdx.x;
+__global__ __launch_bounds__(64) void k_pf_qkv(PfQkv p) {
+    __shared__ __align__(16) float buf[HD];
+    const int vec = blockIdx.x % (G + 2), tg = blockIdx.x / (G + 2);
+    const int t = tg / p.nkv, g = tg % p.nkv, lane = threadIdx.x;
     const int pos = p.pos0 + t;
-    for (int i = 4 * tid; i < (G + 2) * HD; i += 4 * NT) {
-        const int row = i < G * HD ? p.q_off + g * G * HD + i
-                      : i < (G + 1) * HD ? p.k_off + g * HD + (i - G * HD)
-                                         : p.v_off + g * HD + (i - (G + 1) * HD);
-        *(float4*)&buf[i] = sum_splits4(p.part + (size_t)t * p.ld, p.S, p.Pp * p.ld, row >> 2);
+    const int row0 = vec < G ? p.q_off + (g * G + vec) * HD : vec == G ? p.k_off + g * HD : p.v_off + g * HD;
+    for (int i = 4 * lane; i < HD; i += 4 * 64)
+        *(float4*)&buf[i] = sum_splits4(p.part + (size_t)t * p.ld, p.S, p.Pp * p.ld, (row0 + i) >> 2);
+    __syncthreads();
+    if (vec <= G) {
+        if (p.use_qk_norm) wave_head_norm<HD>(buf, vec < G ? p.q_norm : p.k_norm, p.eps, p.zc);
+        wave_head_rope<HD>(buf, (const float2*)p.rope + (size_t)pos * (HD / 2));
     }
     __syncthreads();
-    const float2* cs = (const float2*)p.rope + (size_t)pos * (HD / 2);
-    for (int vec = tid >> 6; vec < G + 1; vec += 4) {
-        float* v = buf + vec * HD;
-        if (p.use_qk_norm) wave_head_norm<HD>(v, vec < G ? p.q_norm : p.k_norm, p.eps, p.zc);
-        wave_head_rope<HD>(v, cs);
-    }
-    __syncthreads();
-    for (int i = tid; i < G * HD; i += NT) p.q[(size_t)t * p.nkv * G * HD + (size_t)g * G * HD + i] = buf[i];
-    for (int i = tid; i < HD; i += NT) {
-        p.kc[((size_t)pos * p.nkv + g) * HD + i] = buf[G * HD + i];
-        p.vc[((size_t)pos * p.nkv + g) * HD + i] = buf[(G + 1) * HD + i];
-    }
+    float* dst = vec < G ? p.q + (size_t)t * p.nkv * G * HD + ((size_t)g * G + vec) * HD
+               : (vec == G ? p.kc : p.vc) + ((size_t)pos * p.nkv + g) * HD;
+    for (int i = lane; i < HD; i += 64) dst[i] = buf[i];
 }
 
 // Attention of token t (kv head g) over its window of the cache: the
@@ -4593,7 +4591,7 @@ int enqueue_prefill(gh_model* m, gh_kv* kv, Sink& sink, int n, int pos0, bool he
             q.kc = kv->k + li * kv_layer;
             q.vc = kv->v + li * kv_layer;
 #define GH_PF_QKV(HD_, G_) \
-    if (hd == HD_ && G == G_) GH_CHECK(sink_launch(sink, "pf_qkv_post", 0.0, k_pf_qkv<HD_, G_>, dim3(n * nkv), dim3(NT), 0, q)); else
+    if (hd == HD_ && G == G_) GH_CHECK(sink_launch(sink, "pf_qkv_post", 0.0, k_pf_qkv<HD_, G_>, dim3(n * nkv * (G_ + 2)), dim3(64), 0, q)); else
             GH_PF_QKV(256, 1) GH_PF_QKV(256, 2) GH_PF_QKV(256, 4) GH_PF_QKV(256, 8)
             GH_PF_QKV(128, 1) GH_PF_QKV(128, 2) GH_PF_QKV(128, 4) GH_PF_QKV(128, 8)
             GH_PF_QKV(32, 1) GH_PF_QKV(32, 2) GH_PF_QKV(32, 4) GH_PF_QKV(32, 8)
