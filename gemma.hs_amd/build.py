@@ -26,7 +26,7 @@ ORACLE_DIR = REPO / "oracle"
 ORACLE_LIB = ORACLE_DIR / "build" / "liboracle.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-KERNEL_TUS = 4  # kernels.hip: step, persistent step, prefill, op level
+KERNEL_TUS = 7  # kernels.hip: step, persistent step, prefill, op level, 3 x step matvec phases
 ARCH = "gfx950"
 # Packed FP32 (v_pk_*_f32) is disabled for every HIP translation unit.
 # MFMA results go to VGPRs (gfx950 allows it): the compiler's default AGPR

@@ -87,6 +87,7 @@ struct Plan {
     int kbw = 1;
     int rl = 2;  // rows per lane: 2 = 128-row workgroups, 1 = 64-row workgroups
     int mfma = 0;  // Q4_0: dot products on the int8 matrix cores (1) or the VALU (0)
+    int ni = 1;    // work items per workgroup (1 or 2; 4 waves each, one prologue)
     int row_tiles(int tiles) const { return rl == 2 ? tiles : 2 * tiles; }
 };
 

@@ -35,7 +35,8 @@
 #include "common.h"
 
 // The library compiles this file as several translation units in parallel
-// (GH_TU = 1 step, 2 persistent step, 3 prefill, 4 op level); each defines
+// (GH_TU = 1 step, 2 persistent step, 3 prefill, 4 op level, 5-7 the step's
+// matvec phases by prologue); each defines
 // its own host entry points and so instantiates only the kernels they
 // launch.  Kernels launched from several units are templates, whose
 // symbols are merged at link time.  GH_TU = 0 (the default) is everything.
@@ -510,6 +511,11 @@ template <class P>
 struct HasSettle<P, std::void_t<decltype(&P::template settle<1>)>> : std::true_type {};
 
 template <class P, class = void>
+struct HasFinishBarriers : std::false_type {};
+template <class P>
+struct HasFinishBarriers<P, std::void_t<decltype(P::kFinishBarriers)>> : std::true_type {};
+
+template <class P, class = void>
 struct HasLoadVariants : std::false_type {};
 template <class P>
 struct HasLoadVariants<P, std::void_t<decltype(&P::template load_v<0>)>> : std::true_type {};
@@ -700,7 +706,11 @@ __device__ __forceinline__ void mv_item_valu(const DMat& w, int rt, int s, int S
     const int tile = RL == 2 ? rt : rt >> 1, rbase = RL == 2 ? 0 : (rt & 1) * 64;
     const int nb = w.nblk;
     const int per_split = (nb + S - 1) / S;
-    const int kb0 = min(nb, s * per_split), kb1 = min(nb, kb0 + per_split);
+    // uniform; the readfirstlane keeps the split bounds, and so the buffer
+    // bases and loop bounds derived from them, in SGPRs (without it some
+    // instances compute them on the VALU and wrap loads in waterfall loops)
+    const int kb0 = __builtin_amdgcn_readfirstlane(min(nb, s * per_split));
+    const int kb1 = __builtin_amdgcn_readfirstlane(min(nb, kb0 + per_split));
     const int nk = kb1 - kb0;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int kw0 = kb0 + (nk * wave >> 2), kw1 = kb0 + (nk * (wave + 1) >> 2);
@@ -748,6 +758,86 @@ __device__ __forceinline__ void mv_item_valu(const DMat& w, int rt, int s, int S
     }
     GH_MARK(5);
     GH_MARK_END();
+}
+
+// NI work items of one column split per workgroup of NI x 4 waves: waves
+// 0-3 build the split's input slice once for all NI items and take item
+// NI*q, waves 4i .. 4i+3 take item NI*q + i and meet the prologue's
+// barriers (Pro::kFinishBarriers of them) without issuing its loads.  A CU
+// then runs one prologue where NI 4-wave workgroups would run NI; the
+// prologue is what bounds these latency-bound items.
+template <int FMT, int KBW, int RL, int V, class Pro, class Epi>
+__device__ __forceinline__ void mv_item_multi_v(const DMat& w, int it, int s, int S, const Pro& pro, const Epi& epi,
+                                                const MvLds& L, float* red) {
+    constexpr int BK = Blk<FMT>::BK;
+    const int lead = wave_id() < 4, wave = wave_id() & 3, lane = threadIdx.x & 63;
+    const int tile = RL == 2 ? it : it >> 1, rbase = RL == 2 ? 0 : (it & 1) * 64;
+    const bool live = tile < w.tiles;
+    const int nb = w.nblk;
+    const int per_split = (nb + S - 1) / S;
+    // uniform: readfirstlane as in mv_item_valu
+    const int kb0 = __builtin_amdgcn_readfirstlane(min(nb, s * per_split));
+    const int kb1 = __builtin_amdgcn_readfirstlane(min(nb, kb0 + per_split));
+    const int nk = kb1 - kb0;
+    const int kw0 = kb0 + (nk * wave >> 2);
+    // an item past the last row tile loads nothing and writes nothing
+    const int kw1 = live ? kb0 + (nk * (wave + 1) >> 2) : kw0;
+    typename Pro::Regs pr;
+    if (lead) {
+        if constexpr (HasLoadVariants<Pro>::value) pro.template load_v<V>(pr, kb0 * BK, nk * BK);
+        else pro.load(pr, kb0 * BK, nk * BK);
+    }
+    typename Epi::Regs er;
+    epi.load(er);
+    __builtin_amdgcn_sched_barrier(0);
+    const MatViews mv(w);
+    WRegs<FMT, KBW> r;
+    mv_load<FMT, KBW, RL>(r, w, mv, tile, rbase, kw0, kw1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (lead) {
+        pro.template finish<FMT>(L, pr, kb0 * BK, nk * BK);
+    } else {
+#pragma unroll
+        for (int i = 0; i < Pro::kFinishBarriers; ++i) __syncthreads();
+    }
+    __syncthreads();
+    float acc0 = 0.0f, acc1 = 0.0f;
+    mv_compute<FMT, KBW, RL>(r, kw0, kw1, kb0, L.xs, L.sxs, acc0, acc1);
+    for (int base = kw0 + KBW; base < kw1; base += KBW) {
+        mv_load<FMT, KBW, RL>(r, w, mv, tile, rbase, base, kw1);
+        mv_compute<FMT, KBW, RL>(r, base, kw1, kb0, L.xs, L.sxs, acc0, acc1);
+    }
+    red[wave * TILE_ROWS + lane] = acc0;
+    if (RL == 2) red[wave * TILE_ROWS + 64 + lane] = acc1;
+    __syncthreads();
+    if (wave == 0 && live) {
+        const float y0 = (red[lane] + red[TILE_ROWS + lane]) + (red[2 * TILE_ROWS + lane] + red[3 * TILE_ROWS + lane]);
+        float y1 = 0.0f;
+        if (RL == 2)
+            y1 = (red[64 + lane] + red[TILE_ROWS + 64 + lane]) + (red[2 * TILE_ROWS + 64 + lane] + red[3 * TILE_ROWS + 64 + lane]);
+        epi.template run<RL>(L, er, it, tile * TILE_ROWS + rbase + lane, s, y0, y1);
+    }
+}
+
+// grid = ceil(items / NI) x S, NI x 256 threads; LDS: k_matvec's carve-up
+// (red_off floats), then the reduction areas of items 1 .. NI-1 (512 floats
+// each)
+template <int FMT, int KBW, int RL, int NI, class Pro, class Epi>
+__global__ __launch_bounds__(NI * NT) void k_matvec_multi(DMat w, int S, Pro pro, Epi epi, int red_off) {
+    extern __shared__ float lds[];
+    const int per_split = (w.nblk + S - 1) / S;
+    const MvLds L = mv_lds<FMT>(lds, per_split);
+    const int i = wave_id() >> 2;
+    float* red = i == 0 ? L.red : lds + red_off + (i - 1) * 512;
+    const int it = blockIdx.x / S * NI + i, s = blockIdx.x % S;
+    if constexpr (HasLoadVariants<Pro>::value) {
+        constexpr int BK = Blk<FMT>::BK;
+        const int kb0 = min(w.nblk, s * per_split), nk = min(w.nblk, kb0 + per_split) - kb0;
+        if (i == 0 && pro.variant(kb0 * BK, nk * BK)) mv_item_multi_v<FMT, KBW, RL, 1>(w, it, s, S, pro, epi, L, red);
+        else mv_item_multi_v<FMT, KBW, RL, 0>(w, it, s, S, pro, epi, L, red);
+    } else {
+        mv_item_multi_v<FMT, KBW, RL, 1>(w, it, s, S, pro, epi, L, red);
+    }
 }
 
 // One workgroup per work item: grid = row tiles x S.
@@ -880,8 +970,7 @@ struct ProPlain {
 // EMB: layer 0 (x is the token's embedding row); a separate instance, so
 // that in the other layers the compiler keeps every prologue load ahead of
 // the weight loads (a runtime branch lets it sink them into the branch).
-template <int MG, bool EMB = false>
-struct ProResid {
+struct ResidFields {
     int from_embedding;  // must equal EMB
     DMat embd;
     const StepState* st;
@@ -895,6 +984,11 @@ struct ProResid {
     int zc, H;
     float* x_out;          // nullable
     float* layer_out_row;  // nullable
+};
+
+template <int MG, bool EMB = false>
+struct ProResid : ResidFields {
+    static constexpr int kFinishBarriers = 1;  // finish<>() holds one __syncthreads
     struct Regs {
         float4 pv[MAXS][MG];
         float4 bv[MG], wp[MG];
@@ -1022,6 +1116,7 @@ __host__ __device__ __forceinline__ void attn_chunks(int n_pos, int nc, int& ch,
 // O-projection input: merge the split-K attention partials {m[G], l[G],
 // o[G][HD]} of every chunk for the slice [c0, c0+n) of o = [nq][hd].
 struct ProAttnCombine {
+    static constexpr int kFinishBarriers = 1;
     const float* part;
     int pos;  // current position (patched per step with set_pos)
     int nc, G, HD;
@@ -1114,6 +1209,7 @@ struct ProAttnCombine {
 // no load instruction is spent on absent splits beyond the next of those).
 template <int NS>
 struct ProGeglu {
+    static constexpr int kFinishBarriers = 0;
     const float* part_gu;
     int Sg, ld_g, up_off;
     int gm;
@@ -1348,11 +1444,21 @@ template <int POS_ARG = -1, class Pro, class Epi>
 static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const Pro& pro,
                      const Epi& epi, int tmp_floats) {
     const int per_split = (w.nblk + p.S - 1) / p.S;
-    const size_t lds = mv_lds_bytes(w.fmt, per_split, tmp_floats);
-    const dim3 grid(p.row_tiles(w.tiles) * p.S), block(NT);
+    // items per workgroup: NI > 1 only on the VALU Q4_0 path, for prologues
+    // that declare their barriers
+    int ni = 1;
+    if constexpr (HasFinishBarriers<Pro>::value)
+        if (w.fmt == FMT_Q4 && !(std::is_same_v<Pro, ProPlain> && p.mfma)) ni = p.ni;
+    if (ni != 1 && ni != 2) return set_error(GH_ERR_INVALID, "unsupported items per workgroup %d", ni);
+    const size_t lds = mv_lds_bytes(w.fmt, per_split, tmp_floats) + (size_t)(ni - 1) * 512 * sizeof(float);
+    const dim3 grid((p.row_tiles(w.tiles) + ni - 1) / ni * p.S), block(ni * NT);
     // POS_ARG counts kernel arguments (DMat, S, Pro, Epi): the prologue is 2
     auto go = [&](void (*fn)(DMat, int, Pro, Epi)) {
         return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, w, p.S, pro, epi);
+    };
+    const int red_off = (int)mv_lds_floats(w.fmt, per_split, tmp_floats);
+    auto go_multi = [&](void (*fn)(DMat, int, Pro, Epi, int)) {
+        return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, w, p.S, pro, epi, red_off);
     };
     auto by_rl = [&](auto kbw) -> int {
         constexpr int KBW = decltype(kbw)::value;
@@ -1361,6 +1467,11 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
         if constexpr (std::is_same_v<Pro, ProPlain>) {
             if (p.mfma)
                 return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
+        }
+        if constexpr (HasFinishBarriers<Pro>::value) {
+            if (ni == 2)
+                return p.rl == 2 ? go_multi(k_matvec_multi<FMT_Q4, KBW, 2, 2, Pro, Epi>)
+                                 : go_multi(k_matvec_multi<FMT_Q4, KBW, 1, 2, Pro, Epi>);
         }
         return p.rl == 2 ? go(k_matvec<FMT_Q4, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4, KBW, 1, Pro, Epi>);
     };
@@ -3632,6 +3743,60 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
 #endif  // GH_IN_TU(2)
 
 // ------------------------------------------------------------------
+// the step's matvec phases, one translation unit per prologue family (their
+// instances are most of the library's kernels): 5 residual + norm (qkv of
+// layers 1.., gate/up), 6 the same from the token embedding (qkv of layer
+// 0), 7 the attention merge (o_proj) and GeGLU (down)
+// ------------------------------------------------------------------
+int launch_resid_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const ResidFields& f,
+                    const EpiPartial& epi);
+int launch_resid_emb_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const ResidFields& f,
+                        const EpiPartial& epi);
+int launch_combine_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const ProAttnCombine& pro,
+                      const EpiPartial& epi);
+int launch_geglu_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const float* part_gu,
+                    int Sg, int ld_g, int up_off, int gm, const EpiPartial& epi);
+
+template <bool EMB>
+static int launch_resid_t(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const ResidFields& f,
+                          const EpiPartial& epi) {
+    if ((f.from_embedding != 0) != EMB) return set_error(GH_ERR_INVALID, "residual prologue: embedding flag");
+    return with_mg(f.H, [&](auto mg) {
+        ProResid<decltype(mg)::value, EMB> pro;
+        static_cast<ResidFields&>(pro) = f;
+        return launch_mv(k, name, bytes, w, p, pro, epi, 0);
+    });
+}
+
+#if GH_IN_TU(5)
+int launch_resid_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const ResidFields& f,
+                    const EpiPartial& epi) {
+    return launch_resid_t<false>(k, name, bytes, w, p, f, epi);
+}
+#endif
+
+#if GH_IN_TU(6)
+int launch_resid_emb_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const ResidFields& f,
+                        const EpiPartial& epi) {
+    return launch_resid_t<true>(k, name, bytes, w, p, f, epi);
+}
+#endif
+
+#if GH_IN_TU(7)
+int launch_combine_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const ProAttnCombine& pro,
+                      const EpiPartial& epi) {
+    const int per_split = (w.nblk + p.S - 1) / p.S * block_cols(w.fmt);
+    return launch_mv<2>(k, name, bytes, w, p, pro, epi, (per_split / pro.HD + 2) * ATTN_MAX_NC);
+}
+
+int launch_geglu_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const float* part_gu,
+                    int Sg, int ld_g, int up_off, int gm, const EpiPartial& epi) {
+    if (gm * Sg <= 4) return launch_mv(k, name, bytes, w, p, ProGeglu<4>{part_gu, Sg, ld_g, up_off, gm}, epi, 0);
+    return launch_mv(k, name, bytes, w, p, ProGeglu<MAXS>{part_gu, Sg, ld_g, up_off, gm}, epi, 0);
+}
+#endif
+
+// ------------------------------------------------------------------
 // the decode step
 // ------------------------------------------------------------------
 #if GH_IN_TU(1)
@@ -3679,29 +3844,27 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
         LayerDev& L = m->layers[li];
         const LayerDev* P = li > 0 ? &m->layers[li - 1] : nullptr;
         // A: residual + pre-attention norm + fused QKV matvec
-        auto qkv = [&](auto mg, auto emb) {
-            ProResid<decltype(mg)::value, decltype(emb)::value> pro;
-            pro.from_embedding = decltype(emb)::value;
-            pro.embd = m->embd;
-            pro.st = kv->st;
-            pro.escale = sqrtf((float)H);
-            pro.base = m->x1;
-            pro.part = m->part_d;
-            pro.S = m->pe.S;
-            pro.ld = P ? P->down.tiles * TILE_ROWS : 0;
-            pro.w_post = P && (c.flags & GH_FLAG_POST_FFN_NORM) ? P->post_ffw : nullptr;
-            pro.w_norm = L.attn_norm;
-            pro.eps = eps;
-            pro.zc = zc;
-            pro.H = H;
-            pro.x_out = m->x_res;
-            pro.layer_out_row = li > 0 ? m->layer_out + (size_t)(li - 1) * H : nullptr;
+        {
+            ResidFields f;
+            f.from_embedding = li == 0;
+            f.embd = m->embd;
+            f.st = kv->st;
+            f.escale = sqrtf((float)H);
+            f.base = m->x1;
+            f.part = m->part_d;
+            f.S = m->pe.S;
+            f.ld = P ? P->down.tiles * TILE_ROWS : 0;
+            f.w_post = P && (c.flags & GH_FLAG_POST_FFN_NORM) ? P->post_ffw : nullptr;
+            f.w_norm = L.attn_norm;
+            f.eps = eps;
+            f.zc = zc;
+            f.H = H;
+            f.x_out = m->x_res;
+            f.layer_out_row = li > 0 ? m->layer_out + (size_t)(li - 1) * H : nullptr;
             EpiPartial epi{m->part_qkv, L.qkv.tiles * TILE_ROWS};
-            return launch_mv(sink, "qkv", mat_bytes(L.qkv), L.qkv, m->pa, pro, epi, H);
-        };
-        GH_CHECK(with_mg(H, [&](auto mg) {
-            return li == 0 ? qkv(mg, std::true_type{}) : qkv(mg, std::false_type{});
-        }));
+            GH_CHECK(li == 0 ? launch_resid_emb_mv(sink, "qkv", mat_bytes(L.qkv), L.qkv, m->pa, f, epi)
+                             : launch_resid_mv(sink, "qkv", mat_bytes(L.qkv), L.qkv, m->pa, f, epi));
+        }
         // B: QK-norm + RoPE + KV append + split-K attention
         {
             AttnArgs a{};
@@ -3735,31 +3898,29 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             ProAttnCombine pro{m->attn_part, pos, m->attn_nc, G, hd, L.global ? 1 : 0, c.sliding_window, c.mode, 0, nkv};
             pro.set_pos(pos);
             EpiPartial epi{m->part_o, L.o.tiles * TILE_ROWS};
-            const int per_split = (L.o.nblk + m->pc.S - 1) / m->pc.S * block_cols(L.o.fmt);
-            GH_CHECK(launch_mv<2>(sink, "o_proj", mat_bytes(L.o), L.o, m->pc, pro, epi,
-                                  (per_split / hd + 2) * ATTN_MAX_NC));
+            GH_CHECK(launch_combine_mv(sink, "o_proj", mat_bytes(L.o), L.o, m->pc, pro, epi));
         }
         // D: post-attention norm + residual + pre-FFN norm + gate/up matvec
-        GH_CHECK(with_mg(H, [&](auto mg) {
-            ProResid<decltype(mg)::value> pro;
-            pro.from_embedding = 0;
-            pro.embd = m->embd;
-            pro.st = kv->st;
-            pro.escale = 1.0f;
-            pro.base = m->x_res;
-            pro.part = m->part_o;
-            pro.S = m->pc.S;
-            pro.ld = L.o.tiles * TILE_ROWS;
-            pro.w_post = (c.flags & GH_FLAG_POST_ATTN_NORM) ? L.post_attn : nullptr;
-            pro.w_norm = L.ffn_norm ? L.ffn_norm : L.post_attn;
-            pro.eps = eps;
-            pro.zc = zc;
-            pro.H = H;
-            pro.x_out = m->x1;
-            pro.layer_out_row = nullptr;
+        {
+            ResidFields f;
+            f.from_embedding = 0;
+            f.embd = m->embd;
+            f.st = kv->st;
+            f.escale = 1.0f;
+            f.base = m->x_res;
+            f.part = m->part_o;
+            f.S = m->pc.S;
+            f.ld = L.o.tiles * TILE_ROWS;
+            f.w_post = (c.flags & GH_FLAG_POST_ATTN_NORM) ? L.post_attn : nullptr;
+            f.w_norm = L.ffn_norm ? L.ffn_norm : L.post_attn;
+            f.eps = eps;
+            f.zc = zc;
+            f.H = H;
+            f.x_out = m->x1;
+            f.layer_out_row = nullptr;
             EpiPartial epi{m->part_gu, L.gu.tiles * TILE_ROWS};
-            return launch_mv(sink, "gate_up", mat_bytes(L.gu), L.gu, m->pd, pro, epi, H);
-        }));
+            GH_CHECK(launch_resid_mv(sink, "gate_up", mat_bytes(L.gu), L.gu, m->pd, f, epi));
+        }
         // E: GeGLU + down projection
         {
             const int gm = geglu_groups(L.down, m->pe);
@@ -3767,13 +3928,8 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
                 return set_error(GH_ERR_INVALID, "down projection split of %d columns with %d gate/up splits",
                                  (L.down.nblk + m->pe.S - 1) / m->pe.S * block_cols(L.down.fmt), m->pd.S);
             EpiPartial epi{m->part_d, L.down.tiles * TILE_ROWS};
-            if (gm * m->pd.S <= 4) {
-                ProGeglu<4> pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad, gm};
-                GH_CHECK(launch_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, pro, epi, 0));
-            } else {
-                ProGeglu<MAXS> pro{m->part_gu, m->pd.S, L.gu.tiles * TILE_ROWS, m->f_pad, gm};
-                GH_CHECK(launch_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, pro, epi, 0));
-            }
+            GH_CHECK(launch_geglu_mv(sink, "down", mat_bytes(L.down), L.down, m->pe, m->part_gu, m->pd.S,
+                                     L.gu.tiles * TILE_ROWS, m->f_pad, gm, epi));
         }
     }
     // final residual + norm, once

@@ -239,6 +239,25 @@ void make_plans(gh_model* m) {
         const DMat& d = p == &m->pa ? L.qkv : p == &m->pc ? L.o : p == &m->pd ? L.gu : L.down;
         p->kbw = kbw_for(m->fmt, ((d.nblk + p->S - 1) / p->S + 3) / 4);
     }
+    // work items per workgroup: where a phase has more work items than the
+    // device has CUs, two items share one 8-wave workgroup and so one
+    // prologue, which is what bounds these items.  Measured on MI355X: 1B
+    // gate/up 432 -> 216 workgroups, 6.15 -> 5.5 us; 4B gate/up 11.6 -> 10.7
+    // us and down (320 items) 793 -> 820 tok/s.  Below the CU count pairing
+    // only halves the CUs in use (1B down, 144 items: 1538 -> 1501 tok/s);
+    // four items per 16-wave workgroup leave 128 VGPRs a lane and spill.
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->ctx->device) != hipSuccess || cus <= 0)
+        cus = 256;
+    for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe}) {
+        const DMat& d = p == &m->pa ? L.qkv : p == &m->pc ? L.o : p == &m->pd ? L.gu : L.down;
+        p->ni = (long long)p->row_tiles(d.tiles) * p->S > cus ? 2 : 1;
+    }
+    m->pa.ni = env_int("GH_PLAN_A_NI", m->pa.ni);
+    m->pc.ni = env_int("GH_PLAN_C_NI", m->pc.ni);
+    m->pd.ni = env_int("GH_PLAN_D_NI", m->pd.ni);
+    m->pe.ni = env_int("GH_PLAN_E_NI", m->pe.ni);
+    for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe}) p->ni = p->ni == 2 ? 2 : 1;
     m->attn_nc = std::max(1, std::min(64, env_int("GH_ATTN_NC", 64)));
 }
 
