@@ -237,10 +237,19 @@ constexpr int CP_NT = GH_CP_WEIGHTS;  // cache policy of streamed weights (2: no
 
 struct BufView {
     __amdgpu_buffer_rsrc_t r;
-    // bytes = 0 (or p = nullptr with bytes = 0): every load reads zeros
-    __device__ __forceinline__ BufView(const void* p, size_t bytes)
-        : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
-                                              (int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu), 0x00020000)) {}
+    // bytes = 0 (or p = nullptr with bytes = 0): every load reads zeros.
+    // p and bytes must be the same in every lane of the wave (the descriptor
+    // is a scalar operand): they are taken from the first active lane, so
+    // that the compiler keeps the descriptor in SGPRs.  Where it cannot prove
+    // a base uniform (loop-carried layer tables, SGPR pressure) it would
+    // otherwise wrap each load in a waterfall loop.
+    __device__ __forceinline__ BufView(const void* p, size_t bytes) {
+        const uint64_t a = (uint64_t)p;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+        const int n = __builtin_amdgcn_readfirstlane((int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu));
+        r = __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+    }
     template <int CP = 0>
     __device__ __forceinline__ float4 f4(uint32_t off) const {
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP));
