@@ -572,8 +572,8 @@ struct QRegs {
 // wave's RL row groups; blocks at or past kb1 read zeros.
 template <int QB, int RL>
 __device__ __forceinline__ void mq_load(QRegs<QB, RL>& r, const DMat& w, const MatViews& v, int tile, int rbase,
-                                        int kq, int kb1) {
-    const int lane = threadIdx.x & 63, wave = wave_id();
+                                        int kq, int kb1, int wave) {
+    const int lane = threadIdx.x & 63;
     const uint32_t tb = (uint32_t)tile * (uint32_t)w.nblk * TILE_ROWS;
 #pragma unroll
     for (int j = 0; j < RL; ++j) {
@@ -643,7 +643,9 @@ __device__ __forceinline__ void mq_item_v(const DMat& w, int rt, int s, int S, c
     const int tile = RL == 2 ? rt : rt >> 1, rbase = RL == 2 ? 0 : (rt & 1) * 64;
     const int nb = w.nblk;
     const int per_split = (nb + S - 1) / S;
-    const int kb0 = min(nb, s * per_split), kb1 = min(nb, kb0 + per_split);
+    // uniform: readfirstlane as in mv_item_valu
+    const int kb0 = __builtin_amdgcn_readfirstlane(min(nb, s * per_split));
+    const int kb1 = __builtin_amdgcn_readfirstlane(min(nb, kb0 + per_split));
     const int nk = kb1 - kb0, nq = (nk + 3) >> 2;
     const int wave = wave_id(), lane = threadIdx.x & 63;
 
@@ -656,7 +658,7 @@ __device__ __forceinline__ void mq_item_v(const DMat& w, int rt, int s, int S, c
     __builtin_amdgcn_sched_barrier(0);
     const MatViews mv(w);
     QRegs<QB, RL> r;
-    mq_load<QB, RL>(r, w, mv, tile, rbase, kb0, kb1);
+    mq_load<QB, RL>(r, w, mv, tile, rbase, kb0, kb1, wave);
     __builtin_amdgcn_sched_barrier(0);
     pro.template finish<FMT_Q4M>(L, pr, kb0 * 32, nk * 32);
     if (threadIdx.x < 4) L.zero[threadIdx.x] = 0.0f;
@@ -668,7 +670,7 @@ __device__ __forceinline__ void mq_item_v(const DMat& w, int rt, int s, int S, c
     for (int j = 0; j < RL; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
     mq_compute<QB, RL>(r, 0, nq, L, acc);
     for (int q0 = QB; q0 < nq; q0 += QB) {
-        mq_load<QB, RL>(r, w, mv, tile, rbase, kb0 + 4 * q0, kb1);
+        mq_load<QB, RL>(r, w, mv, tile, rbase, kb0 + 4 * q0, kb1, wave);
         mq_compute<QB, RL>(r, q0, nq, L, acc);
     }
     GH_MARK(3);
@@ -828,6 +830,68 @@ __device__ __forceinline__ void mv_item_multi_v(const DMat& w, int it, int s, in
     }
 }
 
+// The same on the matrix cores (mq_item_v's dot products): the lead waves'
+// prologue builds the int8 limbs of the slice once for both items.
+template <int QB, int RL, int V, class Pro, class Epi>
+__device__ __forceinline__ void mq_item_multi_v(const DMat& w, int it, int s, int S, const Pro& pro, const Epi& epi,
+                                                const MvLds& L, float* red) {
+    const int lead = wave_id() < 4, wave = wave_id() & 3, lane = threadIdx.x & 63;
+    const int tile = RL == 2 ? it : it >> 1, rbase = RL == 2 ? 0 : (it & 1) * 64;
+    const bool live = tile < w.tiles;
+    const int nb = w.nblk;
+    const int per_split = (nb + S - 1) / S;
+    // uniform: readfirstlane as in mv_item_valu
+    const int kb0 = __builtin_amdgcn_readfirstlane(min(nb, s * per_split));
+    const int kb1 = __builtin_amdgcn_readfirstlane(min(nb, kb0 + per_split));
+    const int nk = kb1 - kb0;
+    // an item past the last row tile loads nothing and writes nothing
+    const int kl = live ? kb1 : kb0, nq = live ? (nk + 3) >> 2 : 0;
+    typename Pro::Regs pr;
+    if (lead) {
+        if constexpr (HasLoadVariants<Pro>::value) pro.template load_v<V>(pr, kb0 * 32, nk * 32);
+        else pro.load(pr, kb0 * 32, nk * 32);
+    }
+    typename Epi::Regs er;
+    epi.load(er);
+    __builtin_amdgcn_sched_barrier(0);
+    const MatViews mv(w);
+    QRegs<QB, RL> r;
+    mq_load<QB, RL>(r, w, mv, tile, rbase, kb0, kl, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    if (lead) {
+        pro.template finish<FMT_Q4M>(L, pr, kb0 * 32, nk * 32);
+        if (threadIdx.x < 4) L.zero[threadIdx.x] = 0.0f;
+    } else {
+#pragma unroll
+        for (int i = 0; i < Pro::kFinishBarriers; ++i) __syncthreads();
+    }
+    __syncthreads();
+    float acc[RL][4];
+#pragma unroll
+    for (int j = 0; j < RL; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+    mq_compute<QB, RL>(r, 0, nq, L, acc);
+    for (int q0 = QB; q0 < nq; q0 += QB) {
+        mq_load<QB, RL>(r, w, mv, tile, rbase, kb0 + 4 * q0, kl, wave);
+        mq_compute<QB, RL>(r, q0, nq, L, acc);
+    }
+    // sum the 16 columns of each row; lane 16g then holds rows 4g .. 4g+3
+#pragma unroll
+    for (int j = 0; j < RL; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[j][k] = row16_sum(acc[j][k]);
+    if ((lane & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < RL; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) red[16 * (wave * RL + j) + 4 * (lane >> 4) + k] = acc[j][k];
+    }
+    __syncthreads();
+    if (wave == 0 && live) {
+        const float y0 = red[lane], y1 = RL == 2 ? red[64 + lane] : 0.0f;
+        epi.template run<RL>(L, er, it, tile * TILE_ROWS + rbase + lane, s, y0, y1);
+    }
+}
+
 // grid = ceil(items / NI) x S, NI x 256 threads; LDS: k_matvec's carve-up
 // (red_off floats), then the reduction areas of items 1 .. NI-1 (512 floats
 // each)
@@ -839,13 +903,18 @@ __global__ __launch_bounds__(NI * NT) void k_matvec_multi(DMat w, int S, Pro pro
     const int i = wave_id() >> 2;
     float* red = i == 0 ? L.red : lds + red_off + (i - 1) * 512;
     const int it = blockIdx.x / S * NI + i, s = blockIdx.x % S;
+    auto item = [&](auto v) {
+        constexpr int V = decltype(v)::value;
+        if constexpr (FMT == FMT_Q4M) mq_item_multi_v<KBW, RL, V>(w, it, s, S, pro, epi, L, red);
+        else mv_item_multi_v<FMT, KBW, RL, V>(w, it, s, S, pro, epi, L, red);
+    };
     if constexpr (HasLoadVariants<Pro>::value) {
         constexpr int BK = Blk<FMT>::BK;
         const int kb0 = min(w.nblk, s * per_split), nk = min(w.nblk, kb0 + per_split) - kb0;
-        if (i == 0 && pro.variant(kb0 * BK, nk * BK)) mv_item_multi_v<FMT, KBW, RL, 1>(w, it, s, S, pro, epi, L, red);
-        else mv_item_multi_v<FMT, KBW, RL, 0>(w, it, s, S, pro, epi, L, red);
+        if (i == 0 && pro.variant(kb0 * BK, nk * BK)) item(std::integral_constant<int, 1>{});
+        else item(std::integral_constant<int, 0>{});
     } else {
-        mv_item_multi_v<FMT, KBW, RL, 1>(w, it, s, S, pro, epi, L, red);
+        item(std::integral_constant<int, 1>{});
     }
 }
 
@@ -1478,6 +1547,9 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
                 return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
         }
         if constexpr (HasFinishBarriers<Pro>::value) {
+            if (ni == 2 && p.mfma)
+                return p.rl == 2 ? go_multi(k_matvec_multi<FMT_Q4M, KBW, 2, 2, Pro, Epi>)
+                                 : go_multi(k_matvec_multi<FMT_Q4M, KBW, 1, 2, Pro, Epi>);
             if (ni == 2)
                 return p.rl == 2 ? go_multi(k_matvec_multi<FMT_Q4, KBW, 2, 2, Pro, Epi>)
                                  : go_multi(k_matvec_multi<FMT_Q4, KBW, 1, 2, Pro, Epi>);
