@@ -1009,6 +1009,9 @@ __device__ __forceinline__ float4 sum_splits4(const float* part, int S, int ld, 
 }
 
 // A vector already in global memory (2 float4 per thread prefetched).
+// (no kFinishBarriers: the LM head measured slower with paired items, 28 ->
+// 31 us on 1B, its many one-item workgroups already overlapping each
+// other's prologues with streaming)
 struct ProPlain {
     const float* x;
     struct Regs {
@@ -1526,7 +1529,7 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
     // that declare their barriers
     int ni = 1;
     if constexpr (HasFinishBarriers<Pro>::value)
-        if (w.fmt == FMT_Q4 && !(std::is_same_v<Pro, ProPlain> && p.mfma)) ni = p.ni;
+        if (w.fmt == FMT_Q4) ni = p.ni;
     if (ni != 1 && ni != 2) return set_error(GH_ERR_INVALID, "unsupported items per workgroup %d", ni);
     const size_t lds = mv_lds_bytes(w.fmt, per_split, tmp_floats) + (size_t)(ni - 1) * 512 * sizeof(float);
     const dim3 grid((p.row_tiles(w.tiles) + ni - 1) / ni * p.S), block(ni * NT);
@@ -1540,12 +1543,6 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
     };
     auto by_rl = [&](auto kbw) -> int {
         constexpr int KBW = decltype(kbw)::value;
-        // the matrix-core dot products are built for plain input vectors
-        // (the LM head, op-level matvecs); other prologues use the VALU
-        if constexpr (std::is_same_v<Pro, ProPlain>) {
-            if (p.mfma)
-                return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
-        }
         if constexpr (HasFinishBarriers<Pro>::value) {
             if (ni == 2 && p.mfma)
                 return p.rl == 2 ? go_multi(k_matvec_multi<FMT_Q4M, KBW, 2, 2, Pro, Epi>)
@@ -1553,6 +1550,13 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
             if (ni == 2)
                 return p.rl == 2 ? go_multi(k_matvec_multi<FMT_Q4, KBW, 2, 2, Pro, Epi>)
                                  : go_multi(k_matvec_multi<FMT_Q4, KBW, 1, 2, Pro, Epi>);
+        }
+        // one item per workgroup: the matrix-core dot products serve plain
+        // input vectors (the LM head, op-level matvecs); other prologues
+        // use the VALU
+        if constexpr (std::is_same_v<Pro, ProPlain>) {
+            if (p.mfma)
+                return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
         }
         return p.rl == 2 ? go(k_matvec<FMT_Q4, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4, KBW, 1, Pro, Epi>);
     };
