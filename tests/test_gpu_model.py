@@ -545,3 +545,43 @@ def test_persistent_step_matches_graph_step(ctx, monkeypatch, shape):
         lp, _, npers = gh.runGemmaInferenceCached(m, int(t), kp)
         wk, margin = orc.sample_top_k(lp, 2.0, 16, orc.philox_uniform(99, pos))
         assert npers == wk or margin < 1e-4, (pos, npers, wk, margin)
+
+
+@pytest.mark.parametrize("mfma", [0, 1])
+@pytest.mark.parametrize("shape", ["tiny", "gemma3-1b", "mini4b"])
+def test_paired_items_match_single_items(ctx, monkeypatch, shape, mfma):
+    """Every per-layer matvec phase forced to two work items per 8-wave
+    workgroup (GH_PLAN_{A,C,D,E}_NI=2: the qkv kernel's embedding and
+    residual prologues, the attention merge, the residual + norms, the
+    GeGLU; row-tile counts that leave the last workgroup's second item
+    empty included), its dot products on the VALU or (mfma=1: qkv, gate/up
+    and down) the int8 matrix cores, against the default plans on the same
+    weights: every layer's hidden state and the logits within ACT_TOL at
+    every position, and the same argmax where the margin allows."""
+    if shape == "tiny":
+        cfg = gh.preset("tiny")
+    elif shape == "gemma3-1b":
+        cfg = gh.preset("gemma3-1b")
+    else:
+        cfg = gh.preset("gemma3-4b")
+        cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 4, 1024
+        cfg.sliding_window, cfg.global_every = 5, 2
+    cfg.max_seq = 64
+    ref = _gpu_model(ctx, cfg, 1234, True)
+    gh.runGemmaInferenceCached(ref, 0, gh.KVCache(ref, 4), want_logits=False)  # fixes ref's plans
+    for ph in "ACDE":
+        monkeypatch.setenv(f"GH_PLAN_{ph}_NI", "2")
+    for ph in "ADE":
+        monkeypatch.setenv(f"GH_PLAN_{ph}_MFMA", str(mfma))
+    m = _gpu_model(ctx, cfg, 1234, True)
+    prompt = gh.synth_tokens(1, "prompt", 12, cfg.vocab)
+    kr, kp = gh.KVCache(ref, 64), gh.KVCache(m, 64)
+    for pos, t in enumerate(prompt):
+        lr, _, yr, nr = gh.runGemmaInferenceCachedWithLayer0(ref, int(t), kr)
+        lp, _, yp, npair = gh.runGemmaInferenceCachedWithLayer0(m, int(t), kp)
+        for l in range(cfg.n_layers):
+            assert rel_err(yp[l], yr[l]) < ACT_TOL, (pos, l)
+        assert rel_err(lp, lr) < ACT_TOL, pos
+        srt = np.sort(lr)
+        if srt[-1] - srt[-2] > 1e-3 * np.max(np.abs(lr)):
+            assert npair == nr, pos
