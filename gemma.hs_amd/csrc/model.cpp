@@ -190,11 +190,12 @@ void make_plans(gh_model* m) {
     // shapes): o_proj, down and the LM head run fastest as 64-row
     // workgroups (RL 1), down with 8 splits; qkv too up to 31 tiles, as
     // 128-row workgroups with 8 splits from 32 tiles (4B: 6.3 vs 7.0 us);
-    // gate/up as 128-row workgroups with about 384 / tiles splits (1B: 4,
-    // 4B: 2).
+    // gate/up as 128-row work items with about 288 / tiles splits (1B: 3,
+    // 4B: 2, raised to 3 below); with paired items 1B runs 5.38 us at 3
+    // splits against 5.45 at 4 (1560 vs 1556 tok/s).
     m->pa = choose_plan(m->fmt, L.qkv.tiles, L.qkv.nblk, 256);
     m->pc = choose_plan(m->fmt, L.o.tiles, L.o.nblk, 256);
-    m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, std::max(1, (384 + L.gu.tiles / 2) / L.gu.tiles) * L.gu.tiles);
+    m->pd = choose_plan(m->fmt, L.gu.tiles, L.gu.nblk, std::max(1, (288 + L.gu.tiles / 2) / L.gu.tiles) * L.gu.tiles);
     // gate/up: more splits until a wave's share of a split fits one register
     // batch of at most 9 blocks of its two rows per lane; a second batch's
     // loads wait for the first's dot products, and a 10-block batch of two
