@@ -1569,6 +1569,7 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
         case 3: return by_rl(std::integral_constant<int, 3>{});
         case 4: return by_rl(std::integral_constant<int, 4>{});
         case 6: return by_rl(std::integral_constant<int, 6>{});
+        case 7: return by_rl(std::integral_constant<int, 7>{});
         case 9: return by_rl(std::integral_constant<int, 9>{});
         case 10: return by_rl(std::integral_constant<int, 10>{});
         default: return set_error(GH_ERR_INVALID, "unsupported register batch %d", p.kbw);
@@ -3771,6 +3772,7 @@ int enqueue_persistent(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     a.host_tick = &m->p_tick;
     a.set_pos(pos);
     int kbw = kbw_for(FMT_Q4, (m->layers[0].qkv.nblk + 3) / 4);
+    if (kbw == 7) kbw = 9;  // the persistent step is built for 1, 2, 3, 4, 6, 9, 10
     void (*fn)(PArgs) = nullptr;
     auto by_kbw = [&](auto hdc, auto gc) {
         constexpr int HD_ = decltype(hdc)::value, G_ = decltype(gc)::value;

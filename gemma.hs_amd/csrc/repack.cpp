@@ -81,7 +81,7 @@ void repack_f32(const float* src, int64_t rows, int64_t cols, float* dst, int64_
 // split keeps at least 4 column blocks, then the per-wave register batch.
 int kbw_for(int fmt, int per_wave) {
     if (fmt != FMT_Q4) return 8;
-    static const int kQ4[] = {1, 2, 3, 4, 6, 9, 10};
+    static const int kQ4[] = {1, 2, 3, 4, 6, 7, 9, 10};
     for (int k : kQ4)
         if (k >= per_wave) return k;
     return 10;
