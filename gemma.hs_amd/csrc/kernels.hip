@@ -1286,7 +1286,7 @@ struct ProAttnCombine {
 // Down-projection input: h = gelu_tanh(sum_s g_s) * sum_s u_s (MLP.hs:384-447).
 // The gate/up split partials of the slice are loaded in one round trip:
 // gm (1 or 2) float4 groups per thread, register slot i < NS holding split
-// i / gm of group i % gm (the host keeps Sg * gm <= NS; NS is 4 or 8, so
+// i / gm of group i % gm (the host keeps Sg * gm <= NS; NS is 3, 4 or 8, so
 // no load instruction is spent on absent splits beyond the next of those).
 template <int NS>
 struct ProGeglu {
@@ -3878,6 +3878,9 @@ int launch_combine_mv(Sink& k, const char* name, double bytes, const DMat& w, co
 
 int launch_geglu_mv(Sink& k, const char* name, double bytes, const DMat& w, const Plan& p, const float* part_gu,
                     int Sg, int ld_g, int up_off, int gm, const EpiPartial& epi) {
+    // slots = gate/up splits x groups where possible: an absent split's
+    // slot still issues its (out-of-range) loads
+    if (gm * Sg == 3) return launch_mv(k, name, bytes, w, p, ProGeglu<3>{part_gu, Sg, ld_g, up_off, gm}, epi, 0);
     if (gm * Sg <= 4) return launch_mv(k, name, bytes, w, p, ProGeglu<4>{part_gu, Sg, ld_g, up_off, gm}, epi, 0);
     return launch_mv(k, name, bytes, w, p, ProGeglu<MAXS>{part_gu, Sg, ld_g, up_off, gm}, epi, 0);
 }
