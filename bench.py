@@ -34,9 +34,9 @@ PROMPT_SEED = 1
 N_PROMPT = 128
 # HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, then
 # WRITE_SIZE, each scaled by bytes / counter of a 256 MiB device copy):
-# gate/up from profiles/step_kernels_gemma3-1b_decode.md (9,653,142 fetched +
+# gate/up from profiles/step_kernels_gemma3-1b_decode.md (9,644,972 fetched +
 # 170,496 written), the LM head from profiles/lm_head_gemma3-1b_decode.md.
-GATE_UP_TRAFFIC_BYTES = 9_823_638
+GATE_UP_TRAFFIC_BYTES = 9_815_468
 LM_HEAD_TRAFFIC_BYTES = 172_340_835
 # Back-to-back replays per kernel kind in the event-timed pass (a few ms
 # each).  The LM head gets 40 (1.1 ms of streaming): inside the decode loop it
