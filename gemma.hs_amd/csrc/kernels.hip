@@ -19,10 +19,13 @@
 //   4. the four waves' row partials are summed in LDS; the epilogue writes a
 //      split partial (summed by the next kernel's prologue) or the logits
 //      and a per-tile argmax key.
-// Batch-1 decode is HBM-bound (3.5 flop/byte for Q4_0), so the matrix
-// cores are not needed for the flops; where the VALU dequant-dot itself
-// costs time (the LM head, large op-level matvecs) the dot products run on
-// the int8 matrix cores instead (FMT_Q4M, mq_item_v).
+// Where a phase has more work items than the device has CUs, two items of
+// one column split share an 8-wave workgroup and its prologue
+// (k_matvec_multi).  Batch-1 decode is HBM-bound (3.5 flop/byte for Q4_0),
+// so the matrix cores are not needed for the flops; where the VALU
+// dequant-dot itself costs time (the LM head, large op-level matvecs,
+// paired items with wide column splits) the dot products run on the int8
+// matrix cores instead (FMT_Q4M, mq_item_v, mq_item_multi_v).
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
