@@ -135,6 +135,7 @@ struct gh_ctx {
     std::vector<gh_model*> models;
     std::vector<gh_q4*> q4s;
     bool released = false;
+    bool dying = false;  // chosen for freeing (by the one thread that saw it collectable)
 };
 
 struct gh_q4 {

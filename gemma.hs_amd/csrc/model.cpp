@@ -23,8 +23,17 @@ using Lock = std::lock_guard<std::recursive_mutex>;
 // touches no memory.  A context or model whose destroy is called while
 // handles created from it are still open is only released: it stays alive
 // (stream, device memory) until the last of them is destroyed, so handles
-// may be destroyed in any order, as finalisers run them.  The registry
-// mutex is taken alone or before a context mutex, never after one.
+// may be destroyed in any order, as finalisers run them.
+//
+// Locking.  The registry mutex is a leaf: it is held only for one map
+// operation (handle_add / handle_live / handle_take) and nothing else is
+// locked or waited for while it is held.  Everything else about a handle --
+// its parent's lists of children, the released flags, device memory -- is
+// guarded by its context's mutex (gh_ctx::mu), and the decision to free a
+// released context or model is taken under that mutex together with the
+// state change that makes it collectable, so exactly one thread frees it.
+// A finaliser destroying one handle while another thread steps on the same
+// context therefore waits for the step and cannot deadlock with it.
 // ---------------------------------------------------------------------
 enum HandleKind { HK_CTX = 1, HK_MODEL, HK_KV, HK_Q4 };
 std::mutex& handles_mu() {
@@ -43,6 +52,14 @@ bool handle_live(const void* h, int kind) {
     std::lock_guard<std::mutex> g(handles_mu());
     auto it = handles().find(h);
     return it != handles().end() && it->second == kind;
+}
+// Unregisters an open handle of `kind`; false if it is not one.
+bool handle_take(const void* h, int kind) {
+    std::lock_guard<std::mutex> g(handles_mu());
+    auto it = handles().find(h);
+    if (it == handles().end() || it->second != kind) return false;
+    handles().erase(it);
+    return true;
 }
 const char* kind_name(int kind) {
     return kind == HK_CTX ? "context" : kind == HK_MODEL ? "model" : kind == HK_KV ? "KV cache" : "Q4_0 tensor";
@@ -367,9 +384,12 @@ int prefill_reserve(gh_model* m, int n) {
     return GH_OK;
 }
 
+int model_check(const gh_model* m);
+
+// Called with the context mutex held, on a handle the caller checked open.
 int model_ready(gh_model* m) {
     if (!m) return set_error(GH_ERR_INVALID, "null model");
-    GH_CHECK(gh_model_check(m));
+    GH_CHECK(model_check(m));
     GH_CHECK(ensure_scratch(m));
     if (m->persistent && !m->p_gi_ok) {  // the persistent step's gate/up layout, from the uploaded weights
         for (int l = 0; l < m->cfg.n_layers; ++l)
@@ -478,61 +498,58 @@ extern "C" int gh_ctx_create(int device, gh_ctx** out) {
     return GH_OK;
 }
 
-// Lifetime helpers (registry mutex held by the caller).
+// Lifetime helpers.  ctx_dead and model_collect_locked run with the
+// context mutex held; ctx_free runs after it is released.
 namespace {
 
-// Frees a released context that has no open model or Q4_0 tensor left.
-void ctx_collect(gh_ctx* ctx) {
-    {
-        Lock lk(ctx->mu);
-        if (!ctx->released || !ctx->models.empty() || !ctx->q4s.empty()) return;
-        hipSetDevice(ctx->device);
-        hipStreamSynchronize(ctx->stream);
-        for (void* p : ctx->bufs) hipFree(p);
-        if (ctx->scratch) hipFree(ctx->scratch);
-        if (ctx->t0) hipEventDestroy(ctx->t0);
-        if (ctx->t1) hipEventDestroy(ctx->t1);
-        hipStreamDestroy(ctx->stream);
-    }
+// True when a released context has no open model or Q4_0 tensor left; the
+// caller that sees this (once: `dying` is set) frees it with ctx_free.
+bool ctx_dead(gh_ctx* ctx) {
+    if (ctx->dying || !ctx->released || !ctx->models.empty() || !ctx->q4s.empty()) return false;
+    ctx->dying = true;
+    return true;
+}
+
+// Frees a context that ctx_dead selected.  No other thread holds a handle
+// made from it, so nothing else can be waiting on its mutex.
+void ctx_free(gh_ctx* ctx) {
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    for (void* p : ctx->bufs) hipFree(p);
+    if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->t0) hipEventDestroy(ctx->t0);
+    if (ctx->t1) hipEventDestroy(ctx->t1);
+    hipStreamDestroy(ctx->stream);
     delete ctx;
 }
 
-// Frees a released model that has no open KV cache left, then its context
-// if that was released too.
-void model_collect(gh_model* m) {
+// Frees a released model that has no open KV cache left (context mutex
+// held); returns whether its context is now to be freed.
+bool model_collect_locked(gh_model* m) {
     gh_ctx* ctx = m->ctx;
-    {
-        Lock lk(ctx->mu);
-        if (!m->released || !m->kvs.empty()) return;
-        hipSetDevice(ctx->device);
-        hipStreamSynchronize(ctx->stream);
-        free_prefill(m);
-        for (auto& b : m->owned) hipFree(b.p);
-        auto& v = ctx->models;
-        v.erase(std::remove(v.begin(), v.end(), m), v.end());
-        delete m;
-    }
-    ctx_collect(ctx);
-}
-
-bool handle_take(const void* h, int kind) {
-    auto it = handles().find(h);
-    if (it == handles().end() || it->second != kind) return false;
-    handles().erase(it);
-    return true;
+    if (!m->released || !m->kvs.empty()) return false;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    free_prefill(m);
+    for (auto& b : m->owned) hipFree(b.p);
+    auto& v = ctx->models;
+    v.erase(std::remove(v.begin(), v.end(), m), v.end());
+    delete m;
+    return ctx_dead(ctx);
 }
 
 }  // namespace
 
 extern "C" int gh_ctx_destroy(gh_ctx* ctx) {
     if (!ctx) return GH_OK;
-    std::lock_guard<std::mutex> g(handles_mu());
     if (!handle_take(ctx, HK_CTX)) return dead_handle("gh_ctx_destroy", HK_CTX);
+    bool dead = false;
     {
         Lock lk(ctx->mu);
         ctx->released = true;
+        dead = ctx_dead(ctx);
     }
-    ctx_collect(ctx);
+    if (dead) ctx_free(ctx);
     return GH_OK;
 }
 
@@ -689,9 +706,9 @@ gh_q4::~gh_q4() {
 
 extern "C" int gh_q4_0_free(gh_q4* t) {
     if (!t) return GH_OK;
-    std::lock_guard<std::mutex> g(handles_mu());
     if (!handle_take(t, HK_Q4)) return dead_handle("gh_q4_0_free", HK_Q4);
     gh_ctx* ctx = t->ctx;
+    bool dead = false;
     {
         Lock lk(ctx->mu);
         hipSetDevice(ctx->device);
@@ -699,8 +716,9 @@ extern "C" int gh_q4_0_free(gh_q4* t) {
         auto& v = ctx->q4s;
         v.erase(std::remove(v.begin(), v.end(), t), v.end());
         delete t;
+        dead = ctx_dead(ctx);
     }
-    ctx_collect(ctx);
+    if (dead) ctx_free(ctx);
     return GH_OK;
 }
 
@@ -861,6 +879,8 @@ extern "C" int gh_gelu_mul(gh_ctx* ctx, const float* g, const float* u, int n, f
     return GH_OK;
 }
 
+static int argmax_locked(gh_ctx* ctx, const float* v, int n, int32_t* idx);
+
 extern "C" int gh_sample_logits(gh_ctx* ctx, const float* logits, int n, float temperature, uint64_t seed,
                                 uint64_t counter, int32_t* token_out) {
     return gh_sample_logits_top_k(ctx, logits, n, temperature, 0, seed, counter, token_out);
@@ -874,7 +894,7 @@ extern "C" int gh_sample_logits_top_k(gh_ctx* ctx, const float* logits, int n, f
         return set_error(GH_ERR_INVALID, "temperature must be finite and >= 0");
     if (top_k < 0 || top_k > GH_TOP_K_MAX)
         return set_error(GH_ERR_RANGE, "top_k %d outside [0, %d]", top_k, GH_TOP_K_MAX);
-    if (temperature == 0.0f) return gh_argmax(ctx, logits, n, token_out);
+    if (temperature == 0.0f) return argmax_locked(ctx, logits, n, token_out);
     const int nblk = (n + 63) / 64;
     void* scratch = nullptr;
     GH_CHECK(ctx_scratch(ctx, sizeof(float) * (2 * (size_t)nblk + 4), &scratch));
@@ -890,6 +910,11 @@ extern "C" int gh_sample_logits_top_k(gh_ctx* ctx, const float* logits, int n, f
 
 extern "C" int gh_argmax(gh_ctx* ctx, const float* v, int n, int32_t* idx) {
     OP_ENTER(ctx);
+    return argmax_locked(ctx, v, n, idx);
+}
+
+// gh_argmax on a bound context whose mutex the caller holds.
+static int argmax_locked(gh_ctx* ctx, const float* v, int n, int32_t* idx) {
     if (!v || !idx || n <= 0) return set_error(GH_ERR_INVALID, "gh_argmax: bad arguments");
     unsigned long long* key = nullptr;  // [0] result, [1..1024] per-block keys
     GH_HIP(hipMallocAsync((void**)&key, 8 * 1025, ctx->stream));
@@ -973,13 +998,15 @@ extern "C" int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out
 
 extern "C" int gh_model_destroy(gh_model* m) {
     if (!m) return GH_OK;
-    std::lock_guard<std::mutex> g(handles_mu());
     if (!handle_take(m, HK_MODEL)) return dead_handle("gh_model_destroy", HK_MODEL);
+    gh_ctx* ctx = m->ctx;
+    bool dead = false;
     {
-        Lock lk(m->ctx->mu);
+        Lock lk(ctx->mu);
         m->released = true;
+        dead = model_collect_locked(m);
     }
-    model_collect(m);
+    if (dead) ctx_free(ctx);
     return GH_OK;
 }
 
@@ -1091,7 +1118,13 @@ extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, con
 
 extern "C" int gh_model_check(gh_model* m) {
     GH_LIVE(m, HK_MODEL);
-    if (!m) return set_error(GH_ERR_INVALID, "null model");
+    GH_CHECK(dev_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    return model_check(m);
+}
+
+namespace {
+int model_check(const gh_model* m) {
     if (!m->has_embd) return set_error(GH_ERR_NOT_FOUND, "missing tensor token_embd.weight");
     if (!m->has_out_norm) return set_error(GH_ERR_NOT_FOUND, "missing tensor output_norm.weight");
     const uint32_t need = required_mask(m->cfg);
@@ -1106,6 +1139,7 @@ extern "C" int gh_model_check(gh_model* m) {
     }
     return GH_OK;
 }
+}  // namespace
 
 extern "C" int gh_model_config(gh_model* m, gh_config* out) {
     GH_LIVE(m, HK_MODEL);
@@ -1167,17 +1201,19 @@ gh_kv::~gh_kv() {
 
 extern "C" int gh_kv_destroy(gh_kv* kv) {
     if (!kv) return GH_OK;
-    std::lock_guard<std::mutex> g(handles_mu());
     if (!handle_take(kv, HK_KV)) return dead_handle("gh_kv_destroy", HK_KV);
     gh_model* m = kv->m;
+    gh_ctx* ctx = m->ctx;
+    bool dead = false;
     {
-        Lock lk(m->ctx->mu);
-        hipSetDevice(m->ctx->device);
-        hipStreamSynchronize(m->ctx->stream);
+        Lock lk(ctx->mu);
+        hipSetDevice(ctx->device);
+        hipStreamSynchronize(ctx->stream);
         m->kvs.erase(std::remove(m->kvs.begin(), m->kvs.end(), kv), m->kvs.end());
         delete kv;
+        dead = model_collect_locked(m);
     }
-    model_collect(m);
+    if (dead) ctx_free(ctx);
     return GH_OK;
 }
 
@@ -1186,22 +1222,27 @@ extern "C" void gh_model_release(gh_model* m) { (void)gh_model_destroy(m); }
 extern "C" void gh_kv_release(gh_kv* kv) { (void)gh_kv_destroy(kv); }
 extern "C" void gh_q4_0_release(gh_q4* t) { (void)gh_q4_0_free(t); }
 
+// The cache's host fields are read and written under its context's mutex,
+// so these calls are ordered with a step, generation or prefill running on
+// the same cache from another thread.
 extern "C" int gh_kv_reset(gh_kv* kv) {
     GH_LIVE(kv, HK_KV);
-    if (!kv) return set_error(GH_ERR_INVALID, "null kv");
+    Lock lk(kv->m->ctx->mu);
     kv->len = 0;
     return GH_OK;
 }
 
 extern "C" int gh_kv_length(gh_kv* kv, int32_t* len) {
     GH_LIVE(kv, HK_KV);
-    if (!kv || !len) return set_error(GH_ERR_INVALID, "null argument");
+    if (!len) return set_error(GH_ERR_INVALID, "null argument");
+    Lock lk(kv->m->ctx->mu);
     *len = kv->len;
     return GH_OK;
 }
 
 extern "C" int gh_kv_truncate(gh_kv* kv, int32_t n) {
     GH_LIVE(kv, HK_KV);
+    Lock lk(kv->m->ctx->mu);
     if (n < 0 || n > kv->len) return set_error(GH_ERR_RANGE, "gh_kv_truncate: %d outside [0, %d]", n, kv->len);
     kv->len = n;
     return GH_OK;
@@ -1209,9 +1250,9 @@ extern "C" int gh_kv_truncate(gh_kv* kv, int32_t n) {
 
 extern "C" int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed) {
     GH_LIVE(kv, HK_KV);
-    if (!kv) return set_error(GH_ERR_INVALID, "null kv");
     if (!(temperature >= 0.0f) || std::isinf(temperature))
         return set_error(GH_ERR_INVALID, "temperature must be finite and >= 0");
+    Lock lk(kv->m->ctx->mu);
     kv->inv_temp = temperature > 0.0f ? 1.0f / temperature : 0.0f;
     kv->seed = seed;
     return GH_OK;
@@ -1219,9 +1260,9 @@ extern "C" int gh_kv_set_sampling(gh_kv* kv, float temperature, uint64_t seed) {
 
 extern "C" int gh_kv_set_top_k(gh_kv* kv, int32_t top_k) {
     GH_LIVE(kv, HK_KV);
-    if (!kv) return set_error(GH_ERR_INVALID, "null kv");
     if (top_k < 0 || top_k > GH_TOP_K_MAX)
         return set_error(GH_ERR_RANGE, "top_k %d outside [0, %d]", top_k, GH_TOP_K_MAX);
+    Lock lk(kv->m->ctx->mu);
     kv->top_k = top_k;
     return GH_OK;
 }

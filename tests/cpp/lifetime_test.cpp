@@ -11,8 +11,17 @@
 //   lifetime_test exit     only the order in which Python finalisers ran at
 //                          interpreter exit when a model outlived its
 //                          context (context first, then model, then cache)
+//   lifetime_test race     one thread steps (and takes a greedy sample)
+//                          while another creates and destroys caches, Q4_0
+//                          tensors and models on the same context, as a
+//                          garbage collector's finaliser thread does; a
+//                          watchdog fails the run if the two deadlock
+#include <atomic>
+#include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "gemma_hip.h"
@@ -108,9 +117,72 @@ int any_order() {
     return 0;
 }
 
+// Concurrent use and destruction on one context (finalisers run on their
+// own thread under a -threaded RTS, gemma.cabal:102).
+int race() {
+    Handles h;
+    if (make(h)) return 1;
+    void* buf = nullptr;
+    CHECK(gh_buf_alloc(h.ctx, 1024 * sizeof(float), &buf) == GH_OK);
+    std::atomic<bool> done{false};
+    std::atomic<int> failed{0};
+    std::thread watchdog([&] {
+        for (int i = 0; i < 600 && !done.load(); ++i) std::this_thread::sleep_for(std::chrono::milliseconds(100));
+        if (!done.load()) {
+            std::fprintf(stderr, "DEADLOCK: stepping and destroying threads did not finish in 60 s\n");
+            std::fflush(stderr);
+            std::_Exit(3);
+        }
+    });
+    const int iters = 300;
+    std::thread stepper([&] {
+        for (int i = 0; i < iters; ++i) {
+            int32_t next = -1, tok = -1, len = -1;
+            if (gh_kv_truncate(h.kv, 0) != GH_OK) failed = 1;
+            if (gh_step(h.m, h.kv, (i * 7) % 1024, nullptr, nullptr, &next) != GH_OK) failed = 2;
+            if (gh_sample_logits(h.ctx, (const float*)buf, 1024, 0.0f, 1, 0, &tok) != GH_OK) failed = 3;
+            if (gh_kv_length(h.kv, &len) != GH_OK || len != 1) failed = 4;
+        }
+    });
+    std::thread finaliser([&] {
+        gh_config c;
+        if (gh_config_preset("tiny", &c) != GH_OK) failed = 10;
+        std::vector<uint8_t> raw(64 * 18, 0);
+        for (int i = 0; i < iters; ++i) {
+            gh_kv* kv2 = nullptr;
+            if (gh_kv_create(h.m, 8, &kv2) != GH_OK) failed = 11;
+            gh_q4* t2 = nullptr;
+            if (gh_q4_0_upload(h.ctx, raw.data(), 64, 32, 0, &t2) != GH_OK) failed = 12;
+            gh_kv_release(kv2);
+            gh_q4_0_release(t2);
+            if (i % 30 == 0) {
+                gh_model* m2 = nullptr;
+                if (gh_model_create(h.ctx, &c, &m2) != GH_OK) failed = 13;
+                gh_kv* kv3 = nullptr;
+                if (gh_kv_create(m2, 4, &kv3) != GH_OK) failed = 14;
+                gh_model_release(m2);  // released first: freed with its cache
+                gh_kv_release(kv3);
+            }
+        }
+    });
+    stepper.join();
+    finaliser.join();
+    done = true;
+    watchdog.join();
+    CHECK(failed.load() == 0);
+    CHECK(gh_buf_free(h.ctx, buf) == GH_OK);
+    for (char w : {'t', 'c', 'k', 'm'}) CHECK(destroy(h, w) == GH_OK);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
+    if (argc > 1 && std::strcmp(argv[1], "race") == 0) {
+        if (race()) return 1;
+        std::printf("race ok\n");
+        return 0;
+    }
     if (argc > 1 && std::strcmp(argv[1], "exit") == 0) {
         Handles h;
         if (make(h)) return 1;
