@@ -9,11 +9,14 @@ one token per step (untimed, as in the reference's generation loop), then W
 warmup steps, then exactly K timed greedy steps (HIP events on the step
 stream, device-synchronised on both sides).
 
-Prints ONE JSON line with tok/s; per-kernel-kind durations (HIP events
-around back-to-back replays of that kernel kind at the last decoded
-position, on the step stream); the roofline of gate/up, the per-layer
-kernel with the largest share of the step (the LM head, the largest single
-matvec, beside it); and the CPU baseline (bounded samples on the host cores).
+Prints ONE JSON line with tok/s; per-kernel-kind execution times measured
+inside real decode steps at C3's positions 128..383 (gh_profile_steps: the
+step's kernels launched eagerly in order, each timed by its own dispatch's
+begin and end timestamps, the quantity a rocprofv3 kernel trace reports;
+every layer's weights are cold there, as in the decode loop); the roofline
+of gate/up, the per-layer kernel with the largest share of the step (the LM
+head, the largest single matvec, beside it); the kernel plan in use
+(gh_model_plan); and the CPU baseline (bounded samples on the host cores).
 """
 from __future__ import annotations
 
@@ -33,18 +36,14 @@ WEIGHT_SEED = 1234
 PROMPT_SEED = 1
 N_PROMPT = 128
 # HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, then
-# WRITE_SIZE, each scaled by bytes / counter of a 256 MiB device copy):
-# gate/up from profiles/step_kernels_gemma3-1b_decode.md (9,644,972 fetched +
-# 170,496 written), the LM head from profiles/lm_head_gemma3-1b_decode.md.
+# WRITE_SIZE, each scaled by bytes / counter of a 256 MiB device copy) over
+# eager decode steps at positions 224..287 (kernel_profile run --decode 64):
+# profiles/step_kernels_gemma3-1b_decode_c3.md.
 GATE_UP_TRAFFIC_BYTES = 9_815_468
 LM_HEAD_TRAFFIC_BYTES = 172_340_835
-# Back-to-back replays per kernel kind in the event-timed pass (a few ms
-# each).  The LM head gets 40 (1.1 ms of streaming): inside the decode loop it
-# runs once per ~700 us of latency-bound kernels, and a longer back-to-back
-# run slows it down (traced: 26.8 us for the first 10 of 200 launches, 33.6 us
-# for the last 50, 28.7 us for the decode loop's own LM heads).
-KERNEL_REPS = {"qkv": 40, "attention": 40, "o_proj": 40, "gate_up": 40, "down": 40, "final_norm": 400,
-               "lm_head": 40}
+TRAFFIC_PROFILE = "profiles/step_kernels_gemma3-1b_decode_c3.md"
+# the in-step kernel timings: C3's decode positions 128..383
+PROFILE_STEPS = 256
 
 
 def log(msg: str) -> None:
@@ -167,7 +166,10 @@ def extras_c4_attention(gh, ctx) -> dict:
     """C4: one decode query (4 q heads, 1 kv head, head_dim 256) over a
     K/V cache of 8192 or 32768 N(0, 1) positions, global (whole cache) and
     local (last 512), scale 1/16: gh_attention_decode (split-K attention
-    plus its merge kernel), 20 calls captured into a graph and replayed."""
+    plus its merge kernel).  The cache exists in enough copies to hold
+    >= 512 MiB (32 of the 8192-position cache, 8 of the 32768 one), one call
+    per copy is captured into a graph and the graph replayed, so no call
+    finds its K/V in the 256 MB Infinity Cache."""
     import numpy as np
     out = {}
     rng = np.random.default_rng(4)
@@ -175,26 +177,38 @@ def extras_c4_attention(gh, ctx) -> dict:
     q = gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=nq * hd).astype(np.float32))
     o = gh.DeviceBuffer(ctx, 4 * nq * hd)
     for L in (8192, 32768):
-        k = gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
-        v = gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
+        cache_bytes = 2 * L * nkv * hd * 4
+        copies = max(4, -(-(512 << 20) // cache_bytes))
+        kv = [(gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32)),
+               gh.DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32)))
+              for _ in range(copies)]
         for kind, pb in (("global", 0), ("local", L - 512)):
-            n = 20
-            call = lambda: gh._lib.check(gh.lib().gh_attention_decode(ctx.h, q.ptr, k.ptr, v.ptr, nq, nkv, hd,
-                                                                      pb, L, 0, o.ptr))
-            call()
+            def call(k, v):
+                gh._lib.check(gh.lib().gh_attention_decode(ctx.h, q.ptr, k.ptr, v.ptr, nq, nkv, hd, pb, L, 0, o.ptr))
+            call(*kv[0])
             ctx.capture_begin()
-            for _ in range(n):
-                call()
-            us = ctx.capture_replay(5) * 1e3 / n
+            for k, v in kv:
+                call(k, v)
+            reps = max(2, 64 // copies)
+            us = ctx.capture_replay(reps) * 1e3 / copies
             algo = 2 * (L - pb) * nkv * hd * 4 + 8 * nq * hd
             out[f"L{L}_{kind}"] = {"avg_us": round(us, 3), "bytes": algo, "gbps": round(algo / us / 1e3, 1),
-                                   "frac": round(algo / us / 1e3 / HBM_PEAK_GBPS, 4)}
-            log(f"  C4 L={L} {kind}: {us:.2f} us, {algo / us / 1e3:.0f} GB/s")
-        k.free()
-        v.free()
+                                   "frac": round(algo / us / 1e3 / HBM_PEAK_GBPS, 4), "copies": copies}
+            log(f"  C4 L={L} {kind}: {us:.2f} us, {algo / us / 1e3:.0f} GB/s ({copies} copies)")
+        for k, v in kv:
+            k.free()
+            v.free()
     q.free()
     o.free()
     return out
+
+
+def in_step_kernels(gh, model, kv, n_steps: int) -> dict:
+    """Execution time of every step kernel kind inside n_steps real greedy
+    decode steps from the cache's position (gh_profile_steps: eager launches
+    in the step's order, each timed by its own dispatch timestamps)."""
+    stats = gh.profile_steps(model, kv, n_steps)
+    return {st.name: st for st in stats}
 
 
 def extras_c5_gemma3_4b(gh, ctx, steps: int = 64, warmup: int = 8) -> dict:
@@ -212,15 +226,18 @@ def extras_c5_gemma3_4b(gh, ctx, steps: int = 64, warmup: int = 8) -> dict:
     prompt = gh.synth_tokens(PROMPT_SEED, "c5", 1, cfg.vocab)
     ms, _ = gh.bench_decode(model, kv, prompt, warmup, steps)
     tok_s = steps / (ms / 1e3)
-    timings = {name: gh.time_kernel(model, kv, name, 10) for name in gh.STEP_KERNELS}
-    step_bytes = sum(t.bytes_per_launch * t.launches_per_step for t in timings.values())
+    n_prof = 8
+    timings = in_step_kernels(gh, model, kv, n_prof)
+    step_bytes = sum(t.bytes_per_launch * t.launches for t in timings.values()) / n_prof
     log(f"  C5 gemma3-4b @ {n0}: {tok_s:.1f} tok/s")
     out = {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4), "steps": steps,
            "start_position": n0 + 1 + warmup, "step_algorithmic_bytes": int(step_bytes),
            "step_frac_of_hbm_peak": round(step_bytes / (ms / steps * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
            "lm_head_gbps": round(timings["lm_head"].gbps, 1),
-           "kernels": {t.name: {"avg_us": round(t.avg_us, 3), "gbps": round(t.gbps, 1), "per_step": t.launches_per_step,
-                                "step_us": round(t.avg_us * t.launches_per_step, 1)} for t in timings.values()}}
+           "kernels_in_step": {t.name: {"avg_us": round(t.avg_us, 3), "gbps": round(t.gbps, 1),
+                                        "per_step": t.launches // n_prof,
+                                        "step_us": round(t.avg_us * t.launches / n_prof, 1)}
+                               for t in timings.values()}}
     del kv, model
     return out
 
@@ -306,20 +323,29 @@ def main(argv=None) -> int:
     tok_s = a.steps / (ms / 1e3)
     log(f"decode: {a.steps} steps in {ms:.3f} ms -> {tok_s:.1f} tok/s")
 
-    # per-kernel HIP-event timing at the last decoded position: each kernel
-    # kind replayed back to back on the step stream (state unchanged)
-    timings = {name: gh.time_kernel(model, kv, name, KERNEL_REPS[name]) for name in gh.STEP_KERNELS}
+    # kernel execution times inside real decode steps at C3's positions
+    # 128..383: a second cache fed the prompt, then PROFILE_STEPS eager greedy
+    # steps, each kernel timed by its own dispatch timestamps
+    kv_p = gh.KVCache(model, N_PROMPT + PROFILE_STEPS + 8)
+    gh.generate(model, kv_p, prompt, 1)
+    pos0 = len(kv_p)
+    timings = in_step_kernels(gh, model, kv_p, PROFILE_STEPS)
+    del kv_p
     for t in timings.values():
-        log(f"  {t.name:10s} x{t.launches_per_step:3d}/step avg {t.avg_us:8.2f} us  {t.gbps:8.1f} GB/s")
-    step_bytes = sum(t.bytes_per_launch * t.launches_per_step for t in timings.values())
+        log(f"  {t.name:10s} x{t.launches // PROFILE_STEPS:3d}/step avg {t.avg_us:8.2f} us  {t.gbps:8.1f} GB/s")
+    step_bytes = sum(t.bytes_per_launch * t.launches for t in timings.values()) / PROFILE_STEPS
+    kernel_us = sum(t.total_ms for t in timings.values()) * 1e3 / PROFILE_STEPS
     # roofline kernel: gate/up (26 launches per token, the largest share of
     # the step); algorithmic bytes per launch = the fused [gate | up] Q4_0
     # weights (2 x 6912 x 1152 / 32 x 18 B) + the input and the output rows
     gu, lm = timings["gate_up"], timings["lm_head"]
     roofline = {"bound": "hbm", "achieved": round(gu.gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(gu.gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
-                "traffic_source": "rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated)", "kernel": "gate_up",
-                "bytes_per_launch": int(gu.bytes_per_launch), "avg_us": round(gu.avg_us, 3),
+                "traffic_source": f"rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated) over eager decode "
+                                  f"steps at positions 224..287: {TRAFFIC_PROFILE}",
+                "kernel": "gate_up", "bytes_per_launch": int(gu.bytes_per_launch), "avg_us": round(gu.avg_us, 3),
+                "timing": f"dispatch begin/end timestamps of every gate/up launch in {PROFILE_STEPS} real decode "
+                          f"steps at positions {pos0}..{pos0 + PROFILE_STEPS - 1} ({gu.launches} launches)",
                 "lm_head": {"achieved": round(lm.gbps, 1), "frac": round(lm.gbps / HBM_PEAK_GBPS, 4),
                             "traffic": LM_HEAD_TRAFFIC_BYTES, "bytes_per_launch": int(lm.bytes_per_launch),
                             "avg_us": round(lm.avg_us, 3)}}
@@ -339,11 +365,16 @@ def main(argv=None) -> int:
                    "global_batch": 1, "parallelism": "single-gpu",
                    "step_algorithmic_bytes": int(step_bytes),
                    "step_frac_of_hbm_peak": round(step_bytes / (ms / a.steps * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
+        "plan": model.plan(),
         "roofline": roofline,
         "kernels": {t.name: {"avg_us": round(t.avg_us, 3), "gbps": round(t.gbps, 1),
-                             "frac": round(t.gbps / HBM_PEAK_GBPS, 4), "per_step": t.launches_per_step,
-                             "step_us": round(t.avg_us * t.launches_per_step, 1)}
+                             "frac": round(t.gbps / HBM_PEAK_GBPS, 4), "per_step": t.launches // PROFILE_STEPS,
+                             "step_us": round(t.total_ms * 1e3 / PROFILE_STEPS, 1)}
                     for t in timings.values()},
+        "kernels_note": f"dispatch begin-to-end intervals inside eager decode steps at positions {pos0}.."
+                        f"{pos0 + PROFILE_STEPS - 1}; each includes that kernel's launch by the command processor, "
+                        f"so their sum, {kernel_us:.1f} us per step, compares with the {1e3 * ms / a.steps:.1f} us "
+                        f"of a timed graph step",
     }
     if not a.no_extras:
         out["extras"] = {"c2_matvec_rotating_2GiB": extras_c2_matvec(gh, ctx),

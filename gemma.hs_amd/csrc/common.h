@@ -205,7 +205,8 @@ struct gh_model {
     int fmt = -1;  // projection format, fixed by the first projection upload
     std::vector<gh::LayerDev> layers;
     std::vector<gh::DevBuf> owned;
-    gh::DMat embd;  // token_embd (tied LM head)
+    gh::DMat embd;  // token_embd (also the LM head when no output.weight is set: tied)
+    gh::DMat lm;    // output.weight, an untied LM head (valid when has_lm)
     float* out_norm = nullptr;
     std::vector<float> inv_freq;  // [2][head_dim/2]: local, global (host)
     // rows of the fused QKV matrix: [q (nq*hd) | k | v], each padded to 128
@@ -213,6 +214,7 @@ struct gh_model {
     int f_pad = 0;  // padded ffn rows (gate block, then up block)
     // plans
     gh::Plan pa, pc, pd, pe, plm;
+    std::string plan_env;  // the GH_* switches set when the plans were made
     int attn_nc = 16;  // attention chunks per kv head
     // scratch
     float* x_res = nullptr;
@@ -229,7 +231,7 @@ struct gh_model {
     float* lm_m = nullptr;                   // per-workgroup max logit (sampling)
     float* lm_s = nullptr;                   // per-workgroup sum of exp((l - max) / T) (sampling)
     // presence tracking
-    bool has_embd = false, has_out_norm = false;
+    bool has_embd = false, has_out_norm = false, has_lm = false;
     std::vector<uint32_t> present;  // per layer bitmask of tensor kinds
     std::vector<gh_kv*> kvs;  // open caches; a released model is freed when the last goes
     bool released = false;    // gh_model_destroy was called
@@ -274,6 +276,10 @@ struct gh_kv {
 };
 
 namespace gh {
+
+// The LM head matrix: output.weight when the model has one, else the tied
+// token embedding (src/Gemma/Model.hs:412-414).
+inline const DMat& lm_mat(const gh_model* m) { return m->has_lm ? m->lm : m->embd; }
 
 // Per-kernel event timing used by gh_profile_steps.
 struct Profiler {

@@ -4,8 +4,9 @@
 // aligned data section).  Differences from the reference, on purpose:
 //  - vocab comes from the token_embd.weight shape (the reference reads the
 //    tokenizer array it skipped while parsing and so always gets 256000);
-//  - the Q4_0 projections and the tied LM head reach the device (the
-//    reference uploads zero placeholders and leaves the LM head undefined).
+//  - the Q4_0 projections and the LM head reach the device (the reference
+//    uploads zero placeholders); the LM head is output.weight when the file
+//    has one (src/Gemma/Model.hs:988), else the tied token_embd.weight.
 // Q4_1 tensors are dequantised to f32 on load, as the reference's getTensor
 // does for the embedding and the norms (src/Gemma/GGUF.hs:649-656,762-795).
 #include <fcntl.h>
@@ -278,8 +279,11 @@ int parse_gguf(const char* path, int32_t max_seq, Parsed& P) {
     if ((int64_t)te->second.dims[0] != c.hidden)
         return set_error(GH_ERR_FORMAT, "token_embd.weight width %llu != embedding_length %d",
                          (unsigned long long)te->second.dims[0], c.hidden);
-    if (P.tens.count("output.weight"))
-        return set_error(GH_ERR_FORMAT, "untied output.weight is not supported (Gemma 3 ties the LM head)");
+    auto ow = P.tens.find("output.weight");
+    if (ow != P.tens.end() && (ow->second.dims.size() != 2 || (int64_t)ow->second.dims[0] != c.hidden ||
+                               (int64_t)ow->second.dims[1] != c.vocab))
+        return set_error(GH_ERR_FORMAT, "output.weight is not %d x %d, the shape of token_embd.weight", c.vocab,
+                         c.hidden);
     return GH_OK;
 }
 

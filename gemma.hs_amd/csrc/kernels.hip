@@ -26,6 +26,7 @@
 // dequant-dot itself costs time (the LM head, large op-level matvecs,
 // paired items with wide column splits) the dot products run on the int8
 // matrix cores instead (FMT_Q4M, mq_item_v, mq_item_multi_v).
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -1464,25 +1465,28 @@ struct NodeArgs : NodeArgsBase {
 };
 
 namespace {
-struct ProfScope {
-    Profiler* p;
-    hipStream_t s;
-    int idx = -1;
-    ProfScope(Profiler* p_, hipStream_t s_, const char* name, double bytes) : p(p_), s(s_) {
-        if (!p) return;
-        Profiler::Rec r;
-        r.kind = p->kind_of(name);
-        r.bytes = bytes;
-        (void)hipEventCreate(&r.a);
-        (void)hipEventCreate(&r.b);
-        (void)hipEventRecord(r.a, s);
-        p->recs.push_back(r);
-        idx = (int)p->recs.size() - 1;
+// Eager launch of fn; with a profiler, the launch carries a start and a stop
+// event that hipExtLaunchKernel fills from the dispatch's own begin and end
+// timestamps, so the recorded duration is the kernel's execution (what a
+// kernel trace reports), without the queue gaps around it.
+static int profiled_launch(Profiler* p, hipStream_t s, const char* name, double bytes, const void* fn, dim3 grid,
+                           dim3 block, void** args, size_t lds) {
+    if (!p) {
+        GH_HIP(hipLaunchKernel(fn, grid, block, args, lds, s));
+        return GH_OK;
     }
-    ~ProfScope() {
-        if (p && idx >= 0) (void)hipEventRecord(p->recs[idx].b, s);
+    Profiler::Rec r;
+    r.kind = p->kind_of(name);
+    r.bytes = bytes;
+    GH_HIP(hipEventCreate(&r.a));
+    if (hipEventCreate(&r.b) != hipSuccess) {
+        (void)hipEventDestroy(r.a);
+        return set_error(GH_ERR_HIP, "hipEventCreate failed");
     }
-};
+    p->recs.push_back(r);
+    GH_HIP(hipExtLaunchKernel(fn, grid, block, args, lds, s, r.a, r.b, 0));
+    return GH_OK;
+}
 
 // Setter of the position-dependent argument I: an int, or a struct with
 // set_pos(int) that also recomputes what derives from the position.
@@ -1519,9 +1523,7 @@ static int sink_launch(Sink& k, const char* name, double bytes, void (*fn)(P...)
         k.store->push_back(std::move(blob));
         return GH_OK;
     }
-    ProfScope ps(k.prof, k.s, name, bytes);
-    GH_HIP(hipLaunchKernel((const void*)fn, grid, block, blob->ptrs.data(), lds, k.s));
-    return GH_OK;
+    return profiled_launch(k.prof, k.s, name, bytes, (const void*)fn, grid, block, blob->ptrs.data(), lds);
 }
 
 template <int POS_ARG = -1, class Pro, class Epi>
@@ -3909,17 +3911,19 @@ namespace {
 }
 }  // namespace
 
-// LM head (tied embedding) on m->xn_final with per-workgroup argmax keys
-// and softmax statistics, then the next-token selection of position pos.
+// LM head (output.weight, or the tied embedding) on m->xn_final with
+// per-workgroup argmax keys and softmax statistics, then the next-token
+// selection of position pos.
 [[maybe_unused]] static int enqueue_head(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
     const gh_config& c = m->cfg;
+    const DMat& W = lm_mat(m);
     {
         ProPlain pro{m->xn_final};
         EpiLogits epi{m->logits, c.vocab, m->lm_cand, kv->st, m->lm_m, m->lm_s};
-        GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(m->embd), m->embd, m->plm, pro, epi, 0));
+        GH_CHECK(launch_mv(sink, "lm_head", mat_bytes(W), W, m->plm, pro, epi, 0));
     }
     return sink_launch<1>(sink, "finish", 0.0, k_step_finish<0>, dim3(1), dim3(NT), 0, kv->st, pos,
-                          (const unsigned long long*)m->lm_cand, m->plm.row_tiles(m->embd.tiles), (const float*)m->lm_m,
+                          (const unsigned long long*)m->lm_cand, m->plm.row_tiles(W.tiles), (const float*)m->lm_m,
                           (const float*)m->lm_s, 64 * m->plm.rl, (const float*)m->logits, c.vocab,
                           (const int32_t*)kv->d_prompt, kv->d_ids);
 }

@@ -200,8 +200,25 @@ int env_int(const char* name, int def) {
     return v && *v ? std::atoi(v) : def;
 }
 
+// The GH_* environment switches that can change what the library runs, as
+// "NAME=value,..." for those set ("" if none).
+std::string env_switches() {
+    static const char* vars[] = {
+        "GH_PLAN_A_S", "GH_PLAN_C_S", "GH_PLAN_D_S", "GH_PLAN_E_S", "GH_PLAN_A_RL", "GH_PLAN_C_RL", "GH_PLAN_D_RL",
+        "GH_PLAN_E_RL", "GH_PLAN_LM_RL", "GH_PLAN_A_NI", "GH_PLAN_C_NI", "GH_PLAN_D_NI", "GH_PLAN_E_NI",
+        "GH_PLAN_A_MFMA", "GH_PLAN_D_MFMA", "GH_PLAN_E_MFMA", "GH_PLAN_LM_MFMA", "GH_ATTN_NC", "GH_ATTN_HSPLIT",
+        "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA"};
+    std::string env;
+    for (const char* v : vars) {
+        const char* val = std::getenv(v);
+        if (val && *val) env += (env.empty() ? "" : ",") + std::string(v) + "=" + val;
+    }
+    return env;
+}
+
 // Work-split plans, overridable for tuning sweeps with GH_PLAN_{A,C,D,E}_S.
 void make_plans(gh_model* m) {
+    m->plan_env = env_switches();
     const LayerDev& L = m->layers[0];
     // Measured on MI355X (sweeps of S x RL on the gemma3-1b and gemma3-4b
     // shapes): o_proj, down and the LM head run fastest as 64-row
@@ -219,7 +236,7 @@ void make_plans(gh_model* m) {
     // rows spills (4B: 2 -> 3 splits, gate/up 14.3 -> 11.9 us, 651 -> 690 tok/s)
     while (m->fmt == FMT_Q4 && m->pd.S < 8 && ((L.gu.nblk + m->pd.S - 1) / m->pd.S + 3) / 4 > 9) ++m->pd.S;
     m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 8 * L.down.tiles);
-    m->plm = choose_plan(m->embd.fmt, m->embd.tiles, m->embd.nblk, 1);
+    m->plm = choose_plan(lm_mat(m).fmt, lm_mat(m).tiles, lm_mat(m).nblk, 1);
     m->pc.rl = m->pe.rl = m->plm.rl = 1;
     m->pa.rl = L.qkv.tiles >= 32 ? 2 : 1;
     auto over = [&](Plan& p, const char* env, const DMat& d) {
@@ -1051,6 +1068,18 @@ extern "C" int gh_model_set_tensor(gh_model* m, const char* name, int dtype, con
         m->has_embd = true;
         return GH_OK;
     }
+    if (!std::strcmp(name, "output.weight")) {
+        // untied LM head (src/Gemma/Model.hs:412-414 lm_head.weight; GGUF
+        // output.weight, src/Gemma/Model.hs:988), in its own format; the
+        // step's plans and graphs are built from it at the first step
+        if (m->x_res) return set_error(GH_ERR_STATE, "output.weight must be set before the model's first step");
+        const int want = dtype == GH_DTYPE_Q4_0 ? FMT_Q4 : FMT_F32;
+        if (!m->lm.codes) GH_CHECK(alloc_mat(m, m->lm, want, c.vocab, c.hidden));
+        else if (m->lm.fmt != want) return set_error(GH_ERR_INVALID, "output.weight was uploaded in another format");
+        GH_CHECK(upload_rows(m->ctx, m->lm, 0, dtype, data, nbytes, c.vocab, c.hidden, ftz));
+        m->has_lm = true;
+        return GH_OK;
+    }
     if (!std::strcmp(name, "output_norm.weight")) {
         GH_CHECK(vec_to_f32(dtype, data, nbytes, c.hidden, ftz, v));
         if (!m->out_norm) GH_CHECK(dev_alloc(m, &m->out_norm, c.hidden));
@@ -1140,6 +1169,37 @@ int model_check(const gh_model* m) {
     return GH_OK;
 }
 }  // namespace
+
+extern "C" int gh_model_plan(gh_model* m, char* buf, size_t cap, size_t* len_out) {
+    GH_LIVE(m, HK_MODEL);
+    if (!buf && cap) return set_error(GH_ERR_INVALID, "null buffer with a non-zero capacity");
+    GH_CHECK(dev_bind(m->ctx));
+    Lock lk(m->ctx->mu);
+    GH_CHECK(model_check(m));
+    if (!m->x_res) make_plans(m);  // what ensure_scratch will choose at the first step
+    const bool persistent = m->x_res ? m->persistent != 0 : env_int("GH_PERSISTENT", 0) && persistent_supported(m);
+    std::string s = std::string("step=") + (persistent ? "persistent" : env_int("GH_NO_GRAPH", 0) ? "eager" : "graph");
+    auto phase = [&](const char* name, const Plan& p) {
+        char t[96];
+        std::snprintf(t, sizeof t, " %s=S%d,rl%d,ni%d,%s", name, p.S, p.rl, p.ni, p.mfma ? "mfma" : "valu");
+        s += t;
+    };
+    phase("qkv", m->pa);
+    phase("o_proj", m->pc);
+    phase("gate_up", m->pd);
+    phase("down", m->pe);
+    phase("lm_head", m->plm);
+    s += " attn_chunks=" + std::to_string(m->attn_nc);
+    s += std::string(" lm=") + (m->has_lm ? "untied" : "tied");
+    s += " env=" + (m->plan_env.empty() ? std::string("none") : m->plan_env);
+    if (len_out) *len_out = s.size();
+    if (cap) {
+        const size_t n = std::min(cap - 1, s.size());
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return GH_OK;
+}
 
 extern "C" int gh_model_config(gh_model* m, gh_config* out) {
     GH_LIVE(m, HK_MODEL);

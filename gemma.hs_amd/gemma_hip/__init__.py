@@ -327,9 +327,21 @@ def center_q4_0(raw: np.ndarray) -> np.ndarray:
     return b.reshape(-1)
 
 
-def tensor_list(cfg: GemmaConfig):
+def flat_scales_q4_0(raw: np.ndarray, d: float) -> np.ndarray:
+    """Raw Q4_0 blocks with every block's fp16 scale set to d (rounded to
+    fp16).  With |N(0, s)| scales a row's norm varies by about 12 % over 36
+    blocks, so among 262144 LM-head rows one stands ~50 % above the rest and
+    wins the greedy argmax from most states; equal scales leave no such
+    row."""
+    b = np.ascontiguousarray(raw, np.uint8).reshape(-1, 18).copy()
+    b[:, :2] = np.array([d], np.float16).view(np.uint8)
+    return b.reshape(-1)
+
+
+def tensor_list(cfg: GemmaConfig, untied: bool = False):
     """(name, kind, shape) of every tensor a config needs; kind 'mat' or 'vec'.
-    GGUF names; the same order gh_synth_model uses."""
+    GGUF names; the same order gh_synth_model uses.  untied: with an
+    output.weight LM head (last), which gh_synth_model does not make."""
     H, hd, F = cfg.hidden, cfg.head_dim, cfg.ffn
     out = [("token_embd.weight", "mat", (cfg.vocab, H)), ("output_norm.weight", "vec", (H,))]
     for l in range(cfg.n_layers):
@@ -349,18 +361,25 @@ def tensor_list(cfg: GemmaConfig):
             (p + "ffn_down.weight", "mat", (H, F)),
             (p + "post_ffw_norm.weight", "vec", (H,)),
         ]
+    if untied:
+        out.append(("output.weight", "mat", (cfg.vocab, H)))
     return out
 
 
 def synth_tensors(cfg: GemmaConfig, seed: int, q4: bool, w_sigma: float = 0.02,
-                  scale_sigma: float = 0.01, norm_sigma: float = 0.02, centered: bool = False):
+                  scale_sigma: float = 0.01, norm_sigma: float = 0.02, centered: bool = False,
+                  untied: bool = False):
     """Yield (name, dtype, array) with exactly the bytes gh_synth_model uploads
-    (centered: Q4_0 codes through center_q4_0)."""
-    for name, kind, shape in tensor_list(cfg):
+    (centered: Q4_0 codes through center_q4_0; untied: plus an output.weight
+    LM head from the same seed, whose Q4_0 blocks all have the scale
+    scale_sigma: flat_scales_q4_0)."""
+    for name, kind, shape in tensor_list(cfg, untied):
         if kind == "vec":
             yield name, DTYPE_F32, synth_f32(seed, name, norm_sigma, shape[0])
         elif q4:
             raw = synth_q4_0(seed, name, scale_sigma, shape[0], shape[1])
+            if name == "output.weight":
+                raw = flat_scales_q4_0(raw, scale_sigma)
             yield name, DTYPE_Q4_0, center_q4_0(raw) if centered else raw
         else:
             yield name, DTYPE_F32, synth_f32(seed, name, w_sigma, shape[0] * shape[1])
@@ -396,15 +415,26 @@ class GemmaModel:
         check(lib().gh_model_set_tensor(self.h, name.encode(), dtype, _ptr(a), a.nbytes))
 
     def synth(self, seed: int, q4: bool, w_sigma: float = 0.02, scale_sigma: float = 0.01,
-              norm_sigma: float = 0.02, centered: bool = False) -> None:
-        if centered:
-            for name, dtype, arr in synth_tensors(self.cfg, seed, q4, w_sigma, scale_sigma, norm_sigma, True):
+              norm_sigma: float = 0.02, centered: bool = False, untied: bool = False) -> None:
+        """The tensors of synth_tensors with the same arguments (gh_synth_model
+        for the plain case)."""
+        if centered or untied:
+            for name, dtype, arr in synth_tensors(self.cfg, seed, q4, w_sigma, scale_sigma, norm_sigma,
+                                                  centered, untied):
                 self.set_tensor(name, arr, dtype)
             return
         check(lib().gh_synth_model(self.h, seed, int(q4), w_sigma, scale_sigma, norm_sigma))
 
     def check(self) -> None:
         check(lib().gh_model_check(self.h))
+
+    def plan(self) -> str:
+        """gh_model_plan: the step's kernel plan and the GH_* switches set."""
+        n = C.c_size_t(0)
+        check(lib().gh_model_plan(self.h, None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value + 1)
+        check(lib().gh_model_plan(self.h, buf, n.value + 1, None))
+        return buf.value.decode()
 
     def close(self) -> None:
         if self.h:

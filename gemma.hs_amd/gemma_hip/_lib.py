@@ -94,6 +94,7 @@ SIGNATURES = {
     "gh_model_set_tensor": (C.c_int, [_P, C.c_char_p, C.c_int, _P, C.c_size_t]),
     "gh_model_check": (C.c_int, [_P]),
     "gh_model_config": (C.c_int, [_P, C.POINTER(GhConfig)]),
+    "gh_model_plan": (C.c_int, [_P, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     "gh_model_load_gguf": (C.c_int, [_P, C.c_char_p, C.c_int32, C.POINTER(_P)]),
     "gh_gguf_inspect": (C.c_int, [C.c_char_p, C.POINTER(GhConfig)]),
     "gh_kv_create": (C.c_int, [_P, C.c_int32, C.POINTER(_P)]),

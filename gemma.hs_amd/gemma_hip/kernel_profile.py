@@ -3,9 +3,11 @@
 Driver (run under rocprofv3 on the GPU box, eagerly: GH_NO_GRAPH=1):
 
   python -m gemma_hip.kernel_profile run [--kernel all|KIND] [--config gemma3-1b] [--reps 20]
-                                         [--kv-synth N] [--copy-mib 256] [--manifest FILE]
+                                         [--prompt 8] [--prefill-prompt] [--kv-synth N] [--copy-mib 256]
+                                         [--manifest FILE]
   python -m gemma_hip.kernel_profile run --prefill 128 [--reps 5] [--copy-mib 256]
-  python -m gemma_hip.kernel_profile run --attention 32768 [--reps 20] [--copy-mib 256]
+  python -m gemma_hip.kernel_profile run --attention 32768 [--reps 20] [--copy-mib 256] [--copies 8]
+  python -m gemma_hip.kernel_profile run --decode 64 [--prompt 128] [--start 224] [--copy-mib 256]
   python -m gemma_hip.kernel_profile exchange [--wgs 8 64 128 256] [--rounds 2000]
 
 It builds the seeded model of the config and decodes a short prompt.  Then,
@@ -17,8 +19,15 @@ device-to-device copy of `copy-mib` MiB: the calibration kernel for the
 byte counters, which reads and writes exactly that many bytes.  With
 --prefill N it instead runs `reps` prefills of a seeded N-token prompt;
 with --attention L, `reps` op-level attention decodes (4 q heads, 1 kv head,
-head_dim 256, global over L positions: the C4 case).  The manifest (JSON)
-lists the segments in order.  `exchange` needs no profiler: it prints the
+head_dim 256, global over L positions: the C4 case), rotating over `copies`
+K/V caches so that replays do not hit the 256 MB Infinity Cache.  With
+--decode N the kernels are measured where they run: a seeded `prompt`-token
+prompt and greedy steps up to position `start` (graph replays), then N
+greedy decode steps launched eagerly in the step's order (gh_profile_steps,
+the measurement bench.py's roofline comes from); the summariser assigns
+each dispatch its kernel kind by its place in the step's launch sequence,
+which the manifest records.  The manifest (JSON) lists the segments in
+order.  `exchange` needs no profiler: it prints the
 cost of one all-to-all word exchange among n co-resident workgroups
 (gh_time_exchange, the persistent step's synchronisation).
 
@@ -45,7 +54,7 @@ from collections import defaultdict
 from pathlib import Path
 
 from . import (GemmaModel, KVCache, Context, DeviceBuffer, STEP_KERNELS, bench_decode, prefill, preset,
-               stream_read_gbps, synth_tokens, time_kernel)
+               profile_steps, stream_read_gbps, synth_tokens, time_kernel)
 from ._lib import check, lib
 
 HIP_MEMCPY_D2D = 3
@@ -84,6 +93,7 @@ def run(a) -> int:
     cfg = preset(a.config)
     ctx = Context(0)
     segments = []
+    replay_pos = None
 
     def separator():
         stream_read_gbps(ctx, 4096, 1)
@@ -92,15 +102,19 @@ def run(a) -> int:
         import numpy as np
         L, hd, nq, nkv = a.attention, 256, 4, 1
         rng = np.random.default_rng(4)
-        # inputs uploaded once; each rep is one gh_attention_decode on device
-        # pointers (the attention kernel and its merge, nothing else)
+        # inputs uploaded once, the K/V cache in `copies` copies; each rep is
+        # one gh_attention_decode on device pointers (the attention kernel
+        # and its merge, nothing else) over the next copy
         q = DeviceBuffer.from_numpy(ctx, rng.normal(size=nq * hd).astype(np.float32))
-        k = DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
-        v = DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32))
+        kvs = [(DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32)),
+                DeviceBuffer.from_numpy(ctx, rng.normal(size=L * nkv * hd).astype(np.float32)))
+               for _ in range(max(1, a.copies))]
         o = DeviceBuffer(ctx, 4 * nq * hd)
+        k, v = kvs[0]
         check(lib().gh_attention_decode(ctx.h, q.ptr, k.ptr, v.ptr, nq, nkv, hd, 0, L, 0, o.ptr))  # scratch
         separator()
-        for _ in range(a.reps):
+        for i in range(a.reps):
+            k, v = kvs[i % len(kvs)]
             check(lib().gh_attention_decode(ctx.h, q.ptr, k.ptr, v.ptr, nq, nkv, hd, 0, L, 0, o.ptr))
         # one unit = the attention kernel + its merge (two dispatches)
         segments.append({"name": f"attention_c4_L{L}", "reps": a.reps, "dispatches_per_unit": 2,
@@ -116,11 +130,32 @@ def run(a) -> int:
                 kv.reset()
                 prefill(model, kv, toks, want_logits=False)
             segments.append({"name": f"prefill_{a.prefill}", "reps": a.reps})
+        elif a.decode > 0:
+            start = max(a.start, a.prompt)
+            kv = KVCache(model, start + a.decode + 8)
+            bench_decode(model, kv, synth_tokens(1, "prompt", a.prompt, cfg.vocab), start - a.prompt, 1)
+            pos0 = len(kv)
+            separator()
+            stats = profile_steps(model, kv, a.decode)
+            seq = [k for _ in range(cfg.n_layers) for k in ("qkv", "attention", "o_proj", "gate_up", "down")]
+            seq += ["final_norm", "lm_head", "finish"]
+            launches = {st.name: st.launches for st in stats}
+            assert sum(launches.values()) == len(seq) * a.decode, (launches, len(seq))
+            segments.append({"name": "decode", "steps": a.decode, "positions": [pos0, pos0 + a.decode - 1],
+                             "sequence": seq,
+                             "kinds": {st.name: {"bytes_per_launch": int(st.bytes_per_launch),
+                                                 "event_avg_us": round(st.avg_us, 3)} for st in stats}})
         else:
             kv = KVCache(model, a.kv_synth + a.prompt + 8)
             if a.kv_synth > 0:  # the C5 start: a prefilled cache of that many positions
                 kv.synth(5, a.kv_synth)
-            bench_decode(model, kv, synth_tokens(1, "prompt", a.prompt, cfg.vocab), 0, 1)
+            toks = synth_tokens(1, "prompt", a.prompt, cfg.vocab)
+            if a.prefill_prompt:  # one batched pass (a few hundred dispatches), then one step
+                prefill(model, kv, toks[:-1], want_logits=False)
+                bench_decode(model, kv, toks[-1:], 0, 1)
+            else:
+                bench_decode(model, kv, toks, 0, 1)
+            replay_pos = len(kv)
             kinds = STEP_KERNELS if a.kernel == "all" else (a.kernel,)
             for kind in kinds:
                 separator()
@@ -129,7 +164,8 @@ def run(a) -> int:
                                  "bytes_per_launch": int(t.bytes_per_launch), "event_avg_us": round(t.avg_us, 3)})
     separator()
     device_copy(a.copy_mib << 20)
-    man = {"config": a.config, "position": a.kv_synth + a.prompt if a.prefill == 0 and a.attention == 0 else None,
+    man = {"config": a.config,
+           "position": replay_pos if a.prefill == 0 and a.attention == 0 and a.decode == 0 else None,
            "copy_bytes": a.copy_mib << 20, "segments": segments}
     if a.manifest:
         Path(a.manifest).write_text(json.dumps(man, indent=1))
@@ -178,20 +214,47 @@ def _segments(disp, n_seg):
     return segs, cal
 
 
+def _units(man, segs, disp):
+    """(row name, dispatch ids, algorithmic bytes per unit, dispatches per
+    unit, event avg us) of every summarised row: one per segment, or one per
+    kernel kind of a decode segment, whose dispatches take their kind from
+    their place in the recorded step sequence (the runtime's copy kernels of
+    the step state, __amd_rocclr_*, left out)."""
+    out = []
+    for k, s in enumerate(man["segments"]):
+        seg = segs[k] if k < len(segs) else []
+        if "sequence" in s:
+            seg = [i for i in seg if not disp[i][0].startswith("__amd_rocclr")]
+            seq = s["sequence"]
+            if len(seg) != len(seq) * s["steps"]:
+                raise SystemExit(f"decode segment: {len(seg)} dispatches, expected {len(seq)} x {s['steps']}")
+            for kind in dict.fromkeys(seq):
+                ids = [seg[i] for i in range(len(seg)) if seq[i % len(seq)] == kind]
+                info = s["kinds"].get(kind, {})
+                out.append((kind, ids, info.get("bytes_per_launch"), 1, info.get("event_avg_us")))
+        else:
+            out.append((s["name"], seg, s.get("bytes_per_launch"), s.get("dispatches_per_unit", 1),
+                        s.get("event_avg_us")))
+    return out
+
+
 def summarize(a) -> int:
     man = json.loads(Path(a.manifest).read_text())
     n = len(man["segments"])
     rows = defaultdict(dict)
     factors = {}
+    names = []
     for label, d in (("fetch", a.fetch), ("write", a.write), ("sq", a.sq), ("trace", a.trace)):
         if not d:
             continue
         disp = _dispatches(Path(d))
         segs, cal = _segments(disp, n)
-        for k, seg in enumerate(segs):
+        units = _units(man, segs, disp)
+        names = [(u[0], u[2], u[3], u[4]) for u in units]
+        for name, seg, _, _, _ in units:
             if not seg:
                 continue
-            r = rows[man["segments"][k]["name"]]
+            r = rows[name]
             ctr_sum = defaultdict(float)
             for i in seg:
                 for c, v in disp[i][1].items():
@@ -211,43 +274,41 @@ def summarize(a) -> int:
     print()
     print("| segment | dispatches | algorithmic B / launch | FETCH B / launch | WRITE B / launch | traffic / algorithmic |")
     print("|---|---|---|---|---|---|")
-    for s in man["segments"]:
-        r = rows.get(s["name"], {})
-        per = s.get("dispatches_per_unit", 1)  # counters are per dispatch; bytes_per_launch per unit
-        algo = s.get("bytes_per_launch")
+    for name, algo, per, _ in names:
+        r = rows.get(name, {})
         fb = r["FETCH_SIZE"] * factors["FETCH_SIZE"] * per if "FETCH_SIZE" in r and "FETCH_SIZE" in factors else None
         wb = r["WRITE_SIZE"] * factors["WRITE_SIZE"] * per if "WRITE_SIZE" in r and "WRITE_SIZE" in factors else None
         ratio = (fb + wb) / algo if fb is not None and wb is not None and algo else None
         f = lambda x: f"{x:,.0f}" if x is not None else "-"
-        print(f"| {s['name']} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | "
-              f"{ratio:.3f} |" if ratio is not None else
-              f"| {s['name']} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | - |")
+        print(f"| {name} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | "
+              + (f"{ratio:.3f} |" if ratio is not None else "- |"))
     sq = [c for c in ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_INSTS_VMEM_RD",
                       "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_ACTIVE_INST_VALU") if any(c in r for r in rows.values())]
     if sq:
         print()
         print("| segment | " + " | ".join(sq) + " | wait / wave cycles | VALU / wave | VMEM rd / wave |")
         print("|---|" + "---|" * (len(sq) + 3))
-        for s in man["segments"]:
-            r = rows.get(s["name"], {})
+        for name, _, _, _ in names:
+            r = rows.get(name, {})
             waves = r.get("SQ_WAVES") or 1.0
             cells = [f"{r.get(c, 0):,.0f}" for c in sq]
             wait = r.get("SQ_WAIT_INST_ANY", 0) / max(r.get("SQ_WAVE_CYCLES", 0), 1)
-            print(f"| {s['name']} | " + " | ".join(cells) +
+            print(f"| {name} | " + " | ".join(cells) +
                   f" | {wait:.3f} | {r.get('SQ_INSTS_VALU', 0) / waves:.1f} | {r.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} |")
     if any("trace_avg_us" in r for r in rows.values()):
         print()
-        print("| segment | kernels | traced avg us / unit | algorithmic GB/s | of 8 TB/s |")
-        print("|---|---|---|---|---|")
-        for s in man["segments"]:
-            r = rows.get(s["name"], {})
+        print("| segment | kernels | traced avg us / unit | algorithmic GB/s | of 8 TB/s | dispatch-event avg us "
+              "(same run) |")
+        print("|---|---|---|---|---|---|")
+        for name, algo, per, ev in names:
+            r = rows.get(name, {})
             if "trace_avg_us" not in r:
                 continue
-            us = r["trace_avg_us"] * s.get("dispatches_per_unit", 1)
-            algo = s.get("bytes_per_launch")
+            us = r["trace_avg_us"] * per
             gbps = algo / (us * 1e3) if algo else None
-            print(f"| {s['name']} | {', '.join(r['kernels'])} | {us:.3f} | "
-                  + (f"{gbps:.0f} | {gbps / 8000:.3f} |" if gbps else "- | - |"))
+            print(f"| {name} | {', '.join(r['kernels'])} | {us:.3f} | "
+                  + (f"{gbps:.0f} | {gbps / 8000:.3f} |" if gbps else "- | - |")
+                  + (f" {ev:.3f} |" if ev is not None else " - |"))
     return 0
 
 
@@ -280,6 +341,12 @@ def main(argv=None) -> int:
     r.add_argument("--kv-synth", type=int, default=0, help="fill the cache with this many positions first")
     r.add_argument("--prefill", type=int, default=0, help="time N-token prefills instead of step kernels")
     r.add_argument("--attention", type=int, default=0, help="op-level C4 attention over L positions")
+    r.add_argument("--copies", type=int, default=1, help="K/V cache copies the attention reps rotate over")
+    r.add_argument("--decode", type=int, default=0, help="profile N eager decode steps in the step's order")
+    r.add_argument("--prefill-prompt", action="store_true",
+                   help="feed all but the last prompt token by batched prefill (kernel replays at a late position "
+                        "with few dispatches before them)")
+    r.add_argument("--start", type=int, default=0, help="--decode: first profiled position (after the prompt)")
     r.add_argument("--manifest", default="")
     x = sub.add_parser("exchange")
     x.add_argument("--wgs", type=int, nargs="+", default=[8, 64, 128, 256])

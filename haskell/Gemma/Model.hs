@@ -1,3 +1,4 @@
+{-# LANGUAGE OverloadedStrings #-}
 {-# LANGUAGE RecordWildCards #-}
 {-# LANGUAGE ScopedTypeVariables #-}
 
@@ -11,9 +12,10 @@ and the inference calls replaced: the weights, the KV cache and every
 kernel of the step live in libgemma_hip (Graphics.HIP) instead of Dawn
 tensors and WGSL shaders.
 
-Unchanged, and imported from their own module: the config record and its
-presets (src/Gemma/Model.hs:106-237) and configFromGGUF
-(src/Gemma/Model.hs:843-902), which are plain host code with no Dawn type.
+Kept here, as in the reference, with no Dawn type in them: the config
+record and its presets (src/Gemma/Model.hs:106-237) and configFromGGUF
+(src/Gemma/Model.hs:843-902), which reads the file's metadata through the
+reference's own Gemma.GGUF.
 
 As in the reference, the device K/V belong to the model (one sequence per
 model), and a KVCache value carries the lengths: its layer-0 cacheLen is
@@ -56,11 +58,103 @@ import Foreign.Ptr (Ptr, castPtr, nullPtr)
 import Foreign.Storable (peek, sizeOf)
 
 import Gemma.KVCache (KVCache(..), LayerKVCache(..), cacheLength, initKVCache)
-import Gemma.Model.Config (GemmaConfig(..), configFromGGUF, gemma1BConfig, gemma2_2BConfig, gemma3_1BConfig,
-                           tinyGemmaConfig)
+import qualified Gemma.GGUF as GGUF
 import Gemma.SafeTensors (getTensor, hasTensor, loadSafeTensors)
 import qualified Graphics.HIP as HIP
 import Graphics.HIP (check)
+
+-- | Hyper-parameters and feature flags (src/Gemma/Model.hs:106-129): the
+-- reference's record, field for field, so callers that build or pattern
+-- match a config compile unchanged.  gcUseFP16 / gcUseVec4 / gcUseFusion
+-- selected WGSL shader variants and have no effect here (the HIP step
+-- computes in f32 on Q4_0 or f32 weights); gcLocalRopeScaling,
+-- gcGlobalRopeScaling and gcQueryHeadDimNormalize are carried as the
+-- reference carries them (its step reads none of them).
+data GemmaConfig = GemmaConfig
+  { gcVocabSize :: Int
+  , gcHiddenDim :: Int
+  , gcNumLayers :: Int
+  , gcNumHeads :: Int
+  , gcNumKVHeads :: Int
+  , gcHeadDim :: Int
+  , gcFFNDim :: Int
+  , gcRopeBase :: Float
+  , gcUseFP16 :: Bool
+  , gcUseVec4 :: Bool
+  , gcUseFusion :: Bool
+  , gcUseQKNorm :: Bool
+  , gcUsePostAttnNorm :: Bool
+  , gcUsePostFFNNorm :: Bool
+  , gcUseSlidingWindow :: Bool
+  , gcSlidingWindowSize :: Int
+  , gcLocalRopeScaling :: Float
+  , gcGlobalRopeScaling :: Float
+  , gcQueryHeadDimNormalize :: Bool
+  , gcUseZeroCenteredRMSNorm :: Bool
+  } deriving (Show, Eq)
+
+-- | The Gemma 1 / 2 layout: none of the Gemma 3 features, one RoPE base.
+plainConfig :: Int -> Int -> Int -> Int -> Int -> Int -> Int -> GemmaConfig
+plainConfig vocab hidden layers heads kvHeads headDim ffn = GemmaConfig
+  { gcVocabSize = vocab, gcHiddenDim = hidden, gcNumLayers = layers, gcNumHeads = heads
+  , gcNumKVHeads = kvHeads, gcHeadDim = headDim, gcFFNDim = ffn, gcRopeBase = 10000.0
+  , gcUseFP16 = False, gcUseVec4 = False, gcUseFusion = False
+  , gcUseQKNorm = False, gcUsePostAttnNorm = False, gcUsePostFFNNorm = False
+  , gcUseSlidingWindow = False, gcSlidingWindowSize = 0
+  , gcLocalRopeScaling = 1.0, gcGlobalRopeScaling = 1.0
+  , gcQueryHeadDimNormalize = False, gcUseZeroCenteredRMSNorm = False
+  }
+
+-- | Gemma 1B (src/Gemma/Model.hs:131-156).
+gemma1BConfig :: GemmaConfig
+gemma1BConfig = plainConfig 256000 2048 24 16 8 128 5504
+
+-- | Gemma 2 2B (src/Gemma/Model.hs:158-183).
+gemma2_2BConfig :: GemmaConfig
+gemma2_2BConfig = plainConfig 256000 2304 26 8 4 256 9216
+
+-- | The reference's tiny synthetic test model (src/Gemma/Model.hs:185-210).
+tinyGemmaConfig :: GemmaConfig
+tinyGemmaConfig = plainConfig 1000 128 2 4 2 32 384
+
+-- | Gemma 3 1B (src/Gemma/Model.hs:212-237): QK-norm, post-norms, a 512
+-- window, zero-centred RMSNorm weights, RoPE base 1e6.
+gemma3_1BConfig :: GemmaConfig
+gemma3_1BConfig = (plainConfig 262144 1152 26 4 1 256 6912)
+  { gcRopeBase = 1000000.0
+  , gcUseQKNorm = True, gcUsePostAttnNorm = True, gcUsePostFFNNorm = True
+  , gcUseSlidingWindow = True, gcSlidingWindowSize = 512
+  , gcQueryHeadDimNormalize = True, gcUseZeroCenteredRMSNorm = True
+  }
+
+-- | configFromGGUF (src/Gemma/Model.hs:843-902): the gemma3.* metadata of a
+-- parsed GGUF file with the Gemma 3 feature flags on.  The vocabulary is the
+-- row count of token_embd.weight when the file has that tensor (what
+-- gh_model_load_gguf uses, so this config and the loaded model agree), else
+-- the length of tokenizer.ggml.tokens, else 256000; the window defaults to
+-- 512.  A missing required key is an error, as in the reference.
+configFromGGUF :: GGUF.GGUFFile -> GemmaConfig
+configFromGGUF gf = gemma3_1BConfig
+  { gcVocabSize = vocab
+  , gcHiddenDim = int "gemma3.embedding_length"
+  , gcNumLayers = int "gemma3.block_count"
+  , gcNumHeads = int "gemma3.attention.head_count"
+  , gcNumKVHeads = int "gemma3.attention.head_count_kv"
+  , gcHeadDim = int "gemma3.attention.key_length"
+  , gcFFNDim = int "gemma3.feed_forward_length"
+  , gcRopeBase = req "gemma3.rope.freq_base" (GGUF.getMetadataFloat gf "gemma3.rope.freq_base")
+  , gcSlidingWindowSize = maybe 512 fromIntegral (GGUF.getMetadataInt gf "gemma3.attention.sliding_window")
+  }
+  where
+    req key = fromMaybe (error ("Missing or invalid metadata: " ++ T.unpack key))
+    int key = fromIntegral (req key (GGUF.getMetadataInt gf key))
+    vocab
+      | GGUF.hasTensor gf "token_embd.weight" = case GGUF.getTensorShape gf "token_embd.weight" of
+          [_, rows] -> fromIntegral rows
+          _ -> error "token_embd.weight is not a matrix"
+      | otherwise = case GGUF.getMetadata gf "tokenizer.ggml.tokens" of
+          Just (GGUF.MetaArray toks) -> length toks
+          _ -> 256000
 
 -- | The model: config plus library handles.  (The reference's record holds
 -- Dawn Context / Tensor / KernelCode fields, src/Gemma/Model.hs:243-257.)
@@ -128,6 +222,9 @@ loadGemmaModel path cfg@GemmaConfig{..} = do
                                         (fromIntegral (V.length v * sizeOf (0 :: Float))))
   put "token_embd.weight" "model.embed_tokens.weight"
   put "output_norm.weight" "model.norm.weight"
+  -- an untied LM head when the checkpoint has one; else the library uses
+  -- the embedding (src/Gemma/Model.hs:412-414)
+  put "output.weight" "lm_head.weight"
   forM_ [0 .. gcNumLayers - 1] $ \l -> do
     let g s = "blk." ++ show l ++ "." ++ s ++ ".weight"
         h s = "model.layers." ++ show l ++ "." ++ s ++ ".weight"
@@ -148,8 +245,9 @@ loadGemmaModel path cfg@GemmaConfig{..} = do
   withModel ctx m cfg defaultMaxSeq
 
 -- | loadGemmaModelFromGGUF (src/Gemma/Model.hs:908): the file is parsed and
--- every tensor, Q4_0 projections and the tied LM head included, uploaded
--- by the library (gh_model_load_gguf).
+-- every tensor, Q4_0 projections and the LM head included (output.weight,
+-- src/Gemma/Model.hs:988, or the tied embedding), uploaded by the library
+-- (gh_model_load_gguf).
 loadGemmaModelFromGGUF :: FilePath -> ContT r IO (GemmaModel dtype)
 loadGemmaModelFromGGUF path = liftIO $ do
   ctx <- HIP.newContext 0

@@ -33,7 +33,7 @@ module Graphics.HIP
   , c_lastError, c_version, c_deviceCount
   , c_ctxCreate, c_ctxDestroy, p_ctxRelease, c_ctxSync
   , c_configPreset, c_modelCreate, c_modelDestroy, p_modelRelease
-  , c_modelSetTensor, c_modelCheck, c_modelConfig, c_modelLoadGGUF, c_ggufInspect
+  , c_modelSetTensor, c_modelCheck, c_modelConfig, c_modelPlan, c_modelLoadGGUF, c_ggufInspect
   , c_kvCreate, c_kvDestroy, p_kvRelease, c_kvReset, c_kvLength, c_kvTruncate, c_kvSetSampling, c_kvSetTopK
   , c_step, c_generate, c_prefill, c_generatePrefill
   , c_q4Upload, c_q4Free, p_q4Release, c_q4Matvec, c_q4Dequant, c_linearQ4
@@ -127,6 +127,7 @@ foreign import ccall safe "gh_model_set_tensor"
   c_modelSetTensor :: Ptr ModelS -> CString -> CInt -> Ptr () -> CSize -> IO CInt
 foreign import ccall safe "gh_model_check" c_modelCheck :: Ptr ModelS -> IO CInt
 foreign import ccall safe "gh_model_config" c_modelConfig :: Ptr ModelS -> Ptr GhConfig -> IO CInt
+foreign import ccall safe "gh_model_plan" c_modelPlan :: Ptr ModelS -> CString -> CSize -> Ptr CSize -> IO CInt
 foreign import ccall safe "gh_model_load_gguf"
   c_modelLoadGGUF :: Ptr CtxS -> CString -> Int32 -> Ptr (Ptr ModelS) -> IO CInt
 foreign import ccall safe "gh_gguf_inspect" c_ggufInspect :: CString -> Ptr GhConfig -> IO CInt

@@ -197,15 +197,34 @@ int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out);
 int gh_model_destroy(gh_model* m);
 void gh_model_release(gh_model* m); /* gh_model_destroy for finalisers */
 /* name: GGUF tensor name (token_embd.weight, output_norm.weight,
- * blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_q_norm,attn_k_norm,
- * attn_output,post_attention_norm,ffn_norm,ffn_gate,ffn_up,ffn_down,
- * post_ffw_norm}.weight).  dtype GH_DTYPE_F32 / F16 / Q4_0 (raw bytes).
- * The projections share one format (Q4_0, or f32 from F32/F16); the
- * embedding may have its own. */
+ * output.weight, blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_q_norm,
+ * attn_k_norm,attn_output,post_attention_norm,ffn_norm,ffn_gate,ffn_up,
+ * ffn_down,post_ffw_norm}.weight).  dtype GH_DTYPE_F32 / F16 / Q4_0 (raw
+ * bytes).  The projections share one format (Q4_0, or f32 from F32/F16);
+ * the embedding and output.weight may each have their own.
+ * output.weight [vocab x hidden] is an untied LM head: the model uses it
+ * instead of the embedding (the reference's lm_head.weight when present,
+ * src/Gemma/Model.hs:412-414, and the GGUF output.weight,
+ * src/Gemma/Model.hs:988).  It is optional and must be set before the
+ * model's first step (GH_ERR_STATE after). */
 int gh_model_set_tensor(gh_model* m, const char* name, int dtype, const void* data, size_t nbytes);
 /* 0 when every tensor the config needs is present. */
 int gh_model_check(gh_model* m);
 int gh_model_config(gh_model* m, gh_config* out);
+/* The kernel plan the model's decode step runs (no reference counterpart:
+ * the reference compiles one fixed set of shaders).  A one-line text of
+ * space-separated key=value items: the step mode (graph, eager or
+ * persistent; GH_NO_GRAPH is read at every step, so eager reflects it now),
+ * then per matvec phase (qkv, o_proj, gate_up, down, lm_head) its column
+ * splits S, rows per lane rl, work items per workgroup ni and dot-product
+ * unit (valu or mfma), the attention chunks per kv head, the LM head (tied
+ * or untied), and env= with every GH_* environment variable that was set
+ * when the plan was made and can change what runs (the tuning and study
+ * switches GH_PLAN_*, GH_Q4_*, GH_ATTN_*, GH_PERSISTENT, GH_NO_GRAPH), or
+ * env=none.  The plan is fixed at the model's first step; before it, this
+ * reports the plan that step will choose.  Writes at most cap bytes including the terminating NUL;
+ * *len_out (may be NULL) receives the full length without it. */
+int gh_model_plan(gh_model* m, char* buf, size_t cap, size_t* len_out);
 /* loadGemmaModelFromGGUF (src/Gemma/Model.hs:908-1234) + configFromGGUF
  * (src/Gemma/Model.hs:843-902): parse a GGUF v3 file, build the config from
  * its metadata (vocab from the token_embd shape) and upload every tensor.
@@ -291,8 +310,11 @@ int gh_bench_decode(gh_model* m, gh_kv* kv, const int32_t* prompt, int32_t n_pro
 /* ================================================================
  * Profiling: replaces the gpu_print_profile_stats /
  * gpu_reset_profile_stats hooks (examples/BenchmarkKVCache.hs:38-42).
- * Runs n_steps greedy steps with HIP events around every kernel and
- * reports per-kernel-kind statistics.
+ * Runs n_steps greedy steps, launched eagerly in the step's order, and
+ * reports per-kernel-kind statistics of every kernel's execution time: the
+ * begin and end timestamps of its own dispatch (hipExtLaunchKernel's start
+ * and stop events), which is what a kernel trace reports, measured inside
+ * real decode steps (each layer's weights cold, as in the decode loop).
  * ================================================================ */
 typedef struct gh_kernel_stat {
     char name[32];

@@ -348,6 +348,7 @@ static const char* k_layer_names[T_NLAYER] = {
 struct orc_model {
     orc_config c;
     orc_tensor embd, out_norm;
+    orc_tensor lm;  /* output.weight: untied LM head (optional) */
     orc_tensor* lt; /* [n_layers][T_NLAYER] */
     float* kc;      /* [n_layers][max_seq][nkv][hd] */
     float* vc;
@@ -372,6 +373,7 @@ void orc_model_destroy(orc_model* m) {
     if (!m) return;
     free_tensor(&m->embd);
     free_tensor(&m->out_norm);
+    free_tensor(&m->lm);
     for (int i = 0; i < m->c.n_layers * T_NLAYER; ++i) free_tensor(&m->lt[i]);
     free(m->lt);
     free(m->kc);
@@ -400,6 +402,8 @@ int orc_model_set_tensor(orc_model* m, const char* name, int dtype, const void* 
         t = &m->embd;
     } else if (strcmp(name, "output_norm.weight") == 0) {
         t = &m->out_norm;
+    } else if (strcmp(name, "output.weight") == 0) {
+        t = &m->lm;
     } else if (strncmp(name, "blk.", 4) == 0) {
         char* end = NULL;
         long l = strtol(name + 4, &end, 10);
@@ -516,12 +520,15 @@ int orc_step(orc_model* m, int32_t token, int32_t pos, float* logits, float* lay
         for (int i = 0; i < H; ++i) x[i] = x1[i] + a[i];
         if (layer_out) memcpy(layer_out + (size_t)l * H, x, sizeof(float) * H);
     }
-    /* fused final norm + LM head (RMSNorm.hs:343-386) on the tied table */
+    /* fused final norm + LM head (RMSNorm.hs:343-386): lm_head.weight when
+     * the model has one, else the tied embedding table
+     * (src/Gemma/Model.hs:412-414; GGUF output.weight, Model.hs:988) */
     orc_rmsnorm_seq(x, (const float*)m->out_norm.data, H, eps, zc, xn);
-    if (m->embd.dtype == ORC_Q4_0)
-        orc_q4_0_matvec((const uint8_t*)m->embd.data, xn, c->vocab, H, ftz_of(m), lg);
+    const orc_tensor* head = m->lm.data ? &m->lm : &m->embd;
+    if (head->dtype == ORC_Q4_0)
+        orc_q4_0_matvec((const uint8_t*)head->data, xn, c->vocab, H, ftz_of(m), lg);
     else
-        orc_f32_matvec((const float*)m->embd.data, xn, c->vocab, H, lg);
+        orc_f32_matvec((const float*)head->data, xn, c->vocab, H, lg);
     int32_t best = orc_argmax(lg, c->vocab);
 
     free(x); free(xn); free(x1); free(a); free(q); free(k); free(v); free(o);

@@ -66,7 +66,7 @@ class TorchModel:
         self.t = {}
         for name, dtype, arr in tensors:
             kind = name.split(".")[-2] if name.startswith("blk.") else name.split(".")[0]
-            if name == "token_embd.weight":
+            if name in ("token_embd.weight", "output.weight"):
                 rc = (cfg.vocab, H)
             elif kind in shapes:
                 rc = shapes[kind]
@@ -137,5 +137,7 @@ class TorchModel:
                 d = _norm(d, T[p + "post_ffw_norm.weight"], eps, zc)
             x = x1 + d
         xn = _norm(x, T["output_norm.weight"], eps, zc)
-        logits = T["token_embd.weight"] @ xn
+        # untied output.weight when present, else the tied embedding
+        # (src/Gemma/Model.hs:412-414)
+        logits = T.get("output.weight", T["token_embd.weight"]) @ xn
         return logits, int(torch.argmax(logits))

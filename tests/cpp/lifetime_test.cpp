@@ -90,10 +90,20 @@ int any_order() {
         }
         for (char w : {'c', 'm', 'k', 't'}) CHECK(destroy(h, w) == GH_ERR_STATE);
     }
-    // gh_kv_truncate rewinds within [0, length]
+    // gh_kv_truncate rewinds within [0, length]; gh_model_plan reports the
+    // step's plan (graph mode, five phases, the tied head) and its length
     {
         Handles h;
         if (make(h)) return 1;
+        char plan[512];
+        size_t n = 0;
+        CHECK(gh_model_plan(h.m, plan, sizeof plan, &n) == GH_OK && n > 0 && n < sizeof plan);
+        CHECK(std::strncmp(plan, "step=", 5) == 0 && std::strstr(plan, " gate_up=S") && std::strstr(plan, " lm=tied") &&
+              std::strstr(plan, " env="));
+        char small[8];
+        size_t n2 = 0;
+        CHECK(gh_model_plan(h.m, small, sizeof small, &n2) == GH_OK && n2 == n && std::strlen(small) == 7);
+        CHECK(gh_model_plan(h.m, nullptr, 4, &n2) == GH_ERR_INVALID);
         int32_t len = -1;
         CHECK(gh_kv_truncate(h.kv, 2) == GH_ERR_RANGE);
         CHECK(gh_kv_truncate(h.kv, -1) == GH_ERR_RANGE);

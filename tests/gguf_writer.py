@@ -97,14 +97,21 @@ def random_q4_1(rows: int, cols: int, seed: int, subnormal_frac: float = 0.02) -
     return b.reshape(-1)
 
 
-def synth_gguf(path, cfg, seed: int, q4: bool, embd_q4_1: bool = False, norms_f16: bool = False, **kw) -> None:
+def synth_gguf(path, cfg, seed: int, q4: bool, embd_q4_1: bool = False, norms_f16: bool = False,
+               untied: bool = False, head_f16: bool = False, **kw) -> None:
     """The seeded synthetic model of gemma_hip.synth_tensors as a GGUF file;
     embd_q4_1 replaces token_embd with random Q4_1 blocks, norms_f16 stores
-    the norm vectors as F16 (with a few subnormal values)."""
+    the norm vectors as F16 (with a few subnormal values); untied adds an
+    output.weight LM head (Q4_0, or F16 values of N(0, 0.02) with head_f16)."""
     import gemma_hip as gh
-    shapes = {n: (k, s) for n, k, s in gh.tensor_list(cfg)}
+    shapes = {n: (k, s) for n, k, s in gh.tensor_list(cfg, untied)}
     tensors = []
-    for name, dtype, arr in gh.synth_tensors(cfg, seed, q4):
+    for name, dtype, arr in gh.synth_tensors(cfg, seed, q4, untied=untied):
+        if name == "output.weight" and head_f16:
+            kind, shape = shapes[name]
+            h = gh.synth_f32(seed, name, 0.02, shape[0] * shape[1]).astype(np.float16)
+            tensors.append((name, "f16", shape[0], shape[1], h))
+            continue
         kind, shape = shapes[name]
         if kind == "vec":
             if norms_f16:

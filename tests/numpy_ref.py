@@ -104,5 +104,5 @@ class NumpyGemma:
             d = rms_norm(t[p + "ffn_down.weight"] @ h, t[p + "post_ffw_norm.weight"], eps)
             x = x1 + d
             layers.append(x.copy())
-        logits = E @ rms_norm(x, t["output_norm.weight"], eps)
+        logits = t.get("output.weight", E) @ rms_norm(x, t["output_norm.weight"], eps)
         return logits, np.stack(layers)

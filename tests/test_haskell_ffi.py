@@ -13,6 +13,7 @@ Gemma.Model / Gemma.Layers.LinearQ4 keep the reference's names
 from __future__ import annotations
 
 import re
+from pathlib import Path
 
 import pytest
 
@@ -25,7 +26,7 @@ SCALARS = {"int": "CInt", "int32_t": "Int32", "int64_t": "Int64", "uint64_t": "W
            "size_t": "CSize", "float": "CFloat", "double": "CDouble"}
 POINTEES = {"float": "CFloat", "double": "CDouble", "int32_t": "Int32", "uint8_t": "Word8", "uint32_t": "Word32",
             "gh_ctx": "CtxS", "gh_model": "ModelS", "gh_kv": "KvS", "gh_q4": "Q4S", "gh_config": "GhConfig",
-            "int": "CInt"}
+            "int": "CInt", "size_t": "CSize"}
 
 
 def c_prototypes() -> dict[str, tuple[str, list[str]]]:
@@ -175,3 +176,127 @@ def test_signature_check_catches_planted_mismatches(planted, monkeypatch):
     monkeypatch.setattr(__import__(__name__), "hs_imports", lambda: bad)
     with pytest.raises(AssertionError):
         test_every_foreign_import_matches_the_header()
+
+
+# ---------------------------------------------------------------- imports
+# The reference library's build-depends (gemma.cabal:58-71) without
+# webgpu-dawn, which Graphics.HIP replaces.
+REFERENCE_DEPENDS = {"base", "vector", "bytestring", "aeson", "text", "containers", "transformers", "mtl", "half",
+                     "directory", "process", "filepath"}
+# Package modules the drop-in imports, by the package that provides them.
+PACKAGE_MODULES = {
+    "base": {"Control.Exception", "Control.Monad", "Control.Monad.IO.Class", "Data.Bits", "Data.Int", "Data.Maybe",
+             "Data.Word", "Foreign.C.String", "Foreign.C.Types", "Foreign.ForeignPtr", "Foreign.Marshal.Alloc",
+             "Foreign.Ptr", "Foreign.Storable"},
+    "vector": {"Data.Vector", "Data.Vector.Storable", "Data.Vector.Storable.Mutable"},
+    "text": {"Data.Text"},
+    "transformers": {"Control.Monad.Trans.Cont"},
+}
+# Modules of the reference library (gemma.cabal exposed-modules) the drop-in
+# imports, with the names it takes from each (constructors under their type).
+REFERENCE_MODULES = {
+    "Gemma.KVCache": {"KVCache", "LayerKVCache", "cacheLength", "initKVCache"},
+    "Gemma.SafeTensors": {"getTensor", "hasTensor", "loadSafeTensors"},
+    "Gemma.GGUF": {"GGUFFile", "MetadataValue", "MetaArray", "getMetadata", "getMetadataInt", "getMetadataFloat",
+                   "getTensorShape", "hasTensor"},
+}
+REFERENCE = Path("/root/reference")
+
+
+def hs_module_imports(text: str) -> list[tuple[str, set[str]]]:
+    """(module, names used from it) for every import of a module's text: the
+    explicit import list, or the Alias.name uses of a qualified import."""
+    out = []
+    for m in re.finditer(r"^import\s+(qualified\s+)?([A-Z][\w.]*)(?:\s+as\s+(\w+))?\s*(\(([^()]*(?:\([^()]*\)[^()]*)*)\))?",
+                         text, re.M):
+        qual, mod, alias, _, items = m.groups()
+        names = set()
+        if items is not None:
+            for it in items.split(","):
+                it = it.strip()
+                if it:
+                    names.add(re.sub(r"\(.*\)$", "", it).strip())
+        if alias:
+            names |= set(re.findall(rf"\b{re.escape(alias)}\.([A-Za-z_]\w*)", text))
+        out.append((mod, names))
+    return out
+
+
+def committed_modules() -> dict[str, Path]:
+    return {".".join(p.relative_to(HS).with_suffix("").parts): p for p in HS.rglob("*.hs")}
+
+
+def exports_of(text: str, mod: str) -> str:
+    m = re.search(rf"module\s+{re.escape(mod)}\s*\((.*?)\)\s*where", text, re.S)
+    assert m, mod
+    return m.group(1)
+
+
+def exported_names(text: str, mod: str) -> set[str]:
+    """Names a module exports: its export list, plus the constructors and
+    record fields of every type exported with (..)."""
+    exp = exports_of(text, mod)
+    names = set(re.findall(r"[A-Za-z_][\w']*", exp))
+    for t in re.findall(r"\b([A-Z]\w*)\(\.\.\)", exp):
+        m = re.search(rf"^data {t}\b(.*?)(?=^\S)", text, re.S | re.M)
+        if m:
+            names |= set(re.findall(r"[A-Za-z_][\w']*", m.group(1)))
+    return names
+
+
+def unresolved_imports(files: dict[str, str]) -> list[str]:
+    """Every import of the given module texts that does not resolve."""
+    bad = []
+    mods = committed_modules()
+    for path, text in files.items():
+        for mod, names in hs_module_imports(text):
+            if mod in mods:
+                exp = exported_names(mods[mod].read_text(), mod)
+                bad += [f"{path}: {mod}.{n} not exported" for n in names if n not in exp and not n.startswith("(")]
+            elif mod in REFERENCE_MODULES:
+                bad += [f"{path}: {mod}.{n} not among the reference names" for n in names - REFERENCE_MODULES[mod]]
+            elif not any(mod in ms and pkg in REFERENCE_DEPENDS for pkg, ms in PACKAGE_MODULES.items()):
+                bad.append(f"{path}: module {mod} is neither committed, nor the reference's, nor a dependency's")
+    return bad
+
+
+def test_every_haskell_import_resolves():
+    """Each import under haskell/ names a committed module (exporting what is
+    imported), a module of the reference library, or a module of a package
+    the reference already depends on: the module graph is complete."""
+    files = {str(p.relative_to(HS)): p.read_text() for p in HS.rglob("*.hs")}
+    assert len(files) >= 3
+    assert unresolved_imports(files) == []
+
+
+def test_reference_modules_export_the_names_the_drop_in_takes():
+    """The reference-side names in REFERENCE_MODULES exist: each module is an
+    exposed module of gemma.cabal and exports the name (or the type whose
+    constructor it is).  Reads the reference tree as text; skipped where it
+    is absent."""
+    if not (REFERENCE / "gemma.cabal").exists():
+        pytest.skip("reference tree not present")
+    cabal = (REFERENCE / "gemma.cabal").read_text()
+    exposed = re.search(r"exposed-modules:\s*(.*?)\n\s*\n|exposed-modules:\s*(.*?)hs-source-dirs", cabal, re.S)
+    block = next(g for g in exposed.groups() if g)
+    for mod, names in REFERENCE_MODULES.items():
+        assert re.search(rf"^\s*{re.escape(mod)}\s*$", block, re.M), mod
+        text = (REFERENCE / "src" / Path(*mod.split("."))).with_suffix(".hs").read_text()
+        exp = exports_of(text, mod)
+        for n in names:
+            ok = re.search(rf"\b{re.escape(n)}\b", exp) or re.search(rf"[=|]\s*{re.escape(n)}\b", text)
+            assert ok, (mod, n)
+    deps = re.search(r"library.*?build-depends:(.*?)\n\s*\n", cabal, re.S).group(1)
+    for pkg in REFERENCE_DEPENDS:
+        assert re.search(rf"\b{re.escape(pkg)}\b", deps), pkg
+
+
+def test_import_check_catches_a_missing_module():
+    """A module the tree does not hold (the former Gemma.Model.Config) and a
+    name a committed module does not export both fail the check."""
+    text = (HS / "Gemma" / "Model.hs").read_text()
+    planted = text.replace("import qualified Gemma.GGUF as GGUF",
+                           "import qualified Gemma.GGUF as GGUF\nimport Gemma.Model.Config (GemmaConfig(..))")
+    assert any("Gemma.Model.Config" in b for b in unresolved_imports({"Model.hs": planted}))
+    planted = text.replace("import Graphics.HIP (check)", "import Graphics.HIP (check, c_noSuchCall)")
+    assert any("c_noSuchCall" in b for b in unresolved_imports({"Model.hs": planted}))

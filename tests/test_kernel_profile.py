@@ -40,3 +40,30 @@ def test_summarize_splits_at_separators_and_calibrates(tmp_path, capsys):
     assert "FETCH_SIZE 2048.00000" in out
     assert "| gate_up | 2 | 430,080 | 215,040 |" in out
     assert "| attention | 4 | 81,920 | 81,920 |" in out
+
+
+def test_summarize_assigns_decode_dispatches_by_their_place_in_the_step(tmp_path, capsys):
+    """A decode segment (eager steps in the step's launch order): each
+    dispatch takes its kernel kind from its index modulo the recorded step
+    sequence, and a segment whose count is not whole steps is refused."""
+    import pytest
+    sep = "gh::k_stream_read(void const*, unsigned int, unsigned int, float*)"
+    a, b, c = "k_a(int)", "k_b(int)", "k_c(int)"
+    step = [(a, 10.0), (b, 20.0), (a, 30.0), (c, 8.0)]
+    seq = [(sep, 1.0), (sep, 1.0)] + step + step + [(sep, 1.0)] * 2 + [("__amd_rocclr_copyBuffer", 4096.0)]
+    _write(tmp_path / "fetch", seq, "FETCH_SIZE")
+    man = {"config": "gemma3-1b", "position": None, "copy_bytes": 8 << 20,
+           "segments": [{"name": "decode", "steps": 2, "positions": [224, 225], "sequence": ["x", "y", "x", "z"],
+                         "kinds": {"x": {"bytes_per_launch": 20 * 2048, "event_avg_us": 0.5},
+                                   "y": {"bytes_per_launch": 20 * 2048, "event_avg_us": 0.5},
+                                   "z": {"bytes_per_launch": 8 * 2048, "event_avg_us": 0.5}}}]}
+    (tmp_path / "m.json").write_text(json.dumps(man))
+    kp.main(["summarize", "--manifest", str(tmp_path / "m.json"), "--fetch", str(tmp_path / "fetch")])
+    out = capsys.readouterr().out
+    assert "| x | 4 | 40,960 | 40,960 |" in out  # (10 + 30) / 2 units of 2048 B
+    assert "| y | 2 | 40,960 | 40,960 |" in out
+    assert "| z | 2 | 16,384 | 16,384 |" in out
+    man["segments"][0]["steps"] = 3
+    (tmp_path / "m.json").write_text(json.dumps(man))
+    with pytest.raises(SystemExit):
+        kp.main(["summarize", "--manifest", str(tmp_path / "m.json"), "--fetch", str(tmp_path / "fetch")])

@@ -360,10 +360,12 @@ def _tiny_cfg(**kw):
     return c
 
 
-def _random_model(cfg, q4, seed):
+def _random_model(cfg, q4, seed, untied=False):
     rng = np.random.default_rng(seed)
     H, hd, F = cfg.hidden, cfg.head_dim, cfg.ffn
     shapes = {"token_embd.weight": (cfg.vocab, H), "output_norm.weight": (H,)}
+    if untied:
+        shapes["output.weight"] = (cfg.vocab, H)
     for l in range(cfg.n_layers):
         p = f"blk.{l}."
         shapes.update({p + "attn_norm.weight": (H,), p + "attn_q.weight": (cfg.n_heads * hd, H),
@@ -393,14 +395,18 @@ def _random_model(cfg, q4, seed):
     return om, dense
 
 
-@pytest.mark.parametrize("q4,extra", [
-    (False, {}),
+@pytest.mark.parametrize("q4,extra,untied", [
+    (False, {}, False),
     (True, {"hidden": 256, "ffn": 512, "head_dim": 32, "n_heads": 8, "n_kv_heads": 2,
-            "sliding_window": 5, "global_every": 2, "rope_theta_global": 1e6, "n_layers": 4}),
+            "sliding_window": 5, "global_every": 2, "rope_theta_global": 1e6, "n_layers": 4}, False),
+    (True, {}, True),
+    (False, {}, True),
 ])
-def test_oracle_model_matches_numpy_fp64(q4, extra):
+def test_oracle_model_matches_numpy_fp64(q4, extra, untied):
+    """The whole step against an fp64 numpy restatement; `untied` gives the
+    model an output.weight LM head (src/Gemma/Model.hs:412-414)."""
     cfg = _tiny_cfg(**extra)
-    om, dense = _random_model(cfg, q4, seed=11)
+    om, dense = _random_model(cfg, q4, seed=11, untied=untied)
     ref = NumpyGemma(cfg, dense)
     rng = np.random.default_rng(12)
     toks = rng.integers(0, cfg.vocab, size=12)
@@ -438,6 +444,23 @@ def test_oracle_ref_mode_prefix_window():
     assert rel_err(outs[1], rlg) > 1e-3
 
 
+def test_untied_head_is_not_the_embedding():
+    """With an output.weight, logits computed on the tied embedding (the
+    mistake of ignoring lm_head.weight) are far from the oracle's, and the
+    oracle's equal the fp64 restatement's on output.weight."""
+    cfg = _tiny_cfg()
+    om, dense = _random_model(cfg, True, seed=31, untied=True)
+    ref = NumpyGemma(cfg, dense)
+    tied = {k: v for k, v in dense.items() if k != "output.weight"}
+    ref_tied = NumpyGemma(cfg, tied)
+    for pos, tok in enumerate([3, 700, 41]):
+        lg, _, _ = om.step(tok, pos)
+        rlg, _ = ref.step(tok, pos)
+        tlg, _ = ref_tied.step(tok, pos)
+        assert rel_err(lg, rlg) < 1e-5
+        assert rel_err(lg, tlg) > 0.5
+
+
 def test_planted_mistakes_are_caught():
     """Each plausible mistake, planted in a copy of an oracle function, fails
     the corresponding check above."""
@@ -459,8 +482,8 @@ def test_planted_mistakes_are_caught():
     assert got[0] == 7.0 and got[16] == -7.0
 
 
-@pytest.mark.parametrize("q4,mode", [(False, 0), (True, 0), (True, 1)])
-def test_torch_cpu_restatement_agrees_with_the_c_oracle(q4, mode):
+@pytest.mark.parametrize("q4,mode,untied", [(False, 0, False), (True, 0, False), (True, 1, False), (True, 0, True)])
+def test_torch_cpu_restatement_agrees_with_the_c_oracle(q4, mode, untied):
     """oracle/torch_ref.py (bench.py's PyTorch-CPU baseline) against the C
     oracle on the tiny model: logits within 1e-5 relative and the same
     argmax at every step of a 24-token run (window 5 binds in both modes)."""
@@ -470,7 +493,7 @@ def test_torch_cpu_restatement_agrees_with_the_c_oracle(q4, mode):
     cfg.sliding_window, cfg.global_every, cfg.max_seq, cfg.mode = 5, 2, 32, mode
     cfg.rope_theta_global = 1e6
     om = orc.OracleModel(cfg)
-    tens = list(gh.synth_tensors(cfg, 11, q4))
+    tens = list(gh.synth_tensors(cfg, 11, q4, untied=untied))
     for name, dtype, arr in tens:
         om.set_tensor(name, arr, dtype)
     tm = torch_ref.TorchModel(cfg, tens)
