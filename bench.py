@@ -37,10 +37,12 @@ PROMPT_SEED = 1
 N_PROMPT = 128
 # HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, then
 # WRITE_SIZE, each scaled by bytes / counter of a 256 MiB device copy) over
-# eager decode steps at positions 224..287 (kernel_profile run --decode 64):
-# profiles/step_kernels_gemma3-1b_decode_c3.md.
-GATE_UP_TRAFFIC_BYTES = 9_815_468
-LM_HEAD_TRAFFIC_BYTES = 172_340_835
+# replays of each kernel kind at position 257 (kernel_profile run --prompt
+# 256 --prefill-prompt): profiles/step_kernels_gemma3-1b_decode_c3.md,
+# gate/up 9,644,236 fetched + 170,496 written, the LM head 171,009,837 +
+# 1,179,648.
+GATE_UP_TRAFFIC_BYTES = 9_814_732
+LM_HEAD_TRAFFIC_BYTES = 172_189_485
 TRAFFIC_PROFILE = "profiles/step_kernels_gemma3-1b_decode_c3.md"
 # the in-step kernel timings: C3's decode positions 128..383
 PROFILE_STEPS = 256
@@ -218,7 +220,8 @@ def extras_c5_gemma3_4b(gh, ctx, steps: int = 64, warmup: int = 8) -> dict:
     a prefill), then greedy steps from position 4096."""
     cfg = gh.preset("gemma3-4b")
     n0 = 4096
-    cfg.max_seq = n0 + warmup + steps + 8
+    n_prof = 8  # in-step kernel timing after the timed steps
+    cfg.max_seq = n0 + warmup + steps + n_prof + 8
     model = gh.GemmaModel(ctx, cfg)
     model.synth(WEIGHT_SEED, q4=True)
     kv = gh.KVCache(model, cfg.max_seq)
@@ -226,7 +229,6 @@ def extras_c5_gemma3_4b(gh, ctx, steps: int = 64, warmup: int = 8) -> dict:
     prompt = gh.synth_tokens(PROMPT_SEED, "c5", 1, cfg.vocab)
     ms, _ = gh.bench_decode(model, kv, prompt, warmup, steps)
     tok_s = steps / (ms / 1e3)
-    n_prof = 8
     timings = in_step_kernels(gh, model, kv, n_prof)
     step_bytes = sum(t.bytes_per_launch * t.launches for t in timings.values()) / n_prof
     log(f"  C5 gemma3-4b @ {n0}: {tok_s:.1f} tok/s")
@@ -341,8 +343,8 @@ def main(argv=None) -> int:
     gu, lm = timings["gate_up"], timings["lm_head"]
     roofline = {"bound": "hbm", "achieved": round(gu.gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(gu.gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
-                "traffic_source": f"rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated) over eager decode "
-                                  f"steps at positions 224..287: {TRAFFIC_PROFILE}",
+                "traffic_source": f"rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (copy-calibrated) at position 257: "
+                                  f"{TRAFFIC_PROFILE}",
                 "kernel": "gate_up", "bytes_per_launch": int(gu.bytes_per_launch), "avg_us": round(gu.avg_us, 3),
                 "timing": f"dispatch begin/end timestamps of every gate/up launch in {PROFILE_STEPS} real decode "
                           f"steps at positions {pos0}..{pos0 + PROFILE_STEPS - 1} ({gu.launches} launches)",
