@@ -1,11 +1,14 @@
 """Build libgemma_hip.so (hipcc, gfx950) and the oracle's liboracle.so (gcc).
 
-Usage: python gemma.hs_amd/build.py [--only lib|oracle] [-j N]
+Usage: python gemma.hs_amd/build.py [--only lib|oracle] [--no-marks] [-j N]
 
 Objects go to gemma.hs_amd/_build/, the library to
 gemma.hs_amd/gemma_hip/libgemma_hip.so and the oracle to
 oracle/build/liboracle.so (all git-ignored; the built .so files travel to
-the GPU box with the source tree).
+the GPU box with the source tree).  Beside the library, the same pool
+builds libgemma_hip_marks.so: the library with the step kernels compiled
+from csrc/marks/marks.hip (phase timestamps, for gemma_hip.kernel_profile
+phases); nothing loads it unless GEMMA_HIP_LIB names it.
 """
 from __future__ import annotations
 
@@ -22,6 +25,9 @@ REPO = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "gemma_hip" / "libgemma_hip.so"
+MARKS_LIB = PKG / "gemma_hip" / "libgemma_hip_marks.so"
+MARKS_SRC = CSRC / "marks" / "marks.hip"
+MARKS_TUS = (1, 5, 6, 7)  # the decode step's kernels: attention, then the matvec phases
 ORACLE_DIR = REPO / "oracle"
 ORACLE_LIB = ORACLE_DIR / "build" / "liboracle.so"
 
@@ -56,9 +62,12 @@ def _run(cmd: list[str]) -> None:
             sys.stderr.write(line + "\n")
 
 
-def build_lib(jobs: int = 8) -> Path:
+def build_lib(jobs: int = 8, marks: bool = True) -> Path:
     OBJ.mkdir(exist_ok=True)
     units = []
+    if marks:  # the longest units first
+        for tu in MARKS_TUS:
+            units.append((MARKS_SRC, [HIPCC, *DEVICE_FLAGS, f"-DGH_TU={tu}", "-x", "hip"], f"marks_tu{tu}"))
     for src in sorted(CSRC.iterdir()):
         if src.name == "kernels.hip":
             # compiled as KERNEL_TUS translation units in parallel (GH_TU in kernels.hip)
@@ -78,10 +87,17 @@ def build_lib(jobs: int = 8) -> Path:
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, units))
+    lib_objs = [o for o in objs if not o.name.startswith("marks_")]
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, lib_objs),
           "-lpthread"])
     os.replace(tmp, LIB)
+    if marks:
+        marked = {f"kernels_tu{tu}.o" for tu in MARKS_TUS}
+        mobjs = [o for o in objs if o.name.startswith("marks_")] + [o for o in lib_objs if o.name not in marked]
+        tmp = MARKS_LIB.with_suffix(".so.tmp")
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, mobjs), "-lpthread"])
+        os.replace(tmp, MARKS_LIB)
     return LIB
 
 
@@ -116,12 +132,13 @@ def build_oracle() -> Path:
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", choices=["lib", "oracle"])  # default: lib, oracle and the C++ host tests
+    ap.add_argument("--no-marks", action="store_true", help="skip libgemma_hip_marks.so")
     ap.add_argument("-j", type=int, default=8)
     a = ap.parse_args(argv)
     if a.only in (None, "oracle"):
         print("built", build_oracle())
     if a.only in (None, "lib"):
-        print("built", build_lib(a.j))
+        print("built", build_lib(a.j, marks=not a.no_marks))
     if a.only is None:
         print("built", build_host_tests())
 

@@ -797,6 +797,7 @@ __device__ __forceinline__ void mv_item_multi_v(const DMat& w, int it, int s, in
     const int kw0 = kb0 + (nk * wave >> 2);
     // an item past the last row tile loads nothing and writes nothing
     const int kw1 = live ? kb0 + (nk * (wave + 1) >> 2) : kw0;
+    GH_MARK(0);
     typename Pro::Regs pr;
     if (lead) {
         if constexpr (HasLoadVariants<Pro>::value) pro.template load_v<V>(pr, kb0 * BK, nk * BK);
@@ -815,16 +816,20 @@ __device__ __forceinline__ void mv_item_multi_v(const DMat& w, int it, int s, in
 #pragma unroll
         for (int i = 0; i < Pro::kFinishBarriers; ++i) __syncthreads();
     }
+    GH_MARK(1);
     __syncthreads();
+    GH_MARK(2);
     float acc0 = 0.0f, acc1 = 0.0f;
     mv_compute<FMT, KBW, RL>(r, kw0, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     for (int base = kw0 + KBW; base < kw1; base += KBW) {
         mv_load<FMT, KBW, RL>(r, w, mv, tile, rbase, base, kw1);
         mv_compute<FMT, KBW, RL>(r, base, kw1, kb0, L.xs, L.sxs, acc0, acc1);
     }
+    GH_MARK(3);
     red[wave * TILE_ROWS + lane] = acc0;
     if (RL == 2) red[wave * TILE_ROWS + 64 + lane] = acc1;
     __syncthreads();
+    GH_MARK(4);
     if (wave == 0 && live) {
         const float y0 = (red[lane] + red[TILE_ROWS + lane]) + (red[2 * TILE_ROWS + lane] + red[3 * TILE_ROWS + lane]);
         float y1 = 0.0f;
@@ -832,6 +837,8 @@ __device__ __forceinline__ void mv_item_multi_v(const DMat& w, int it, int s, in
             y1 = (red[64 + lane] + red[TILE_ROWS + 64 + lane]) + (red[2 * TILE_ROWS + 64 + lane] + red[3 * TILE_ROWS + 64 + lane]);
         epi.template run<RL>(L, er, it, tile * TILE_ROWS + rbase + lane, s, y0, y1);
     }
+    GH_MARK(5);
+    GH_MARK_END();
 }
 
 // The same on the matrix cores (mq_item_v's dot products): the lead waves'

@@ -9,6 +9,7 @@ Driver (run under rocprofv3 on the GPU box, eagerly: GH_NO_GRAPH=1):
   python -m gemma_hip.kernel_profile run --attention 32768 [--reps 20] [--copy-mib 256] [--copies 8]
   python -m gemma_hip.kernel_profile run --decode 64 [--prompt 128] [--start 224] [--copy-mib 256]
   python -m gemma_hip.kernel_profile exchange [--wgs 8 64 128 256] [--rounds 2000]
+  python -m gemma_hip.kernel_profile phases [--config gemma3-1b] [--prompt 128] [--reps 20] [--kernel KIND]
 
 It builds the seeded model of the config and decodes a short prompt.  Then,
 for each step-kernel kind asked for, it launches a separator (two launches
@@ -29,7 +30,11 @@ each dispatch its kernel kind by its place in the step's launch sequence,
 which the manifest records.  The manifest (JSON) lists the segments in
 order.  `exchange` needs no profiler: it prints the
 cost of one all-to-all word exchange among n co-resident workgroups
-(gh_time_exchange, the persistent step's synchronisation).
+(gh_time_exchange, the persistent step's synchronisation).  `phases` needs
+no profiler either: it loads libgemma_hip_marks.so (the step kernels built
+with phase timestamps, build.py) and prints, per step-kernel kind, when
+each workgroup reaches each phase of its latency chain (medians over the
+workgroups of the last replayed launch, us since the workgroup started).
 
 Summariser (on any host, from rocprofv3's CSV output):
 
@@ -312,6 +317,80 @@ def summarize(a) -> int:
     return 0
 
 
+# Phase points of the step kernels (GH_MARK slots in kernels.hip): the
+# matvec work items (mv_item_valu, mv_item_multi_v, mq_item_v with the
+# residual-norm prologue's own points) and the step attention.
+MATVEC_SLOTS = {6: "norm reduced", 7: "residual out", 1: "prologue done", 2: "slice in LDS", 3: "dots done",
+                4: "rows reduced", 5: "epilogue done"}
+ATTN_SLOTS = {1: "loads issued", 2: "q/k/v in LDS", 4: "rounds done", 5: "wave states merged",
+              6: "state written"}
+MARKS_TUS = (1, 5, 6, 7)
+MARK_WAVES, MARK_SLOTS, MARK_MAXWG = 8, 16, 8192
+TICK_US = 0.01  # s_memrealtime runs at 100 MHz
+
+
+def phases(a) -> int:
+    import os
+    import numpy as np
+    marks = Path(__file__).resolve().parent / "libgemma_hip_marks.so"
+    if not marks.exists():
+        raise SystemExit(f"{marks} is not built (python gemma.hs_amd/build.py)")
+    os.environ["GEMMA_HIP_LIB"] = str(marks)
+    L = lib()
+    fetch = {tu: getattr(L, f"gh_marks_fetch_tu{tu}") for tu in MARKS_TUS}
+    clear = {tu: getattr(L, f"gh_marks_clear_tu{tu}") for tu in MARKS_TUS}
+    for f in fetch.values():
+        f.argtypes, f.restype = [C.c_void_p, C.c_size_t], C.c_int
+    for f in clear.values():
+        f.argtypes, f.restype = [], C.c_int
+    cfg = preset(a.config)
+    ctx = Context(0)
+    model = GemmaModel(ctx, cfg)
+    model.synth(1234, q4=True)
+    kv = KVCache(model, a.prompt + 8)
+    bench_decode(model, kv, synth_tokens(1, "prompt", a.prompt, cfg.vocab), 0, 1)
+    print(f"{a.config}, position {len(kv)}; medians over the workgroups of the last replayed launch, "
+          f"us since each workgroup's start (wave 0)")
+    print()
+    buf = np.zeros((MARK_MAXWG, MARK_WAVES, MARK_SLOTS), np.uint64)
+    kinds = [k for k in STEP_KERNELS if k not in ("final_norm", "lm_head")] if a.kernel == "all" else [a.kernel]
+    for kind in kinds:
+        for f in clear.values():
+            if f() != 0:
+                raise RuntimeError("gh_marks_clear failed")
+        t = time_kernel(model, kv, kind, a.reps)
+        got = []
+        for tu, f in fetch.items():
+            buf[:] = 0
+            if f(buf.ctypes.data, buf.nbytes) != 0:
+                raise RuntimeError("gh_marks_fetch failed")
+            used = np.nonzero(buf[:, 0, 0])[0]
+            if len(used):
+                got.append(buf[used].astype(np.int64))
+        if not got:
+            print(f"| {kind} | no marks |")
+            continue
+        b = max(got, key=len)  # the kind's kernels live in one unit
+        t0 = b[:, 0, 0].min()
+        labels = ATTN_SLOTS if kind == "attention" else MATVEC_SLOTS
+        cols = [(sl, lab) for sl, lab in labels.items() if (b[:, 0, sl] > 0).any()]
+        print(f"**{kind}** ({t.avg_us:.2f} us per replayed launch, {len(b)} workgroups; start of the last "
+              f"workgroup {np.max(b[:, 0, 0] - t0) * TICK_US:.2f} us after the first)")
+        print()
+        print("| " + " | ".join(lab for _, lab in cols) + " | workgroup done |")
+        print("|" + "---|" * (len(cols) + 1))
+        cells = []
+        for sl, _ in cols:
+            v = b[:, 0, sl]
+            ok = v > 0
+            cells.append(f"{np.median((v[ok] - b[ok, 0, 0]) * TICK_US):.2f}")
+        done = b.max(axis=(1, 2))
+        cells.append(f"{np.median((done - b[:, 0, 0]) * TICK_US):.2f}")
+        print("| " + " | ".join(cells) + " |")
+        print()
+    return 0
+
+
 def exchange(a) -> int:
     """Cost of one all-to-all word exchange among n co-resident workgroups
     (gh_time_exchange), for each n of --wgs: a markdown table."""
@@ -328,7 +407,7 @@ def exchange(a) -> int:
 
 def main(argv=None) -> int:
     argv = list(sys.argv[1:] if argv is None else argv)
-    if not argv or argv[0] not in ("run", "summarize", "exchange"):
+    if not argv or argv[0] not in ("run", "summarize", "exchange", "phases"):
         argv = ["run", *argv]
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd")
@@ -348,6 +427,11 @@ def main(argv=None) -> int:
                         "with few dispatches before them)")
     r.add_argument("--start", type=int, default=0, help="--decode: first profiled position (after the prompt)")
     r.add_argument("--manifest", default="")
+    ph = sub.add_parser("phases")
+    ph.add_argument("--config", default="gemma3-1b")
+    ph.add_argument("--prompt", type=int, default=128)
+    ph.add_argument("--reps", type=int, default=20)
+    ph.add_argument("--kernel", default="all", choices=("all",) + STEP_KERNELS)
     x = sub.add_parser("exchange")
     x.add_argument("--wgs", type=int, nargs="+", default=[8, 64, 128, 256])
     x.add_argument("--rounds", type=int, default=2000)
@@ -358,6 +442,8 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.cmd == "exchange":
         return exchange(a)
+    if a.cmd == "phases":
+        return phases(a)
     return run(a) if a.cmd == "run" else summarize(a)
 
 
