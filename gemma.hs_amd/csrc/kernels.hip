@@ -5087,10 +5087,14 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     Sink k;
     k.s = s;
     const int G = nq / nkv;
-    // head_dim 256, chunks of 64 positions or more: the step kernel's
-    // streaming body (16 % faster than a separate wave-streaming kernel at
-    // 8192 and 32768 positions on MI355X); shorter chunks: the 32-position
-    // sub-chunk kernel (0.3 us faster on the last 512)
+    // head_dim 256, chunks of 64 positions or more, or 64+ chunks: the step
+    // kernel's streaming body (16 % faster than a separate wave-streaming
+    // kernel at 8192 and 32768 positions on MI355X; at 8192 positions, 256
+    // chunks of 32, it takes one round per wave and one HBM round trip:
+    // 10.2 us against 11.6 with the sub-chunk kernel over cold caches);
+    // fewer, shorter chunks: the 32-position sub-chunk kernel (0.3 us faster
+    // on the last 512).  Eight waves per workgroup, to have every round of a
+    // 128-position chunk in flight, need more than 256 VGPRs and spill.
     const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8;
     const bool views_ok = (size_t)p_end * nkv * hd * 4 <= 0x7fffffffu;  // the body's buffer views
     // few chunks and 4+ q heads per kv head: one workgroup per (chunk, q
@@ -5102,7 +5106,7 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
         const dim3 grid(nkv * a.nc * G);
         if (G == 4) hipLaunchKernelGGL((k_attn_op<256, 4, 4>), grid, dim3(NT), 0, s, a);
         else hipLaunchKernelGGL((k_attn_op<256, 8, 8>), grid, dim3(NT), 0, s, a);
-    } else if (hd == 256 && g_ok && views_ok && a.ch >= 64) {
+    } else if (hd == 256 && g_ok && views_ok && (a.ch >= 64 || a.n_used >= 64)) {
         const dim3 grid(nkv * a.nc);
         if (G == 1) hipLaunchKernelGGL((k_attn_op<256, 1>), grid, dim3(NT), 0, s, a);
         else if (G == 2) hipLaunchKernelGGL((k_attn_op<256, 2>), grid, dim3(NT), 0, s, a);

@@ -700,9 +700,14 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     d.scales = t->scales;
     GH_CHECK(upload(ctx, t->codes, codes.data(), codes.size()));
     GH_CHECK(upload(ctx, t->scales, sc.data(), sc.size() * 2));
-    // 64-row workgroups, about 512 of them, up to 16 column splits (an
-    // MI355X sweep of the C2 shapes: 6912x1152 5.5 us, 1152x6912 6.1 us)
-    t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, env_int("GH_Q4_TARGET", 512), env_int("GH_Q4_MAXS", 16));
+    // 64-row workgroups.  One column split, so one kernel with no
+    // partial-sum pass, where the rows alone give at least 96 workgroups;
+    // otherwise about 512 workgroups with up to 16 column splits.  An
+    // MI355X sweep of the C2 shapes over rotating cold copies: 6912x1152
+    // 4.42 us with one split against 5.42 us with 8 and the partial-sum
+    // kernel; 1152x6912 (18 row items) 5.85 us at 16 splits, 18.2 at one.
+    const int max_s = env_int("GH_Q4_MAXS", 2 * d.tiles >= 96 ? 1 : 16);
+    t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, env_int("GH_Q4_TARGET", 512), max_s);
     t->plan.rl = env_int("GH_Q4_RL", 1) == 2 ? 2 : 1;
     // matrix-core dot products when the matvec is dot-bound (at least 8
     // workgroups per CU: 262144 x 1152 31.6 us vs 34.5 us on the VALU; the

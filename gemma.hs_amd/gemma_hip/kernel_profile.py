@@ -134,7 +134,7 @@ def run(a) -> int:
             for _ in range(a.reps):
                 kv.reset()
                 prefill(model, kv, toks, want_logits=False)
-            segments.append({"name": f"prefill_{a.prefill}", "reps": a.reps})
+            segments.append({"name": f"prefill_{a.prefill}", "reps": a.reps, "by_kernel": True})
         elif a.decode > 0:
             start = max(a.start, a.prompt)
             kv = KVCache(model, start + a.decode + 8)
@@ -237,6 +237,12 @@ def _units(man, segs, disp):
                 ids = [seg[i] for i in range(len(seg)) if seq[i % len(seq)] == kind]
                 info = s["kinds"].get(kind, {})
                 out.append((kind, ids, info.get("bytes_per_launch"), 1, info.get("event_avg_us")))
+        elif s.get("by_kernel"):  # one row per kernel of the segment
+            names = {}
+            for i in seg:
+                names.setdefault(disp[i][0].split("(")[0].replace("void gh::", ""), []).append(i)
+            for kname, ids in names.items():
+                out.append((f"{s['name']}: {kname}", ids, None, 1, None))
         else:
             out.append((s["name"], seg, s.get("bytes_per_launch"), s.get("dispatches_per_unit", 1),
                         s.get("event_avg_us")))
@@ -249,7 +255,8 @@ def summarize(a) -> int:
     rows = defaultdict(dict)
     factors = {}
     names = []
-    for label, d in (("fetch", a.fetch), ("write", a.write), ("sq", a.sq), ("trace", a.trace)):
+    passes = [("fetch", a.fetch), ("write", a.write)] + [("sq", d) for d in (a.sq or [])] + [("trace", a.trace)]
+    for label, d in passes:
         if not d:
             continue
         disp = _dispatches(Path(d))
@@ -268,6 +275,7 @@ def summarize(a) -> int:
             r.setdefault("kernels", sorted({disp[i][0].split("(")[0] for i in seg}))
             for c, v in ctr_sum.items():
                 r[c] = v / len(seg)
+                r["sum:" + c] = v
             if label == "trace":
                 r["trace_avg_us"] = sum(disp[i][2] for i in seg) / len(seg) / 1e3
         for c in ("FETCH_SIZE", "WRITE_SIZE"):
@@ -288,7 +296,8 @@ def summarize(a) -> int:
         print(f"| {name} | {r.get('dispatches', '-')} | {f(algo)} | {f(fb)} | {f(wb)} | "
               + (f"{ratio:.3f} |" if ratio is not None else "- |"))
     sq = [c for c in ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_INSTS_VMEM_RD",
-                      "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_ACTIVE_INST_VALU") if any(c in r for r in rows.values())]
+                      "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_MFMA",
+                      "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_LDS_BANK_CONFLICT") if any(c in r for r in rows.values())]
     if sq:
         print()
         print("| segment | " + " | ".join(sq) + " | wait / wave cycles | VALU / wave | VMEM rd / wave |")
@@ -300,6 +309,18 @@ def summarize(a) -> int:
             wait = r.get("SQ_WAIT_INST_ANY", 0) / max(r.get("SQ_WAVE_CYCLES", 0), 1)
             print(f"| {name} | " + " | ".join(cells) +
                   f" | {wait:.3f} | {r.get('SQ_INSTS_VALU', 0) / waves:.1f} | {r.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} |")
+        mf = [(name, rows.get(name, {})) for name, _, _, _ in names if rows.get(name, {}).get("SQ_INSTS_MFMA")]
+        if mf:
+            print()
+            print("| segment | MFMA instructions (sum) | VALU / MFMA | LDS / MFMA | LDS bank-conflict cycles / LDS "
+                  "instruction |")
+            print("|---|---|---|---|---|")
+            for name, r in mf:
+                m = r["sum:SQ_INSTS_MFMA"]
+                bc = (f"{r['sum:SQ_LDS_BANK_CONFLICT'] / max(r.get('sum:SQ_INSTS_LDS', 0), 1):.3f}"
+                      if "sum:SQ_LDS_BANK_CONFLICT" in r else "-")
+                print(f"| {name} | {m:,.0f} | {r.get('sum:SQ_INSTS_VALU', 0) / m:.2f} | "
+                      f"{r.get('sum:SQ_INSTS_LDS', 0) / m:.2f} | {bc} |")
     if any("trace_avg_us" in r for r in rows.values()):
         print()
         print("| segment | kernels | traced avg us / unit | algorithmic GB/s | of 8 TB/s | dispatch-event avg us "
@@ -437,8 +458,9 @@ def main(argv=None) -> int:
     x.add_argument("--rounds", type=int, default=2000)
     s = sub.add_parser("summarize")
     s.add_argument("--manifest", required=True)
-    for k in ("fetch", "write", "sq", "trace"):
+    for k in ("fetch", "write", "trace"):
         s.add_argument(f"--{k}", default="")
+    s.add_argument("--sq", action="append", help="an SQ counter pass (may be given more than once)")
     a = ap.parse_args(argv)
     if a.cmd == "exchange":
         return exchange(a)
