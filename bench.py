@@ -5,9 +5,11 @@
 A step is one decode token through the whole model (26 layers + LM head +
 on-device argmax).  The seeded synthetic weights are generated on the host,
 uploaded once, and stay resident in HBM; a seeded 128-token prompt is fed
-one token per step (untimed, as in the reference's generation loop), then W
-warmup steps, then exactly K timed greedy steps (HIP events on the step
-stream, device-synchronised on both sides).
+one token per step (untimed, as in the reference's generation loop); W
+warmup steps run on a scratch cache, and exactly K timed greedy steps
+(HIP events on the step stream, device-synchronised on both sides) are
+centred on C3's mean position 256: positions 128..383 at the default K =
+256, 246..265 at K = 20.
 
 Prints ONE JSON line with tok/s; per-kernel-kind execution times measured
 inside real decode steps at C3's positions 128..383 (gh_profile_steps: the
@@ -35,6 +37,7 @@ HBM_PEAK_GBPS = 8000.0
 WEIGHT_SEED = 1234
 PROMPT_SEED = 1
 N_PROMPT = 128
+C3_MEAN_POSITION = 256  # C3: prompt 128, greedy generation at positions 128..383
 # HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, then
 # WRITE_SIZE, each scaled by bytes / counter of a 256 MiB device copy) over
 # replays of each kernel kind at position 257 (kernel_profile run --prompt
@@ -319,11 +322,18 @@ def main(argv=None) -> int:
     model.synth(WEIGHT_SEED, q4=True)
     log(f"model ready in {time.time() - t0:.1f}s")
     prompt = gh.synth_tokens(PROMPT_SEED, "prompt", N_PROMPT, cfg.vocab)
-    max_seq = N_PROMPT + a.warmup + a.steps + 8
-    kv = gh.KVCache(model, max_seq)
-    ms, ids = gh.bench_decode(model, kv, prompt, a.warmup, a.steps)
+    # C3 generates at positions 128..383 (mean 256).  The K timed steps are
+    # centred on that mean, from s0 = max(128, 256 - K/2): with the default
+    # K = 256 exactly C3's positions.  The W warmup steps run on a scratch
+    # cache of the same model; the timed cache is fed the prompt and
+    # advanced to s0 with untimed greedy steps, then K steps are timed.
+    s0 = max(N_PROMPT, C3_MEAN_POSITION - a.steps // 2)
+    if a.warmup > 0:
+        gh.bench_decode(model, gh.KVCache(model, N_PROMPT + a.warmup + 8), prompt, a.warmup - 1, 1)
+    kv = gh.KVCache(model, s0 + a.steps + 8)
+    ms, ids = gh.bench_decode(model, kv, prompt, s0 - N_PROMPT, a.steps)
     tok_s = a.steps / (ms / 1e3)
-    log(f"decode: {a.steps} steps in {ms:.3f} ms -> {tok_s:.1f} tok/s")
+    log(f"decode: {a.steps} steps at positions {s0}..{s0 + a.steps - 1} in {ms:.3f} ms -> {tok_s:.1f} tok/s")
 
     # kernel execution times inside real decode steps at C3's positions
     # 128..383: a second cache fed the prompt, then PROFILE_STEPS eager greedy
@@ -363,7 +373,8 @@ def main(argv=None) -> int:
         "warmup": a.warmup, "ms_per_step": round(ms / a.steps, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "gemma3-1b Q4_0 greedy decode, batch 1", "weights": "seeded synthetic Q4_0",
-                   "prompt_tokens": N_PROMPT, "timed_positions": [N_PROMPT + a.warmup, N_PROMPT + a.warmup + a.steps],
+                   "prompt_tokens": N_PROMPT, "timed_positions": [s0, s0 + a.steps - 1],
+                   "warmup_note": "W greedy steps on a scratch cache of the same model, before the timed cache",
                    "global_batch": 1, "parallelism": "single-gpu",
                    "step_algorithmic_bytes": int(step_bytes),
                    "step_frac_of_hbm_peak": round(step_bytes / (ms / a.steps * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
