@@ -297,7 +297,8 @@ def summarize(a) -> int:
               + (f"{ratio:.3f} |" if ratio is not None else "- |"))
     sq = [c for c in ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_INSTS_VMEM_RD",
                       "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_MFMA",
-                      "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_LDS_BANK_CONFLICT") if any(c in r for r in rows.values())]
+                      "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_LDS_BANK_CONFLICT", "SQ_WAIT_ANY", "SQ_ACTIVE_INST_LDS")
+          if any(c in r for r in rows.values())]
     if sq:
         print()
         print("| segment | " + " | ".join(sq) + " | wait / wave cycles | VALU / wave | VMEM rd / wave |")
