@@ -290,7 +290,14 @@ struct Profiler {
     };
     std::vector<Rec> recs;
     std::vector<std::string> names;
+    // events created before the launches (reserve), so that the enqueue
+    // loop only launches and keeps ahead of the GPU; the timed kernels then
+    // run back to back as in a graph replay
+    std::vector<hipEvent_t> pool;
     int kind_of(const char* name);
+    int reserve(size_t n_events);
+    void release_pool();
+    ~Profiler() { release_pool(); }
 };
 
 // kernels.hip: one decode step at position `pos` (patched per replay in graphs)

@@ -1485,10 +1485,17 @@ static int profiled_launch(Profiler* p, hipStream_t s, const char* name, double 
     Profiler::Rec r;
     r.kind = p->kind_of(name);
     r.bytes = bytes;
-    GH_HIP(hipEventCreate(&r.a));
-    if (hipEventCreate(&r.b) != hipSuccess) {
-        (void)hipEventDestroy(r.a);
-        return set_error(GH_ERR_HIP, "hipEventCreate failed");
+    if (p->pool.size() >= 2) {
+        r.b = p->pool.back();
+        p->pool.pop_back();
+        r.a = p->pool.back();
+        p->pool.pop_back();
+    } else {
+        GH_HIP(hipEventCreate(&r.a));
+        if (hipEventCreate(&r.b) != hipSuccess) {
+            (void)hipEventDestroy(r.a);
+            return set_error(GH_ERR_HIP, "hipEventCreate failed");
+        }
     }
     p->recs.push_back(r);
     GH_HIP(hipExtLaunchKernel(fn, grid, block, args, lds, s, r.a, r.b, 0));

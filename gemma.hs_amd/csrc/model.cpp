@@ -1453,6 +1453,24 @@ extern "C" int gh_bench_decode(gh_model* m, gh_kv* kv, const int32_t* prompt, in
 }
 
 // Per-kernel-kind totals of a profiled run; releases the events.
+int Profiler::reserve(size_t n_events) {
+    pool.reserve(pool.size() + n_events);
+    for (size_t i = 0; i < n_events; ++i) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) {
+            release_pool();
+            return set_error(GH_ERR_HIP, "hipEventCreate failed");
+        }
+        pool.push_back(e);
+    }
+    return GH_OK;
+}
+
+void Profiler::release_pool() {
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+    pool.clear();
+}
+
 static int collect_stats(Profiler& prof, gh_kernel_stat* stats, int32_t max_stats, int32_t* n_stats) {
     std::vector<double> tot(prof.names.size(), 0.0), bytes(prof.names.size(), 0.0);
     std::vector<int> cnt(prof.names.size(), 0);
@@ -1466,6 +1484,7 @@ static int collect_stats(Profiler& prof, gh_kernel_stat* stats, int32_t max_stat
         hipEventDestroy(r.b);
     }
     prof.recs.clear();
+    prof.release_pool();
     const int n = std::min<int>((int)prof.names.size(), max_stats);
     for (int i = 0; i < n; ++i) {
         std::memset(&stats[i], 0, sizeof(gh_kernel_stat));
@@ -1557,6 +1576,9 @@ extern "C" int gh_profile_steps(gh_model* m, gh_kv* kv, int32_t n_steps, gh_kern
     int tok = kv->h_st->last >= 0 && kv->h_st->last < m->cfg.vocab ? kv->h_st->last : 0;
     GH_CHECK(put_state(kv, kv->len, tok, kv->len, 0, 0));
     Profiler prof;
+    // two events per launch of the graph step (5 per layer + final norm, LM
+    // head, finish; the persistent step launches fewer)
+    GH_CHECK(prof.reserve(2 * (size_t)n_steps * (5 * (size_t)m->cfg.n_layers + 3)));
     Sink sink;
     sink.s = s;
     sink.prof = &prof;
