@@ -857,6 +857,7 @@ __device__ __forceinline__ void mq_item_multi_v(const DMat& w, int it, int s, in
     const int nk = kb1 - kb0;
     // an item past the last row tile loads nothing and writes nothing
     const int kl = live ? kb1 : kb0, nq = live ? (nk + 3) >> 2 : 0;
+    GH_MARK(0);
     typename Pro::Regs pr;
     if (lead) {
         if constexpr (HasLoadVariants<Pro>::value) pro.template load_v<V>(pr, kb0 * 32, nk * 32);
@@ -876,7 +877,9 @@ __device__ __forceinline__ void mq_item_multi_v(const DMat& w, int it, int s, in
 #pragma unroll
         for (int i = 0; i < Pro::kFinishBarriers; ++i) __syncthreads();
     }
+    GH_MARK(1);
     __syncthreads();
+    GH_MARK(2);
     float acc[RL][4];
 #pragma unroll
     for (int j = 0; j < RL; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
@@ -885,6 +888,7 @@ __device__ __forceinline__ void mq_item_multi_v(const DMat& w, int it, int s, in
         mq_load<QB, RL>(r, w, mv, tile, rbase, kb0 + 4 * q0, kl, wave);
         mq_compute<QB, RL>(r, q0, nq, L, acc);
     }
+    GH_MARK(3);
     // sum the 16 columns of each row; lane 16g then holds rows 4g .. 4g+3
 #pragma unroll
     for (int j = 0; j < RL; ++j)
@@ -897,10 +901,13 @@ __device__ __forceinline__ void mq_item_multi_v(const DMat& w, int it, int s, in
             for (int k = 0; k < 4; ++k) red[16 * (wave * RL + j) + 4 * (lane >> 4) + k] = acc[j][k];
     }
     __syncthreads();
+    GH_MARK(4);
     if (wave == 0 && live) {
         const float y0 = red[lane], y1 = RL == 2 ? red[64 + lane] : 0.0f;
         epi.template run<RL>(L, er, it, tile * TILE_ROWS + rbase + lane, s, y0, y1);
     }
+    GH_MARK(5);
+    GH_MARK_END();
 }
 
 // grid = ceil(items / NI) x S, NI x 256 threads; LDS: k_matvec's carve-up
