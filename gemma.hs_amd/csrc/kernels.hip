@@ -4765,12 +4765,17 @@ __global__ __launch_bounds__(NT) void k_pf_geglu(const float* part, int ld, int 
     for (int k = 4 * threadIdx.x; k < F; k += 4 * NT) a.put4(t, k, *(const float4*)&rowbuf[k], sc);
 }
 
-// Split count of a prefill GEMM over Pp token rows: enough for two
-// workgroups per CU, at most 8 (the workgroups' own latency chain, not the
-// partials' traffic, is what bounds these GEMMs at prompt sizes).
+// Split count of a prefill GEMM over Pp token rows, at most 8: enough for
+// two workgroups per CU where the columns are many (K >= 4096: the FFN's
+// down projection, whose workgroups' latency chain bounds it), one per CU
+// otherwise (QKV, O: there the next kernel's reads of the partials cost
+// more than the extra workgroups save).  Measured on MI355X, 512-token
+// prefill: QKV 426 -> 355 us and O 302 -> 267 us at one workgroup per CU;
+// down 831 -> 1048 us, so it keeps two.
 int pf_splits(const DMat& w, int Pp, int* kb_per) {
     const int wgs = (w.fmt == FMT_Q4 ? w.tiles * (8 / pf_ns(w, Pp)) : 2 * w.tiles) * (Pp / 64);
-    int S = std::max(1, std::min(8, (512 + wgs - 1) / wgs));
+    const int target = w.cols >= 4096 ? 512 : 256;
+    int S = std::max(1, std::min(8, (target + wgs - 1) / wgs));
     S = std::min(S, w.nblk);
     const int per = (w.nblk + S - 1) / S;
     if (kb_per) *kb_per = per;
