@@ -410,6 +410,14 @@ def phases(a) -> int:
         cells.append(f"{np.median((done - b[:, 0, 0]) * TICK_US):.2f}")
         print("| " + " | ".join(cells) + " |")
         print()
+        # the launch's span: when the workgroups finish, counted from the
+        # first workgroup's start (the kernel's tail beyond the median chain)
+        fin = (done - t0) * TICK_US
+        last = int(np.argmax(done))
+        print(f"Workgroups done, us after the first one started: p50 {np.median(fin):.2f}, "
+              f"p90 {np.percentile(fin, 90):.2f}, last {fin.max():.2f} (that workgroup started "
+              f"{(b[last, 0, 0] - t0) * TICK_US:.2f} us in and ran {(done[last] - b[last, 0, 0]) * TICK_US:.2f} us)")
+        print()
     return 0
 
 
