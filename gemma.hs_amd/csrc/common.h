@@ -297,6 +297,9 @@ struct Profiler {
     int kind_of(const char* name);
     int reserve(size_t n_events);
     void release_pool();
+    Profiler() = default;
+    Profiler(const Profiler&) = delete;  // owns the pooled events
+    Profiler& operator=(const Profiler&) = delete;
     ~Profiler() { release_pool(); }
 };
 
