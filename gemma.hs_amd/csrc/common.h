@@ -216,6 +216,7 @@ struct gh_model {
     gh::Plan pa, pc, pd, pe, plm;
     std::string plan_env;  // the GH_* switches set when the plans were made
     int attn_nc = 16;  // attention chunks per kv head
+    int attn_xcd = 1;  // a chunk's attention workgroups on one XCD (groups of 4+ q heads)
     // scratch
     float* x_res = nullptr;
     float* x1 = nullptr;

@@ -1654,6 +1654,7 @@ struct AttnArgs {
     float scale;
     float* part;
     int nc;
+    int xcd;  // HSP > 1: a chunk's workgroups on one XCD (attn_wg)
     // attended positions [pb, pe) in chunks of ch, n_used of them (host-derived)
     int pb, pe, ch, n_used;
     __host__ __device__ void set_range(int b, int e) {
@@ -2269,11 +2270,31 @@ __device__ __forceinline__ void attn_step_body(const AttnArgs& a, int g, int j, 
     GH_MARK_END();
 }
 
+// Workgroup b of a launch runs on XCD b % 8.  With HSP > 1 workgroups per
+// chunk (q heads split between them), chunk gj's workgroups are
+// b = 8 * (HSP * (gj / 8) + hs) + gj % 8, all on XCD gj % 8, so that the
+// chunk's K/V rows come into one L2 instead of HSP of them; the grid is
+// rounded up to whole groups of 8 chunks (false: a workgroup past the last
+// chunk).  AttnArgs::xcd = 0 keeps b = HSP * gj + hs.
+template <int HSP>
+__device__ __forceinline__ bool attn_wg(const AttnArgs& a, int& gj, int& hs) {
+    if (HSP == 1 || !a.xcd) {
+        hs = blockIdx.x % HSP;
+        gj = blockIdx.x / HSP;
+        return true;
+    }
+    const int r = blockIdx.x & 7, q = blockIdx.x >> 3;
+    hs = q % HSP;
+    gj = (q / HSP) * 8 + r;
+    return gj < a.nkv * a.nc;
+}
+
 // HSP workgroups per chunk, each taking G / HSP of the group's q heads.
 template <int HD, int G, int HSP = 1>
 __global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
     constexpr int GW = G / HSP;
-    const int hs = blockIdx.x % HSP, gj = blockIdx.x / HSP;
+    int hs, gj;
+    if (!attn_wg<HSP>(a, gj, hs)) return;
     const int g = gj / a.nc, j = gj % a.nc;
     if (j >= a.n_used) return;  // uniform per workgroup
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
@@ -2300,7 +2321,8 @@ __global__ __launch_bounds__(NT) void k_attn_step(AttnArgs a) {
 template <int HD, int G, int HSP = 1>
 __global__ __launch_bounds__(NT) void k_attn_op(AttnArgs a) {
     constexpr int GW = G / HSP;
-    const int hs = blockIdx.x % HSP, gj = blockIdx.x / HSP;
+    int hs, gj;
+    if (!attn_wg<HSP>(a, gj, hs)) return;
     const int g = gj / a.nc, j = gj % a.nc;
     if (j >= a.n_used) return;  // uniform per workgroup
     const int c0 = a.pb + j * a.ch, c1 = min(a.pe, c0 + a.ch);
@@ -2317,10 +2339,13 @@ static int launch_attn_step(Sink& k, double bytes, int hd, int G, const AttnArgs
     // Measured on MI355X, 1B (4 heads per kv head): attention 5.15 us with
     // one workgroup per chunk, 4.28 with two (two heads each), 3.91 with
     // four; 1450 -> 1495 -> 1511 tok/s.  With 2 heads per kv head (4B) one
-    // head per workgroup is slower (4.33 -> 4.88 us), so those stay whole.
+    // head per workgroup is slower (4.33 -> 4.88 us; with a chunk's two
+    // workgroups on one XCD, C5 740 vs 759 tok/s), so those stay whole.
+    // A chunk's workgroups share one XCD (attn_wg): 1B 1632-1633 tok/s
+    // against 1605-1606 with consecutive workgroups on different XCDs.
     static const char* hs_env = std::getenv("GH_ATTN_HSPLIT");  // 0: one workgroup per chunk
     const int hsp = G >= 4 && !(hs_env && *hs_env == '0') ? G : 1;
-    const dim3 grid(nkv * a.nc * hsp), block(NT);
+    const dim3 grid(hsp > 1 && a.xcd ? 8 * hsp * ((nkv * a.nc + 7) / 8) : nkv * a.nc * hsp), block(NT);
 #define GH_ATTN_CASE(HD_, G_)                                                                                  \
     if (hd == HD_ && G == G_)                                                                                  \
         return hsp > 1 ? sink_launch<0>(k, "attention", bytes, k_attn_step<HD_, G_, (G_ >= 4 ? G_ : 1)>, grid,   \
@@ -4008,6 +4033,7 @@ int enqueue_step(gh_model* m, gh_kv* kv, Sink& sink, int pos) {
             a.scale = 1.0f / sqrtf((float)hd);
             a.part = m->attn_part;
             a.nc = m->attn_nc;
+            a.xcd = m->attn_xcd;
             a.set_pos(pos);
             GH_CHECK(launch_attn_step(sink, 2.0 * 4.0 * hd * nkv * (a.pe - a.pb), hd, G, a, nkv));
         }
@@ -5122,7 +5148,9 @@ int launch_attention(const float* q, const float* kc, const float* vc, int nq, i
     const bool hsplit = hd == 256 && views_ok && (G == 4 || G == 8) && nkv * a.n_used * G <= 256 &&
                         !(hs_env && *hs_env == '0');
     if (hsplit) {
-        const dim3 grid(nkv * a.nc * G);
+        const char* xe = std::getenv("GH_ATTN_XCD");  // 0: workgroups in plain order
+        a.xcd = xe && *xe == '0' ? 0 : 1;
+        const dim3 grid(a.xcd ? 8 * G * ((nkv * a.nc + 7) / 8) : nkv * a.nc * G);
         if (G == 4) hipLaunchKernelGGL((k_attn_op<256, 4, 4>), grid, dim3(NT), 0, s, a);
         else hipLaunchKernelGGL((k_attn_op<256, 8, 8>), grid, dim3(NT), 0, s, a);
     } else if (hd == 256 && g_ok && views_ok && (a.ch >= 64 || a.n_used >= 64)) {

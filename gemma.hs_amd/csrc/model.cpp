@@ -207,7 +207,7 @@ std::string env_switches() {
         "GH_PLAN_A_S", "GH_PLAN_C_S", "GH_PLAN_D_S", "GH_PLAN_E_S", "GH_PLAN_A_RL", "GH_PLAN_C_RL", "GH_PLAN_D_RL",
         "GH_PLAN_E_RL", "GH_PLAN_LM_RL", "GH_PLAN_A_NI", "GH_PLAN_C_NI", "GH_PLAN_D_NI", "GH_PLAN_E_NI",
         "GH_PLAN_A_MFMA", "GH_PLAN_D_MFMA", "GH_PLAN_E_MFMA", "GH_PLAN_LM_MFMA", "GH_ATTN_NC", "GH_ATTN_HSPLIT",
-        "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA"};
+        "GH_ATTN_XCD", "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA"};
     std::string env;
     for (const char* v : vars) {
         const char* val = std::getenv(v);
@@ -308,6 +308,7 @@ void make_plans(gh_model* m) {
     m->pd.mfma = env_int("GH_PLAN_D_MFMA", m->pd.mfma);
     m->pe.mfma = env_int("GH_PLAN_E_MFMA", m->pe.mfma);
     m->attn_nc = std::max(1, std::min(64, env_int("GH_ATTN_NC", 64)));
+    m->attn_xcd = env_int("GH_ATTN_XCD", 1) ? 1 : 0;
 }
 
 int ensure_scratch(gh_model* m) {
@@ -1194,7 +1195,7 @@ extern "C" int gh_model_plan(gh_model* m, char* buf, size_t cap, size_t* len_out
     phase("gate_up", m->pd);
     phase("down", m->pe);
     phase("lm_head", m->plm);
-    s += " attn_chunks=" + std::to_string(m->attn_nc);
+    s += " attn_chunks=" + std::to_string(m->attn_nc) + (m->attn_xcd ? "" : ",xcd_off");
     s += std::string(" lm=") + (m->has_lm ? "untied" : "tied");
     s += " env=" + (m->plan_env.empty() ? std::string("none") : m->plan_env);
     if (len_out) *len_out = s.size();

@@ -223,6 +223,39 @@ def test_long_attention_chunks_live_oracle(ctx, nq, nkv, monkeypatch):
             assert rel_err(logits, olog) < ACT_TOL, pos
 
 
+def test_attention_workgroup_order_is_bit_identical_live_oracle(ctx, monkeypatch):
+    """Groups of 4 q heads run one attention workgroup per (chunk, q head).
+    By default a chunk's four workgroups sit on one XCD (blockIdx rounded to
+    whole groups of 8 chunks); GH_ATTN_XCD=0 numbers them consecutively.
+    Only which workgroup computes which chunk differs, so every layer state
+    and the logits are bit-identical, and within tolerance of the live
+    oracle.  2 kv heads x 5 chunks (GH_ATTN_NC=5): 10 chunks, not a
+    multiple of 8, so the rounded grid has workgroups past the last chunk."""
+    monkeypatch.setenv("GH_ATTN_NC", "5")
+    cfg = gh.preset("gemma3-1b")
+    cfg.n_heads, cfg.n_kv_heads = 8, 2
+    cfg.vocab, cfg.hidden, cfg.n_layers, cfg.ffn = 2048, 512, 3, 1024
+    cfg.sliding_window, cfg.global_every, cfg.max_seq = 24, 3, 64
+    models = []
+    for xcd in ("0", "1"):
+        monkeypatch.setenv("GH_ATTN_XCD", xcd)
+        m = _gpu_model(ctx, cfg, 31, True)
+        assert ("xcd_off" in m.plan()) == (xcd == "0")
+        models.append((m, gh.KVCache(m, 64)))
+    om = _oracle_model(cfg, 31, True)
+    toks = gh.synth_tokens(10, "t", 40, cfg.vocab)
+    for pos, t in enumerate(toks):
+        (l0, _, y0, n0), (l1, _, y1, n1) = (gh.runGemmaInferenceCachedWithLayer0(m, int(t), kv) for m, kv in models)
+        assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32)), pos
+        assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32)), pos
+        assert n0 == n1
+        olog, olay, _ = om.step(int(t), pos, want_layers=True)
+        if pos % 5 == 0 or pos >= 36:
+            for l in range(cfg.n_layers):
+                assert rel_err(y1[l], olay[l]) < ACT_TOL, (pos, l)
+            assert rel_err(l1, olog) < ACT_TOL, pos
+
+
 def test_errors_kv_full_bad_token_incomplete_model(ctx):
     cfg = gh.preset("tiny")
     m = _gpu_model(ctx, cfg, 1, False)
