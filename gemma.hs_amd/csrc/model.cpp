@@ -995,6 +995,16 @@ extern "C" int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out
     if (c.hidden % 32 || c.ffn % 32 || (c.n_heads * c.head_dim) % 32)
         return set_error(GH_ERR_INVALID, "config: hidden, ffn and n_heads*head_dim must be multiples of 32");
     if (c.mode != GH_MODE_GEMMA3 && c.mode != GH_MODE_REF) return set_error(GH_ERR_INVALID, "config: bad mode");
+    // the residual prologues hold at most 3 float4 groups of the hidden
+    // vector per thread of a 256-thread workgroup
+    if (c.hidden > 3072) return set_error(GH_ERR_INVALID, "config: hidden %d above 3072", c.hidden);
+    if (c.sliding_window < 0 || c.global_every < 0)
+        return set_error(GH_ERR_INVALID, "config: sliding_window and global_every must be >= 0");
+    if (!(c.rope_theta_local > 0.0f) || !(c.rope_theta_global > 0.0f) || std::isinf(c.rope_theta_local) ||
+        std::isinf(c.rope_theta_global))
+        return set_error(GH_ERR_INVALID, "config: RoPE theta must be finite and > 0");
+    if (!(c.rms_eps >= 0.0f) || std::isinf(c.rms_eps))
+        return set_error(GH_ERR_INVALID, "config: rms_eps must be finite and >= 0");
     Lock lk(ctx->mu);
     std::unique_ptr<gh_model> m(new gh_model);
     m->ctx = ctx;

@@ -193,6 +193,11 @@ typedef struct gh_config {
 int gh_config_preset(const char* name, gh_config* out);
 
 typedef struct gh_model gh_model;
+/* GH_ERR_INVALID for shapes the kernels do not support: head_dim other than
+ * 32/128/256, n_heads/n_kv_heads other than 1/2/4/8, hidden above 3072,
+ * hidden/ffn/n_heads*head_dim not multiples of 32; and for a negative
+ * window or global period, RoPE theta not finite and > 0, rms_eps negative
+ * or not finite. */
 int gh_model_create(gh_ctx* ctx, const gh_config* cfg, gh_model** out);
 int gh_model_destroy(gh_model* m);
 void gh_model_release(gh_model* m); /* gh_model_destroy for finalisers */

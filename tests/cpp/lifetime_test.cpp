@@ -185,9 +185,52 @@ int race() {
     return 0;
 }
 
+// gh_model_create rejects configurations the kernels do not support, and
+// creates nothing for them.
+int config_checks() {
+    gh_ctx* ctx = nullptr;
+    CHECK(gh_ctx_create(0, &ctx) == GH_OK);
+    gh_config base;
+    CHECK(gh_config_preset("gemma3-4b", &base) == GH_OK);
+    gh_model* m = nullptr;
+    CHECK(gh_model_create(ctx, &base, &m) == GH_OK && m);
+    CHECK(gh_model_destroy(m) == GH_OK);
+    auto rejects = [&](void (*edit)(gh_config&)) {
+        gh_config c = base;
+        edit(c);
+        gh_model* bad = nullptr;
+        return gh_model_create(ctx, &c, &bad) == GH_ERR_INVALID && bad == nullptr;
+    };
+    CHECK(rejects([](gh_config& c) { c.hidden = 3104; }));
+    CHECK(rejects([](gh_config& c) { c.hidden = 1000; }));
+    CHECK(rejects([](gh_config& c) { c.head_dim = 64; }));
+    CHECK(rejects([](gh_config& c) { c.n_kv_heads = 3; }));
+    CHECK(rejects([](gh_config& c) { c.n_heads = 48; }));  // group 12
+    CHECK(rejects([](gh_config& c) { c.sliding_window = -1; }));
+    CHECK(rejects([](gh_config& c) { c.global_every = -6; }));
+    CHECK(rejects([](gh_config& c) { c.rope_theta_local = 0.0f; }));
+    CHECK(rejects([](gh_config& c) { c.rope_theta_global = -1e6f; }));
+    CHECK(rejects([](gh_config& c) { c.rope_theta_global = 1.0f / 0.0f; }));
+    CHECK(rejects([](gh_config& c) { c.rms_eps = -1e-6f; }));
+    CHECK(rejects([](gh_config& c) { c.rms_eps = 0.0f / 0.0f; }));
+    CHECK(rejects([](gh_config& c) { c.mode = 7; }));
+    CHECK(rejects([](gh_config& c) { c.max_seq = 0; }));
+    gh_config wide = base;
+    wide.hidden = 3072;
+    CHECK(gh_model_create(ctx, &wide, &m) == GH_OK);
+    CHECK(gh_model_destroy(m) == GH_OK);
+    CHECK(gh_ctx_destroy(ctx) == GH_OK);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
+    if (argc > 1 && std::strcmp(argv[1], "config") == 0) {
+        if (config_checks()) return 1;
+        std::printf("config ok\n");
+        return 0;
+    }
     if (argc > 1 && std::strcmp(argv[1], "race") == 0) {
         if (race()) return 1;
         std::printf("race ok\n");

@@ -85,3 +85,14 @@ def test_interpreter_exit_finaliser_order_is_clean_under_asan(lifetime_exe):
     that, before handles were reference counted, read the freed context."""
     r = _run(lifetime_exe, "exit")
     assert r.returncode == 0 and "exit order ok" in r.stdout, r.stdout + r.stderr[-4000:]
+
+
+def test_model_create_rejects_unsupported_configs(lifetime_exe):
+    """gh_model_create refuses, with GH_ERR_INVALID and no handle, the
+    configurations the kernels do not support (hidden above 3072 or not a
+    multiple of 32, head_dim other than 32/128/256, groups other than
+    1/2/4/8) and malformed ones (negative window or global period, RoPE
+    theta not finite and > 0, eps negative or NaN, unknown mode, no KV
+    capacity); hidden 3072 is accepted."""
+    r = _run(lifetime_exe, "config")
+    assert r.returncode == 0 and "config ok" in r.stdout, r.stdout + r.stderr[-4000:]
