@@ -556,20 +556,22 @@ __device__ __forceinline__ void mv_item(const DMat& w, int rt, int s, int S, con
 // ------------------------------------------------------------------
 // A wave takes 16-row groups; one MFMA pair covers a group's rows x a quad
 // of 4 column blocks:
-//   A (16 rows x 64): lane m + 16g holds the 16 code bytes of row m, block
+//   B (64 x 16): lane m + 16g holds the 16 code bytes of row m, block
 //     4q+g; their low nibbles feed the first MFMA and the high ones the
 //     second, each as the int8 16*(q-8) (q ^ 8 is q-8 as a signed nibble);
-//   B (64 x 16): column n = 4*b + limb; lane n + 16g holds limb n%4 of
+//   A (16 x 64): row n = 4*b + limb; lane n + 16g holds limb n%4 of
 //     elements 0..15 (first MFMA) or 16..31 (second) of block 4q+g when
 //     n/4 == g, and zeros otherwise;
-//   D[m][n] = 16 * sum_p (q_mp - 8) * limb_{n%4}(X_p) over block 4q + n/4,
-//     exact in int32; lane L holds rows 4(L/16)+i of column L%16.
-// Each lane scales its D by the rows' fp16 block scales and the block/limb
-// multiplier and accumulates in f32; a 16-lane sum adds a row's columns.
+//   D[n][m] = 16 * sum_p (q_mp - 8) * limb_{n%4}(X_p) over block 4q + n/4,
+//     exact in int32 (|D| < 2^19); lane L holds D[4(L/16)+i][L%16], i.e.
+//     row L%16, block 4q + L/16, limbs 0..3.
+// Each lane combines its four limbs (X = L0 + 2^7 L1 + 2^14 L2 + 2^21 L3),
+// scales by the row's fp16 block scale and the block multiplier, and
+// accumulates in f32; the four blocks of a quad meet in a cross-row sum.
 template <int QB, int RL>
 struct QRegs {
-    u32x4 c[RL][QB];  // codes: row (lane & 15) of the row group, block 4q + lane/16
-    u32x2 s[RL][QB];  // fp16 scales: rows 4*(lane/16) .. +3, block 4q + (lane & 15)/4
+    u32x4 c[RL][QB];     // codes: row (lane & 15) of the row group, block 4q + lane/16
+    uint16_t s[RL][QB];  // fp16 scale of the same row and block
 };
 
 // Loads of one register batch: quads q0 .. q0+QB-1 (first block kq) of the
@@ -584,11 +586,10 @@ __device__ __forceinline__ void mq_load(QRegs<QB, RL>& r, const DMat& w, const M
         const int r16 = rbase + 16 * (wave * RL + j);
 #pragma unroll
         for (int i = 0; i < QB; ++i) {
-            const int ka = kq + 4 * i + (lane >> 4), ks = kq + 4 * i + ((lane & 15) >> 2);
+            const int ka = kq + 4 * i + (lane >> 4);
             const uint32_t ea = tb + (uint32_t)ka * TILE_ROWS + (uint32_t)(r16 + (lane & 15));
-            const uint32_t es = tb + (uint32_t)ks * TILE_ROWS + (uint32_t)(r16 + 4 * (lane >> 4));
             r.c[j][i] = v.codes.template u4<CP_NT>(ka < kb1 ? ea * 16u : OOB);
-            r.s[j][i] = v.scales.template u2<CP_NT>(ks < kb1 ? es * 2u : OOB);
+            r.s[j][i] = v.scales.template h1<CP_NT>(ka < kb1 ? ea * 2u : OOB);
         }
     }
 }
@@ -596,15 +597,14 @@ __device__ __forceinline__ void mq_load(QRegs<QB, RL>& r, const DMat& w, const M
 // The MFMA pairs of quad i of a register batch; bl = first block of the quad
 // within the slice.
 template <int QB, int RL>
-__device__ __forceinline__ void mq_quad(const QRegs<QB, RL>& r, int i, int bl, const MvLds& L, float (&acc)[RL][4]) {
+__device__ __forceinline__ void mq_quad(const QRegs<QB, RL>& r, int i, int bl, const MvLds& L, float (&acc)[RL]) {
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const bool act = (n >> 2) == g;
-    const float lp = (float)(1u << (7 * (n & 3)));
     // 16-byte limb chunks: block * 8 + half * 4 + limb
     const i32x4* lb = (const i32x4*)L.xs + ((bl + g) * 8 + (n & 3));
     const i32x4* zero = (const i32x4*)L.zero;
     const i32x4 b0 = *(act ? lb : zero), b1 = *(act ? lb + 4 : zero);
-    const float mq = L.sxs[bl + (n >> 2)] * lp;
+    const float mq = L.sxs[bl + g];
 #pragma unroll
     for (int j = 0; j < RL; ++j) {
         const u32x4 c = r.c[j][i];
@@ -614,20 +614,19 @@ __device__ __forceinline__ void mq_quad(const QRegs<QB, RL>& r, int i, int bl, c
             ahi[k] = (int)((c[k] ^ 0x80808080u) & 0xF0F0F0F0u);
             alo[k] = (int)(((c[k] << 4) ^ 0x80808080u) & 0xF0F0F0F0u);
         }
-        i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, b0, (i32x4){0, 0, 0, 0}, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, b1, d, 0, 0, 0);
-        const u32x2 sc = r.s[j][i];
-        acc[j][0] = fmaf((float)d[0], h2f((uint16_t)sc.x) * mq, acc[j][0]);
-        acc[j][1] = fmaf((float)d[1], h2f((uint16_t)(sc.x >> 16)) * mq, acc[j][1]);
-        acc[j][2] = fmaf((float)d[2], h2f((uint16_t)sc.y) * mq, acc[j][2]);
-        acc[j][3] = fmaf((float)d[3], h2f((uint16_t)(sc.y >> 16)) * mq, acc[j][3]);
+        i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(b0, alo, (i32x4){0, 0, 0, 0}, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(b1, ahi, d, 0, 0, 0);
+        // limbs 0+1 and 2+3 exactly in int32 (|D| < 2^19), then in f32
+        const int lo01 = d[0] + d[1] * 128, hi23 = d[2] + d[3] * 128;
+        const float x = fmaf((float)hi23, 16384.0f, (float)lo01);
+        acc[j] = fmaf(x, h2f(r.s[j][i]) * mq, acc[j]);
     }
 }
 
 // The MFMA pairs of quads q0 .. min(q0+QB, nq)-1 (quad q: blocks 4q.. of the slice).
 template <int QB, int RL>
 __device__ __forceinline__ void mq_compute(const QRegs<QB, RL>& r, int q0, int nq, const MvLds& L,
-                                           float (&acc)[RL][4]) {
+                                           float (&acc)[RL]) {
     if (q0 + QB <= nq) {  // full batch: straight-line (nq is wave-uniform)
 #pragma unroll
         for (int i = 0; i < QB; ++i) mq_quad<QB, RL>(r, i, 4 * (q0 + i), L, acc);
@@ -669,25 +668,24 @@ __device__ __forceinline__ void mq_item_v(const DMat& w, int rt, int s, int S, c
     GH_MARK(1);
     __syncthreads();
     GH_MARK(2);
-    float acc[RL][4];
+    float acc[RL];
 #pragma unroll
-    for (int j = 0; j < RL; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+    for (int j = 0; j < RL; ++j) acc[j] = 0.0f;
     mq_compute<QB, RL>(r, 0, nq, L, acc);
     for (int q0 = QB; q0 < nq; q0 += QB) {
         mq_load<QB, RL>(r, w, mv, tile, rbase, kb0 + 4 * q0, kb1, wave);
         mq_compute<QB, RL>(r, q0, nq, L, acc);
     }
     GH_MARK(3);
-    // sum the 16 columns of each row; lane 16g then holds rows 4g .. 4g+3
+    // sum the four blocks of each row; lane m < 16 then holds row m
 #pragma unroll
-    for (int j = 0; j < RL; ++j)
+    for (int j = 0; j < RL; ++j) {
+        acc[j] += __shfl_xor(acc[j], 32, 64);
+        acc[j] += __shfl_xor(acc[j], 16, 64);
+    }
+    if (lane < 16) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc[j][k] = row16_sum(acc[j][k]);
-    if ((lane & 15) == 0) {
-#pragma unroll
-        for (int j = 0; j < RL; ++j)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) L.red[16 * (wave * RL + j) + 4 * (lane >> 4) + k] = acc[j][k];
+        for (int j = 0; j < RL; ++j) L.red[16 * (wave * RL + j) + lane] = acc[j];
     }
     __syncthreads();
     GH_MARK(4);
@@ -880,25 +878,24 @@ __device__ __forceinline__ void mq_item_multi_v(const DMat& w, int it, int s, in
     GH_MARK(1);
     __syncthreads();
     GH_MARK(2);
-    float acc[RL][4];
+    float acc[RL];
 #pragma unroll
-    for (int j = 0; j < RL; ++j) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+    for (int j = 0; j < RL; ++j) acc[j] = 0.0f;
     mq_compute<QB, RL>(r, 0, nq, L, acc);
     for (int q0 = QB; q0 < nq; q0 += QB) {
         mq_load<QB, RL>(r, w, mv, tile, rbase, kb0 + 4 * q0, kl, wave);
         mq_compute<QB, RL>(r, q0, nq, L, acc);
     }
     GH_MARK(3);
-    // sum the 16 columns of each row; lane 16g then holds rows 4g .. 4g+3
+    // sum the four blocks of each row; lane m < 16 then holds row m
 #pragma unroll
-    for (int j = 0; j < RL; ++j)
+    for (int j = 0; j < RL; ++j) {
+        acc[j] += __shfl_xor(acc[j], 32, 64);
+        acc[j] += __shfl_xor(acc[j], 16, 64);
+    }
+    if (lane < 16) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc[j][k] = row16_sum(acc[j][k]);
-    if ((lane & 15) == 0) {
-#pragma unroll
-        for (int j = 0; j < RL; ++j)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) red[16 * (wave * RL + j) + 4 * (lane >> 4) + k] = acc[j][k];
+        for (int j = 0; j < RL; ++j) red[16 * (wave * RL + j) + lane] = acc[j];
     }
     __syncthreads();
     GH_MARK(4);
@@ -3322,8 +3319,8 @@ __device__ void ps_prefetch(const PLayer& P, int c, float* pf, bool down) {
 
 // The staged chunk's 64 gate/up rows on the int8 matrix cores, against the
 // whole-row slice in xs/sxs in the FMT_Q4M limb format (L.zero cleared):
-// wave w takes rows 16w .. 16w + 15,
-// one MFMA pair per quad of column blocks as in mq_quad, with the codes and
+// wave w takes rows 16w .. 16w + 15, one MFMA pair per quad of column
+// blocks with the operands and combination of mq_quad, the codes and
 // scales read from the staged LDS copy (blocks past nb: zero codes and
 // scales against zero limbs).
 __device__ void ps_gu_lds_mfma(const float* pf, int nb, const MvLds& L, float* y) {
@@ -3332,37 +3329,31 @@ __device__ void ps_gu_lds_mfma(const float* pf, int nb, const MvLds& L, float* y
     const u32x4* cw = (const u32x4*)(pf + Y.gc);
     const uint16_t* sw = (const uint16_t*)(pf + Y.gs);
     const bool act = (n >> 2) == g;
-    const float lp = (float)(1u << (7 * (n & 3)));
     const i32x4* zero = (const i32x4*)L.zero;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc = 0.0f;
     const int nq = (nb + 3) >> 2;
     for (int q = 0; q < nq; ++q) {
-        const int ka = 4 * q + g, ks = 4 * q + (n >> 2);
+        const int ka = 4 * q + g;
         const u32x4 c = ka < nb ? cw[ka * 64 + r16 + n] : (u32x4){0u, 0u, 0u, 0u};
-        const u32x2 sc = ks < nb ? *(const u32x2*)(sw + ks * 64 + r16 + 4 * g) : (u32x2){0u, 0u};
+        const uint16_t sc = ka < nb ? sw[ka * 64 + r16 + n] : (uint16_t)0;
         const i32x4* lb = (const i32x4*)L.xs + ((4 * q + g) * 8 + (n & 3));
         const i32x4 b0 = *(act ? lb : zero), b1 = *(act ? lb + 4 : zero);
-        const float mq = L.sxs[4 * q + (n >> 2)] * lp;
+        const float mq = L.sxs[4 * q + g];
         i32x4 alo, ahi;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {  // 16 * (q - 8) as int8: q ^ 8 is q - 8 as a signed nibble
             ahi[k] = (int)((c[k] ^ 0x80808080u) & 0xF0F0F0F0u);
             alo[k] = (int)(((c[k] << 4) ^ 0x80808080u) & 0xF0F0F0F0u);
         }
-        i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, b0, (i32x4){0, 0, 0, 0}, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, b1, d, 0, 0, 0);
-        acc[0] = fmaf((float)d[0], h2f((uint16_t)sc.x) * mq, acc[0]);
-        acc[1] = fmaf((float)d[1], h2f((uint16_t)(sc.x >> 16)) * mq, acc[1]);
-        acc[2] = fmaf((float)d[2], h2f((uint16_t)sc.y) * mq, acc[2]);
-        acc[3] = fmaf((float)d[3], h2f((uint16_t)(sc.y >> 16)) * mq, acc[3]);
+        i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(b0, alo, (i32x4){0, 0, 0, 0}, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(b1, ahi, d, 0, 0, 0);
+        const int lo01 = d[0] + d[1] * 128, hi23 = d[2] + d[3] * 128;
+        acc = fmaf(fmaf((float)hi23, 16384.0f, (float)lo01), h2f(sc) * mq, acc);
     }
-    // sum the 16 columns of each row; lane 16g then holds rows 4g .. 4g + 3
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc[k] = row16_sum(acc[k]);
-    if (n == 0) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) L.red[r16 + 4 * g + k] = acc[k];
-    }
+    // sum the four blocks of each row; lane m < 16 then holds row m
+    acc += __shfl_xor(acc, 32, 64);
+    acc += __shfl_xor(acc, 16, 64);
+    if (lane < 16) L.red[r16 + lane] = acc;
     __syncthreads();
     if (wave == 0) y[lane] = L.red[lane];
 }
