@@ -295,15 +295,15 @@ void make_plans(gh_model* m) {
     m->pd.ni = env_int("GH_PLAN_D_NI", m->pd.ni);
     m->pe.ni = env_int("GH_PLAN_E_NI", m->pe.ni);
     for (Plan* p : {&m->pa, &m->pc, &m->pd, &m->pe}) p->ni = p->ni == 2 ? 2 : 1;
-    // Paired items may run their dot products on the matrix cores: the lead
+    // Paired items run their dot products on the matrix cores: the lead
     // waves then build int8 limbs of the slice (a longer prologue) and the
-    // dot phase shrinks, which pays on wide splits only.  Measured on
-    // MI355X: 1B gate/up (9 blocks per split) 5.45 -> 5.66 us; 4B gate/up
-    // (27) 10.42 -> 10.20 us; 4B down (40) 7.0 -> 6.6 us, 822 -> 835 tok/s.
-    for (Plan* p : {&m->pa, &m->pd, &m->pe}) {
-        const DMat& d = p == &m->pa ? L.qkv : p == &m->pd ? L.gu : L.down;
-        p->mfma = m->fmt == FMT_Q4 && p->ni == 2 && (d.nblk + p->S - 1) / p->S >= 24 ? 1 : 0;
-    }
+    // dot phase shrinks.  Measured on MI355X, models differing only in this
+    // choice alternating in one process: 1B gate/up (12 blocks per split)
+    // 5.96 -> 5.74 us, 1618 -> 1632 tok/s; 4B 751 -> 773 tok/s (gate/up)
+    // and 762 -> 773 (down).  One item per workgroup stays on the VALU: 1B
+    // qkv on the matrix cores 1618 -> 1626 tok/s but 4B qkv 773 -> 771, 1B
+    // down 1618 -> 1615.
+    for (Plan* p : {&m->pa, &m->pd, &m->pe}) p->mfma = m->fmt == FMT_Q4 && p->ni == 2 ? 1 : 0;
     m->pa.mfma = env_int("GH_PLAN_A_MFMA", m->pa.mfma);
     m->pd.mfma = env_int("GH_PLAN_D_MFMA", m->pd.mfma);
     m->pe.mfma = env_int("GH_PLAN_E_MFMA", m->pe.mfma);
