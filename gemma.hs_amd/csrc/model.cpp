@@ -710,10 +710,10 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     const int max_s = env_int("GH_Q4_MAXS", 2 * d.tiles >= 96 ? 1 : 16);
     t->plan = choose_plan(FMT_Q4, d.tiles, d.nblk, env_int("GH_Q4_TARGET", 512), max_s);
     t->plan.rl = env_int("GH_Q4_RL", 1) == 2 ? 2 : 1;
-    // matrix-core dot products when the matvec is dot-bound (at least 8
-    // workgroups per CU: 262144 x 1152 31.6 us vs 34.5 us on the VALU; the
-    // 6912-row shapes are faster on the VALU)
-    t->plan.mfma = env_int("GH_Q4_MFMA", t->plan.row_tiles(d.tiles) * t->plan.S >= 2048 ? 1 : 0);
+    // dot products on the matrix cores: over cold copies on MI355X,
+    // 262144 x 1152 29.5 us against 34.5 on the VALU, 6912 x 1152 4.01
+    // against 4.41, 1152 x 6912 5.76 against 5.87
+    t->plan.mfma = env_int("GH_Q4_MFMA", 1);
     if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
     ctx->q4s.push_back(t.get());
     *out = t.release();
