@@ -57,6 +57,7 @@ struct DMat {
     int cols = 0;   // logical columns
     int nblk = 0;   // column blocks (cols/32 for Q4_0, cols/4 for F32)
     int tiles = 0;  // ceil(rows / 128)
+    int order_in = 0;  // matvec: a barrier between the input loads and the weight loads
 };
 
 inline int block_cols(int fmt) { return fmt == FMT_F32 ? 4 : 32; }
@@ -88,6 +89,7 @@ struct Plan {
     int rl = 2;  // rows per lane: 2 = 128-row workgroups, 1 = 64-row workgroups
     int mfma = 0;  // Q4_0: dot products on the int8 matrix cores (1) or the VALU (0)
     int ni = 1;    // work items per workgroup (1 or 2; 4 waves each, one prologue)
+    int order_in = 1;  // every wave's input loads issue before any wave's weight loads
     int row_tiles(int tiles) const { return rl == 2 ? tiles : 2 * tiles; }
 };
 

@@ -659,6 +659,8 @@ __device__ __forceinline__ void mq_item_v(const DMat& w, int rt, int s, int S, c
     typename Epi::Regs er;
     epi.load(er);
     __builtin_amdgcn_sched_barrier(0);
+    if (w.order_in) __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     const MatViews mv(w);
     QRegs<QB, RL> r;
     mq_load<QB, RL>(r, w, mv, tile, rbase, kb0, kb1, wave);
@@ -740,6 +742,8 @@ __device__ __forceinline__ void mv_item_valu(const DMat& w, int rt, int s, int S
     // the scheduler may not interleave the three groups: a prologue add
     // hoisted above a weight load would make that load wait for the inputs
     __builtin_amdgcn_sched_barrier(0);
+    if (w.order_in) __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     const MatViews mv(w);
     WRegs<FMT, KBW> r;
     mv_load<FMT, KBW, RL>(r, w, mv, tile, rbase, kw0, kw1);
@@ -804,6 +808,8 @@ __device__ __forceinline__ void mv_item_multi_v(const DMat& w, int it, int s, in
     typename Epi::Regs er;
     epi.load(er);
     __builtin_amdgcn_sched_barrier(0);
+    if (w.order_in) __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     const MatViews mv(w);
     WRegs<FMT, KBW> r;
     mv_load<FMT, KBW, RL>(r, w, mv, tile, rbase, kw0, kw1);
@@ -863,6 +869,8 @@ __device__ __forceinline__ void mq_item_multi_v(const DMat& w, int it, int s, in
     }
     typename Epi::Regs er;
     epi.load(er);
+    __builtin_amdgcn_sched_barrier(0);
+    if (w.order_in) __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     const MatViews mv(w);
     QRegs<QB, RL> r;
@@ -1557,12 +1565,14 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
     const size_t lds = mv_lds_bytes(w.fmt, per_split, tmp_floats) + (size_t)(ni - 1) * 512 * sizeof(float);
     const dim3 grid((p.row_tiles(w.tiles) + ni - 1) / ni * p.S), block(ni * NT);
     // POS_ARG counts kernel arguments (DMat, S, Pro, Epi): the prologue is 2
+    DMat wk = w;
+    wk.order_in = p.order_in;
     auto go = [&](void (*fn)(DMat, int, Pro, Epi)) {
-        return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, w, p.S, pro, epi);
+        return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, wk, p.S, pro, epi);
     };
     const int red_off = (int)mv_lds_floats(w.fmt, per_split, tmp_floats);
     auto go_multi = [&](void (*fn)(DMat, int, Pro, Epi, int)) {
-        return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, w, p.S, pro, epi, red_off);
+        return sink_launch<POS_ARG>(k, name, bytes, fn, grid, block, lds, wk, p.S, pro, epi, red_off);
     };
     auto by_rl = [&](auto kbw) -> int {
         constexpr int KBW = decltype(kbw)::value;

@@ -206,8 +206,8 @@ std::string env_switches() {
     static const char* vars[] = {
         "GH_PLAN_A_S", "GH_PLAN_C_S", "GH_PLAN_D_S", "GH_PLAN_E_S", "GH_PLAN_A_RL", "GH_PLAN_C_RL", "GH_PLAN_D_RL",
         "GH_PLAN_E_RL", "GH_PLAN_LM_RL", "GH_PLAN_A_NI", "GH_PLAN_C_NI", "GH_PLAN_D_NI", "GH_PLAN_E_NI",
-        "GH_PLAN_A_MFMA", "GH_PLAN_D_MFMA", "GH_PLAN_E_MFMA", "GH_PLAN_LM_MFMA", "GH_ATTN_NC", "GH_ATTN_HSPLIT",
-        "GH_ATTN_XCD", "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA"};
+        "GH_PLAN_A_MFMA", "GH_PLAN_D_MFMA", "GH_PLAN_E_MFMA", "GH_PLAN_LM_MFMA", "GH_PLAN_ORDER_IN", "GH_ATTN_NC", "GH_ATTN_HSPLIT",
+        "GH_ATTN_XCD", "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA", "GH_Q4_ORDER_IN"};
     std::string env;
     for (const char* v : vars) {
         const char* val = std::getenv(v);
@@ -309,6 +309,24 @@ void make_plans(gh_model* m) {
     m->pe.mfma = env_int("GH_PLAN_E_MFMA", m->pe.mfma);
     m->attn_nc = std::max(1, std::min(64, env_int("GH_ATTN_NC", 64)));
     m->attn_xcd = env_int("GH_ATTN_XCD", 1) ? 1 : 0;
+    // A barrier after the input loads, so that every wave's input loads
+    // (the prologue's) go out before any wave's weight loads: without it a
+    // CU's later waves queue their inputs behind the earlier waves' weights
+    // and the norm, which needs all of them, waits for most of the stream.
+    // Bits: 1 qkv, 2 o_proj, 4 gate/up, 8 down, 16 LM head.  Measured on
+    // MI355X, models differing only in this alternating in one process
+    // (three rounds each): 1B 1657 (none) / 1680 (matvec phases) / 1684
+    // (and the LM head) tok/s, 4B 773 / 786 / 788.  The same barrier in
+    // the step attention, between its prologue and its K/V loads, gained
+    // nothing (1B 1678, 4B 784 with it).
+    {
+        const int oi = env_int("GH_PLAN_ORDER_IN", 31);
+        m->pa.order_in = oi & 1;
+        m->pc.order_in = (oi >> 1) & 1;
+        m->pd.order_in = (oi >> 2) & 1;
+        m->pe.order_in = (oi >> 3) & 1;
+        m->plm.order_in = (oi >> 4) & 1;
+    }
 }
 
 int ensure_scratch(gh_model* m) {
@@ -714,6 +732,7 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     // 262144 x 1152 29.5 us against 34.5 on the VALU, 6912 x 1152 4.01
     // against 4.41, 1152 x 6912 5.76 against 5.87
     t->plan.mfma = env_int("GH_Q4_MFMA", 1);
+    t->plan.order_in = env_int("GH_Q4_ORDER_IN", 1) ? 1 : 0;
     if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
     ctx->q4s.push_back(t.get());
     *out = t.release();
@@ -1197,7 +1216,8 @@ extern "C" int gh_model_plan(gh_model* m, char* buf, size_t cap, size_t* len_out
     std::string s = std::string("step=") + (persistent ? "persistent" : env_int("GH_NO_GRAPH", 0) ? "eager" : "graph");
     auto phase = [&](const char* name, const Plan& p) {
         char t[96];
-        std::snprintf(t, sizeof t, " %s=S%d,rl%d,ni%d,%s", name, p.S, p.rl, p.ni, p.mfma ? "mfma" : "valu");
+        std::snprintf(t, sizeof t, " %s=S%d,rl%d,ni%d,%s%s", name, p.S, p.rl, p.ni, p.mfma ? "mfma" : "valu",
+                      p.order_in ? ",in_first" : "");
         s += t;
     };
     phase("qkv", m->pa);
