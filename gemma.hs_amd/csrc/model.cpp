@@ -274,13 +274,15 @@ void make_plans(gh_model* m) {
         const DMat& d = p == &m->pa ? L.qkv : p == &m->pc ? L.o : p == &m->pd ? L.gu : L.down;
         p->kbw = kbw_for(m->fmt, ((d.nblk + p->S - 1) / p->S + 3) / 4);
     }
-    // work items per workgroup: where a phase has more work items than the
-    // device has CUs, two items share one 8-wave workgroup and so one
-    // prologue, which is what bounds these items.  Measured on MI355X: 1B
-    // gate/up 432 -> 216 workgroups, 6.15 -> 5.5 us; 4B gate/up 11.6 -> 10.7
-    // us and down (320 items) 793 -> 820 tok/s.  Below the CU count pairing
-    // only halves the CUs in use (1B down, 144 items: 1538 -> 1501 tok/s);
-    // four items per 16-wave workgroup leave 128 VGPRs a lane and spill.
+    // work items per workgroup: where a phase has at least as many work
+    // items as the device has CUs, two items share one 8-wave workgroup and
+    // so one prologue, which is what bounds these items.  Measured on
+    // MI355X: 1B gate/up 432 -> 216 workgroups, 6.15 -> 5.5 us; 4B gate/up
+    // 11.6 -> 10.7 us and down (320 items) 793 -> 820 tok/s; 4B qkv (256
+    // items, with the inputs ordered ahead of the weights) 785 -> 792 tok/s.
+    // Below the CU count pairing only halves the CUs in use (1B down, 144
+    // items: 1538 -> 1501 tok/s; 1B qkv, 192 items: 1670 -> 1652); four
+    // items per 16-wave workgroup leave 128 VGPRs a lane and spill.
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->ctx->device) != hipSuccess || cus <= 0)
         cus = 256;
@@ -288,7 +290,7 @@ void make_plans(gh_model* m) {
     // paired measured 4.25 -> 4.29 us on 4B.
     for (Plan* p : {&m->pa, &m->pd, &m->pe}) {
         const DMat& d = p == &m->pa ? L.qkv : p == &m->pd ? L.gu : L.down;
-        p->ni = (long long)p->row_tiles(d.tiles) * p->S > cus ? 2 : 1;
+        p->ni = (long long)p->row_tiles(d.tiles) * p->S >= cus ? 2 : 1;
     }
     m->pa.ni = env_int("GH_PLAN_A_NI", m->pa.ni);
     m->pc.ni = env_int("GH_PLAN_C_NI", m->pc.ni);
@@ -300,9 +302,9 @@ void make_plans(gh_model* m) {
     // dot phase shrinks.  Measured on MI355X, models differing only in this
     // choice alternating in one process: 1B gate/up (12 blocks per split)
     // 5.96 -> 5.74 us, 1618 -> 1632 tok/s; 4B 751 -> 773 tok/s (gate/up)
-    // and 762 -> 773 (down).  One item per workgroup stays on the VALU: 1B
-    // qkv on the matrix cores 1618 -> 1626 tok/s but 4B qkv 773 -> 771, 1B
-    // down 1618 -> 1615.
+    // and 762 -> 773 (down); 4B qkv, paired, 791.6 -> 792.5.  One item per
+    // workgroup stays on the VALU: 1B qkv on the matrix cores 1618 -> 1626
+    // tok/s but 4B qkv 773 -> 771, 1B down 1618 -> 1615.
     for (Plan* p : {&m->pa, &m->pd, &m->pe}) p->mfma = m->fmt == FMT_Q4 && p->ni == 2 ? 1 : 0;
     m->pa.mfma = env_int("GH_PLAN_A_MFMA", m->pa.mfma);
     m->pd.mfma = env_int("GH_PLAN_D_MFMA", m->pd.mfma);
