@@ -90,6 +90,7 @@ struct Plan {
     int mfma = 0;  // Q4_0: dot products on the int8 matrix cores (1) or the VALU (0)
     int ni = 1;    // work items per workgroup (1 or 2; 4 waves each, one prologue)
     int order_in = 1;  // every wave's input loads issue before any wave's weight loads
+    int rg16 = 0;      // op level: rows per workgroup (4, 8, 16) over all columns (k_mq_rows); 0 = off
     int row_tiles(int tiles) const { return rl == 2 ? tiles : 2 * tiles; }
 };
 

@@ -207,7 +207,7 @@ std::string env_switches() {
         "GH_PLAN_A_S", "GH_PLAN_C_S", "GH_PLAN_D_S", "GH_PLAN_E_S", "GH_PLAN_A_RL", "GH_PLAN_C_RL", "GH_PLAN_D_RL",
         "GH_PLAN_E_RL", "GH_PLAN_LM_RL", "GH_PLAN_A_NI", "GH_PLAN_C_NI", "GH_PLAN_D_NI", "GH_PLAN_E_NI",
         "GH_PLAN_A_MFMA", "GH_PLAN_D_MFMA", "GH_PLAN_E_MFMA", "GH_PLAN_LM_MFMA", "GH_PLAN_ORDER_IN", "GH_ATTN_NC", "GH_ATTN_HSPLIT",
-        "GH_ATTN_XCD", "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA", "GH_Q4_ORDER_IN"};
+        "GH_ATTN_XCD", "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA", "GH_Q4_ORDER_IN", "GH_Q4_RG16"};
     std::string env;
     for (const char* v : vars) {
         const char* val = std::getenv(v);
@@ -735,7 +735,20 @@ extern "C" int gh_q4_0_upload(gh_ctx* ctx, const void* raw, int64_t rows, int64_
     // against 4.41, 1152 x 6912 5.76 against 5.87
     t->plan.mfma = env_int("GH_Q4_MFMA", 1);
     t->plan.order_in = env_int("GH_Q4_ORDER_IN", 1) ? 1 : 0;
-    if (t->plan.S > 1) GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
+    // A split plan with at most 5120 columns on the matrix cores runs as
+    // one kernel instead, one workgroup per 16 rows over all the columns
+    // (k_mq_rows).  Over rotating cold copies on MI355X: 1536 x 1152 4.70
+    // -> 3.53 us, 1152 x 1024 4.50 -> 3.48, 1024 x 2560 4.84 -> 4.02,
+    // 4096 x 2560 5.93 -> 4.63, 2560 x 5120 6.25 -> 6.08; with longer rows
+    // each workgroup's input prologue costs more than the split saves
+    // (1152 x 6912 5.70 -> 6.49, 2560 x 8192 6.91 -> 8.59).  8 or 4 rows per
+    // workgroup were slower at every shape but 640 x 4096 (4.57 vs 4.78).
+    {
+        const int R = env_int("GH_Q4_RG16", cols <= 5120 ? 16 : 0);
+        t->plan.rg16 = t->plan.mfma && t->plan.S > 1 && cols <= 8192 && (R == 4 || R == 8 || R == 16) ? R : 0;
+    }
+    if (t->plan.S > 1 && !t->plan.rg16)
+        GH_HIP(hipMalloc((void**)&t->part, sizeof(float) * t->plan.S * d.tiles * TILE_ROWS));
     ctx->q4s.push_back(t.get());
     *out = t.release();
     handle_add(*out, HK_Q4);

@@ -68,6 +68,7 @@ def test_q4_0_matvec_shapes(ctx, rows, cols, rl, mfma, monkeypatch):
     inside the bound).  480 columns: 15 blocks, a partial last quad."""
     monkeypatch.setenv("GH_Q4_RL", str(rl))
     monkeypatch.setenv("GH_Q4_MFMA", str(mfma))
+    monkeypatch.setenv("GH_Q4_RG16", "0")  # the row-group kernel has its own test
     raw = _random_q4(rows, cols, rows + cols, subnormal_frac=0.005)
     x = np.random.default_rng(rows).normal(size=cols).astype(np.float32)
     t = gh.Q4Tensor(ctx, raw, rows, cols)
@@ -77,6 +78,36 @@ def test_q4_0_matvec_shapes(ctx, rows, cols, rl, mfma, monkeypatch):
     bound = 2 * cols * np.finfo(np.float32).eps * ay
     assert np.all(np.abs(y - y64) <= bound + 1e-30)
     assert rel_err(y, orc.q4_0_matvec(raw, x, rows, cols)) < 1e-5
+
+
+@pytest.mark.parametrize("rg", ["default", "16", "8", "4"])
+@pytest.mark.parametrize("rows,cols", [(1536, 1152), (1152, 1024), (1000, 2560), (130, 96), (4, 64), (200, 480),
+                                       (1152, 6912), (40, 8192)])
+def test_q4_0_matvec_row_groups(ctx, rows, cols, rg, monkeypatch):
+    """The row-group kernel (k_mq_rows: one workgroup per 16, 8 or 4 rows over
+    all columns, the waves splitting the quads): the default routes split
+    plans of up to 5120 columns to it.  Ragged row counts (1000, 130, 200, 4)
+    leave part of the last group unstored; 8192 columns fill the input
+    registers; 480 columns end on a partial quad.  Against the f64 oracle's
+    bound, the f32 oracle, and the split-K path (GH_Q4_RG16=0) within f32
+    summation-order differences; with the soft-cap epilogue too."""
+    if rg != "default":
+        monkeypatch.setenv("GH_Q4_RG16", rg)
+    raw = _random_q4(rows, cols, rows * 3 + cols, subnormal_frac=0.005)
+    x = np.random.default_rng(cols + 1).normal(size=cols).astype(np.float32)
+    t = gh.Q4Tensor(ctx, raw, rows, cols)
+    y = t.matvec(x)
+    y64, ay = orc.q4_0_matvec_f64(raw, x, rows, cols)
+    bound = 2 * cols * np.finfo(np.float32).eps * ay
+    assert np.all(np.abs(y - y64) <= bound + 1e-30)
+    assert rel_err(y, orc.q4_0_matvec(raw, x, rows, cols)) < 1e-5
+    monkeypatch.setenv("GH_Q4_RG16", "0")
+    y_split = gh.Q4Tensor(ctx, raw, rows, cols).matvec(x)
+    assert np.all(np.abs(y - y_split) <= 2 * bound + 1e-30)
+    # soft-capped: cap * tanh(y / cap) of the same sums (runLinearQ4's arm)
+    cap = float(np.median(np.abs(y64))) + 1e-3
+    yc = t.matvec(x, softcap=True, cap=cap)
+    assert np.allclose(yc, cap * np.tanh(y.astype(np.float64) / cap), rtol=4e-6, atol=1e-7 * cap)
 
 
 @pytest.mark.parametrize("mfma", [0, 1])
