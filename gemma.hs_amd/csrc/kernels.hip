@@ -949,6 +949,72 @@ __global__ __launch_bounds__(NT) void k_matvec(DMat w, int S, Pro pro, Epi epi) 
     mv_item<FMT, KBW, RL>(w, blockIdx.x / S, blockIdx.x % S, S, pro, epi, mv_lds<FMT>(lds, per_split));
 }
 
+constexpr int RG16_QB = 14;  // quads per register batch: a wave's share of 224 blocks in one batch
+
+// Q4_0 matvec for matrices of few rows (the op level's 1536 x 1152): one
+// workgroup per group of R rows (16, 8 or 4; R divides 128) over all the
+// columns, on the matrix cores.  Lane l's MFMA row is row (l & 15) of the
+// group; rows past R load nothing (their products are zeros and are not
+// stored).  The four waves split the quads and add their dot products in
+// LDS: one kernel and no split partials, where 64-row items need up to 16
+// column splits and a partial-sum kernel to fill the device.  As the step's
+// qkv (the residual prologue then lays out the whole vector once per 16
+// rows, and attention reads one vector instead of 8 split partials) it was
+// slower on MI355X: 1B 1673 -> 1598 tok/s, 4B 796 -> 768.
+template <class Pro, class Epi>
+__global__ __launch_bounds__(NT) void k_mq_rows(DMat w, int R, Pro pro, Epi epi) {
+    extern __shared__ float lds[];
+    const int nb = w.nblk;
+    const MvLds L = mv_lds<FMT_Q4M>(lds, nb);
+    const int row0 = blockIdx.x * R, tile = row0 / TILE_ROWS, rt0 = row0 % TILE_ROWS;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int nq = (nb + 3) >> 2;
+    const int q_lo = __builtin_amdgcn_readfirstlane(nq * wave >> 2);
+    const int q_hi = __builtin_amdgcn_readfirstlane(nq * (wave + 1) >> 2);
+    const int kb1 = min(nb, 4 * q_hi);  // blocks of later waves read zeros
+    const bool row_ok = (lane & 15) < R;
+    typename Pro::Regs pr;
+    pro.load(pr, 0, nb * 32);
+    typename Epi::Regs er;
+    epi.load(er);
+    __builtin_amdgcn_sched_barrier(0);
+    if (w.order_in) __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const MatViews mv(w);
+    const uint32_t tb = (uint32_t)tile * (uint32_t)nb * TILE_ROWS + (uint32_t)(rt0 + (lane & 15));
+    QRegs<RG16_QB, 1> r;
+    auto load = [&](int kq) {
+#pragma unroll
+        for (int i = 0; i < RG16_QB; ++i) {
+            const int ka = kq + 4 * i + (lane >> 4);
+            const uint32_t ea = tb + (uint32_t)ka * TILE_ROWS;
+            const bool ok = row_ok && ka < kb1;
+            r.c[0][i] = mv.codes.template u4<CP_NT>(ok ? ea * 16u : OOB);
+            r.s[0][i] = mv.scales.template h1<CP_NT>(ok ? ea * 2u : OOB);
+        }
+    };
+    load(4 * q_lo);
+    __builtin_amdgcn_sched_barrier(0);
+    pro.template finish<FMT_Q4M>(L, pr, 0, nb * 32);
+    if (threadIdx.x < 4) L.zero[threadIdx.x] = 0.0f;
+    __syncthreads();
+    float acc[1] = {0.0f};
+    mq_compute<RG16_QB, 1>(r, q_lo, q_hi, L, acc);
+    for (int q0 = q_lo + RG16_QB; q0 < q_hi; q0 += RG16_QB) {
+        load(4 * q0);
+        mq_compute<RG16_QB, 1>(r, q0, q_hi, L, acc);
+    }
+    // the four blocks of each row, then the four waves; lane m < R holds row m
+    acc[0] += __shfl_xor(acc[0], 32, 64);
+    acc[0] += __shfl_xor(acc[0], 16, 64);
+    if (lane < 16) L.red[16 * wave + lane] = acc[0];
+    __syncthreads();
+    if (wave == 0 && lane < R) {
+        const float y = (L.red[lane] + L.red[16 + lane]) + (L.red[32 + lane] + L.red[48 + lane]);
+        epi.template run<1>(L, er, blockIdx.x, row0 + lane, 0, y, 0.0f);
+    }
+}
+
 // ------------------------------------------------------------------
 // prologues: load() issues the global loads of the input, finish<FMT>()
 // builds xs[0 .. n) = input[c0 .. c0+n) in LDS through emit_x4
@@ -5052,85 +5118,27 @@ __global__ void k_sum_partials(const float* part, int S, int ld, int rows, int s
 }
 
 // The whole input vector (up to 256 * MG float4 groups) in registers, loaded
-// in one round trip, for the 16-row-group kernel below.
+// in one round trip, for the row-group kernel (k_mq_rows).
 template <int MG>
 struct ProWide {
     const float* x;
     struct Regs {
         float4 v[MG];
     };
-    __device__ void load(Regs& r, int n) const {
-        const BufView X(x, (size_t)n * 4);
+    __device__ void load(Regs& r, int c0, int n) const {
+        const BufView X(x + c0, (size_t)n * 4);
 #pragma unroll
         for (int k = 0; k < MG; ++k) r.v[k] = X.f4(16u * (threadIdx.x + k * NT));
     }
-    __device__ void finish(const MvLds& L, Regs& r, int n) const {
+    template <int FMT>
+    __device__ void finish(const MvLds& L, Regs& r, int, int n) const {
         const int ng = n >> 2;
 #pragma unroll
         for (int k = 0; k < MG; ++k)
-            if (k * NT < ng) emit_x4<FMT_Q4M>(L, threadIdx.x + k * NT, ng, r.v[k]);
+            if (k * NT < ng) emit_x4<FMT>(L, threadIdx.x + k * NT, ng, r.v[k]);
     }
 };
 constexpr int RG16_MG = 8;   // input columns up to 8192
-constexpr int RG16_QB = 14;  // quads per register batch: a wave's share of 224 blocks in one batch
-
-// Op-level Q4_0 matvec for matrices of few rows (1152 x 6912, 1536 x 1152):
-// one workgroup per group of R rows (16, 8 or 4; R divides 128) over all the
-// columns, on the matrix cores.  Lane l's MFMA row is row (l & 15) of the
-// group; rows past R load nothing (their products are zeros and are not
-// stored).  The four waves split the quads and add their dot products in
-// LDS: one kernel and no split partials, where 64-row items need up to 16
-// column splits and a partial-sum kernel to fill the device.
-__global__ __launch_bounds__(NT) void k_mq_rows(DMat w, int R, ProWide<RG16_MG> pro, EpiOut epi) {
-    extern __shared__ float lds[];
-    const int nb = w.nblk;
-    const MvLds L = mv_lds<FMT_Q4M>(lds, nb);
-    const int row0 = blockIdx.x * R, tile = row0 / TILE_ROWS, rt0 = row0 % TILE_ROWS;
-    const int wave = wave_id(), lane = threadIdx.x & 63;
-    const int nq = (nb + 3) >> 2;
-    const int q_lo = __builtin_amdgcn_readfirstlane(nq * wave >> 2);
-    const int q_hi = __builtin_amdgcn_readfirstlane(nq * (wave + 1) >> 2);
-    const int kb1 = min(nb, 4 * q_hi);  // blocks of later waves read zeros
-    const bool row_ok = (lane & 15) < R;
-    typename ProWide<RG16_MG>::Regs pr;
-    pro.load(pr, nb * 32);
-    __builtin_amdgcn_sched_barrier(0);
-    if (w.order_in) __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    const MatViews mv(w);
-    const uint32_t tb = (uint32_t)tile * (uint32_t)nb * TILE_ROWS + (uint32_t)(rt0 + (lane & 15));
-    QRegs<RG16_QB, 1> r;
-    auto load = [&](int kq) {
-#pragma unroll
-        for (int i = 0; i < RG16_QB; ++i) {
-            const int ka = kq + 4 * i + (lane >> 4);
-            const uint32_t ea = tb + (uint32_t)ka * TILE_ROWS;
-            const bool ok = row_ok && ka < kb1;
-            r.c[0][i] = mv.codes.template u4<CP_NT>(ok ? ea * 16u : OOB);
-            r.s[0][i] = mv.scales.template h1<CP_NT>(ok ? ea * 2u : OOB);
-        }
-    };
-    load(4 * q_lo);
-    __builtin_amdgcn_sched_barrier(0);
-    pro.finish(L, pr, nb * 32);
-    if (threadIdx.x < 4) L.zero[threadIdx.x] = 0.0f;
-    __syncthreads();
-    float acc[1] = {0.0f};
-    mq_compute<RG16_QB, 1>(r, q_lo, q_hi, L, acc);
-    for (int q0 = q_lo + RG16_QB; q0 < q_hi; q0 += RG16_QB) {
-        load(4 * q0);
-        mq_compute<RG16_QB, 1>(r, q0, q_hi, L, acc);
-    }
-    // the four blocks of each row, then the four waves; lane m < R holds row m
-    acc[0] += __shfl_xor(acc[0], 32, 64);
-    acc[0] += __shfl_xor(acc[0], 16, 64);
-    if (lane < 16) L.red[16 * wave + lane] = acc[0];
-    __syncthreads();
-    if (wave == 0 && lane < R) {
-        const float y = (L.red[lane] + L.red[16 + lane]) + (L.red[32 + lane] + L.red[48 + lane]);
-        epi.template run<1>(L, typename EpiOut::Regs{}, blockIdx.x, row0 + lane, 0, y, 0.0f);
-    }
-}
 
 int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* part, float* y, int softcap, float cap,
                         hipStream_t s) {
@@ -5144,7 +5152,8 @@ int launch_matvec_plain(const DMat& w, const Plan& p, const float* x, float* par
         ProWide<RG16_MG> pro{x};
         EpiOut epi{y, w.rows, softcap, cap};
         const size_t lds = mv_lds_bytes(FMT_Q4M, w.nblk, 0);
-        hipLaunchKernelGGL(k_mq_rows, dim3((w.rows + R - 1) / R), dim3(NT), lds, s, wk, R, pro, epi);
+        hipLaunchKernelGGL((k_mq_rows<ProWide<RG16_MG>, EpiOut>), dim3((w.rows + R - 1) / R), dim3(NT), lds, s, wk, R,
+                           pro, epi);
         GH_HIP(hipGetLastError());
         return GH_OK;
     }
