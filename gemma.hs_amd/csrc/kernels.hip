@@ -1650,13 +1650,10 @@ static int launch_mv(Sink& k, const char* name, double bytes, const DMat& w, con
                 return p.rl == 2 ? go_multi(k_matvec_multi<FMT_Q4, KBW, 2, 2, Pro, Epi>)
                                  : go_multi(k_matvec_multi<FMT_Q4, KBW, 1, 2, Pro, Epi>);
         }
-        // one item per workgroup: the matrix-core dot products serve plain
-        // input vectors (the LM head, op-level matvecs); other prologues
-        // use the VALU
-        if constexpr (std::is_same_v<Pro, ProPlain>) {
-            if (p.mfma)
-                return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
-        }
+        // one item per workgroup on the matrix cores: the LM head and the
+        // op-level matvecs by default
+        if (p.mfma)
+            return p.rl == 2 ? go(k_matvec<FMT_Q4M, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4M, KBW, 1, Pro, Epi>);
         return p.rl == 2 ? go(k_matvec<FMT_Q4, KBW, 2, Pro, Epi>) : go(k_matvec<FMT_Q4, KBW, 1, Pro, Epi>);
     };
     if (p.rl != 1 && p.rl != 2) return set_error(GH_ERR_INVALID, "unsupported rows per lane %d", p.rl);

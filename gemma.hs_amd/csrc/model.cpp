@@ -206,7 +206,7 @@ std::string env_switches() {
     static const char* vars[] = {
         "GH_PLAN_A_S", "GH_PLAN_C_S", "GH_PLAN_D_S", "GH_PLAN_E_S", "GH_PLAN_A_RL", "GH_PLAN_C_RL", "GH_PLAN_D_RL",
         "GH_PLAN_E_RL", "GH_PLAN_LM_RL", "GH_PLAN_A_NI", "GH_PLAN_C_NI", "GH_PLAN_D_NI", "GH_PLAN_E_NI",
-        "GH_PLAN_A_MFMA", "GH_PLAN_D_MFMA", "GH_PLAN_E_MFMA", "GH_PLAN_LM_MFMA", "GH_PLAN_ORDER_IN", "GH_ATTN_NC", "GH_ATTN_HSPLIT",
+        "GH_PLAN_A_MFMA", "GH_PLAN_C_MFMA", "GH_PLAN_D_MFMA", "GH_PLAN_E_MFMA", "GH_PLAN_LM_MFMA", "GH_PLAN_ORDER_IN", "GH_ATTN_NC", "GH_ATTN_HSPLIT",
         "GH_ATTN_XCD", "GH_PERSISTENT", "GH_NO_GRAPH", "GH_Q4_TARGET", "GH_Q4_MAXS", "GH_Q4_RL", "GH_Q4_MFMA", "GH_Q4_ORDER_IN", "GH_Q4_RG16"};
     std::string env;
     for (const char* v : vars) {
@@ -302,11 +302,16 @@ void make_plans(gh_model* m) {
     // dot phase shrinks.  Measured on MI355X, models differing only in this
     // choice alternating in one process: 1B gate/up (12 blocks per split)
     // 5.96 -> 5.74 us, 1618 -> 1632 tok/s; 4B 751 -> 773 tok/s (gate/up)
-    // and 762 -> 773 (down); 4B qkv, paired, 791.6 -> 792.5.  One item per
-    // workgroup stays on the VALU: 1B qkv on the matrix cores 1618 -> 1626
-    // tok/s but 4B qkv 773 -> 771, 1B down 1618 -> 1615.
+    // and 762 -> 773 (down); 4B qkv, paired, 791.6 -> 792.5.  The down
+    // projection takes the matrix cores as single items too (its VALU dot
+    // phase was 1.4 us of a 3 us chain on 1B): 1B 1678 -> 1728 tok/s once
+    // the inputs were ordered ahead of the weights (1618 -> 1615 before).
+    // Single-item qkv and o_proj stay on the VALU: 1B 1674 and 1670 against
+    // 1678, 4B o_proj 790 against 796.
     for (Plan* p : {&m->pa, &m->pd, &m->pe}) p->mfma = m->fmt == FMT_Q4 && p->ni == 2 ? 1 : 0;
+    if (m->fmt == FMT_Q4) m->pe.mfma = 1;
     m->pa.mfma = env_int("GH_PLAN_A_MFMA", m->pa.mfma);
+    m->pc.mfma = m->fmt == FMT_Q4 ? env_int("GH_PLAN_C_MFMA", m->pc.mfma) : 0;
     m->pd.mfma = env_int("GH_PLAN_D_MFMA", m->pd.mfma);
     m->pe.mfma = env_int("GH_PLAN_E_MFMA", m->pe.mfma);
     m->attn_nc = std::max(1, std::min(64, env_int("GH_ATTN_NC", 64)));
