@@ -221,10 +221,10 @@ void make_plans(gh_model* m) {
     m->plan_env = env_switches();
     const LayerDev& L = m->layers[0];
     // Measured on MI355X (sweeps of S x RL on the gemma3-1b and gemma3-4b
-    // shapes): o_proj, down and the LM head run fastest as 64-row
-    // workgroups (RL 1), down with 8 splits; qkv too up to 31 tiles, as
-    // 128-row workgroups with 8 splits from 32 tiles (4B: 6.3 vs 7.0 us);
-    // gate/up as 128-row work items with about 288 / tiles splits (1B: 3,
+    // shapes): qkv, o_proj, down and the LM head run fastest as 64-row
+    // work items (RL 1), qkv, o_proj and down with 8 splits (4B qkv, paired
+    // on the matrix cores: 805 tok/s against 798 as 128-row items, which
+    // won on the VALU, 6.3 vs 7.0 us; 1B 1734 against 1712); gate/up as 128-row work items with about 288 / tiles splits (1B: 3,
     // 4B: 2, raised to 3 below); with paired items 1B runs 5.38 us at 3
     // splits against 5.45 at 4 (1560 vs 1556 tok/s).
     m->pa = choose_plan(m->fmt, L.qkv.tiles, L.qkv.nblk, 256);
@@ -237,8 +237,7 @@ void make_plans(gh_model* m) {
     while (m->fmt == FMT_Q4 && m->pd.S < 8 && ((L.gu.nblk + m->pd.S - 1) / m->pd.S + 3) / 4 > 9) ++m->pd.S;
     m->pe = choose_plan(m->fmt, L.down.tiles, L.down.nblk, 8 * L.down.tiles);
     m->plm = choose_plan(lm_mat(m).fmt, lm_mat(m).tiles, lm_mat(m).nblk, 1);
-    m->pc.rl = m->pe.rl = m->plm.rl = 1;
-    m->pa.rl = L.qkv.tiles >= 32 ? 2 : 1;
+    m->pa.rl = m->pc.rl = m->pe.rl = m->plm.rl = 1;
     auto over = [&](Plan& p, const char* env, const DMat& d) {
         int s = env_int(env, 0);
         if (s > 0) {
