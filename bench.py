@@ -42,10 +42,10 @@ C3_MEAN_POSITION = 256  # C3: prompt 128, greedy generation at positions 128..38
 # WRITE_SIZE, each scaled by bytes / counter of a 256 MiB device copy) over
 # replays of each kernel kind at position 257 (kernel_profile run --prompt
 # 256 --prefill-prompt): profiles/step_kernels_gemma3-1b_decode_c3.md,
-# gate/up 9,637,433 fetched + 170,496 written, the LM head 172,229,479 +
-# 1,179,648.
-GATE_UP_TRAFFIC_BYTES = 9_807_929
-LM_HEAD_TRAFFIC_BYTES = 173_409_127
+# gate/up 9,641,342 fetched + 170,496 written, the LM head 172,293,019 +
+# 1,179,657.
+GATE_UP_TRAFFIC_BYTES = 9_811_838
+LM_HEAD_TRAFFIC_BYTES = 173_472_676
 TRAFFIC_PROFILE = "profiles/step_kernels_gemma3-1b_decode_c3.md"
 # the in-step kernel timings: C3's decode positions 128..383
 PROFILE_STEPS = 256
