@@ -221,8 +221,9 @@ int gh_model_config(gh_model* m, gh_config* out);
  * space-separated key=value items: the step mode (graph, eager or
  * persistent; GH_NO_GRAPH is read at every step, so eager reflects it now),
  * then per matvec phase (qkv, o_proj, gate_up, down, lm_head) its column
- * splits S, rows per lane rl, work items per workgroup ni and dot-product
- * unit (valu or mfma), the attention chunks per kv head, the LM head (tied
+ * splits S, rows per lane rl, work items per workgroup ni, dot-product unit
+ * (valu or mfma) and in_first when every wave's input loads are issued before
+ * any weight load, the attention chunks per kv head, the LM head (tied
  * or untied), and env= with every GH_* environment variable that was set
  * when the plan was made and can change what runs (the tuning and study
  * switches GH_PLAN_*, GH_Q4_*, GH_ATTN_*, GH_PERSISTENT, GH_NO_GRAPH), or
