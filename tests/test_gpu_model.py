@@ -240,8 +240,10 @@ def test_attention_workgroup_order_is_bit_identical_live_oracle(ctx, monkeypatch
     for xcd in ("0", "1"):
         monkeypatch.setenv("GH_ATTN_XCD", xcd)
         m = _gpu_model(ctx, cfg, 31, True)
-        assert ("xcd_off" in m.plan()) == (xcd == "0")
+        gh.runGemmaInferenceCached(m, 0, gh.KVCache(m, 4), want_logits=False)  # the plan is fixed at the first step
         models.append((m, gh.KVCache(m, 64)))
+    for (m, _), xcd in zip(models, ("0", "1")):
+        assert ("xcd_off" in m.plan()) == (xcd == "0")
     om = _oracle_model(cfg, 31, True)
     toks = gh.synth_tokens(10, "t", 40, cfg.vocab)
     for pos, t in enumerate(toks):
@@ -254,6 +256,32 @@ def test_attention_workgroup_order_is_bit_identical_live_oracle(ctx, monkeypatch
             for l in range(cfg.n_layers):
                 assert rel_err(y1[l], olay[l]) < ACT_TOL, (pos, l)
             assert rel_err(l1, olog) < ACT_TOL, pos
+
+
+def test_input_load_ordering_is_bit_identical(ctx, monkeypatch):
+    """GH_PLAN_ORDER_IN sets which matvec phases put a barrier between their
+    input loads and their weight loads (bits: qkv, o_proj, gate/up, down,
+    LM head; default all).  The barrier orders only when loads are issued,
+    not the arithmetic, so layer states and logits are bit-identical with
+    none, some and all of them, on the VALU and matrix-core phases alike
+    (the mini-4B shapes: paired qkv, gate/up and down on the matrix cores)."""
+    cfg = _mini4b_cfg()
+    models = []
+    for oi in ("0", "5", "31"):
+        monkeypatch.setenv("GH_PLAN_ORDER_IN", oi)
+        m = _gpu_model(ctx, cfg, 17, True)
+        gh.runGemmaInferenceCached(m, 0, gh.KVCache(m, 4), want_logits=False)  # the plan is fixed at the first step
+        models.append((m, gh.KVCache(m, 32)))
+    for (m, _), n_first in zip(models, (0, 2, 5)):
+        assert m.plan().count("in_first") == n_first, m.plan()
+    toks = gh.synth_tokens(5, "oi", 12, cfg.vocab)
+    for pos, t in enumerate(toks):
+        outs = [gh.runGemmaInferenceCachedWithLayer0(m, int(t), kv) for m, kv in models]
+        l0, _, y0, n0 = outs[0]
+        for l1, _, y1, n1 in outs[1:]:
+            assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32)), pos
+            assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32)), pos
+            assert n0 == n1
 
 
 def test_errors_kv_full_bad_token_incomplete_model(ctx):

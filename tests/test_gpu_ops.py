@@ -80,6 +80,19 @@ def test_q4_0_matvec_shapes(ctx, rows, cols, rl, mfma, monkeypatch):
     assert rel_err(y, orc.q4_0_matvec(raw, x, rows, cols)) < 1e-5
 
 
+@pytest.mark.parametrize("rows,cols", [(6912, 1152), (1152, 6912), (1536, 1152)])
+def test_q4_0_matvec_input_ordering_is_bit_identical(ctx, rows, cols, monkeypatch):
+    """GH_Q4_ORDER_IN=0 drops the barrier between the input and weight loads;
+    the arithmetic is the same, so the outputs are bit-identical."""
+    raw = _random_q4(rows, cols, rows + 2 * cols)
+    x = np.random.default_rng(5).normal(size=cols).astype(np.float32)
+    ys = []
+    for oi in ("0", "1"):
+        monkeypatch.setenv("GH_Q4_ORDER_IN", oi)
+        ys.append(gh.Q4Tensor(ctx, raw, rows, cols).matvec(x))
+    assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("rg", ["default", "16", "8", "4"])
 @pytest.mark.parametrize("rows,cols", [(1536, 1152), (1152, 1024), (1000, 2560), (130, 96), (4, 64), (200, 480),
                                        (1152, 6912), (40, 8192)])
